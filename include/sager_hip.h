@@ -1,0 +1,195 @@
+/* sager_hip.h - C ABI of libsager_hip.so, the MI355X (gfx950) implementation
+ * of SAGER's quantized MoE decode hot path.
+ *
+ * This header is the drop-in boundary. It replaces the hot subset of the
+ * reference's launcher API `namespace sager::cuda` in
+ * include/sager/kernels/cuda_ops.hpp (the "ONLY surface the session loop
+ * sees", cuda_ops.hpp:1-7) with extern "C" functions on plain pointers:
+ *
+ *   - every pointer argument is a DEVICE pointer unless stated otherwise;
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream);
+ *   - every call is stream-ordered and never synchronizes (cuda_ops.hpp:4-6);
+ *   - the caller owns every buffer; no function allocates device memory
+ *     (the fused layer takes a caller-provided workspace);
+ *   - the return value is a status (0 = ok) instead of the reference's
+ *     `void` + cudaGetLastError; sg_last_error() gives the message of the
+ *     last failure on the calling thread.
+ *
+ * Formats (include/sager/kernels/q4_k.hpp:39-62), both byte-packed:
+ *   sg_block_q4k: 256 weights in 144 B  - fp16 d | fp16 dmin | 12 B packed
+ *                 6-bit scales/mins | 128 B nibbles (group g = bytes
+ *                 32g..32g+31: low nibbles are sub-block 2g, high 2g+1).
+ *   sg_block_q8k: 256 activations in 276 B - fp32 d | 256 x int8 |
+ *                 8 x int16 sub-block sums.
+ * A matrix is n_rows x (k/256) blocks, row-major; k must be a multiple of
+ * 256. Activation rows are k/256 consecutive Q8_K blocks per token.
+ */
+#ifndef SAGER_HIP_H
+#define SAGER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#pragma pack(push, 1)
+typedef struct sg_block_q4k {
+  uint16_t d;
+  uint16_t dmin;
+  uint8_t scales[12];
+  uint8_t qs[128];
+} sg_block_q4k;
+
+typedef struct sg_block_q8k {
+  float d;
+  int8_t qs[256];
+  int16_t bsums[8];
+} sg_block_q8k;
+#pragma pack(pop)
+
+/* Status codes; numeric values follow sager::Status (common.hpp:68-79). */
+enum {
+  SG_OK = 0,
+  SG_ERR_INVALID_ARGUMENT = 1,
+  SG_ERR_GEOMETRY = 4,
+  SG_ERR_HIP = 7,
+  SG_ERR_UNSUPPORTED = 8
+};
+
+/* Message of the last non-zero status returned on this thread ("" if none). */
+const char* sg_last_error(void);
+/* Library version string. */
+const char* sg_version(void);
+
+/* ---- Q8_K activation quantization ------------------------------------
+ * out[r] = Q8_K(x[r]) for n_rows rows of n values (n % 256 == 0):
+ * per block amax (start 1e-30), d = amax/127, q = round-half-even(x/d)
+ * clamped to +-127, bsums = per-32 sums.  Bit-exact with
+ * quantize_row_q8_K (q4_k.cpp:44-61).
+ * Replaces cuda::quantize_q8_k (cuda_ops.hpp:271-273), which takes fp16
+ * input; this one takes fp32 rows (the CPU chain's input, q4_avx2.cpp:180). */
+int sg_quantize_q8_k(const float* x, sg_block_q8k* out, int n, int n_rows,
+                     void* stream);
+/* fp16 input, the exact argument meaning of cuda::quantize_q8_k. */
+int sg_quantize_q8_k_f16(const uint16_t* x, sg_block_q8k* out, int n,
+                         int n_rows, void* stream);
+
+/* ---- Q4_K x Q8_K GEMV family -----------------------------------------
+ * Row result, fp32, in the reference CPU order (q4_avx2.cpp:124-145 as
+ * built): per super-block sum_s fma(xd, fma(sd, ip_s, -(sm*bsum_s)), .),
+ * then the block sums added in block order. */
+
+/* y[r] = W[r] . x.  Replaces cuda::gemv_q4_k_q8 (cuda_ops.hpp:41-42). */
+int sg_gemv_q4_k_q8(const sg_block_q4k* w, const sg_block_q8k* x, float* y,
+                    int n_rows, int k, void* stream);
+
+/* y[t*n_rows + r] = W[r] . x[t] for t < n_tokens (1..16); each weight row is
+ * read once for all tokens.  Replaces cuda::gemv_q4_k_q8_batched
+ * (cuda_ops.hpp:72-74) and the mtok tiled variants (cuda_ops.hpp:88-90). */
+int sg_gemv_q4_k_q8_batched(const sg_block_q4k* w, const sg_block_q8k* x,
+                            float* y, int n_rows, int k, int n_tokens,
+                            void* stream);
+
+/* Pointer-table GEMV: row r is row (r % rows_per) of matrix ptrs[r/rows_per]
+ * (ptrs is a DEVICE array of n_ptrs device pointers); y[r] fp32 for
+ * r < n_ptrs*rows_per.  Replaces cuda::gemv_ptrs_q4_k_q8_f16out
+ * (cuda_ops.hpp:60-63) with an fp32 output. */
+int sg_gemv_ptrs_q4_k_q8(const sg_block_q4k* const* ptrs,
+                         const sg_block_q8k* x, float* y, int n_ptrs,
+                         int rows_per, int k, void* stream);
+
+/* Test hook: the int32 sub-block dot sums the GEMVs use,
+ * dots[(r*(k/256) + b)*8 + s] = sum_l nibble * xq for sub-block s of block b.
+ * No launcher counterpart; the device routine it exposes is the reference's
+ * dp4a_subblock (q4_k.cu:38-53). */
+int sg_q4k_subblock_dots(const sg_block_q4k* w, const sg_block_q8k* x,
+                         int32_t* dots, int n_rows, int k, void* stream);
+
+/* ---- router, SiLU, combine -------------------------------------------- */
+
+/* Per row: softmax over n_expert logits, n_expert_used rounds of argmax
+ * (NaN skipped, lower index wins ties), weights renormalized by their sum,
+ * weight[row*idx_stride + n_expert_used] = shared_w.  idx/weight rows have
+ * stride idx_stride >= n_expert_used + 1.  n_expert <= 1024.
+ * Replaces cuda::router_topk / router_topk_batched (cuda_ops.hpp:351-360),
+ * moe.cu:25-85, 165-234. */
+int sg_router_topk(const float* logits, int* idx, float* weight, int n_expert,
+                   int n_expert_used, int idx_stride, int n_rows,
+                   float shared_w, void* stream);
+
+/* out[i] = g[i] / (1 + exp(-g[i])) * u[i], fp32 (q4_avx2.cpp:187-191).
+ * Replaces cuda::silu_mul_f16 (cuda_ops.hpp:305-306) with fp32 buffers. */
+int sg_silu_mul(float* out, const float* g, const float* u, int n,
+                void* stream);
+
+/* out[r][i] = residual[r][i] + sum_{kk=0..n_used} weight[r][kk] *
+ * expert_y[r][kk][i] (one fma per slot, kk order); weight rows have stride
+ * n_used+1 and expert_y is [n_rows][n_used+1][hidden]. residual may be NULL
+ * (zero) and may alias out.  Replaces cuda::moe_combine_batched_f16
+ * (cuda_ops.hpp:397-399, moe.cu:265-280) with fp32 buffers. */
+int sg_moe_combine(float* out, const float* residual, const float* expert_y,
+                   const float* weight, int n_used, int hidden, int n_rows,
+                   void* stream);
+
+/* ---- fused MoE layer (decode step / verify window) --------------------
+ * One MoE layer for n_tokens (1..16) tokens, in the stage order of the
+ * reference's device path Session::moe_dispatch_device
+ * (session.cpp:2482-3030): Q8_K(x) -> router top-k -> every routed expert
+ * and the shared expert as gate/up GEMV, h = SiLU(g)*u, Q8_K(h), down GEMV
+ * -> combine with slot k = shared expert (weight shared_w).  Experts shared
+ * by several tokens are read from HBM once for all of them.
+ *
+ *   tab_gate/up/down: DEVICE arrays [n_expert] of expert matrices
+ *                     (gate/up n_ff x hidden, down hidden x n_ff) - one
+ *                     layer's slice of the [3][layer][E] pointer table
+ *                     (session.cpp:2787-2796).
+ *   sh_gate/up/down:  shared expert (n_ff x hidden etc.), or all NULL.
+ *   x:        fp32 [n_tokens][hidden] layer input.
+ *   logits:   fp32 [n_tokens][n_expert]; if NULL, idx/weight are INPUTS
+ *             (routing decided by the caller, e.g. sampled routing).
+ *   residual: fp32 [n_tokens][hidden] or NULL (zero); may alias out.
+ *   out:      fp32 [n_tokens][hidden].
+ *   idx, weight: [n_tokens][k+1] (slot k of weight = shared_w).
+ *   workspace: device buffer of at least sg_moe_layer_workspace_bytes().
+ * Routes with an id outside [0, n_expert) zero that token's whole weight row
+ * (shared slot included), as moe_dispatch_scan does (moe.cu:385-396); a null
+ * table entry is an absent expert and contributes zero (q4_k.cu:697-710).
+ * Limits: hidden <= 8192 and n_ff <= 16384 (multiples of 256), k <= 32,
+ * n_expert <= 1024.  Calls that share a workspace must be stream-ordered. */
+size_t sg_moe_layer_workspace_bytes(int n_tokens, int hidden, int n_ff,
+                                    int n_expert, int k);
+int sg_moe_layer(const sg_block_q4k* const* tab_gate,
+                 const sg_block_q4k* const* tab_up,
+                 const sg_block_q4k* const* tab_down,
+                 const sg_block_q4k* sh_gate, const sg_block_q4k* sh_up,
+                 const sg_block_q4k* sh_down, const float* x,
+                 const float* logits, const float* residual, float* out,
+                 int* idx, float* weight, void* workspace,
+                 size_t workspace_bytes, int n_tokens, int hidden, int n_ff,
+                 int n_expert, int k, float shared_w, void* stream);
+
+/* The three launches of sg_moe_layer, selectable: bit 0 = route (Q8_K of
+ * x, top-k, plan), bit 1 = gate/up + SiLU, bit 2 = down + combine.  A stage
+ * reads what the earlier stages left in `workspace`, so a caller may run them
+ * separately on one stream (e.g. to overlap other work between them or to
+ * time one stage); stages = 7 is sg_moe_layer.  The reference issues these
+ * as separate launchers from Session::moe_dispatch_device
+ * (session.cpp:2524-2556 route, :2791-2803 gate/up + SiLU + requant,
+ * :2820-2843 down + scatter, :3029 combine). */
+int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate,
+                        const sg_block_q4k* const* tab_up,
+                        const sg_block_q4k* const* tab_down,
+                        const sg_block_q4k* sh_gate, const sg_block_q4k* sh_up,
+                        const sg_block_q4k* sh_down, const float* x,
+                        const float* logits, const float* residual, float* out,
+                        int* idx, float* weight, void* workspace,
+                        size_t workspace_bytes, int n_tokens, int hidden,
+                        int n_ff, int n_expert, int k, float shared_w,
+                        int stages, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SAGER_HIP_H */

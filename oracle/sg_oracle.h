@@ -1,0 +1,116 @@
+/* sg_oracle.h - CPU oracle for the quantized MoE decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP product
+ * library (libsager_hip.so). Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it; the product path never calls it.
+ *
+ * It restates, in plain C, the reference's CPU semantics for:
+ *   - the Q4_K / Q8_K formats          include/sager/kernels/q4_k.hpp:39-118
+ *   - Q8_K activation quantization     src/kernels/q4_k.cpp:44-61
+ *   - int32 sub-block dots             src/kernels/q4_k.cpp:195-199
+ *   - the fp32 Q4_K x Q8_K GEMV        src/kernels/cpu/q4_avx2.cpp:124-145
+ *   - the fp32 expert FFN              src/kernels/cpu/q4_avx2.cpp:175-196
+ *   - router softmax/top-k/renorm      src/kernels/cuda/moe.cu:25-85
+ *   - the fp32 combine                 src/kernels/cuda/moe.cu:265-280
+ *   - the MoE layer stage order        src/core/session.cpp:2482-3030
+ *
+ * Every function is pinned by a test (golden vectors from the reference's own
+ * CPU sources, closed forms, brute force, or order-free invariants); see the
+ * oracle tests under tests/.
+ */
+#ifndef SG_ORACLE_H
+#define SG_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORC_QK_K 256
+#define ORC_Q4K_BYTES 144
+#define ORC_Q8K_BYTES 276
+
+/* fp16 bits -> fp32 (exact). q4_k.hpp:66-88 */
+float orc_half_to_float(uint16_t h);
+/* 6-bit scale/min of sub-block j (0..7) from the 12 packed bytes. q4_k.hpp:110-118 */
+void orc_get_scale_min(int j, const uint8_t* q, uint8_t* d, uint8_t* m);
+/* Q4_K row(s) -> fp32 weights. q4_k.cpp:13-42 */
+void orc_dequant(const void* w, float* out, int64_t n);
+
+/* fp32 [n_rows][n] -> Q8_K blocks (n % 256 == 0). q4_k.cpp:44-61 */
+void orc_quantize_q8_k(const float* x, void* out, int n, int n_rows);
+
+/* int32 dots per sub-block: dots[r][b*8+s] = sum_l nib * xq. q4_k.cpp:195-199 */
+void orc_subblock_dots(const void* w, const void* xq, int32_t* dots, int n_rows,
+                       int k);
+
+/* y[tok][r] = W[r] . xq[tok], fp32 in the AVX2 order (q4_avx2.cpp:124-145):
+ * per super-block sum_s xd*(sd*ip - sm*bsum), then acc += block sum. */
+void orc_gemv_q4k_q8(const void* w, const void* xq, float* y, int n_rows, int k,
+                     int n_tokens);
+
+/* exp for float arguments, evaluated in double and rounded once (stands in
+ * for std::exp(float) of q4_avx2.cpp:189 and expf of moe.cu:38-43). */
+float orc_expf(float x);
+/* h = g/(1+exp(-g))*u, the fp32 chain of q4_avx2.cpp:187-191 */
+void orc_silu_mul(const float* g, const float* u, float* h, int n);
+
+/* Full fp32 expert FFN on one token. q4_avx2.cpp:175-196 */
+void orc_expert_ffn(const void* wg, const void* wu, const void* wd,
+                    const float* x, float* y, int hidden, int n_ff);
+
+/* Router: softmax, k rounds of first-strict-max (NaN skipped, lower index
+ * wins ties), renormalize, weight[k] = shared_w. Outputs use stride `stride`
+ * (>= k+1). moe.cu:25-85, 165-234 */
+void orc_router_topk(const float* logits, int* idx, float* weight, int n_expert,
+                     int k, int stride, int n_rows, float shared_w);
+
+/* out[r][i] = residual[r][i] + sum_{kk=0..n_used} w[r][kk]*y[r][kk][i], fp32,
+ * kk order. out may alias residual. moe.cu:265-280 */
+void orc_moe_combine(float* out, const float* residual, const float* expert_y,
+                     const float* weight, int n_used, int hidden, int n_rows);
+
+/* One MoE layer for n_tokens tokens, device-path stage order
+ * (session.cpp:2482-3030): quantize x, route, each routed expert and the
+ * shared expert through orc_expert_ffn semantics, combine with slot k =
+ * shared (weight shared_w). tab_* are [n_expert] pointers; sh_* may be NULL
+ * (no shared expert: slot k contributes 0). residual may be NULL (= 0).
+ * idx/weight outputs: [n_tokens][k+1]. n_threads > 1 runs the expert jobs
+ * on a worker pool (same results). */
+void orc_moe_layer(const void* const* tab_gate, const void* const* tab_up,
+                   const void* const* tab_down, const void* sh_gate,
+                   const void* sh_up, const void* sh_down, const float* x,
+                   const float* logits, const float* residual, float* out,
+                   int* idx, float* weight, int n_tokens, int hidden, int n_ff,
+                   int n_expert, int k, float shared_w, int n_threads);
+
+/* Same as orc_moe_layer but with routing given (idx/weight [n_tokens][k+1]
+ * already filled, e.g. sampled routing); no softmax. */
+void orc_moe_layer_routed(const void* const* tab_gate,
+                          const void* const* tab_up,
+                          const void* const* tab_down, const void* sh_gate,
+                          const void* sh_up, const void* sh_down,
+                          const float* x, const int* idx, const float* weight,
+                          const float* residual, float* out, int n_tokens,
+                          int hidden, int n_ff, int n_expert, int k,
+                          int n_threads);
+
+/* Device-plan semantics of moe_dispatch_scan (moe.cu:366-444), made
+ * deterministic: routes ordered by (expert, row, kk). off/toff [n_expert+1],
+ * meta {R, tiles, bad}, gslot [n_rows*k], grows [n_rows*k]. Bad ids zero
+ * that row's weights (stride k+1). */
+void orc_dispatch_scan(const int* idx, float* weight, int* gslot, int* grows,
+                       int* off, int* toff, int* meta, int n_rows, int k,
+                       int n_expert, int tok_per);
+
+/* Test helper: number of x in a sample where orc_expf(x) != libm expf(x). */
+int64_t orc_count_expf_mismatch(int64_t n_samples, uint64_t seed, float lo,
+                                float hi);
+/* Test helper: 1 if this build took the AVX2 integer-dot path. */
+int orc_have_avx2(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SG_ORACLE_H */

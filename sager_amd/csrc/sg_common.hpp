@@ -1,0 +1,299 @@
+// sg_common.hpp - device helpers shared by the gfx950 kernels: block
+// formats, exact fp16 decode, 6-bit scale unpack, the int8 sub-block dot,
+// the super-block epilogue, exp, and wave64 helpers.
+//
+// Numerics contract (all kernels): compiled with -ffp-contract=off; every
+// fused multiply-add below is written as an explicit fmaf so the fp32 results
+// are bit-identical to the reference's CPU build on the same Q8_K input.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sager_hip.h"
+
+namespace sg {
+
+constexpr int kQK = 256;          // weights per super-block
+constexpr int kQ4Bytes = 144;     // Q4_K super-block
+constexpr int kQ8Bytes = 276;     // Q8_K block
+constexpr int kWave = 64;
+
+// ---- status plumbing (host) -------------------------------------------
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// ---- exact fp16 -> fp32 --------------------------------------------------
+__device__ __forceinline__ float half_bits_to_float(uint32_t h16) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h16)));
+}
+
+// ---- the 8 sub-block scales and mins of one super-block ----------------
+// The 12 packed bytes are words A (bytes 0-3), B (4-7), C (8-11):
+//   scale j<4 = A.byte j & 63          min j<4 = B.byte j & 63
+//   scale j>=4 = (C.byte(j-4) & 15) | (A.byte(j-4) >> 6) << 4
+//   min   j>=4 = (C.byte(j-4) >> 4) | (B.byte(j-4) >> 6) << 4
+// (q4_k.hpp:110-118, evaluated four sub-blocks per 32-bit operation.)
+struct ScaleMins {
+  uint32_t sc_lo, sc_hi, mn_lo, mn_hi;  // one 6-bit value per byte
+};
+__device__ __forceinline__ ScaleMins unpack_scales(uint32_t A, uint32_t B, uint32_t C) {
+  ScaleMins r;
+  r.sc_lo = A & 0x3F3F3F3Fu;
+  r.mn_lo = B & 0x3F3F3F3Fu;
+  r.sc_hi = (C & 0x0F0F0F0Fu) | ((A >> 2) & 0x30303030u);
+  r.mn_hi = ((C >> 4) & 0x0F0F0F0Fu) | ((B >> 2) & 0x30303030u);
+  return r;
+}
+__device__ __forceinline__ float byte_f(uint32_t w, int i) {
+  return static_cast<float>((w >> (8 * i)) & 0xFFu);
+}
+
+// ---- int8 sub-block dots of one super-block -----------------------------
+// q: the 32 qs words of the block; x: the 64 qs words of the matching Q8_K
+// block. ip[s] = sum over the 32 weights of sub-block s of nibble * x.
+// Nibbles (0..15) are exact as signed int8, so v_dot4 i8 x i8 is exact.
+__device__ __forceinline__ void subblock_dots(const uint32_t* q, const int32_t* x,
+                                              int32_t ip[8]) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    int32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w = q[8 * g + j];
+      lo = __builtin_amdgcn_sdot4(static_cast<int>(w & 0x0F0F0F0Fu), x[16 * g + j], lo, false);
+      hi = __builtin_amdgcn_sdot4(static_cast<int>((w >> 4) & 0x0F0F0F0Fu), x[16 * g + 8 + j], hi,
+                                  false);
+    }
+    ip[2 * g] = lo;
+    ip[2 * g + 1] = hi;
+  }
+}
+
+// ---- super-block epilogue in the reference order -------------------------
+// sum_s fma(xd, fma(sd_s, ip_s, -(sm_s * bsum_s)), sum), sd = d*scale,
+// sm = dmin*min (q4_avx2.cpp:30-39,112-121,134-141 as compiled).
+__device__ __forceinline__ float block_sum(uint32_t dd, const ScaleMins& sm8, const int32_t ip[8],
+                                           float xd, const float bsf[8]) {
+  const float d = half_bits_to_float(dd & 0xFFFFu);
+  const float dmin = half_bits_to_float(dd >> 16);
+  float sum = 0.f;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const uint32_t scw = s < 4 ? sm8.sc_lo : sm8.sc_hi;
+    const uint32_t mnw = s < 4 ? sm8.mn_lo : sm8.mn_hi;
+    const float sd = d * byte_f(scw, s & 3);
+    const float smv = dmin * byte_f(mnw, s & 3);
+    const float t = __builtin_fmaf(sd, static_cast<float>(ip[s]), -(smv * bsf[s]));
+    sum = __builtin_fmaf(xd, t, sum);
+  }
+  return sum;
+}
+
+// Full dot of one Q4_K block (36 words) with one Q8_K block held as
+// 64 qs words + d + float bsums.
+__device__ __forceinline__ float q4k_block_dot(const uint32_t* w36, const int32_t* xq64, float xd,
+                                               const float bsf[8]) {
+  int32_t ip[8];
+  subblock_dots(w36 + 4, xq64, ip);
+  const ScaleMins sm8 = unpack_scales(w36[1], w36[2], w36[3]);
+  return block_sum(w36[0], sm8, ip, xd, bsf);
+}
+
+// Load one 144-B Q4_K block (16-B aligned) as 9 x 128-bit loads.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void load_q4k(const sg_block_q4k* b, uint32_t* w36) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(b);
+#pragma unroll
+  for (int i = 0; i < 9; ++i) {
+    const u32x4 v = __builtin_nontemporal_load(p + i);
+    w36[4 * i + 0] = v.x;
+    w36[4 * i + 1] = v.y;
+    w36[4 * i + 2] = v.z;
+    w36[4 * i + 3] = v.w;
+  }
+}
+
+// ---- exp: double evaluation, one rounding to float ------------------------
+// x = k ln2 + r (|r| <= ln2/2, ln2 split in two doubles), e^r by its Taylor
+// series to degree 13 (remainder < 5e-18), scaled by 2^k, rounded once.
+// Correctly rounded except for arguments within ~1e-16 relative of a float
+// rounding boundary.  Host and device evaluate the same IEEE operations.
+__host__ __device__ __forceinline__ float expf_sg(float xf) {
+  if (xf != xf) return xf;
+  if (xf > 100.f) return __builtin_inff();
+  if (xf < -110.f) return 0.f;
+  const double x = static_cast<double>(xf);
+  const double kd = __builtin_rint(x * 1.4426950408889634);
+  double r = __builtin_fma(-kd, 6.9314718055994529e-01, x);
+  r = __builtin_fma(-kd, 2.3190468138462996e-17, r);
+  double p = 1.0 / 6227020800.0;
+  p = __builtin_fma(p, r, 1.0 / 479001600.0);
+  p = __builtin_fma(p, r, 1.0 / 39916800.0);
+  p = __builtin_fma(p, r, 1.0 / 3628800.0);
+  p = __builtin_fma(p, r, 1.0 / 362880.0);
+  p = __builtin_fma(p, r, 1.0 / 40320.0);
+  p = __builtin_fma(p, r, 1.0 / 5040.0);
+  p = __builtin_fma(p, r, 1.0 / 720.0);
+  p = __builtin_fma(p, r, 1.0 / 120.0);
+  p = __builtin_fma(p, r, 1.0 / 24.0);
+  p = __builtin_fma(p, r, 1.0 / 6.0);
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const long long k = static_cast<long long>(kd);
+  const double scale = __builtin_bit_cast(double, static_cast<unsigned long long>(k + 1023) << 52);
+  return static_cast<float>(p * scale);
+}
+
+// SiLU(g) * u in the CPU chain's operation order (q4_avx2.cpp:187-191).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g / (1.f + expf_sg(-g)) * u;
+}
+
+// ---- Q8_K code of one scaled value ----------------------------------------
+// round-half-even, then the x86 float->int conversion the reference runs on
+// (NaN and out-of-range -> INT_MIN), then the +-127 clamp.
+__device__ __forceinline__ int q8_code(float v) {
+  const float r = __builtin_rintf(v);
+  int q;
+  if (!(r == r) || r >= 2147483648.0f || r < -2147483648.0f)
+    q = INT32_MIN;
+  else
+    q = static_cast<int>(r);
+  return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+
+// ---- wave64 helpers ---------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_isum(int v, int width) {
+  for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Quantize one 256-value block with the calling wave; `lane` in 0..63.
+// v[0..3] are the lane's values 4*lane..4*lane+3 of the block.
+__device__ __forceinline__ void quantize_block_wave(const float v[4], unsigned char* ob, int lane) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = fmaxf(wave_max(amax), 1e-30f);
+  const float d = amax / 127.f;
+  const float id = d > 0 ? 1.f / d : 0.f;
+  int q[4];
+  uint32_t packed = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    q[i] = q8_code(v[i] * id);
+    packed |= (static_cast<uint32_t>(q[i]) & 0xFFu) << (8 * i);
+  }
+  const int s = wave_isum(q[0] + q[1] + q[2] + q[3], 8);
+  *reinterpret_cast<uint32_t*>(ob + 4 + 4 * lane) = packed;
+  if (lane == 0) *reinterpret_cast<float*>(ob) = d;
+  if ((lane & 7) == 0)
+    *reinterpret_cast<int16_t*>(ob + 260 + 2 * (lane >> 3)) = static_cast<int16_t>(s);
+}
+
+
+// ---- Q8_K activations staged in LDS ------------------------------------------
+// Each 276-B block becomes 80 dwords: [0,64) qs words, [64] d, [65,73) the
+// eight bsums as floats (exact), rest padding; stride 320 B keeps the qs
+// words 16-B aligned for ds_read_b128.
+constexpr int kXStride = 80;
+
+__device__ __forceinline__ void stage_q8k(const unsigned char* __restrict__ xq, int n_blocks,
+                                          uint32_t* lds, int tid, int nthreads) {
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(xq);  // 276 B blocks are 4-B aligned
+  for (int j = tid; j < n_blocks * 69; j += nthreads) {
+    const int b = j / 69, w = j - b * 69;
+    const uint32_t v = src[j];
+    uint32_t* dst = lds + b * kXStride;
+    if (w == 0) {
+      dst[64] = v;
+    } else if (w <= 64) {
+      dst[w - 1] = v;
+    } else {
+      const int p = 2 * (w - 65);
+      dst[65 + p] = __builtin_bit_cast(uint32_t, static_cast<float>(static_cast<int16_t>(v & 0xFFFFu)));
+      dst[66 + p] = __builtin_bit_cast(uint32_t, static_cast<float>(static_cast<int16_t>(v >> 16)));
+    }
+  }
+}
+
+// Read one staged block into registers.
+__device__ __forceinline__ void load_x_regs(const uint32_t* lds_blk, int32_t* xq64, float& xd,
+                                            float* bsf) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(lds_blk);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const u32x4 v = p[i];
+    xq64[4 * i + 0] = static_cast<int32_t>(v.x);
+    xq64[4 * i + 1] = static_cast<int32_t>(v.y);
+    xq64[4 * i + 2] = static_cast<int32_t>(v.z);
+    xq64[4 * i + 3] = static_cast<int32_t>(v.w);
+  }
+  xd = __builtin_bit_cast(float, lds_blk[64]);
+#pragma unroll
+  for (int s = 0; s < 8; ++s) bsf[s] = __builtin_bit_cast(float, lds_blk[65 + s]);
+}
+
+// Sum the per-block partial sums of the `lpr` lanes of a row group in block
+// order (acc = 0; acc += s_0; ...; acc += s_{nb-1}), the reference's row
+// accumulation.  Every lane of the group returns the row result.
+__device__ __forceinline__ float row_sum_in_order(float s, int lane, int lpr, int nb) {
+  const int base = lane & ~(lpr - 1);
+  float acc = 0.f;
+  for (int j = 0; j < nb; ++j) acc += __shfl(s, base + j, 64);
+  return acc;
+}
+
+// Quantize one 256-value block with the calling wave straight into the LDS
+// staging layout (qs words, d, float bsums); same arithmetic as
+// quantize_block_wave.
+__device__ __forceinline__ void quantize_block_wave_lds(const float v[4], uint32_t* dst,
+                                                        int lane) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = fmaxf(wave_max(amax), 1e-30f);
+  const float d = amax / 127.f;
+  const float id = d > 0 ? 1.f / d : 0.f;
+  uint32_t packed = 0;
+  int qsum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = q8_code(v[i] * id);
+    qsum += q;
+    packed |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * i);
+  }
+  const int s = wave_isum(qsum, 8);
+  dst[lane] = packed;
+  if (lane == 0) dst[64] = __builtin_bit_cast(uint32_t, d);
+  if ((lane & 7) == 0) dst[65 + (lane >> 3)] = __builtin_bit_cast(uint32_t, static_cast<float>(s));
+}
+
+// Stage the Q8_K rows of n tokens (token ids in `tok`, nb blocks per row)
+// into LDS: token j's block b goes to lds + (j*nb + b)*kXStride.
+__device__ __forceinline__ void stage_q8k_rows(const unsigned char* __restrict__ xq,
+                                               const int* tok, int n, int nb, uint32_t* lds,
+                                               int tid, int nthreads) {
+  const int per = nb * 69;
+  for (int j = tid; j < n * per; j += nthreads) {
+    const int r = j / per, jj = j - r * per;
+    const int b = jj / 69, w = jj - b * 69;
+    const uint32_t v =
+        reinterpret_cast<const uint32_t*>(xq + static_cast<long long>(tok[r]) * nb * kQ8Bytes)[jj];
+    uint32_t* dst = lds + (r * nb + b) * kXStride;
+    if (w == 0) {
+      dst[64] = v;
+    } else if (w <= 64) {
+      dst[w - 1] = v;
+    } else {
+      const int p = 2 * (w - 65);
+      dst[65 + p] = __builtin_bit_cast(uint32_t, static_cast<float>(static_cast<int16_t>(v & 0xFFFFu)));
+      dst[66 + p] = __builtin_bit_cast(uint32_t, static_cast<float>(static_cast<int16_t>(v >> 16)));
+    }
+  }
+}
+
+}  // namespace sg

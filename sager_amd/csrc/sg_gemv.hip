@@ -1,0 +1,232 @@
+// sg_gemv.hip - the Q4_K x Q8_K GEMV family on gfx950.
+//
+// Lane-per-super-block mapping.  A row of k = 256*nb weights is nb
+// consecutive 144-B super-blocks; a wave covers 64/lpr rows at once, lane
+// l handling block (l mod lpr) of row (l / lpr), with lpr the power of two
+// >= nb.  Because rows are contiguous, a wave's 9 x 128-bit loads per lane
+// sweep one contiguous stretch of the matrix, and every byte fetched is
+// used.  Each lane keeps its Q8_K activation block in registers (64 qs
+// words + d + bsums), computes the eight int32 sub-block dots with
+// v_dot4_i32_i8, applies the fp32 super-block epilogue, and the row's block
+// sums are added in block order across the lpr lanes (the reference's
+// acc += sum order, q4_avx2.cpp:130-143).
+//
+// Reference kernels replaced: gemv_q4_k_q8 / gemv_mtok_ro_f32_kernel
+// (q4_k.cu:57-91, 1360-1422, 1534-1562), gemv_q4_k_q8_batched and the mtok
+// variants (q4_k.cu:218-282, 359-498), gemv_ptrs_q4_k_q8_f16out
+// (q4_k.cu:184-213).
+#include "sg_common.hpp"
+
+namespace sg {
+
+constexpr int kMaxNb = 64;       // k <= 16384
+constexpr int kMaxTokens = 16;   // batched GEMV token tile
+
+struct PlainRows {
+  const sg_block_q4k* w;
+  int nb;
+  __device__ const sg_block_q4k* row(int r) const {
+    return w + static_cast<long long>(r) * nb;
+  }
+};
+
+struct TableRows {
+  const sg_block_q4k* const* ptrs;
+  int rows_per, nb;
+  __device__ const sg_block_q4k* row(int r) const {
+    const int e = r / rows_per;
+    return ptrs[e] + static_cast<long long>(r - e * rows_per) * nb;
+  }
+};
+
+__host__ __device__ inline int lanes_per_row(int nb) {
+  int l = 1;
+  while (l < nb) l <<= 1;
+  return l;
+}
+
+// y[r] = W[r] . x, one token; grid-stride over row groups.
+template <typename Rows>
+__global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned char* __restrict__ xq,
+                                                    float* __restrict__ y, int n_rows, int nb,
+                                                    int lpr) {
+  __shared__ __attribute__((aligned(16))) uint32_t xs[kMaxNb * kXStride];
+  stage_q8k(xq, nb, xs, threadIdx.x, blockDim.x);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int blk = lane & (lpr - 1);
+  const int rpw = 64 / lpr;
+  const bool active = blk < nb;
+  int32_t xr[64];
+  float xd = 0.f, bsf[8];
+  load_x_regs(xs + (active ? blk : 0) * kXStride, xr, xd, bsf);
+
+  const int n_groups = (n_rows + rpw - 1) / rpw;
+  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int n_waves = gridDim.x * (blockDim.x >> 6);
+  for (int g = wave; g < n_groups; g += n_waves) {
+    const int r = g * rpw + lane / lpr;
+    float s = 0.f;
+    if (active && r < n_rows) {
+      uint32_t w36[36];
+      load_q4k(rows.row(r) + blk, w36);
+      s = q4k_block_dot(w36, xr, xd, bsf);
+    }
+    const float acc = row_sum_in_order(s, lane, lpr, nb);
+    if (blk == 0 && r < n_rows) y[r] = acc;
+  }
+}
+
+// y[t*n_rows + r] = W[r] . x[t] for t < n_tokens; weights read once.
+__global__ void __launch_bounds__(256) gemv_batched_kernel(const sg_block_q4k* __restrict__ w,
+                                                           const unsigned char* __restrict__ xq,
+                                                           float* __restrict__ y, int n_rows,
+                                                           int nb, int lpr, int n_tokens) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t xs_dyn[];
+  stage_q8k(xq, nb * n_tokens, xs_dyn, threadIdx.x, blockDim.x);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int blk = lane & (lpr - 1);
+  const int rpw = 64 / lpr;
+  const bool active = blk < nb;
+  const int n_groups = (n_rows + rpw - 1) / rpw;
+  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int n_waves = gridDim.x * (blockDim.x >> 6);
+  for (int g = wave; g < n_groups; g += n_waves) {
+    const int r = g * rpw + lane / lpr;
+    const bool live = active && r < n_rows;
+    uint32_t w36[36];
+    int32_t ip[8];
+    ScaleMins sm8{};
+    if (live) {
+      load_q4k(w + static_cast<long long>(r) * nb + blk, w36);
+      sm8 = unpack_scales(w36[1], w36[2], w36[3]);
+    }
+    for (int t = 0; t < n_tokens; ++t) {
+      float s = 0.f;
+      if (live) {
+        int32_t xr[64];
+        float xd, bsf[8];
+        load_x_regs(xs_dyn + (t * nb + blk) * kXStride, xr, xd, bsf);
+        subblock_dots(w36 + 4, xr, ip);
+        s = block_sum(w36[0], sm8, ip, xd, bsf);
+      }
+      const float acc = row_sum_in_order(s, lane, lpr, nb);
+      if (blk == 0 && r < n_rows) y[static_cast<long long>(t) * n_rows + r] = acc;
+    }
+  }
+}
+
+// dots[(r*nb + b)*8 + s] = int32 sub-block dot (test hook).
+__global__ void __launch_bounds__(256) subblock_dots_kernel(const sg_block_q4k* __restrict__ w,
+                                                            const unsigned char* __restrict__ xq,
+                                                            int32_t* __restrict__ dots,
+                                                            int n_rows, int nb, int lpr) {
+  __shared__ __attribute__((aligned(16))) uint32_t xs[kMaxNb * kXStride];
+  stage_q8k(xq, nb, xs, threadIdx.x, blockDim.x);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int blk = lane & (lpr - 1);
+  const int rpw = 64 / lpr;
+  const int g = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int r = g * rpw + lane / lpr;
+  if (blk >= nb || r >= n_rows) return;
+  int32_t xr[64];
+  float xd, bsf[8];
+  load_x_regs(xs + blk * kXStride, xr, xd, bsf);
+  uint32_t w36[36];
+  load_q4k(w + static_cast<long long>(r) * nb + blk, w36);
+  int32_t ip[8];
+  subblock_dots(w36 + 4, xr, ip);
+  int32_t* o = dots + (static_cast<long long>(r) * nb + blk) * 8;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) o[s] = ip[s];
+}
+
+// Grid for a grid-stride row loop: enough waves to cover every row group
+// once, capped at 8 workgroups of 4 waves per CU (256 CUs).
+static unsigned gemv_grid(long long n_groups) {
+  const long long wgs = (n_groups + 3) / 4;
+  const long long cap = 256LL * 8;
+  return static_cast<unsigned>(wgs < cap ? (wgs > 0 ? wgs : 1) : cap);
+}
+
+static int check_gemv_geometry(const char* name, int n_rows, int k) {
+  if (n_rows <= 0 || k <= 0 || k % kQK != 0)
+    return set_error(SG_ERR_GEOMETRY, "%s: n_rows=%d k=%d (k must be a positive multiple of 256)",
+                     name, n_rows, k);
+  if (k / kQK > kMaxNb)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: k=%d exceeds %d", name, k, kMaxNb * kQK);
+  return SG_OK;
+}
+
+}  // namespace sg
+
+using namespace sg;
+
+extern "C" {
+
+int sg_gemv_q4_k_q8(const sg_block_q4k* w, const sg_block_q8k* x, float* y, int n_rows, int k,
+                    void* stream) {
+  if (!w || !x || !y) return set_error(SG_ERR_INVALID_ARGUMENT, "sg_gemv_q4_k_q8: null pointer");
+  if (int st = check_gemv_geometry("sg_gemv_q4_k_q8", n_rows, k)) return st;
+  const int nb = k / kQK, lpr = lanes_per_row(nb);
+  const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
+  hipLaunchKernelGGL(gemv1_kernel<PlainRows>, dim3(gemv_grid(n_groups)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), PlainRows{w, nb},
+                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr);
+  return check_launch("sg_gemv_q4_k_q8");
+}
+
+int sg_gemv_ptrs_q4_k_q8(const sg_block_q4k* const* ptrs, const sg_block_q8k* x, float* y,
+                         int n_ptrs, int rows_per, int k, void* stream) {
+  if (!ptrs || !x || !y)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "sg_gemv_ptrs_q4_k_q8: null pointer");
+  if (n_ptrs <= 0 || rows_per <= 0 || static_cast<long long>(n_ptrs) * rows_per > 0x7fffffffLL)
+    return set_error(SG_ERR_GEOMETRY, "sg_gemv_ptrs_q4_k_q8: n_ptrs=%d rows_per=%d", n_ptrs,
+                     rows_per);
+  const int n_rows = n_ptrs * rows_per;
+  if (int st = check_gemv_geometry("sg_gemv_ptrs_q4_k_q8", n_rows, k)) return st;
+  const int nb = k / kQK, lpr = lanes_per_row(nb);
+  const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
+  hipLaunchKernelGGL(gemv1_kernel<TableRows>, dim3(gemv_grid(n_groups)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), TableRows{ptrs, rows_per, nb},
+                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr);
+  return check_launch("sg_gemv_ptrs_q4_k_q8");
+}
+
+int sg_gemv_q4_k_q8_batched(const sg_block_q4k* w, const sg_block_q8k* x, float* y, int n_rows,
+                            int k, int n_tokens, void* stream) {
+  if (!w || !x || !y)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "sg_gemv_q4_k_q8_batched: null pointer");
+  if (int st = check_gemv_geometry("sg_gemv_q4_k_q8_batched", n_rows, k)) return st;
+  if (n_tokens <= 0 || n_tokens > kMaxTokens)
+    return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_q4_k_q8_batched: n_tokens=%d not in [1,%d]",
+                     n_tokens, kMaxTokens);
+  const int nb = k / kQK, lpr = lanes_per_row(nb);
+  const size_t lds = static_cast<size_t>(nb) * n_tokens * kXStride * 4;
+  if (lds > 160 * 1024)
+    return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_q4_k_q8_batched: k*n_tokens too large for LDS");
+  const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
+  hipLaunchKernelGGL(gemv_batched_kernel, dim3(gemv_grid(n_groups)), dim3(256), lds,
+                     static_cast<hipStream_t>(stream), w,
+                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr, n_tokens);
+  return check_launch("sg_gemv_q4_k_q8_batched");
+}
+
+int sg_q4k_subblock_dots(const sg_block_q4k* w, const sg_block_q8k* x, int32_t* dots, int n_rows,
+                         int k, void* stream) {
+  if (!w || !x || !dots)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "sg_q4k_subblock_dots: null pointer");
+  if (int st = check_gemv_geometry("sg_q4k_subblock_dots", n_rows, k)) return st;
+  const int nb = k / kQK, lpr = lanes_per_row(nb);
+  const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
+  hipLaunchKernelGGL(subblock_dots_kernel, dim3(static_cast<unsigned>((n_groups + 3) / 4)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), w,
+                     reinterpret_cast<const unsigned char*>(x), dots, n_rows, nb, lpr);
+  return check_launch("sg_q4k_subblock_dots");
+}
+
+}  // extern "C"

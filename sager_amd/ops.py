@@ -1,0 +1,162 @@
+"""Host-side mirror of the reference's launcher API over libsager_hip.so.
+
+Each function keeps the name and argument meaning of the ``sager::cuda``
+launcher it replaces (include/sager/kernels/cuda_ops.hpp) and takes torch
+tensors that live on the GPU; it enqueues on torch's current stream and
+never synchronizes.  Errors raise :class:`SagerError` with the library's
+message (the reference's launchers return void and surface failures through
+cudaGetLastError).  Block tensors are uint8 views of the packed formats:
+Q4_K ``[..., 144]`` per 256 weights, Q8_K ``[..., 276]`` per 256 values.
+"""
+import torch
+
+from . import Q4K_BYTES, Q8K_BYTES, QK, load
+
+
+class SagerError(RuntimeError):
+    pass
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise SagerError("tensor must be on the GPU")
+    if not t.is_contiguous():
+        raise SagerError("tensor must be contiguous")
+    return t.data_ptr()
+
+
+def _check(status):
+    if status != 0:
+        raise SagerError(f"status {status}: {load().sg_last_error().decode()}")
+
+
+def q8k_empty(n_tokens, n, device="cuda"):
+    return torch.empty((n_tokens, (n // QK) * Q8K_BYTES), dtype=torch.uint8, device=device)
+
+
+def quantize_q8_k(x, out=None):
+    """cuda::quantize_q8_k (cuda_ops.hpp:271-273): rows of x (fp32 or fp16,
+    [..., n]) -> Q8_K blocks [rows, n/256*276]."""
+    n = x.shape[-1]
+    rows = x.numel() // n
+    if out is None:
+        out = q8k_empty(rows, n, x.device)
+    fn = load().sg_quantize_q8_k_f16 if x.dtype == torch.float16 else load().sg_quantize_q8_k
+    if x.dtype not in (torch.float16, torch.float32):
+        raise SagerError("x must be fp32 or fp16")
+    _check(fn(_ptr(x), _ptr(out), n, rows, _stream()))
+    return out
+
+
+def gemv_q4_k_q8(w, x_q8, n_rows, k, y=None):
+    """cuda::gemv_q4_k_q8 (cuda_ops.hpp:41-42): y[n_rows] fp32 = W . x."""
+    if y is None:
+        y = torch.empty(n_rows, dtype=torch.float32, device=w.device)
+    _check(load().sg_gemv_q4_k_q8(_ptr(w), _ptr(x_q8), _ptr(y), n_rows, k, _stream()))
+    return y
+
+
+def gemv_q4_k_q8_batched(w, x_q8, n_rows, k, n_tokens, y=None):
+    """cuda::gemv_q4_k_q8_batched (cuda_ops.hpp:72-74): y[n_tokens, n_rows]."""
+    if y is None:
+        y = torch.empty((n_tokens, n_rows), dtype=torch.float32, device=w.device)
+    _check(load().sg_gemv_q4_k_q8_batched(_ptr(w), _ptr(x_q8), _ptr(y), n_rows, k, n_tokens,
+                                          _stream()))
+    return y
+
+
+def gemv_ptrs_q4_k_q8(ptrs, x_q8, n_ptrs, rows_per, k, y=None):
+    """cuda::gemv_ptrs_q4_k_q8_f16out (cuda_ops.hpp:60-63), fp32 out.
+    ptrs: int64 device tensor of n_ptrs matrix addresses."""
+    if y is None:
+        y = torch.empty(n_ptrs * rows_per, dtype=torch.float32, device=x_q8.device)
+    _check(load().sg_gemv_ptrs_q4_k_q8(_ptr(ptrs), _ptr(x_q8), _ptr(y), n_ptrs, rows_per, k,
+                                       _stream()))
+    return y
+
+
+def subblock_dots(w, x_q8, n_rows, k):
+    """int32 sub-block dot sums [n_rows, k/256, 8] (test hook)."""
+    d = torch.empty((n_rows, k // QK, 8), dtype=torch.int32, device=w.device)
+    _check(load().sg_q4k_subblock_dots(_ptr(w), _ptr(x_q8), _ptr(d), n_rows, k, _stream()))
+    return d
+
+
+def router_topk_batched(logits, n_expert_used, shared_w=1.0, idx_stride=None):
+    """cuda::router_topk_batched (cuda_ops.hpp:175-177 / 351-360):
+    logits [n_rows, n_expert] -> idx int32, weight fp32 [n_rows, idx_stride]."""
+    n_rows, n_expert = logits.shape
+    stride = idx_stride or n_expert_used + 1
+    idx = torch.full((n_rows, stride), -1, dtype=torch.int32, device=logits.device)
+    w = torch.zeros((n_rows, stride), dtype=torch.float32, device=logits.device)
+    _check(load().sg_router_topk(_ptr(logits), _ptr(idx), _ptr(w), n_expert, n_expert_used,
+                                 stride, n_rows, float(shared_w), _stream()))
+    return idx, w
+
+
+def router_topk(logits, n_expert_used, shared_w=1.0):
+    """cuda::router_topk (cuda_ops.hpp:351-352): one row."""
+    idx, w = router_topk_batched(logits.reshape(1, -1), n_expert_used, shared_w)
+    return idx[0], w[0]
+
+
+def silu_mul(g, u, out=None):
+    """cuda::silu_mul_f16 (cuda_ops.hpp:305-306), fp32."""
+    if out is None:
+        out = torch.empty_like(g)
+    _check(load().sg_silu_mul(_ptr(out), _ptr(g), _ptr(u), g.numel(), _stream()))
+    return out
+
+
+def moe_combine_batched(expert_y, weight, residual=None, out=None):
+    """cuda::moe_combine_batched_f16 (cuda_ops.hpp:397-399), fp32:
+    expert_y [n_rows, n_used+1, hidden], weight [n_rows, n_used+1]."""
+    n_rows, slots, hidden = expert_y.shape
+    if out is None:
+        out = torch.empty((n_rows, hidden), dtype=torch.float32, device=expert_y.device)
+    _check(load().sg_moe_combine(_ptr(out), _ptr(residual), _ptr(expert_y), _ptr(weight),
+                                 slots - 1, hidden, n_rows, _stream()))
+    return out
+
+
+class MoeLayer:
+    """One MoE layer's device-side pointer tables and workspace; ``forward``
+    is the device-path dispatch of Session::moe_dispatch_device
+    (session.cpp:2482-3030) as one fused call."""
+
+    def __init__(self, tab_gate, tab_up, tab_down, shared=None, hidden=2048, n_ff=512,
+                 n_expert=256, k=8, max_tokens=1, shared_w=1.0):
+        self.tab_gate, self.tab_up, self.tab_down = tab_gate, tab_up, tab_down
+        self.shared = shared
+        self.hidden, self.n_ff, self.n_expert, self.k = hidden, n_ff, n_expert, k
+        self.shared_w = float(shared_w)
+        self.max_tokens = max_tokens
+        nbytes = load().sg_moe_layer_workspace_bytes(max_tokens, hidden, n_ff, n_expert, k)
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=tab_gate.device)
+
+    def forward(self, x, logits=None, residual=None, out=None, idx=None, weight=None,
+                stages=7, workspace=None):
+        T = x.shape[0]
+        if T > self.max_tokens:
+            raise SagerError(f"{T} tokens > max_tokens={self.max_tokens}")
+        dev = x.device
+        if out is None:
+            out = torch.empty((T, self.hidden), dtype=torch.float32, device=dev)
+        if idx is None:
+            idx = torch.full((T, self.k + 1), -1, dtype=torch.int32, device=dev)
+        if weight is None:
+            weight = torch.zeros((T, self.k + 1), dtype=torch.float32, device=dev)
+        sg, su, sd = self.shared if self.shared is not None else (None, None, None)
+        ws = self.workspace if workspace is None else workspace
+        _check(load().sg_moe_layer_stages(
+            _ptr(self.tab_gate), _ptr(self.tab_up), _ptr(self.tab_down), _ptr(sg), _ptr(su),
+            _ptr(sd), _ptr(x), _ptr(logits), _ptr(residual), _ptr(out), _ptr(idx), _ptr(weight),
+            _ptr(ws), ws.numel(), T, self.hidden, self.n_ff, self.n_expert, self.k,
+            self.shared_w, stages, _stream()))
+        return out, idx, weight
