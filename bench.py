@@ -157,7 +157,7 @@ def main():
     idx = torch.empty((n_in, K + 1), dtype=torch.int32, device="cuda")
     wgt = torch.empty((n_in, K + 1), dtype=torch.float32, device="cuda")
 
-    def step(i, stages=7, ws=None):
+    def step(i, stages=3, ws=None):
         layers[i % N_LAYERS].forward(xs_d[i:i + 1], lgs_d[i:i + 1], out=out[i:i + 1],
                                      idx=idx[i:i + 1], weight=wgt[i:i + 1], stages=stages,
                                      workspace=ws)
@@ -195,26 +195,26 @@ def main():
                                       np.maximum(np.abs(ref[0]), floor)).max()))
         bit_exact &= bool((out_h[i] == ref[0]).all())
 
-    # dominant kernel: gate/up stage timed alone over 128 distinct (layer, step) plans
-    log("[bench] gate/up stage roofline")
+    # per-kernel timing over 128 distinct (layer, step) workspaces: the front
+    # kernel (routing + gate/up + SiLU) and the back kernel (down + combine)
+    log("[bench] per-kernel timing")
     S = 128
     wss = [torch.empty_like(layers[0].workspace) for _ in range(S)]
     for j in range(S):
-        step(j % n_in, stages=1, ws=wss[j])
+        step(j % n_in, stages=3, ws=wss[j])
     torch.cuda.synchronize()
     reps = 10
-    ms_gu, _ = time_graph(torch, lambda: [step(j % n_in, stages=2, ws=wss[j]) for j in range(S)],
+    ms_fr, _ = time_graph(torch, lambda: [step(j % n_in, stages=1, ws=wss[j]) for j in range(S)],
                           reps)
-    gu_us = ms_gu * 1e3 / S
-    gu_bytes = 9 * 2 * MAT_BYTES + (H // 256) * 276 + 9 * F * 4
-    ms_dn, _ = time_graph(torch, lambda: [step(j % n_in, stages=4, ws=wss[j]) for j in range(S)],
+    ms_bk, _ = time_graph(torch, lambda: [step(j % n_in, stages=2, ws=wss[j]) for j in range(S)],
                           reps)
-    dn_us = ms_dn * 1e3 / S
-    dn_bytes = 9 * MAT_BYTES + 9 * F * 4 + 9 * H * 4
-    ms_rt, _ = time_graph(torch, lambda: [step(j % n_in, stages=1, ws=wss[j]) for j in range(S)],
-                          reps)
-    rt_us = ms_rt * 1e3 / S
-    layer_bytes = 9 * 3 * MAT_BYTES + (H // 256) * 276 + E * 4 + H * 4
+    front_us = ms_fr * 1e3 / S
+    back_us = ms_bk * 1e3 / S
+    # algorithmic bytes: 9 experts' gate+up rows, x, logits, h written
+    front_bytes = 9 * 2 * MAT_BYTES + H * 4 + E * 4 + 9 * F * 4
+    # 9 experts' down rows, h read, slot outputs written and re-read, out
+    back_bytes = 9 * MAT_BYTES + 9 * F * 4 + 2 * 9 * H * 4 + H * 4
+    layer_bytes = 9 * 3 * MAT_BYTES + H * 4 + E * 4 + H * 4
     del wss
 
     # config 1: Q4_K GEMV 2048x2048 batch 1, 256 rotated copies (604 MB)
@@ -245,7 +245,7 @@ def main():
         log("[bench] CPU baseline (AVX2 oracle)")
         cpu, _ = cpu_baseline(l0, xs, lgs)
 
-    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+    fr_gbs = front_bytes / (front_us * 1e-6) / 1e9
     res = {
         "metric": "MoE layer decode us/token at top-8/256 (Q4_K experts, batch 1)",
         "value": round(us_per_token, 3),
@@ -262,15 +262,14 @@ def main():
         "config": {"workload": "config 2: MoE layer decode, hidden 2048, 256 experts "
                                "(gate/up 512x2048, down 2048x512) + shared, top-8, batch 1",
                    "layers_rotated": N_LAYERS, "timing": "HIP graph of K steps"},
-        "roofline": {"kernel": "layer_gateup_kernel (9 experts x gate+up, 1 token)",
-                     "bound": "hbm", "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "algorithmic_bytes": gu_bytes, "avg_us": round(gu_us, 3)},
+        "roofline": {"kernel": "layer_front_kernel (routing + 9 experts x gate/up + SiLU)",
+                     "bound": "hbm", "achieved": round(fr_gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(fr_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": front_bytes, "avg_us": round(front_us, 3)},
         "cpu_baseline": cpu,
         "parity": {"checked_steps": len(chk), "max_rel_err": max_rel, "bit_exact": bit_exact},
-        "stages_us": {"route": round(rt_us, 3), "gateup": round(gu_us, 3),
-                      "down_combine": round(dn_us, 3),
-                      "down_gbs": round(dn_bytes / (dn_us * 1e-6) / 1e9, 1)},
+        "kernels_us": {"front": round(front_us, 3), "back": round(back_us, 3),
+                       "back_gbs": round(back_bytes / (back_us * 1e-6) / 1e9, 1)},
         "layer_gbs": round(layer_bytes / (us_per_token * 1e-6) / 1e9, 1),
         "eager_us_per_token": round(eager_us, 2),
         "config1_gemv": {"us_per_gemv": round(gemv_us, 3),

@@ -170,14 +170,14 @@ int sg_moe_layer(const sg_block_q4k* const* tab_gate,
                  size_t workspace_bytes, int n_tokens, int hidden, int n_ff,
                  int n_expert, int k, float shared_w, void* stream);
 
-/* The three launches of sg_moe_layer, selectable: bit 0 = route (Q8_K of
- * x, top-k, plan), bit 1 = gate/up + SiLU, bit 2 = down + combine.  A stage
- * reads what the earlier stages left in `workspace`, so a caller may run them
- * separately on one stream (e.g. to overlap other work between them or to
- * time one stage); stages = 7 is sg_moe_layer.  The reference issues these
- * as separate launchers from Session::moe_dispatch_device
- * (session.cpp:2524-2556 route, :2791-2803 gate/up + SiLU + requant,
- * :2820-2843 down + scatter, :3029 combine). */
+/* The two launches of sg_moe_layer, selectable: bit 0 = front (top-k,
+ * Q8_K of x, the expert-major plan, gate/up GEMV + SiLU), bit 1 = back
+ * (Q8_K of h, down GEMV, combine).  The back stage reads what the front left
+ * in `workspace`, so a caller may run them separately on one stream (to put
+ * other work between them, or to time one); stages = 3 is sg_moe_layer.
+ * The reference issues these steps as separate launchers from
+ * Session::moe_dispatch_device (session.cpp:2524-2556 route, :2791-2803
+ * gate/up + SiLU + requant, :2820-2843 down + scatter, :3029 combine). */
 int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate,
                         const sg_block_q4k* const* tab_up,
                         const sg_block_q4k* const* tab_down,

@@ -100,13 +100,47 @@ __device__ __forceinline__ float q4k_block_dot(const uint32_t* w36, const int32_
   return block_sum(w36[0], sm8, ip, xd, bsf);
 }
 
-// Load one 144-B Q4_K block (16-B aligned) as 9 x 128-bit loads.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void load_q4k(const sg_block_q4k* b, uint32_t* w36) {
+typedef __attribute__((address_space(3))) void* lds_void_p;
+typedef __attribute__((address_space(1))) void* glb_void_p;
+
+// ---- weight streaming: global -> LDS without passing through VGPRs ---------
+// A wave copies n_chunks (<= 576) 16-B chunks with global_load_lds_dwordx4:
+// instruction i moves chunk c = lane + 64*i to dst + 16*c, so each
+// instruction reads 1 KB of consecutive global memory when the source is
+// contiguous (fully coalesced), and nothing occupies registers while the
+// data is in flight.  src(c) returns the global address of chunk c.
+template <typename Src>
+__device__ __forceinline__ void dma_chunks(Src src, int n_chunks, uint32_t* dst, int lane) {
+#pragma unroll
+  for (int i = 0; i < 9; ++i) {
+    const int c = lane + 64 * i;
+    if (i * 64 < n_chunks && c < n_chunks)
+      __builtin_amdgcn_global_load_lds((glb_void_p)src(c), (lds_void_p)(dst + 256 * i), 16, 0, 0);
+  }
+}
+// Same for any number of chunks (576 per round).
+template <typename Src>
+__device__ __forceinline__ void dma_range(Src src, int n_chunks, uint32_t* dst, int lane) {
+  for (int c0 = 0; c0 < n_chunks; c0 += 576)
+    dma_chunks([&](int c) { return src(c0 + c); }, min(576, n_chunks - c0), dst + 4 * c0, lane);
+}
+// Wait for every outstanding global load of this wave (the DMA included).
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+// Wait for this wave's LDS reads, so the buffer can be refilled.
+__device__ __forceinline__ void wait_lds() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+}
+// One 144-B block from LDS (16-B aligned) into 36 registers.
+__device__ __forceinline__ void read_block_lds(const uint32_t* b, uint32_t* w36) {
   const u32x4* p = reinterpret_cast<const u32x4*>(b);
 #pragma unroll
   for (int i = 0; i < 9; ++i) {
-    const u32x4 v = __builtin_nontemporal_load(p + i);
+    const u32x4 v = p[i];
     w36[4 * i + 0] = v.x;
     w36[4 * i + 1] = v.y;
     w36[4 * i + 2] = v.z;
@@ -165,21 +199,75 @@ __device__ __forceinline__ int q8_code(float v) {
 }
 
 // ---- wave64 helpers ---------------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
+// DPP lane exchanges within a 16-lane row: xor 1, xor 2 (quad_perm), the
+// 8-lane and 16-lane mirrors.  Applied in that order they reduce a row with
+// any associative, commutative combine; the four row results are then read
+// with v_readlane and combined in a fixed order, so every lane returns the
+// same value regardless of how the reduction is scheduled.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Maximum over the wave (NaN ignored as by fmaxf), same value in every lane.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)),
+               fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+// Sum over each aligned group of 8 lanes (every lane of the group gets it).
+__device__ __forceinline__ int sum8_dpp(int v) {
+  v += dpp_i<kDppXor1>(v);
+  v += dpp_i<kDppXor2>(v);
+  v += dpp_i<kDppHalfMirror>(v);
+  return v;
+}
+
+// (value, index) argmax: a valid index (>= 0) beats an invalid one, then the
+// larger value, then the lower index.  Total order, so the result is exact.
+__device__ __forceinline__ void argmax_take(float& bv, int& bi, float ov, int oi) {
+  if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+    bv = ov;
+    bi = oi;
+  }
+}
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& bv, int& bi) {
+  argmax_take(bv, bi, dpp_f<CTRL>(bv), dpp_i<CTRL>(bi));
+}
+__device__ __forceinline__ void wave_argmax_dpp(float& bv, int& bi) {
+  argmax_step<kDppXor1>(bv, bi);
+  argmax_step<kDppXor2>(bv, bi);
+  argmax_step<kDppHalfMirror>(bv, bi);
+  argmax_step<kDppMirror>(bv, bi);
+  float v = readlane_f(bv, 0);
+  int i = __builtin_amdgcn_readlane(bi, 0);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  for (int r = 16; r < 64; r += 16)
+    argmax_take(v, i, readlane_f(bv, r), __builtin_amdgcn_readlane(bi, r));
+  bv = v;
+  bi = i;
 }
-__device__ __forceinline__ int wave_isum(int v, int width) {
-  for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+
 
 // Quantize one 256-value block with the calling wave; `lane` in 0..63.
 // v[0..3] are the lane's values 4*lane..4*lane+3 of the block.
 __device__ __forceinline__ void quantize_block_wave(const float v[4], unsigned char* ob, int lane) {
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = fmaxf(wave_max(amax), 1e-30f);
+  amax = fmaxf(wave_max_dpp(amax), 1e-30f);
   const float d = amax / 127.f;
   const float id = d > 0 ? 1.f / d : 0.f;
   int q[4];
@@ -189,7 +277,7 @@ __device__ __forceinline__ void quantize_block_wave(const float v[4], unsigned c
     q[i] = q8_code(v[i] * id);
     packed |= (static_cast<uint32_t>(q[i]) & 0xFFu) << (8 * i);
   }
-  const int s = wave_isum(q[0] + q[1] + q[2] + q[3], 8);
+  const int s = sum8_dpp(q[0] + q[1] + q[2] + q[3]);
   *reinterpret_cast<uint32_t*>(ob + 4 + 4 * lane) = packed;
   if (lane == 0) *reinterpret_cast<float*>(ob) = d;
   if ((lane & 7) == 0)
@@ -255,7 +343,7 @@ __device__ __forceinline__ float row_sum_in_order(float s, int lane, int lpr, in
 __device__ __forceinline__ void quantize_block_wave_lds(const float v[4], uint32_t* dst,
                                                         int lane) {
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = fmaxf(wave_max(amax), 1e-30f);
+  amax = fmaxf(wave_max_dpp(amax), 1e-30f);
   const float d = amax / 127.f;
   const float id = d > 0 ? 1.f / d : 0.f;
   uint32_t packed = 0;
@@ -266,7 +354,7 @@ __device__ __forceinline__ void quantize_block_wave_lds(const float v[4], uint32
     qsum += q;
     packed |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * i);
   }
-  const int s = wave_isum(qsum, 8);
+  const int s = sum8_dpp(qsum);
   dst[lane] = packed;
   if (lane == 0) dst[64] = __builtin_bit_cast(uint32_t, d);
   if ((lane & 7) == 0) dst[65 + (lane >> 3)] = __builtin_bit_cast(uint32_t, static_cast<float>(s));

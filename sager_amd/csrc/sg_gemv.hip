@@ -1,15 +1,16 @@
 // sg_gemv.hip - the Q4_K x Q8_K GEMV family on gfx950.
 //
-// Lane-per-super-block mapping.  A row of k = 256*nb weights is nb
-// consecutive 144-B super-blocks; a wave covers 64/lpr rows at once, lane
-// l handling block (l mod lpr) of row (l / lpr), with lpr the power of two
-// >= nb.  Because rows are contiguous, a wave's 9 x 128-bit loads per lane
-// sweep one contiguous stretch of the matrix, and every byte fetched is
-// used.  Each lane keeps its Q8_K activation block in registers (64 qs
-// words + d + bsums), computes the eight int32 sub-block dots with
-// v_dot4_i32_i8, applies the fp32 super-block epilogue, and the row's block
-// sums are added in block order across the lpr lanes (the reference's
-// acc += sum order, q4_avx2.cpp:130-143).
+// Work unit: a wave owns a row group of 64/lpr rows, lpr = the power of two
+// >= nb (nb = k/256 super-blocks per row).  The group's bytes are contiguous
+// in HBM, so the wave streams them into its own 9 KB LDS buffer with
+// global_load_lds_dwordx4 (1 KB of consecutive memory per instruction, no
+// registers held while in flight).  Lane l then reads super-block (l mod
+// lpr) of row (l / lpr) from LDS (144-B stride: conflict-free), computes the
+// eight int32 sub-block dots with v_dot4_i32_i8 against its Q8_K activation
+// block kept in registers, applies the fp32 super-block epilogue, and the
+// lpr block sums of a row are added in block order (the reference's
+// acc += sum order, q4_avx2.cpp:130-143).  The next group's copy is issued
+// as soon as the block is in registers, so it overlaps the arithmetic.
 //
 // Reference kernels replaced: gemv_q4_k_q8 / gemv_mtok_ro_f32_kernel
 // (q4_k.cu:57-91, 1360-1422, 1534-1562), gemv_q4_k_q8_batched and the mtok
@@ -21,21 +22,23 @@ namespace sg {
 
 constexpr int kMaxNb = 64;       // k <= 16384
 constexpr int kMaxTokens = 16;   // batched GEMV token tile
+constexpr int kWaves = 4;        // waves per workgroup
+constexpr int kBufWords = 64 * 36;  // one wave's 9216-B weight buffer
 
 struct PlainRows {
   const sg_block_q4k* w;
   int nb;
-  __device__ const sg_block_q4k* row(int r) const {
-    return w + static_cast<long long>(r) * nb;
+  __device__ const char* row(int r) const {
+    return reinterpret_cast<const char*>(w + static_cast<long long>(r) * nb);
   }
 };
 
 struct TableRows {
   const sg_block_q4k* const* ptrs;
   int rows_per, nb;
-  __device__ const sg_block_q4k* row(int r) const {
+  __device__ const char* row(int r) const {
     const int e = r / rows_per;
-    return ptrs[e] + static_cast<long long>(r - e * rows_per) * nb;
+    return reinterpret_cast<const char*>(ptrs[e] + static_cast<long long>(r - e * rows_per) * nb);
   }
 };
 
@@ -45,36 +48,52 @@ __host__ __device__ inline int lanes_per_row(int nb) {
   return l;
 }
 
+// Issue the copy of row group g (rows r0 .. r0+rows-1) into buf.
+template <typename Rows>
+__device__ __forceinline__ void dma_rows(const Rows& rows, int r0, int n, int nb, uint32_t* buf,
+                                         int lane) {
+  const int cpr = nb * 9;  // 16-B chunks per row
+  dma_chunks([&](int c) { return rows.row(r0 + c / cpr) + 16 * (c % cpr); }, n * cpr, buf, lane);
+}
+
 // y[r] = W[r] . x, one token; grid-stride over row groups.
 template <typename Rows>
 __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned char* __restrict__ xq,
                                                     float* __restrict__ y, int n_rows, int nb,
                                                     int lpr) {
-  __shared__ __attribute__((aligned(16))) uint32_t xs[kMaxNb * kXStride];
-  stage_q8k(xq, nb, xs, threadIdx.x, blockDim.x);
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[kWaves][kBufWords];
+  extern __shared__ __attribute__((aligned(16))) uint32_t xs_dyn[];  // nb * kXStride
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int rpw = 64 / lpr;
+  const int n_groups = (n_rows + rpw - 1) / rpw;
+  const int n_waves = gridDim.x * kWaves;
+  int g = blockIdx.x * kWaves + wv;
+  uint32_t* buf = wbuf[wv];
+  // weights first: their HBM latency overlaps the activation staging
+  if (g < n_groups) dma_rows(rows, g * rpw, min(rpw, n_rows - g * rpw), nb, buf, lane);
+  stage_q8k(xq, nb, xs_dyn, threadIdx.x, blockDim.x);
   __syncthreads();
 
-  const int lane = threadIdx.x & 63;
   const int blk = lane & (lpr - 1);
-  const int rpw = 64 / lpr;
+  const int rr = lane / lpr;
   const bool active = blk < nb;
   int32_t xr[64];
   float xd = 0.f, bsf[8];
-  load_x_regs(xs + (active ? blk : 0) * kXStride, xr, xd, bsf);
+  load_x_regs(xs_dyn + (active ? blk : 0) * kXStride, xr, xd, bsf);
 
-  const int n_groups = (n_rows + rpw - 1) / rpw;
-  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int n_waves = gridDim.x * (blockDim.x >> 6);
-  for (int g = wave; g < n_groups; g += n_waves) {
-    const int r = g * rpw + lane / lpr;
-    float s = 0.f;
-    if (active && r < n_rows) {
-      uint32_t w36[36];
-      load_q4k(rows.row(r) + blk, w36);
-      s = q4k_block_dot(w36, xr, xd, bsf);
-    }
+  for (; g < n_groups; g += n_waves) {
+    const int r0 = g * rpw;
+    const int n = min(rpw, n_rows - r0);
+    wait_vm();
+    uint32_t w36[36];
+    const bool live = active && rr < n;
+    if (live) read_block_lds(buf + (rr * nb + blk) * 36, w36);
+    wait_lds();
+    const int gn = g + n_waves;
+    if (gn < n_groups) dma_rows(rows, gn * rpw, min(rpw, n_rows - gn * rpw), nb, buf, lane);
+    const float s = live ? q4k_block_dot(w36, xr, xd, bsf) : 0.f;
     const float acc = row_sum_in_order(s, lane, lpr, nb);
-    if (blk == 0 && r < n_rows) y[r] = acc;
+    if (blk == 0 && rr < n) y[r0 + rr] = acc;
   }
 }
 
@@ -83,38 +102,45 @@ __global__ void __launch_bounds__(256) gemv_batched_kernel(const sg_block_q4k* _
                                                            const unsigned char* __restrict__ xq,
                                                            float* __restrict__ y, int n_rows,
                                                            int nb, int lpr, int n_tokens) {
-  extern __shared__ __attribute__((aligned(16))) uint32_t xs_dyn[];
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[kWaves][kBufWords];
+  extern __shared__ __attribute__((aligned(16))) uint32_t xs_dyn[];  // T * nb * kXStride
+  const PlainRows rows{w, nb};
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int rpw = 64 / lpr;
+  const int n_groups = (n_rows + rpw - 1) / rpw;
+  const int n_waves = gridDim.x * kWaves;
+  int g = blockIdx.x * kWaves + wv;
+  uint32_t* buf = wbuf[wv];
+  if (g < n_groups) dma_rows(rows, g * rpw, min(rpw, n_rows - g * rpw), nb, buf, lane);
   stage_q8k(xq, nb * n_tokens, xs_dyn, threadIdx.x, blockDim.x);
   __syncthreads();
 
-  const int lane = threadIdx.x & 63;
   const int blk = lane & (lpr - 1);
-  const int rpw = 64 / lpr;
+  const int rr = lane / lpr;
   const bool active = blk < nb;
-  const int n_groups = (n_rows + rpw - 1) / rpw;
-  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int n_waves = gridDim.x * (blockDim.x >> 6);
-  for (int g = wave; g < n_groups; g += n_waves) {
-    const int r = g * rpw + lane / lpr;
-    const bool live = active && r < n_rows;
+  for (; g < n_groups; g += n_waves) {
+    const int r0 = g * rpw;
+    const int n = min(rpw, n_rows - r0);
+    wait_vm();
     uint32_t w36[36];
-    int32_t ip[8];
+    const bool live = active && rr < n;
+    if (live) read_block_lds(buf + (rr * nb + blk) * 36, w36);
+    wait_lds();
+    const int gn = g + n_waves;
+    if (gn < n_groups) dma_rows(rows, gn * rpw, min(rpw, n_rows - gn * rpw), nb, buf, lane);
     ScaleMins sm8{};
-    if (live) {
-      load_q4k(w + static_cast<long long>(r) * nb + blk, w36);
-      sm8 = unpack_scales(w36[1], w36[2], w36[3]);
-    }
+    if (live) sm8 = unpack_scales(w36[1], w36[2], w36[3]);
     for (int t = 0; t < n_tokens; ++t) {
       float s = 0.f;
       if (live) {
-        int32_t xr[64];
+        int32_t xr[64], ip[8];
         float xd, bsf[8];
         load_x_regs(xs_dyn + (t * nb + blk) * kXStride, xr, xd, bsf);
         subblock_dots(w36 + 4, xr, ip);
         s = block_sum(w36[0], sm8, ip, xd, bsf);
       }
       const float acc = row_sum_in_order(s, lane, lpr, nb);
-      if (blk == 0 && r < n_rows) y[static_cast<long long>(t) * n_rows + r] = acc;
+      if (blk == 0 && rr < n) y[static_cast<long long>(t) * n_rows + r0 + rr] = acc;
     }
   }
 }
@@ -124,32 +150,40 @@ __global__ void __launch_bounds__(256) subblock_dots_kernel(const sg_block_q4k* 
                                                             const unsigned char* __restrict__ xq,
                                                             int32_t* __restrict__ dots,
                                                             int n_rows, int nb, int lpr) {
-  __shared__ __attribute__((aligned(16))) uint32_t xs[kMaxNb * kXStride];
-  stage_q8k(xq, nb, xs, threadIdx.x, blockDim.x);
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
-  const int blk = lane & (lpr - 1);
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[kWaves][kBufWords];
+  extern __shared__ __attribute__((aligned(16))) uint32_t xs_dyn[];
+  const PlainRows rows{w, nb};
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int rpw = 64 / lpr;
-  const int g = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int r = g * rpw + lane / lpr;
-  if (blk >= nb || r >= n_rows) return;
+  const int g = blockIdx.x * kWaves + wv;
+  const int n_groups = (n_rows + rpw - 1) / rpw;
+  const int r0 = g * rpw;
+  const int n = g < n_groups ? min(rpw, n_rows - r0) : 0;
+  if (n > 0) dma_rows(rows, r0, n, nb, wbuf[wv], lane);
+  stage_q8k(xq, nb, xs_dyn, threadIdx.x, blockDim.x);
+  __syncthreads();
+  const int blk = lane & (lpr - 1);
+  const int rr = lane / lpr;
+  if (blk >= nb || rr >= n) return;
   int32_t xr[64];
   float xd, bsf[8];
-  load_x_regs(xs + blk * kXStride, xr, xd, bsf);
+  load_x_regs(xs_dyn + blk * kXStride, xr, xd, bsf);
+  wait_vm();
   uint32_t w36[36];
-  load_q4k(w + static_cast<long long>(r) * nb + blk, w36);
+  read_block_lds(wbuf[wv] + (rr * nb + blk) * 36, w36);
   int32_t ip[8];
   subblock_dots(w36 + 4, xr, ip);
-  int32_t* o = dots + (static_cast<long long>(r) * nb + blk) * 8;
+  int32_t* o = dots + (static_cast<long long>(r0 + rr) * nb + blk) * 8;
 #pragma unroll
   for (int s = 0; s < 8; ++s) o[s] = ip[s];
 }
 
-// Grid for a grid-stride row loop: enough waves to cover every row group
-// once, capped at 8 workgroups of 4 waves per CU (256 CUs).
+// Grid for a grid-stride row loop: every row group once, capped at two
+// workgroups of four waves per CU (256 CUs) - enough copies in flight to
+// stream HBM at full rate.
 static unsigned gemv_grid(long long n_groups) {
-  const long long wgs = (n_groups + 3) / 4;
-  const long long cap = 256LL * 8;
+  const long long wgs = (n_groups + kWaves - 1) / kWaves;
+  const long long cap = 256LL * 2;
   return static_cast<unsigned>(wgs < cap ? (wgs > 0 ? wgs : 1) : cap);
 }
 
@@ -174,8 +208,8 @@ int sg_gemv_q4_k_q8(const sg_block_q4k* w, const sg_block_q8k* x, float* y, int 
   if (int st = check_gemv_geometry("sg_gemv_q4_k_q8", n_rows, k)) return st;
   const int nb = k / kQK, lpr = lanes_per_row(nb);
   const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
-  hipLaunchKernelGGL(gemv1_kernel<PlainRows>, dim3(gemv_grid(n_groups)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), PlainRows{w, nb},
+  hipLaunchKernelGGL(gemv1_kernel<PlainRows>, dim3(gemv_grid(n_groups)), dim3(256),
+                     nb * kXStride * 4, static_cast<hipStream_t>(stream), PlainRows{w, nb},
                      reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr);
   return check_launch("sg_gemv_q4_k_q8");
 }
@@ -191,9 +225,10 @@ int sg_gemv_ptrs_q4_k_q8(const sg_block_q4k* const* ptrs, const sg_block_q8k* x,
   if (int st = check_gemv_geometry("sg_gemv_ptrs_q4_k_q8", n_rows, k)) return st;
   const int nb = k / kQK, lpr = lanes_per_row(nb);
   const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
-  hipLaunchKernelGGL(gemv1_kernel<TableRows>, dim3(gemv_grid(n_groups)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), TableRows{ptrs, rows_per, nb},
-                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr);
+  hipLaunchKernelGGL(gemv1_kernel<TableRows>, dim3(gemv_grid(n_groups)), dim3(256),
+                     nb * kXStride * 4, static_cast<hipStream_t>(stream),
+                     TableRows{ptrs, rows_per, nb}, reinterpret_cast<const unsigned char*>(x), y,
+                     n_rows, nb, lpr);
   return check_launch("sg_gemv_ptrs_q4_k_q8");
 }
 
@@ -207,7 +242,7 @@ int sg_gemv_q4_k_q8_batched(const sg_block_q4k* w, const sg_block_q8k* x, float*
                      n_tokens, kMaxTokens);
   const int nb = k / kQK, lpr = lanes_per_row(nb);
   const size_t lds = static_cast<size_t>(nb) * n_tokens * kXStride * 4;
-  if (lds > 160 * 1024)
+  if (lds > 96 * 1024)
     return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_q4_k_q8_batched: k*n_tokens too large for LDS");
   const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
   hipLaunchKernelGGL(gemv_batched_kernel, dim3(gemv_grid(n_groups)), dim3(256), lds,
@@ -224,7 +259,7 @@ int sg_q4k_subblock_dots(const sg_block_q4k* w, const sg_block_q8k* x, int32_t* 
   const int nb = k / kQK, lpr = lanes_per_row(nb);
   const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
   hipLaunchKernelGGL(subblock_dots_kernel, dim3(static_cast<unsigned>((n_groups + 3) / 4)),
-                     dim3(256), 0, static_cast<hipStream_t>(stream), w,
+                     dim3(256), nb * kXStride * 4, static_cast<hipStream_t>(stream), w,
                      reinterpret_cast<const unsigned char*>(x), dots, n_rows, nb, lpr);
   return check_launch("sg_q4k_subblock_dots");
 }

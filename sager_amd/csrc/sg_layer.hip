@@ -1,0 +1,899 @@
+// sg_layer.hip - one fused MoE layer (decode step or verify window) on gfx950.
+//
+// Two launches per layer, on one stream:
+//
+//   front  grid (row chunks of 16, groups): routing + the expert-major plan,
+//          then the gate and up rows of one (group, chunk) and
+//          h = SiLU(g) * u for every token of the group.
+//   back   grid (row chunks of hidden/256 rows): every group's down rows for
+//          the chunk, the Q8_K of h done in the workgroup, and the combine of
+//          the chunk for every token in slot order - all inside one
+//          workgroup, so there are no cross-workgroup counters or fences.
+//
+// Weights stream from HBM into LDS with global_load_lds_dwordx4 (1 KB of
+// consecutive memory per instruction) and are read back per lane at the
+// 144-B super-block stride.  A group is the shared expert (group 0, tokens
+// 0..T-1 in slot k) or one distinct routed expert (ascending id) with its
+// (token, slot) routes; an expert shared by several tokens is streamed once.
+//
+// Stage order and semantics: Session::moe_dispatch_device
+// (session.cpp:2482-3030); router moe.cu:25-85 / 165-234; dispatch plan
+// moe.cu:366-444 (made deterministic); combine moe.cu:265-280; expert chain
+// q4_avx2.cpp:175-196.
+#include "sg_common.hpp"
+#include "sg_router.hpp"
+
+namespace sg {
+
+constexpr int kLMaxExperts = 1024;
+constexpr int kLMaxK = 32;
+constexpr int kLMaxTokens = 16;
+constexpr int kMaxEpt = 16;        // experts per routing thread (1-wave teams, E = 1024)
+constexpr int kBackBufs = 3;       // down-row buffers per wave in the back kernel
+
+__host__ __device__ inline int pow2_ceil(int n) {
+  int l = 1;
+  while (l < n) l <<= 1;
+  return l;
+}
+
+// ---- workspace ------------------------------------------------------------------
+
+struct LayerPlan {
+  int* meta;    // [0] groups, [1] has_shared, [2] valid routes
+  int* off;     // [gmax+1] entry offsets per group
+  int* expert;  // [gmax] expert id per group, -1 = shared expert
+  int* tok;     // [emax] entry token
+  int* slot;    // [emax] entry slot
+  unsigned long long* wdown;  // [gmax] down matrix of the group, 0 = absent expert
+};
+
+struct LayerWs {
+  size_t meta, off, expert, tok, slot, wdown, h, total;
+  int gmax, emax;
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+static LayerWs layer_ws(int T, int n_ff, int E, int k) {
+  LayerWs w{};
+  w.gmax = (T * k < E ? T * k : E) + 1;
+  w.emax = T * k + T;
+  size_t o = 0;
+  w.meta = o;   o = align256(o + 4 * sizeof(int));
+  w.off = o;    o = align256(o + (w.gmax + 1) * sizeof(int));
+  w.expert = o; o = align256(o + w.gmax * sizeof(int));
+  w.tok = o;    o = align256(o + w.emax * sizeof(int));
+  w.slot = o;   o = align256(o + w.emax * sizeof(int));
+  w.wdown = o;  o = align256(o + w.gmax * sizeof(unsigned long long));
+  w.h = o;      o = align256(o + static_cast<size_t>(T) * (k + 1) * n_ff * sizeof(float));
+  w.total = o;
+  return w;
+}
+
+struct LayerArgs {
+  const sg_block_q4k* const* tab_gate;
+  const sg_block_q4k* const* tab_up;
+  const sg_block_q4k* const* tab_down;
+  const sg_block_q4k* sh_gate;
+  const sg_block_q4k* sh_up;
+  const sg_block_q4k* sh_down;
+  const float* x;
+  const float* logits;
+  const float* residual;
+  float* out;
+  int* idx;
+  float* weight;
+  LayerPlan plan;
+  float* h;
+  int T, hidden, n_ff, n_expert, k, has_shared, gmax, emax;
+  float shared_w;
+  int back_rows, back_lrow;  // rows per back workgroup, lanes per row there
+  int back_bufs;             // groups a back wave has in flight (<= kBackBufs)
+};
+
+// ---- front kernel LDS layout (dwords) -----------------------------------------------
+// Routing runs in teams: one team of 4 waves per token for T = 1, two teams
+// of 2 waves for T = 2, four one-wave teams otherwise (tokens in passes).
+struct FrontLds {
+  int nteams, tw, TT, ept, m, ng, npad, e32, ncp;
+  int tabg, tabu, tabd, keys, lv, ev, cand, top, red, zs, spec, ridx, rw, re, rfirst, poff, pexp,
+      ptok, pslot, ctrl, xs, total;
+};
+
+__host__ __device__ inline FrontLds front_lds(int T, int nbh, int E, int k, bool routed) {
+  FrontLds L{};
+  L.nteams = T == 1 ? 1 : (T == 2 ? 2 : 4);
+  L.tw = 4 / L.nteams;
+  L.TT = 64 * L.tw;
+  L.ept = (E + L.TT - 1) / L.TT;
+  L.m = k + 1;
+  L.ng = (E + 63) / 64;
+  L.npad = L.ng * 64;
+  L.e32 = (E + 31) & ~31;
+  L.ncp = (L.ng * L.m + 3) & ~3;
+  const int gmax = (T * k < E ? T * k : E) + 1;
+  int o = 0;
+  auto take = [&](int words) {
+    o = (o + 3) & ~3;  // 16-B alignment for every array
+    const int at = o;
+    o += words;
+    return at;
+  };
+  L.xs = take(T * nbh * kXStride);
+  if (routed) {
+    L.tabg = take(E * 2);
+    L.tabu = take(E * 2);
+    L.tabd = take(E * 2);
+    L.keys = take(L.nteams * L.npad * 2);
+    L.lv = take(L.nteams * L.e32);
+    L.ev = take(L.nteams * L.e32);
+    L.cand = take(L.nteams * L.ncp * 2);
+    L.top = take(L.nteams * L.m * 2);
+    L.red = take(L.nteams * 4);
+    L.zs = take(L.nteams);
+    L.spec = take(T * L.m);
+    L.ridx = take(T * k);
+    L.rw = take(T * (k + 1));
+    L.re = take(T * k);
+    L.rfirst = take(T * k);
+    L.poff = take(gmax + 1);
+    L.pexp = take(gmax);
+    L.ptok = take(T * k + T);
+    L.pslot = take(T * k + T);
+    L.ctrl = take(8);
+  }
+  L.total = o;
+  return L;
+}
+
+// rank of `key` among 64 keys (16-B aligned): how many are larger.
+__device__ __forceinline__ int rank64(const uint64_t* g, uint64_t key) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(g);
+  int r = 0;
+#pragma unroll
+  for (int q = 0; q < 32; ++q) {
+    const u32x4 v = p[q];
+    const uint64_t a = (static_cast<uint64_t>(v.y) << 32) | v.x;
+    const uint64_t b = (static_cast<uint64_t>(v.w) << 32) | v.z;
+    r += (a > key) + (b > key);
+  }
+  return r;
+}
+// rank among n (multiple of 4) keys, 16-B aligned.
+__device__ __forceinline__ int rank_n(const uint64_t* c, int n, uint64_t key) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(c);
+  int r = 0;
+#pragma unroll 4
+  for (int q = 0; q < n / 2; ++q) {
+    const u32x4 v = p[q];
+    const uint64_t a = (static_cast<uint64_t>(v.y) << 32) | v.x;
+    const uint64_t b = (static_cast<uint64_t>(v.w) << 32) | v.z;
+    r += (a > key) + (b > key);
+  }
+  return r;
+}
+
+// Top-m selection of a team over keys[0..npad) (own keys also in kr[]):
+// per 64-key group the m largest, then the m largest of those.  Three
+// workgroup barriers; every thread of the workgroup takes part.
+template <int EPT>
+__device__ void team_select(const FrontLds& L, int E, const uint64_t* keys, const uint64_t* kr,
+                            uint64_t* cand, uint64_t* top, int tt) {
+  const int m = L.m;
+  for (int i = tt; i < L.ncp; i += L.TT) cand[i] = 0;
+  for (int i = tt; i < m; i += L.TT) top[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tt + L.TT * j;
+    if (j < L.ept && i < E && kr[j] != 0) {
+      const int r = rank64(keys + (i & ~63), kr[j]);
+      if (r < m) cand[(i >> 6) * m + r] = kr[j];
+    }
+  }
+  __syncthreads();
+  for (int c = tt; c < L.ng * m; c += L.TT) {
+    const uint64_t kc = cand[c];
+    if (kc == 0) continue;
+    const int r = rank_n(cand, L.ncp, kc);
+    if (r < m) top[r] = kc;
+  }
+  __syncthreads();
+}
+
+// Expert-major plan from ridx[T*k] (ids outside [0, E) skipped): group 0 =
+// shared expert when present, then distinct routed experts ascending;
+// entries in (expert, token, slot) order.  ctrl[0] = valid routes,
+// ctrl[1] = distinct experts.  Runs on wave 0 when T*k <= 64 (cross-lane
+// reads), else on the whole workgroup; ends with a workgroup barrier.
+__device__ void build_plan(uint32_t* dyn, const FrontLds& L, int T, int k, int E, int has_shared,
+                           int tid) {
+  const int* ridx = reinterpret_cast<const int*>(dyn + L.ridx);
+  int* re = reinterpret_cast<int*>(dyn + L.re);
+  int* rfirst = reinterpret_cast<int*>(dyn + L.rfirst);
+  int* poff = reinterpret_cast<int*>(dyn + L.poff);
+  int* pexp = reinterpret_cast<int*>(dyn + L.pexp);
+  int* ptok = reinterpret_cast<int*>(dyn + L.ptok);
+  int* pslot = reinterpret_cast<int*>(dyn + L.pslot);
+  int* ctrl = reinterpret_cast<int*>(dyn + L.ctrl);
+  const int R = T * k;
+  const int gbase = has_shared, ebase = has_shared ? T : 0;
+  if (R <= 64) {
+    if (tid < 64) {
+      const int lane = tid;
+      int e = lane < R ? ridx[lane] : -1;
+      if (e >= E) e = -1;
+      bool first = e >= 0;
+      for (int j = 0; j < R; ++j) {
+        const int ej = __builtin_amdgcn_readlane(e, j);
+        first &= !(j < lane && ej == e);
+      }
+      const int fi = first;
+      int rank = 0, grp = 0;
+      for (int j = 0; j < R; ++j) {
+        const int ej = __builtin_amdgcn_readlane(e, j);
+        const int fj = __builtin_amdgcn_readlane(fi, j);
+        if (ej >= 0) {
+          rank += ej < e || (ej == e && j < lane);
+          grp += fj && ej < e;
+        }
+      }
+      const int nv = __popcll(__ballot(e >= 0));
+      const int nf = __popcll(__ballot(first));
+      if (lane < R) re[lane] = e;
+      if (e >= 0) {
+        ptok[ebase + rank] = lane / k;
+        pslot[ebase + rank] = lane % k;
+        if (first) {
+          poff[gbase + grp] = ebase + rank;
+          pexp[gbase + grp] = e;
+        }
+      }
+      if (has_shared && lane < T) {
+        ptok[lane] = lane;
+        pslot[lane] = k;
+      }
+      if (lane == 0) {
+        poff[0] = 0;
+        poff[gbase + nf] = ebase + nv;
+        if (has_shared) pexp[0] = -1;
+        ctrl[0] = nv;
+        ctrl[1] = nf;
+      }
+    }
+    __syncthreads();
+    return;
+  }
+  if (tid == 0) ctrl[0] = ctrl[1] = 0;
+  for (int i = tid; i < R; i += 256) {
+    const int e = ridx[i];
+    re[i] = (e >= 0 && e < E) ? e : -1;
+  }
+  __syncthreads();
+  for (int i = tid; i < R; i += 256) {
+    const int e = re[i];
+    int first = e >= 0;
+    for (int j = 0; j < i && first; ++j) first = re[j] != e;
+    rfirst[i] = first;
+    if (e >= 0) atomicAdd(&ctrl[0], 1);
+    if (first) atomicAdd(&ctrl[1], 1);
+  }
+  __syncthreads();
+  for (int i = tid; i < R; i += 256) {
+    const int e = re[i];
+    if (e < 0) continue;
+    int rank = 0, grp = 0;
+    for (int j = 0; j < R; ++j) {
+      const int ej = re[j];
+      if (ej < 0) continue;
+      rank += ej < e || (ej == e && j < i);
+      grp += rfirst[j] && ej < e;
+    }
+    ptok[ebase + rank] = i / k;
+    pslot[ebase + rank] = i % k;
+    if (rfirst[i]) {
+      poff[gbase + grp] = ebase + rank;
+      pexp[gbase + grp] = e;
+    }
+  }
+  if (has_shared && tid < T) {
+    ptok[tid] = tid;
+    pslot[tid] = k;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    poff[0] = 0;
+    poff[gbase + ctrl[1]] = ebase + ctrl[0];
+    if (has_shared) pexp[0] = -1;
+  }
+  __syncthreads();
+}
+
+// ---- front kernel ---------------------------------------------------------------------
+// Routing is recomputed by every routed workgroup, split so the weight
+// stream starts early: the top-k by LOGIT (index tie rule) fixes the plan and
+// the copy is issued; then the exact probabilities are computed (max, exp,
+// the normalizer summed serially in index order, p = e / z).  p is a
+// monotone function of the logit, so the logit order is the probability
+// order unless two neighbours collide on one float; that is checked (p
+// strictly decreasing across the k+1 leading candidates, or equal logits),
+// and a collision or a degenerate row (NaN, empty normalizer) falls back to
+// selecting on the probabilities themselves.  If the final plan gives this
+// workgroup another expert, its copy is redone.  Chunk 0 of the first
+// routed group publishes idx, weight and the plan for the back kernel.
+template <int EPT>
+__global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
+  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = a.T, k = a.k, E = a.n_expert, stride = k + 1;
+  const int g = blockIdx.y;
+  const int nbh = a.hidden / kQK, lpr = pow2_ceil(nbh);
+  const bool shared_grp = a.has_shared && g == 0;
+  const FrontLds L = front_lds(T, nbh, E, k, !shared_grp);
+  const int rpw = 32 / lpr;
+  const int row0 = blockIdx.x * 4 * rpw + wave * rpw;
+  const int nrw = max(0, min(rpw, a.n_ff - row0));
+  const int gbase = a.has_shared;
+  uint32_t* buf = wbuf[wave];
+  uint32_t* xs = dyn + L.xs;
+
+  auto dma = [&](const sg_block_q4k* wg, const sg_block_q4k* wu) {
+    const char* pg = reinterpret_cast<const char*>(wg + static_cast<long long>(row0) * nbh);
+    const char* pu = reinterpret_cast<const char*>(wu + static_cast<long long>(row0) * nbh);
+    const int ncg = nrw * nbh * 9;
+    dma_chunks([&](int c) { return c < ncg ? pg + 16 * c : pu + 16 * (c - ncg); }, 2 * ncg, buf,
+               lane);
+  };
+
+  const sg_block_q4k* wg = nullptr;
+  const sg_block_q4k* wu = nullptr;
+  int beg = 0, end = T;  // shared group: tokens 0..T-1 in slot k
+  const int* ptok = nullptr;
+  const int* pslot = nullptr;
+
+  if (shared_grp) {
+    wg = a.sh_gate;
+    wu = a.sh_up;
+    if (nrw > 0) dma(wg, wu);
+  } else {
+    const int tw = L.tw, team = wave / tw, wit = wave - team * tw;
+    const int tt = tid - team * L.TT;
+    const int m = L.m;
+    const unsigned long long* tabg = reinterpret_cast<const unsigned long long*>(dyn + L.tabg);
+    const unsigned long long* tabu = reinterpret_cast<const unsigned long long*>(dyn + L.tabu);
+    const unsigned long long* tabd = reinterpret_cast<const unsigned long long*>(dyn + L.tabd);
+    uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + L.keys) + team * L.npad;
+    float* lv = reinterpret_cast<float*>(dyn + L.lv) + team * L.e32;
+    float* ev = reinterpret_cast<float*>(dyn + L.ev) + team * L.e32;
+    uint64_t* cand = reinterpret_cast<uint64_t*>(dyn + L.cand) + team * L.ncp;
+    uint64_t* top = reinterpret_cast<uint64_t*>(dyn + L.top) + team * m;
+    float* red = reinterpret_cast<float*>(dyn + L.red) + team * 4;
+    float* zs = reinterpret_cast<float*>(dyn + L.zs);
+    int* spec = reinterpret_cast<int*>(dyn + L.spec);
+    int* ridx = reinterpret_cast<int*>(dyn + L.ridx);
+    float* rw = reinterpret_cast<float*>(dyn + L.rw);
+    int* ctrl = reinterpret_cast<int*>(dyn + L.ctrl);
+    const int* pexp = reinterpret_cast<const int*>(dyn + L.pexp);
+    const int* poff = reinterpret_cast<const int*>(dyn + L.poff);
+    ptok = reinterpret_cast<const int*>(dyn + L.ptok);
+    pslot = reinterpret_cast<const int*>(dyn + L.pslot);
+
+    // expert pointer tables into LDS (waves 0-2, one table each)
+    if (wave < 3) {
+      const sg_block_q4k* const* tab = wave == 0 ? a.tab_gate : (wave == 1 ? a.tab_up : a.tab_down);
+      const char* src = reinterpret_cast<const char*>(tab);
+      uint32_t* dst = dyn + (wave == 0 ? L.tabg : (wave == 1 ? L.tabu : L.tabd));
+      dma_range([&](int c) { return src + 16 * c; }, E / 2, dst, lane);
+      if ((E & 1) && lane == 0)  // odd table length: the last pointer by a plain load
+        reinterpret_cast<unsigned long long*>(dst)[E - 1] =
+            reinterpret_cast<unsigned long long>(tab[E - 1]);
+    }
+
+    // 1) plan from the logit order (or from the caller's ids)
+    float lr[EPT];
+    if (a.logits) {
+      for (int t0 = 0; t0 < T; t0 += L.nteams) {
+        const int t = t0 + team;
+        const bool ok = t < T;
+        const float* lg = a.logits + static_cast<long long>(t) * E;
+        uint64_t kr[EPT];
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+          const int i = tt + L.TT * j;
+          const bool in = j < L.ept && i < E && ok;
+          lr[j] = in ? lg[i] : 0.f;
+          kr[j] = in ? sel_key(lr[j], i) : 0;
+          if (j < L.ept && i < L.npad) keys[i] = kr[j];
+          if (j < L.ept && i < L.e32) lv[i] = lr[j];
+        }
+        team_select<EPT>(L, E, keys, kr, cand, top, tt);
+        if (ok && tt < m) spec[t * m + tt] = top[tt] ? sel_idx(top[tt]) : -1;
+        if (T > L.nteams) __syncthreads();
+      }
+      __syncthreads();
+      for (int i = tid; i < T * k; i += 256) ridx[i] = spec[(i / k) * m + (i % k)];
+    } else {
+      for (int i = tid; i < T * k; i += 256) ridx[i] = a.idx[(i / k) * stride + (i % k)];
+      for (int i = tid; i < T * stride; i += 256) rw[i] = a.weight[i];
+    }
+    __syncthreads();
+    build_plan(dyn, L, T, k, E, a.has_shared, tid);
+    int n_groups = gbase + ctrl[1];
+    if (wave < 3) wait_vm();  // pointer tables
+    __syncthreads();
+    const int e_spec = g < n_groups ? pexp[g] : -1;
+    if (e_spec >= 0) {
+      wg = reinterpret_cast<const sg_block_q4k*>(tabg[e_spec]);
+      wu = reinterpret_cast<const sg_block_q4k*>(tabu[e_spec]);
+      if (wg && wu && nrw > 0) dma(wg, wu);
+    }
+
+    // 2) exact probabilities and weights (single pass when T <= teams)
+    if (a.logits) {
+      if (tid == 0) ctrl[3] = 0;  // set when the final selection differs from the plan's
+      for (int t0 = 0; t0 < T; t0 += L.nteams) {
+        const int t = t0 + team;
+        const bool ok = t < T;
+        if (T > L.nteams) {  // later passes: reload this token's logits
+          const float* lg = a.logits + static_cast<long long>(t) * E;
+#pragma unroll
+          for (int j = 0; j < EPT; ++j) {
+            const int i = tt + L.TT * j;
+            lr[j] = (j < L.ept && i < E && ok) ? lg[i] : 0.f;
+            if (j < L.ept && i < L.e32) lv[i] = lr[j];
+          }
+        }
+        if (tid == 0) ctrl[2] = 0;
+        float mx = -1e30f;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+          if (j < L.ept && tt + L.TT * j < E && ok) mx = fmaxf(mx, lr[j]);
+        mx = team_max(mx, red, wit, tw, lane);
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+          const int i = tt + L.TT * j;
+          if (j < L.ept && i < L.e32) ev[i] = (ok && i < E) ? expf_sg(lr[j] - mx) : 0.f;
+        }
+        __syncthreads();
+        if (tt == 0) zs[team] = serial_sum(ev, L.e32);
+        __syncthreads();
+        const float z = zs[team];
+        const bool degen = !(z == z) || z == 0.f;
+        // the check, on the team's first wave: lane kk holds candidate kk
+        bool fast = false;
+        float pk = -1.f;
+        int ik = -1;
+        if (wit == 0) {
+          ik = (ok && lane < m) ? spec[t * m + lane] : -1;
+          pk = (ik >= 0 && !degen) ? ev[ik] / z : -1.f;
+          const float lk = ik >= 0 ? lv[ik] : 0.f;
+          const float pn = __shfl(pk, lane + 1, 64);
+          const float ln = __shfl(lk, lane + 1, 64);
+          const int in = __shfl(ik, lane + 1, 64);
+          bool cond = true;
+          if (lane + 1 < k) cond = ik >= 0 && in >= 0 && (pk > pn || lk == ln);
+          else if (lane + 1 == k && E > k) cond = ik >= 0 && in >= 0 && pk > pn;
+          fast = ok && !degen && __ballot(!cond) == 0;
+          if (lane == 0) {
+            ctrl[4 + team] = ok && !degen && !fast;
+            if (ok && !degen && !fast) atomicOr(&ctrl[2], 1);
+          }
+        }
+        __syncthreads();
+        if (ctrl[2] != 0) {  // selection on the probabilities for the colliding rows
+          const bool slow_team = ctrl[4 + team] != 0;
+          uint64_t kr[EPT];
+#pragma unroll
+          for (int j = 0; j < EPT; ++j) {
+            const int i = tt + L.TT * j;
+            kr[j] = (j < L.ept && i < E && slow_team) ? sel_key(ev[i] / z, i) : 0;
+            if (j < L.ept && i < L.npad) keys[i] = kr[j];
+          }
+          team_select<EPT>(L, E, keys, kr, cand, top, tt);
+        }
+        if (wit == 0 && ok) {
+          int fi;
+          float pv;
+          if (degen) {
+            fi = lane % E;
+            pv = -1.f;
+          } else if (fast) {
+            fi = ik;
+            pv = pk;
+          } else {
+            fi = lane < m && top[lane] ? sel_idx(top[lane]) : 0;
+            pv = ev[fi] / z;
+          }
+          float wsum = 0.f;
+          for (int kk = 0; kk < k; ++kk) wsum += readlane_f(pv, kk);
+          const float wv = wsum > 0.f ? pv / wsum : pv;
+          if (lane < k) {
+            if (fi != ridx[t * k + lane]) atomicOr(&ctrl[3], 1);
+            ridx[t * k + lane] = fi;
+            rw[t * stride + lane] = wv;
+          }
+          if (lane == 0) rw[t * stride + k] = a.shared_w;
+        }
+        __syncthreads();
+      }
+      if (ctrl[3]) {  // the final selection differs from the logit order
+        build_plan(dyn, L, T, k, E, a.has_shared, tid);
+        n_groups = gbase + ctrl[1];
+      }
+    }
+
+    if (blockIdx.x == 0 && g == gbase && wave == 3) {  // publish for the back kernel
+      const int* re = reinterpret_cast<const int*>(dyn + L.re);
+      const int nv = ctrl[0];
+      for (int t = lane; t < T; t += 64) {
+        bool bad = false;  // bounds-kill: a row with an invalid id loses all its weights
+        for (int kk = 0; kk < k; ++kk) bad |= re[t * k + kk] < 0;
+        for (int q = 0; q <= k; ++q) a.weight[t * stride + q] = bad ? 0.f : rw[t * stride + q];
+        if (a.logits)
+          for (int kk = 0; kk < k; ++kk) a.idx[t * stride + kk] = ridx[t * k + kk];
+      }
+      for (int i = lane; i <= n_groups; i += 64) a.plan.off[i] = poff[i];
+      for (int i = lane; i < n_groups; i += 64) {
+        const int e = pexp[i];
+        a.plan.expert[i] = e;
+        const unsigned long long gp = e >= 0 ? tabg[e] : reinterpret_cast<unsigned long long>(a.sh_gate);
+        const unsigned long long up = e >= 0 ? tabu[e] : reinterpret_cast<unsigned long long>(a.sh_up);
+        const unsigned long long dp = e >= 0 ? tabd[e] : reinterpret_cast<unsigned long long>(a.sh_down);
+        a.plan.wdown[i] = (gp && up) ? dp : 0ull;
+      }
+      for (int i = lane; i < (a.has_shared ? T : 0) + nv; i += 64) {
+        a.plan.tok[i] = ptok[i];
+        a.plan.slot[i] = pslot[i];
+      }
+      if (lane == 0) {
+        a.plan.meta[0] = n_groups;
+        a.plan.meta[1] = a.has_shared;
+        a.plan.meta[2] = nv;
+      }
+    }
+    if (g >= n_groups) {
+      wait_vm();  // retire a copy issued for a group that no longer exists
+      return;
+    }
+    const int e = pexp[g];
+    if (e != e_spec) {
+      wait_vm();
+      wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
+      wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
+      if (wg && wu && nrw > 0) dma(wg, wu);
+    }
+    beg = poff[g];
+    end = poff[g + 1];
+  }
+
+  // Q8_K of every token's x into LDS, while the weights are in flight
+  for (int b = wave; b < T * nbh; b += 4) {
+    const float* xb = a.x + static_cast<long long>(b) * kQK + 4 * lane;
+    float v[4] = {xb[0], xb[1], xb[2], xb[3]};
+    quantize_block_wave_lds(v, xs + b * kXStride, lane);
+  }
+  __syncthreads();
+
+  const bool present = wg != nullptr && wu != nullptr;
+  const int half = lane >> 5, hl = lane & 31;
+  const int blk = hl & (lpr - 1), rr = hl / lpr;
+  const bool live = present && blk < nbh && rr < nrw;
+  wait_vm();
+  uint32_t w36[36];
+  ScaleMins sm8{};
+  if (live) {
+    read_block_lds(buf + 36 * (half * nrw * nbh + rr * nbh + blk), w36);
+    sm8 = unpack_scales(w36[1], w36[2], w36[3]);
+  }
+  for (int j = beg; j < end; ++j) {
+    const int t = shared_grp ? j : ptok[j];
+    const int sl = shared_grp ? k : pslot[j];
+    float s = 0.f;
+    if (live) {
+      int32_t xr[64], ip[8];
+      float xd, bsf[8];
+      load_x_regs(xs + (t * nbh + blk) * kXStride, xr, xd, bsf);
+      subblock_dots(w36 + 4, xr, ip);
+      s = block_sum(w36[0], sm8, ip, xd, bsf);
+    }
+    const float acc = row_sum_in_order(s, lane, lpr, nbh);
+    const float up = __shfl_xor(acc, 32, 64);
+    if (half == 0 && blk == 0 && rr < nrw)
+      a.h[(static_cast<long long>(t) * stride + sl) * a.n_ff + row0 + rr] =
+          present ? silu_mul(acc, up) : 0.f;
+  }
+}
+
+// ---- back kernel ------------------------------------------------------------------------
+// One workgroup per chunk of `rows` output rows.  Wave w takes groups w,
+// w+4, w+8, ... (kBackBufs at a time): it streams the group's down rows for
+// the chunk and the group's h rows into LDS, quantizes h to Q8_K with the
+// wave, and writes the slot outputs of the chunk into LDS.  Then the
+// workgroup combines: out = residual + sum_kk fma(w_kk, y_kk), slot order.
+struct BackLds {
+  int wbuf, hbuf, hq, ys, off, wdown, tok, slot, wt, ix, meta, total;
+};
+
+__host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, int nbuf, int gmax,
+                                            int emax) {
+  BackLds L{};
+  const int nbf = n_ff / kQK;
+  int o = 0;
+  auto take = [&](int words) {
+    o = (o + 3) & ~3;
+    const int at = o;
+    o += words;
+    return at;
+  };
+  L.wbuf = take(4 * nbuf * rows * nbf * 36);
+  L.hbuf = take(4 * nbuf * n_ff);
+  L.hq = take(4 * nbf * kXStride);
+  L.ys = take(T * (k + 1) * rows);
+  L.off = take(gmax + 1);
+  L.wdown = take(gmax * 2);
+  L.tok = take(emax);
+  L.slot = take(emax);
+  L.wt = take(T * (k + 1));
+  L.ix = take(T * (k + 1));
+  L.meta = take(4);
+  L.total = o;
+  return L;
+}
+
+__global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = a.T, k = a.k, stride = k + 1;
+  const int nbf = a.n_ff / kQK;
+  const int rows = a.back_rows, lrow = a.back_lrow;
+  const int nbuf = a.back_bufs;
+  const BackLds L = back_lds(T, k, a.n_ff, rows, nbuf, a.gmax, a.emax);
+  int* off = reinterpret_cast<int*>(dyn + L.off);
+  unsigned long long* wdown = reinterpret_cast<unsigned long long*>(dyn + L.wdown);
+  int* tok = reinterpret_cast<int*>(dyn + L.tok);
+  int* slot = reinterpret_cast<int*>(dyn + L.slot);
+  float* wt = reinterpret_cast<float*>(dyn + L.wt);
+  int* ix = reinterpret_cast<int*>(dyn + L.ix);
+  int* meta = reinterpret_cast<int*>(dyn + L.meta);
+  float* ys = reinterpret_cast<float*>(dyn + L.ys);
+
+  // the plan, routing and weights (one round of loads)
+  for (int i = tid; i <= a.gmax; i += 256) off[i] = a.plan.off[i];
+  for (int i = tid; i < a.gmax; i += 256) wdown[i] = a.plan.wdown[i];
+  for (int i = tid; i < a.emax; i += 256) {
+    tok[i] = a.plan.tok[i];
+    slot[i] = a.plan.slot[i];
+  }
+  for (int i = tid; i < T * stride; i += 256) {
+    wt[i] = a.weight[i];
+    ix[i] = a.idx[i];
+  }
+  if (tid < 2) meta[tid] = a.plan.meta[tid];
+  for (int i = tid; i < T * stride * rows; i += 256) ys[i] = 0.f;
+  __syncthreads();
+  const int G = meta[0];
+  const int row0 = blockIdx.x * rows;
+  const int nr = max(0, min(rows, a.hidden - row0));
+  const int rwords = rows * nbf * 36;
+  uint32_t* wb = dyn + L.wbuf + wave * nbuf * rwords;
+  float* hb = reinterpret_cast<float*>(dyn + L.hbuf) + wave * nbuf * a.n_ff;
+  uint32_t* hq = dyn + L.hq + wave * nbf * kXStride;
+  const int blk = lane & (lrow - 1), rr = lane / lrow;
+
+  for (int gb = 0; gb < G; gb += 4 * nbuf) {
+    // issue: down rows and the first entry's h of each of this wave's groups
+#pragma unroll
+    for (int b = 0; b < kBackBufs; ++b) {
+      const int gq = gb + wave + 4 * b;
+      if (b >= nbuf || gq >= G) break;
+      const char* wd = reinterpret_cast<const char*>(wdown[gq]);
+      if (wd && nr > 0) {
+        const char* src = wd + static_cast<long long>(row0) * nbf * kQ4Bytes;
+        dma_chunks([&](int c) { return src + 16 * c; }, nr * nbf * 9, wb + b * rwords, lane);
+      }
+      const int j0 = off[gq];
+      const char* hsrc = reinterpret_cast<const char*>(
+          a.h + (static_cast<long long>(tok[j0]) * stride + slot[j0]) * a.n_ff);
+      dma_range([&](int c) { return hsrc + 16 * c; }, a.n_ff / 4,
+                reinterpret_cast<uint32_t*>(hb + b * a.n_ff), lane);
+    }
+    wait_vm();
+#pragma unroll
+    for (int b = 0; b < kBackBufs; ++b) {
+      const int gq = gb + wave + 4 * b;
+      if (b >= nbuf || gq >= G) break;
+      const bool present = wdown[gq] != 0ull;
+      const bool live = present && blk < nbf && rr < nr;
+      uint32_t w36[36];
+      ScaleMins sm8{};
+      if (live) {
+        read_block_lds(wb + b * rwords + 36 * (rr * nbf + blk), w36);
+        sm8 = unpack_scales(w36[1], w36[2], w36[3]);
+      }
+      for (int j = off[gq]; j < off[gq + 1]; ++j) {
+        const float* hsrc = hb + b * a.n_ff;
+        if (j != off[gq]) {  // a further token of this expert: fetch its h row
+          const char* hg = reinterpret_cast<const char*>(
+              a.h + (static_cast<long long>(tok[j]) * stride + slot[j]) * a.n_ff);
+          uint32_t* hd = reinterpret_cast<uint32_t*>(hb + b * a.n_ff);
+          wait_lds();
+          dma_range([&](int c) { return hg + 16 * c; }, a.n_ff / 4, hd, lane);
+          wait_vm();
+        }
+        for (int bb = 0; bb < nbf; ++bb) {
+          const float* hp = hsrc + bb * kQK + 4 * lane;
+          float v[4] = {hp[0], hp[1], hp[2], hp[3]};
+          quantize_block_wave_lds(v, hq + bb * kXStride, lane);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float s = 0.f;
+        if (live) {
+          int32_t xr[64], ip[8];
+          float xd, bsf[8];
+          load_x_regs(hq + blk * kXStride, xr, xd, bsf);
+          subblock_dots(w36 + 4, xr, ip);
+          s = block_sum(w36[0], sm8, ip, xd, bsf);
+        }
+        const float acc = row_sum_in_order(s, lane, lrow, nbf);
+        if (blk == 0 && rr < nr)
+          ys[(tok[j] * stride + slot[j]) * rows + rr] = present ? acc : 0.f;
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+    wait_lds();
+  }
+  __syncthreads();
+  const int has_shared = meta[1];
+  for (int q = tid; q < T * nr; q += 256) {
+    const int t = q / nr, r = q - t * nr;
+    const long long o = static_cast<long long>(t) * a.hidden + row0 + r;
+    float acc = a.residual ? a.residual[o] : 0.f;
+    for (int kk = 0; kk <= k; ++kk) {
+      bool ok;
+      if (kk < k) {
+        const int ee = ix[t * stride + kk];
+        ok = ee >= 0 && ee < a.n_expert;
+      } else {
+        ok = has_shared != 0;
+      }
+      const float yv = ok ? ys[(t * stride + kk) * rows + r] : 0.f;
+      acc = __builtin_fmaf(wt[t * stride + kk], yv, acc);
+    }
+    a.out[o] = acc;
+  }
+}
+
+static void back_geometry(int hidden, int n_ff, int& rows, int& lrow) {
+  const int lpr = pow2_ceil(n_ff / kQK);
+  int r = 64 / lpr;                  // rows a wave covers with every lane busy
+  while (r > 1 && hidden / r < 256) r >>= 1;  // at least 256 workgroups when possible
+  rows = r;
+  lrow = 64 / r;
+}
+
+}  // namespace sg
+
+using namespace sg;
+
+extern "C" {
+
+size_t sg_moe_layer_workspace_bytes(int n_tokens, int hidden, int n_ff, int n_expert, int k) {
+  if (n_tokens <= 0 || hidden <= 0 || n_ff <= 0 || n_expert <= 0 || k <= 0) return 0;
+  return layer_ws(n_tokens, n_ff, n_expert, k).total;
+}
+
+int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
+                        const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
+                        const sg_block_q4k* sh_up, const sg_block_q4k* sh_down, const float* x,
+                        const float* logits, const float* residual, float* out, int* idx,
+                        float* weight, void* workspace, size_t workspace_bytes, int n_tokens,
+                        int hidden, int n_ff, int n_expert, int k, float shared_w, int stages,
+                        void* stream) {
+  const char* nm = "sg_moe_layer";
+  if (stages <= 0 || stages > 3)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: stages=%d not in 1..3", nm, stages);
+  if (!tab_gate || !tab_up || !tab_down || !x || !out || !idx || !weight || !workspace)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  const int n_sh = (sh_gate != nullptr) + (sh_up != nullptr) + (sh_down != nullptr);
+  if (n_sh != 0 && n_sh != 3)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: shared expert needs gate, up and down", nm);
+  if (n_tokens <= 0 || n_tokens > kLMaxTokens)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: n_tokens=%d not in [1,%d]", nm, n_tokens,
+                     kLMaxTokens);
+  if (hidden <= 0 || hidden % kQK || n_ff <= 0 || n_ff % kQK)
+    return set_error(SG_ERR_GEOMETRY, "%s: hidden=%d n_ff=%d must be multiples of 256", nm, hidden,
+                     n_ff);
+  if (hidden > 32 * kQK || n_ff > 64 * kQK)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: hidden=%d (<=8192) n_ff=%d (<=16384)", nm, hidden,
+                     n_ff);
+  if (k <= 0 || k > kLMaxK || n_expert < k || n_expert > kLMaxExperts)
+    return set_error(SG_ERR_GEOMETRY, "%s: k=%d (<=%d) n_expert=%d (k..%d)", nm, k, kLMaxK,
+                     n_expert, kLMaxExperts);
+  const LayerWs ws = layer_ws(n_tokens, n_ff, n_expert, k);
+  if (workspace_bytes < ws.total)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: workspace %zu < %zu bytes", nm,
+                     workspace_bytes, ws.total);
+  int rows = 1, lrow = 64;
+  back_geometry(hidden, n_ff, rows, lrow);
+  const size_t lds_f =
+      static_cast<size_t>(front_lds(n_tokens, hidden / kQK, n_expert, k, true).total) * 4;
+  int nbuf = kBackBufs;
+  size_t lds_b = 0;
+  for (; nbuf >= 1; --nbuf) {
+    lds_b = static_cast<size_t>(back_lds(n_tokens, k, n_ff, rows, nbuf, ws.gmax, ws.emax).total) * 4;
+    if (lds_b <= 64 * 1024) break;
+  }
+  if (lds_f + 4 * 64 * 36 * 4 > 160 * 1024 || nbuf < 1)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: this shape needs more LDS than a workgroup has",
+                     nm);
+  unsigned char* base = static_cast<unsigned char*>(workspace);
+  LayerArgs a{};
+  a.tab_gate = tab_gate;
+  a.tab_up = tab_up;
+  a.tab_down = tab_down;
+  a.sh_gate = sh_gate;
+  a.sh_up = sh_up;
+  a.sh_down = sh_down;
+  a.x = x;
+  a.logits = logits;
+  a.residual = residual;
+  a.out = out;
+  a.idx = idx;
+  a.weight = weight;
+  a.plan = LayerPlan{reinterpret_cast<int*>(base + ws.meta), reinterpret_cast<int*>(base + ws.off),
+                     reinterpret_cast<int*>(base + ws.expert),
+                     reinterpret_cast<int*>(base + ws.tok), reinterpret_cast<int*>(base + ws.slot),
+                     reinterpret_cast<unsigned long long*>(base + ws.wdown)};
+  a.h = reinterpret_cast<float*>(base + ws.h);
+  a.T = n_tokens;
+  a.hidden = hidden;
+  a.n_ff = n_ff;
+  a.n_expert = n_expert;
+  a.k = k;
+  a.has_shared = n_sh == 3;
+  a.gmax = ws.gmax;
+  a.emax = ws.emax;
+  a.shared_w = shared_w;
+  a.back_rows = rows;
+  a.back_lrow = lrow;
+  a.back_bufs = nbuf;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (stages & 1) {
+    const int rows_wg = 4 * (32 / pow2_ceil(hidden / kQK));
+    const FrontLds fl = front_lds(n_tokens, hidden / kQK, n_expert, k, true);
+    const dim3 grid((n_ff + rows_wg - 1) / rows_wg, ws.gmax);
+    if (fl.ept <= 1)
+      hipLaunchKernelGGL(layer_front_kernel<1>, grid, dim3(256), lds_f, s, a);
+    else if (fl.ept <= 2)
+      hipLaunchKernelGGL(layer_front_kernel<2>, grid, dim3(256), lds_f, s, a);
+    else if (fl.ept <= 4)
+      hipLaunchKernelGGL(layer_front_kernel<4>, grid, dim3(256), lds_f, s, a);
+    else
+      hipLaunchKernelGGL(layer_front_kernel<kMaxEpt>, grid, dim3(256), lds_f, s, a);
+    if (int st = check_launch("sg_moe_layer/front")) return st;
+  }
+  if (stages & 2) {
+    hipLaunchKernelGGL(layer_back_kernel, dim3((hidden + rows - 1) / rows), dim3(256), lds_b, s,
+                       a);
+    if (int st = check_launch("sg_moe_layer/back")) return st;
+  }
+  return SG_OK;
+}
+
+int sg_moe_layer(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
+                 const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
+                 const sg_block_q4k* sh_up, const sg_block_q4k* sh_down, const float* x,
+                 const float* logits, const float* residual, float* out, int* idx,
+                 float* weight, void* workspace, size_t workspace_bytes, int n_tokens, int hidden,
+                 int n_ff, int n_expert, int k, float shared_w, void* stream) {
+  return sg_moe_layer_stages(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, x, logits,
+                             residual, out, idx, weight, workspace, workspace_bytes, n_tokens,
+                             hidden, n_ff, n_expert, k, shared_w, 3, stream);
+}
+
+}  // extern "C"

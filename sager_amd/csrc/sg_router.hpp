@@ -1,0 +1,86 @@
+// sg_router.hpp - top-k selection building blocks for the fused MoE layer.
+//
+// Selection order everywhere: value descending, then index ascending - the
+// order the reference's k rounds of first-strict-max produce
+// (moe.cu:46-76).  A candidate is a 64-bit key, high word = the value mapped
+// to an unsigned int that orders like the float (NaN lowest), low word =
+// ~index, so "larger key" is exactly "earlier in the selection" and keys are
+// distinct.
+#pragma once
+
+#include "sg_common.hpp"
+
+namespace sg {
+
+__device__ __forceinline__ uint64_t sel_key(float v, int i) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  const uint32_t o = (v != v) ? 0u : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
+  return (static_cast<uint64_t>(o) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
+}
+__device__ __forceinline__ int sel_idx(uint64_t key) {
+  return static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(key));
+}
+
+// Top-m keys (m <= 33) of keys[0..n) for a team of nthr threads (thread tt).
+// Two levels: the top m of every 64-key group (rank by direct comparison
+// inside the group), then the top m of those candidates.  Results in
+// top[0..m) in selection order (0 = missing).  cand holds ceil(n/64)*m keys.
+// Every thread of the workgroup must call this together: it contains three
+// workgroup barriers.
+__device__ void team_top_m(const uint64_t* keys, int n, int m, uint64_t* cand, uint64_t* top,
+                           int tt, int nthr) {
+  const int ng = (n + 63) >> 6;
+  for (int i = tt; i < ng * m; i += nthr) cand[i] = 0;
+  for (int i = tt; i < m; i += nthr) top[i] = 0;
+  __syncthreads();
+  for (int i = tt; i < n; i += nthr) {
+    const uint64_t ki = keys[i];
+    const int g0 = i & ~63, g1 = min(n, g0 + 64);
+    int r = 0;
+    for (int j = g0; j < g1; ++j) r += keys[j] > ki;
+    if (r < m && ki != 0) cand[(g0 >> 6) * m + r] = ki;
+  }
+  __syncthreads();
+  const int nc = ng * m;
+  for (int c = tt; c < nc; c += nthr) {
+    const uint64_t kc = cand[c];
+    if (kc == 0) continue;
+    int r = 0;
+    for (int d = 0; d < nc; ++d) r += cand[d] > kc;
+    if (r < m) top[r] = kc;
+  }
+  __syncthreads();
+}
+
+// Maximum of v over a team of nw waves (fmaxf semantics); `red` holds nw
+// floats of team scratch.  Contains one workgroup barrier.
+__device__ __forceinline__ float team_max(float v, float* red, int wave_in_team, int nw, int lane) {
+  v = wave_max_dpp(v);
+  if (lane == 0) red[wave_in_team] = v;
+  __syncthreads();
+  float m = red[0];
+  for (int w = 1; w < nw; ++w) m = fmaxf(m, red[w]);
+  return m;
+}
+
+// Serial sum x[0] + x[1] + ... + x[n-1] in index order by ONE thread, from
+// LDS padded with +0 to a multiple of 32 (adding +0 changes nothing).
+__device__ __forceinline__ float serial_sum(const float* x, int n32) {
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float z = 0.f;
+  for (int i = 0; i < n32 / 4; i += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = x4[i + q];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      z += v[q].x;
+      z += v[q].y;
+      z += v[q].z;
+      z += v[q].w;
+    }
+  }
+  return z;
+}
+
+}  // namespace sg

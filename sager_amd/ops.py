@@ -141,7 +141,7 @@ class MoeLayer:
         self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=tab_gate.device)
 
     def forward(self, x, logits=None, residual=None, out=None, idx=None, weight=None,
-                stages=7, workspace=None):
+                stages=3, workspace=None):
         T = x.shape[0]
         if T > self.max_tokens:
             raise SagerError(f"{T} tokens > max_tokens={self.max_tokens}")

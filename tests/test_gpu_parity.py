@@ -272,3 +272,65 @@ def test_moe_layer_routed_edge_cases():
                                n_ff=F, k=K)
     np.testing.assert_array_equal(host(wgt), rw)
     assert_fp32_parity(host(out), ref)
+
+
+@pytest.mark.parametrize("T", [2, 3, 4, 5])
+def test_moe_layer_routing_edge_cases(T):
+    """Fused routing against the oracle where the logit order and the
+    probability order can part: boundary ties, all-equal rows, a NaN row
+    (degenerate selection), -inf logits; T = 2..5 covers the 2-wave teams,
+    an idle team and two routing passes."""
+    rng = np.random.default_rng(900 + T)
+    H, F, E, K = 512, 256, 32, 8
+    g, u, d = _expert_pool(rng, E + 1, H, F)
+    shared = (g.pop(), u.pop(), d.pop())
+    x = rng.normal(0, 1, (T, H)).astype(np.float32)
+    lg = rng.normal(0, 1, (T, E)).astype(np.float32)
+    lg[0, [4, 9, 20]] = lg[0].max() + 0.5          # 3-way tie at the top
+    o = np.argsort(-lg[0], kind="stable")
+    lg[0, o[8]] = lg[0, o[7]]                        # tie across the k boundary
+    lg[1] = 0.125                                    # all equal
+    if T > 2:
+        lg[2, 7] = np.nan                            # degenerate row
+    if T > 3:
+        lg[3, :5] = -np.inf
+    layer = _layer(g, u, d, shared, H, F, K, T)
+    out, idx, w = layer.forward(dev(x), dev(lg))
+    ref, ri, rw = orc.moe_layer(g, u, d, shared, x, logits=lg, hidden=H, n_ff=F, k=K)
+    np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K])
+    np.testing.assert_array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+    np.testing.assert_array_equal(host(out).view(np.uint32), ref.view(np.uint32))
+
+
+def _collision_logits(E, K, seed):
+    """Search (on the oracle) for a logit row where two distinct logits, one
+    float ulp apart, give the same probability, so the probability order
+    (lower index first) differs from the logit order."""
+    rng = np.random.default_rng(seed)
+    for _ in range(20000):
+        lg = (rng.normal(0, 1, E) - 4.0).astype(np.float32)
+        top = rng.choice(E, 2, replace=False)
+        hi_i, lo_i = max(top), min(top)               # higher index gets the larger logit
+        base = np.float32(rng.uniform(0.5, 2.0))
+        lg[lo_i] = base
+        lg[hi_i] = np.nextafter(base, np.float32(9.0))
+        idx, _ = orc.router_topk(lg[None], K)
+        if idx[0, 0] == lo_i:                         # probabilities tied -> lower index first
+            return lg[None]
+    raise AssertionError("no collision found")
+
+
+def test_moe_layer_near_collision_probabilities():
+    """Distinct logits whose probabilities round to the same float: the fused
+    routing must fall back from the logit order to the exact selection."""
+    H, F, E, K = 512, 256, 64, 8
+    rng = np.random.default_rng(5150)
+    g, u, d = _expert_pool(rng, E, H, F)
+    x = rng.normal(0, 1, (1, H)).astype(np.float32)
+    lg = _collision_logits(E, K, 77)
+    layer = _layer(g, u, d, None, H, F, K, 1)
+    out, idx, w = layer.forward(dev(x), dev(lg))
+    ref, ri, rw = orc.moe_layer(g, u, d, None, x, logits=lg, hidden=H, n_ff=F, k=K)
+    np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K])
+    np.testing.assert_array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+    np.testing.assert_array_equal(host(out).view(np.uint32), ref.view(np.uint32))
