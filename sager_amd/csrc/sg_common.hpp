@@ -327,13 +327,18 @@ __device__ __forceinline__ void load_x_regs(const uint32_t* lds_blk, int32_t* xq
   for (int s = 0; s < 8; ++s) bsf[s] = __builtin_bit_cast(float, lds_blk[65 + s]);
 }
 
-// Sum the per-block partial sums of the `lpr` lanes of a row group in block
-// order (acc = 0; acc += s_0; ...; acc += s_{nb-1}), the reference's row
-// accumulation.  Every lane of the group returns the row result.
-__device__ __forceinline__ float row_sum_in_order(float s, int lane, int lpr, int nb) {
-  const int base = lane & ~(lpr - 1);
-  float acc = 0.f;
-  for (int j = 0; j < nb; ++j) acc += __shfl(s, base + j, 64);
+// Sum the per-block partial sums of a row in block order
+// (acc = 0; acc += s_0; ...; acc += s_{nb-1}), the reference's row
+// accumulation (q4_avx2.cpp:130-143).  Lane `blk` of the row holds s_blk;
+// each step moves the running sum one lane up with a DPP wave shift, so the
+// complete row sum ends in the lane with blk == nb - 1.  All lanes active.
+constexpr int kDppWaveShr1 = 0x138;
+__device__ __forceinline__ float row_sum_last(float s, int blk, int nb) {
+  float acc = 0.f + s;
+  for (int j = 1; j < nb; ++j) {
+    const float prev = dpp_f<kDppWaveShr1>(acc);
+    if (blk == j) acc = prev + s;
+  }
   return acc;
 }
 

@@ -9,7 +9,7 @@
 // eight int32 sub-block dots with v_dot4_i32_i8 against its Q8_K activation
 // block kept in registers, applies the fp32 super-block epilogue, and the
 // lpr block sums of a row are added in block order (the reference's
-// acc += sum order, q4_avx2.cpp:130-143).  The next group's copy is issued
+// acc += sum order, q4_avx2.cpp:130-143) with DPP lane shifts.  The next group's copy is issued
 // as soon as the block is in registers, so it overlaps the arithmetic.
 //
 // Reference kernels replaced: gemv_q4_k_q8 / gemv_mtok_ro_f32_kernel
@@ -92,8 +92,8 @@ __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned ch
     const int gn = g + n_waves;
     if (gn < n_groups) dma_rows(rows, gn * rpw, min(rpw, n_rows - gn * rpw), nb, buf, lane);
     const float s = live ? q4k_block_dot(w36, xr, xd, bsf) : 0.f;
-    const float acc = row_sum_in_order(s, lane, lpr, nb);
-    if (blk == 0 && rr < n) y[r0 + rr] = acc;
+    const float acc = row_sum_last(s, blk, nb);
+    if (blk == nb - 1 && rr < n) y[r0 + rr] = acc;
   }
 }
 
@@ -139,8 +139,8 @@ __global__ void __launch_bounds__(256) gemv_batched_kernel(const sg_block_q4k* _
         subblock_dots(w36 + 4, xr, ip);
         s = block_sum(w36[0], sm8, ip, xd, bsf);
       }
-      const float acc = row_sum_in_order(s, lane, lpr, nb);
-      if (blk == 0 && rr < n) y[static_cast<long long>(t) * n_rows + r0 + rr] = acc;
+      const float acc = row_sum_last(s, blk, nb);
+      if (blk == nb - 1 && rr < n) y[static_cast<long long>(t) * n_rows + r0 + rr] = acc;
     }
   }
 }

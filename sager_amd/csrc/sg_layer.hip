@@ -46,10 +46,12 @@ struct LayerPlan {
   int* tok;     // [emax] entry token
   int* slot;    // [emax] entry slot
   unsigned long long* wdown;  // [gmax] down matrix of the group, 0 = absent expert
+  int* fix;     // [T*(k+1)] 1 = take this slot's h from hfix
+  float* hfix;  // [T*(k+1)][n_ff] repaired h rows
 };
 
 struct LayerWs {
-  size_t meta, off, expert, tok, slot, wdown, h, total;
+  size_t meta, off, expert, tok, slot, wdown, fix, hfix, h, total;
   int gmax, emax;
 };
 
@@ -66,6 +68,8 @@ static LayerWs layer_ws(int T, int n_ff, int E, int k) {
   w.tok = o;    o = align256(o + w.emax * sizeof(int));
   w.slot = o;   o = align256(o + w.emax * sizeof(int));
   w.wdown = o;  o = align256(o + w.gmax * sizeof(unsigned long long));
+  w.fix = o;    o = align256(o + static_cast<size_t>(T) * (k + 1) * sizeof(int));
+  w.hfix = o;   o = align256(o + static_cast<size_t>(T) * (k + 1) * n_ff * sizeof(float));
   w.h = o;      o = align256(o + static_cast<size_t>(T) * (k + 1) * n_ff * sizeof(float));
   w.total = o;
   return w;
@@ -141,7 +145,7 @@ __host__ __device__ inline FrontLds front_lds(int T, int nbh, int E, int k, bool
     L.pexp = take(gmax);
     L.ptok = take(T * k + T);
     L.pslot = take(T * k + T);
-    L.ctrl = take(8);
+    L.ctrl = take(8 + T * k);
   }
   L.total = o;
   return L;
@@ -311,273 +315,15 @@ __device__ void build_plan(uint32_t* dyn, const FrontLds& L, int T, int k, int E
 }
 
 // ---- front kernel ---------------------------------------------------------------------
-// Routing is recomputed by every routed workgroup, split so the weight
-// stream starts early: the top-k by LOGIT (index tie rule) fixes the plan and
-// the copy is issued; then the exact probabilities are computed (max, exp,
-// the normalizer summed serially in index order, p = e / z).  p is a
-// monotone function of the logit, so the logit order is the probability
-// order unless two neighbours collide on one float; that is checked (p
-// strictly decreasing across the k+1 leading candidates, or equal logits),
-// and a collision or a degenerate row (NaN, empty normalizer) falls back to
-// selecting on the probabilities themselves.  If the final plan gives this
-// workgroup another expert, its copy is redone.  Chunk 0 of the first
-// routed group publishes idx, weight and the plan for the back kernel.
-template <int EPT>
-__global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
-  __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
-  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int T = a.T, k = a.k, E = a.n_expert, stride = k + 1;
-  const int g = blockIdx.y;
-  const int nbh = a.hidden / kQK, lpr = pow2_ceil(nbh);
-  const bool shared_grp = a.has_shared && g == 0;
-  const FrontLds L = front_lds(T, nbh, E, k, !shared_grp);
-  const int rpw = 32 / lpr;
-  const int row0 = blockIdx.x * 4 * rpw + wave * rpw;
-  const int nrw = max(0, min(rpw, a.n_ff - row0));
-  const int gbase = a.has_shared;
-  uint32_t* buf = wbuf[wave];
-  uint32_t* xs = dyn + L.xs;
-
-  auto dma = [&](const sg_block_q4k* wg, const sg_block_q4k* wu) {
-    const char* pg = reinterpret_cast<const char*>(wg + static_cast<long long>(row0) * nbh);
-    const char* pu = reinterpret_cast<const char*>(wu + static_cast<long long>(row0) * nbh);
-    const int ncg = nrw * nbh * 9;
-    dma_chunks([&](int c) { return c < ncg ? pg + 16 * c : pu + 16 * (c - ncg); }, 2 * ncg, buf,
-               lane);
-  };
-
-  const sg_block_q4k* wg = nullptr;
-  const sg_block_q4k* wu = nullptr;
-  int beg = 0, end = T;  // shared group: tokens 0..T-1 in slot k
-  const int* ptok = nullptr;
-  const int* pslot = nullptr;
-
-  if (shared_grp) {
-    wg = a.sh_gate;
-    wu = a.sh_up;
-    if (nrw > 0) dma(wg, wu);
-  } else {
-    const int tw = L.tw, team = wave / tw, wit = wave - team * tw;
-    const int tt = tid - team * L.TT;
-    const int m = L.m;
-    const unsigned long long* tabg = reinterpret_cast<const unsigned long long*>(dyn + L.tabg);
-    const unsigned long long* tabu = reinterpret_cast<const unsigned long long*>(dyn + L.tabu);
-    const unsigned long long* tabd = reinterpret_cast<const unsigned long long*>(dyn + L.tabd);
-    uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + L.keys) + team * L.npad;
-    float* lv = reinterpret_cast<float*>(dyn + L.lv) + team * L.e32;
-    float* ev = reinterpret_cast<float*>(dyn + L.ev) + team * L.e32;
-    uint64_t* cand = reinterpret_cast<uint64_t*>(dyn + L.cand) + team * L.ncp;
-    uint64_t* top = reinterpret_cast<uint64_t*>(dyn + L.top) + team * m;
-    float* red = reinterpret_cast<float*>(dyn + L.red) + team * 4;
-    float* zs = reinterpret_cast<float*>(dyn + L.zs);
-    int* spec = reinterpret_cast<int*>(dyn + L.spec);
-    int* ridx = reinterpret_cast<int*>(dyn + L.ridx);
-    float* rw = reinterpret_cast<float*>(dyn + L.rw);
-    int* ctrl = reinterpret_cast<int*>(dyn + L.ctrl);
-    const int* pexp = reinterpret_cast<const int*>(dyn + L.pexp);
-    const int* poff = reinterpret_cast<const int*>(dyn + L.poff);
-    ptok = reinterpret_cast<const int*>(dyn + L.ptok);
-    pslot = reinterpret_cast<const int*>(dyn + L.pslot);
-
-    // expert pointer tables into LDS (waves 0-2, one table each)
-    if (wave < 3) {
-      const sg_block_q4k* const* tab = wave == 0 ? a.tab_gate : (wave == 1 ? a.tab_up : a.tab_down);
-      const char* src = reinterpret_cast<const char*>(tab);
-      uint32_t* dst = dyn + (wave == 0 ? L.tabg : (wave == 1 ? L.tabu : L.tabd));
-      dma_range([&](int c) { return src + 16 * c; }, E / 2, dst, lane);
-      if ((E & 1) && lane == 0)  // odd table length: the last pointer by a plain load
-        reinterpret_cast<unsigned long long*>(dst)[E - 1] =
-            reinterpret_cast<unsigned long long>(tab[E - 1]);
-    }
-
-    // 1) plan from the logit order (or from the caller's ids)
-    float lr[EPT];
-    if (a.logits) {
-      for (int t0 = 0; t0 < T; t0 += L.nteams) {
-        const int t = t0 + team;
-        const bool ok = t < T;
-        const float* lg = a.logits + static_cast<long long>(t) * E;
-        uint64_t kr[EPT];
-#pragma unroll
-        for (int j = 0; j < EPT; ++j) {
-          const int i = tt + L.TT * j;
-          const bool in = j < L.ept && i < E && ok;
-          lr[j] = in ? lg[i] : 0.f;
-          kr[j] = in ? sel_key(lr[j], i) : 0;
-          if (j < L.ept && i < L.npad) keys[i] = kr[j];
-          if (j < L.ept && i < L.e32) lv[i] = lr[j];
-        }
-        team_select<EPT>(L, E, keys, kr, cand, top, tt);
-        if (ok && tt < m) spec[t * m + tt] = top[tt] ? sel_idx(top[tt]) : -1;
-        if (T > L.nteams) __syncthreads();
-      }
-      __syncthreads();
-      for (int i = tid; i < T * k; i += 256) ridx[i] = spec[(i / k) * m + (i % k)];
-    } else {
-      for (int i = tid; i < T * k; i += 256) ridx[i] = a.idx[(i / k) * stride + (i % k)];
-      for (int i = tid; i < T * stride; i += 256) rw[i] = a.weight[i];
-    }
-    __syncthreads();
-    build_plan(dyn, L, T, k, E, a.has_shared, tid);
-    int n_groups = gbase + ctrl[1];
-    if (wave < 3) wait_vm();  // pointer tables
-    __syncthreads();
-    const int e_spec = g < n_groups ? pexp[g] : -1;
-    if (e_spec >= 0) {
-      wg = reinterpret_cast<const sg_block_q4k*>(tabg[e_spec]);
-      wu = reinterpret_cast<const sg_block_q4k*>(tabu[e_spec]);
-      if (wg && wu && nrw > 0) dma(wg, wu);
-    }
-
-    // 2) exact probabilities and weights (single pass when T <= teams)
-    if (a.logits) {
-      if (tid == 0) ctrl[3] = 0;  // set when the final selection differs from the plan's
-      for (int t0 = 0; t0 < T; t0 += L.nteams) {
-        const int t = t0 + team;
-        const bool ok = t < T;
-        if (T > L.nteams) {  // later passes: reload this token's logits
-          const float* lg = a.logits + static_cast<long long>(t) * E;
-#pragma unroll
-          for (int j = 0; j < EPT; ++j) {
-            const int i = tt + L.TT * j;
-            lr[j] = (j < L.ept && i < E && ok) ? lg[i] : 0.f;
-            if (j < L.ept && i < L.e32) lv[i] = lr[j];
-          }
-        }
-        if (tid == 0) ctrl[2] = 0;
-        float mx = -1e30f;
-#pragma unroll
-        for (int j = 0; j < EPT; ++j)
-          if (j < L.ept && tt + L.TT * j < E && ok) mx = fmaxf(mx, lr[j]);
-        mx = team_max(mx, red, wit, tw, lane);
-#pragma unroll
-        for (int j = 0; j < EPT; ++j) {
-          const int i = tt + L.TT * j;
-          if (j < L.ept && i < L.e32) ev[i] = (ok && i < E) ? expf_sg(lr[j] - mx) : 0.f;
-        }
-        __syncthreads();
-        if (tt == 0) zs[team] = serial_sum(ev, L.e32);
-        __syncthreads();
-        const float z = zs[team];
-        const bool degen = !(z == z) || z == 0.f;
-        // the check, on the team's first wave: lane kk holds candidate kk
-        bool fast = false;
-        float pk = -1.f;
-        int ik = -1;
-        if (wit == 0) {
-          ik = (ok && lane < m) ? spec[t * m + lane] : -1;
-          pk = (ik >= 0 && !degen) ? ev[ik] / z : -1.f;
-          const float lk = ik >= 0 ? lv[ik] : 0.f;
-          const float pn = __shfl(pk, lane + 1, 64);
-          const float ln = __shfl(lk, lane + 1, 64);
-          const int in = __shfl(ik, lane + 1, 64);
-          bool cond = true;
-          if (lane + 1 < k) cond = ik >= 0 && in >= 0 && (pk > pn || lk == ln);
-          else if (lane + 1 == k && E > k) cond = ik >= 0 && in >= 0 && pk > pn;
-          fast = ok && !degen && __ballot(!cond) == 0;
-          if (lane == 0) {
-            ctrl[4 + team] = ok && !degen && !fast;
-            if (ok && !degen && !fast) atomicOr(&ctrl[2], 1);
-          }
-        }
-        __syncthreads();
-        if (ctrl[2] != 0) {  // selection on the probabilities for the colliding rows
-          const bool slow_team = ctrl[4 + team] != 0;
-          uint64_t kr[EPT];
-#pragma unroll
-          for (int j = 0; j < EPT; ++j) {
-            const int i = tt + L.TT * j;
-            kr[j] = (j < L.ept && i < E && slow_team) ? sel_key(ev[i] / z, i) : 0;
-            if (j < L.ept && i < L.npad) keys[i] = kr[j];
-          }
-          team_select<EPT>(L, E, keys, kr, cand, top, tt);
-        }
-        if (wit == 0 && ok) {
-          int fi;
-          float pv;
-          if (degen) {
-            fi = lane % E;
-            pv = -1.f;
-          } else if (fast) {
-            fi = ik;
-            pv = pk;
-          } else {
-            fi = lane < m && top[lane] ? sel_idx(top[lane]) : 0;
-            pv = ev[fi] / z;
-          }
-          float wsum = 0.f;
-          for (int kk = 0; kk < k; ++kk) wsum += readlane_f(pv, kk);
-          const float wv = wsum > 0.f ? pv / wsum : pv;
-          if (lane < k) {
-            if (fi != ridx[t * k + lane]) atomicOr(&ctrl[3], 1);
-            ridx[t * k + lane] = fi;
-            rw[t * stride + lane] = wv;
-          }
-          if (lane == 0) rw[t * stride + k] = a.shared_w;
-        }
-        __syncthreads();
-      }
-      if (ctrl[3]) {  // the final selection differs from the logit order
-        build_plan(dyn, L, T, k, E, a.has_shared, tid);
-        n_groups = gbase + ctrl[1];
-      }
-    }
-
-    if (blockIdx.x == 0 && g == gbase && wave == 3) {  // publish for the back kernel
-      const int* re = reinterpret_cast<const int*>(dyn + L.re);
-      const int nv = ctrl[0];
-      for (int t = lane; t < T; t += 64) {
-        bool bad = false;  // bounds-kill: a row with an invalid id loses all its weights
-        for (int kk = 0; kk < k; ++kk) bad |= re[t * k + kk] < 0;
-        for (int q = 0; q <= k; ++q) a.weight[t * stride + q] = bad ? 0.f : rw[t * stride + q];
-        if (a.logits)
-          for (int kk = 0; kk < k; ++kk) a.idx[t * stride + kk] = ridx[t * k + kk];
-      }
-      for (int i = lane; i <= n_groups; i += 64) a.plan.off[i] = poff[i];
-      for (int i = lane; i < n_groups; i += 64) {
-        const int e = pexp[i];
-        a.plan.expert[i] = e;
-        const unsigned long long gp = e >= 0 ? tabg[e] : reinterpret_cast<unsigned long long>(a.sh_gate);
-        const unsigned long long up = e >= 0 ? tabu[e] : reinterpret_cast<unsigned long long>(a.sh_up);
-        const unsigned long long dp = e >= 0 ? tabd[e] : reinterpret_cast<unsigned long long>(a.sh_down);
-        a.plan.wdown[i] = (gp && up) ? dp : 0ull;
-      }
-      for (int i = lane; i < (a.has_shared ? T : 0) + nv; i += 64) {
-        a.plan.tok[i] = ptok[i];
-        a.plan.slot[i] = pslot[i];
-      }
-      if (lane == 0) {
-        a.plan.meta[0] = n_groups;
-        a.plan.meta[1] = a.has_shared;
-        a.plan.meta[2] = nv;
-      }
-    }
-    if (g >= n_groups) {
-      wait_vm();  // retire a copy issued for a group that no longer exists
-      return;
-    }
-    const int e = pexp[g];
-    if (e != e_spec) {
-      wait_vm();
-      wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
-      wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
-      if (wg && wu && nrw > 0) dma(wg, wu);
-    }
-    beg = poff[g];
-    end = poff[g + 1];
-  }
-
-  // Q8_K of every token's x into LDS, while the weights are in flight
-  for (int b = wave; b < T * nbh; b += 4) {
-    const float* xb = a.x + static_cast<long long>(b) * kQK + 4 * lane;
-    float v[4] = {xb[0], xb[1], xb[2], xb[3]};
-    quantize_block_wave_lds(v, xs + b * kXStride, lane);
-  }
-  __syncthreads();
-
-  const bool present = wg != nullptr && wu != nullptr;
+// gate/up + SiLU of one wave's rows [row0, row0+nrw) of (wg, wu), whose
+// bytes the wave already copied into buf (gate rows, then up rows), for the
+// n entries (tok[j], slot[j]); x in LDS as staged Q8_K (xs).  Lanes 0-31
+// hold gate super-blocks, lanes 32-63 the same up rows.
+template <typename Entry>
+__device__ __forceinline__ void gateup_wave(bool present, int row0, int nrw, int nbh, int lpr,
+                                            const uint32_t* buf, const uint32_t* xs, Entry entry,
+                                            int n, int stride, int n_ff, float* h, int lane) {
   const int half = lane >> 5, hl = lane & 31;
   const int blk = hl & (lpr - 1), rr = hl / lpr;
   const bool live = present && blk < nbh && rr < nrw;
@@ -588,9 +334,9 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
     read_block_lds(buf + 36 * (half * nrw * nbh + rr * nbh + blk), w36);
     sm8 = unpack_scales(w36[1], w36[2], w36[3]);
   }
-  for (int j = beg; j < end; ++j) {
-    const int t = shared_grp ? j : ptok[j];
-    const int sl = shared_grp ? k : pslot[j];
+  for (int j = 0; j < n; ++j) {
+    int t, sl;
+    entry(j, t, sl);
     float s = 0.f;
     if (live) {
       int32_t xr[64], ip[8];
@@ -599,11 +345,384 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
       subblock_dots(w36 + 4, xr, ip);
       s = block_sum(w36[0], sm8, ip, xd, bsf);
     }
-    const float acc = row_sum_in_order(s, lane, lpr, nbh);
+    const float acc = row_sum_last(s, blk, nbh);
     const float up = __shfl_xor(acc, 32, 64);
-    if (half == 0 && blk == 0 && rr < nrw)
-      a.h[(static_cast<long long>(t) * stride + sl) * a.n_ff + row0 + rr] =
+    if (half == 0 && blk == nbh - 1 && rr < nrw)
+      h[(static_cast<long long>(t) * stride + sl) * n_ff + row0 + rr] =
           present ? silu_mul(acc, up) : 0.f;
+  }
+}
+
+// Copy gate rows [row0, row0+nrw) and the same up rows into a wave buffer.
+__device__ __forceinline__ void dma_gateup(const sg_block_q4k* wg, const sg_block_q4k* wu,
+                                           int row0, int nrw, int nbh, uint32_t* buf, int lane) {
+  const char* pg = reinterpret_cast<const char*>(wg + static_cast<long long>(row0) * nbh);
+  const char* pu = reinterpret_cast<const char*>(wu + static_cast<long long>(row0) * nbh);
+  const int ncg = nrw * nbh * 9;
+  dma_chunks([&](int c) { return c < ncg ? pg + 16 * c : pu + 16 * (c - ncg); }, 2 * ncg, buf,
+             lane);
+}
+
+// Q8_K of every token's x into LDS (4 waves, one block per wave per step).
+__device__ __forceinline__ void quantize_x(const float* x, int n_blocks, uint32_t* xs, int wave,
+                                           int lane) {
+  for (int b = wave; b < n_blocks; b += 4) {
+    const float* xb = x + static_cast<long long>(b) * kQK + 4 * lane;
+    float v[4] = {xb[0], xb[1], xb[2], xb[3]};
+    quantize_block_wave_lds(v, xs + b * kXStride, lane);
+  }
+}
+
+// Logit-order top-(k+1) of every token: spec[t*m + r] = r-th expert (or -1).
+// Teams of tw waves; each thread keeps its logits in lr[] (last pass's
+// token).  Workgroup-wide.
+template <int EPT>
+__device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
+                            int tid, int lane) {
+  const int T = a.T, E = a.n_expert, m = L.m;
+  const int wave = tid >> 6, team = wave / L.tw, tt = tid - team * L.TT;
+  uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + L.keys) + team * L.npad;
+  float* lv = reinterpret_cast<float*>(dyn + L.lv) + team * L.e32;
+  uint64_t* cand = reinterpret_cast<uint64_t*>(dyn + L.cand) + team * L.ncp;
+  uint64_t* top = reinterpret_cast<uint64_t*>(dyn + L.top) + team * m;
+  int* spec = reinterpret_cast<int*>(dyn + L.spec);
+  for (int t0 = 0; t0 < T; t0 += L.nteams) {
+    const int t = t0 + team;
+    const bool ok = t < T;
+    const float* lg = a.logits + static_cast<long long>(t) * E;
+    uint64_t kr[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int i = tt + L.TT * j;
+      const bool in = j < L.ept && i < E && ok;
+      lr[j] = in ? lg[i] : 0.f;
+      kr[j] = in ? sel_key(lr[j], i) : 0;
+      if (j < L.ept && i < L.npad) keys[i] = kr[j];
+      if (j < L.ept && i < L.e32) lv[i] = lr[j];
+    }
+    team_select<EPT>(L, E, keys, kr, cand, top, tt);
+    if (ok && tt < m) spec[t * m + tt] = top[tt] ? sel_idx(top[tt]) : -1;
+    if (T > L.nteams) __syncthreads();
+  }
+  __syncthreads();
+}
+
+// Plan for T == 1 straight from distinct, valid ids ridx[0..k): group
+// gbase + r = the expert of rank r, its single entry (token 0, slot j).
+__device__ void plan_t1(uint32_t* dyn, const FrontLds& L, int k, int has_shared, int tid) {
+  const int* ridx = reinterpret_cast<const int*>(dyn + L.ridx);
+  int* re = reinterpret_cast<int*>(dyn + L.re);
+  int* poff = reinterpret_cast<int*>(dyn + L.poff);
+  int* pexp = reinterpret_cast<int*>(dyn + L.pexp);
+  int* ptok = reinterpret_cast<int*>(dyn + L.ptok);
+  int* pslot = reinterpret_cast<int*>(dyn + L.pslot);
+  int* ctrl = reinterpret_cast<int*>(dyn + L.ctrl);
+  const int gbase = has_shared, ebase = has_shared ? 1 : 0;
+  if (tid < k) {
+    const int e = ridx[tid];
+    int r = 0;
+    for (int j = 0; j < k; ++j) r += ridx[j] < e;
+    re[tid] = e;
+    poff[gbase + r] = ebase + r;
+    pexp[gbase + r] = e;
+    ptok[ebase + r] = 0;
+    pslot[ebase + r] = tid;
+  }
+  if (tid == 0) {
+    if (has_shared) {
+      poff[0] = 0;
+      pexp[0] = -1;
+      ptok[0] = 0;
+      pslot[0] = k;
+    }
+    poff[gbase + k] = ebase + k;
+    ctrl[0] = k;
+    ctrl[1] = k;
+  }
+  __syncthreads();
+}
+
+// True when ridx[0..T*k) are k distinct valid ids per token (what routing
+// produces); then the T == 1 plan needs no general build.
+__device__ __forceinline__ bool ids_distinct_valid(const int* ridx, int n, int E) {
+  bool ok = true;
+  for (int i = 0; i < n; ++i) {
+    ok &= ridx[i] >= 0 && ridx[i] < E;
+    for (int j = 0; j < i; ++j) ok &= ridx[j] != ridx[i];
+  }
+  return ok;
+}
+
+// Compute workgroups (blockIdx.y < gmax): one (group, chunk of 16 rows).
+// The shared expert's group streams at once; a routed group takes its
+// expert from the top-k by LOGIT (index tie rule) and writes h for the
+// (token, slot) entries of that expert.  The publisher workgroup
+// (blockIdx.y == gmax) derives the exact selection from the probabilities
+// and repairs any slot where the two differ (see the publisher below).
+template <int EPT>
+__global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
+  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = a.T, k = a.k, E = a.n_expert, stride = k + 1;
+  const int g = blockIdx.y;
+  const int nbh = a.hidden / kQK, lpr = pow2_ceil(nbh);
+  const bool publisher = g == a.gmax;
+  if (publisher && blockIdx.x != 0) return;  // one publisher per launch
+  const bool shared_grp = a.has_shared && g == 0;
+  const FrontLds L = front_lds(T, nbh, E, k, !shared_grp);
+  const int rpw = 32 / lpr;
+  const int row0 = blockIdx.x * 4 * rpw + wave * rpw;
+  const int nrw = max(0, min(rpw, a.n_ff - row0));
+  const int gbase = a.has_shared;
+  uint32_t* buf = wbuf[wave];
+  uint32_t* xs = dyn + L.xs;
+
+  if (shared_grp) {
+    if (nrw > 0) dma_gateup(a.sh_gate, a.sh_up, row0, nrw, nbh, buf, lane);
+    quantize_x(a.x, T * nbh, xs, wave, lane);
+    __syncthreads();
+    // entries: tokens 0..T-1 in slot k, no plan needed
+    gateup_wave(true, row0, nrw, nbh, lpr, buf, xs,
+                [&](int j, int& t, int& sl) { t = j; sl = k; }, T, stride, a.n_ff, a.h, lane);
+    return;
+  }
+
+  const unsigned long long* tabg = reinterpret_cast<const unsigned long long*>(dyn + L.tabg);
+  const unsigned long long* tabu = reinterpret_cast<const unsigned long long*>(dyn + L.tabu);
+  const unsigned long long* tabd = reinterpret_cast<const unsigned long long*>(dyn + L.tabd);
+  int* ridx = reinterpret_cast<int*>(dyn + L.ridx);
+  int* spec = reinterpret_cast<int*>(dyn + L.spec);
+  float* rw = reinterpret_cast<float*>(dyn + L.rw);
+  int* ctrl = reinterpret_cast<int*>(dyn + L.ctrl);
+  const int* pexp = reinterpret_cast<const int*>(dyn + L.pexp);
+  const int* poff = reinterpret_cast<const int*>(dyn + L.poff);
+  const int* ptok = reinterpret_cast<const int*>(dyn + L.ptok);
+  const int* pslot = reinterpret_cast<const int*>(dyn + L.pslot);
+
+  // expert pointer tables into LDS (waves 0-2, one table each)
+  if (wave < 3 && (wave < 2 || publisher)) {
+    const sg_block_q4k* const* tab = wave == 0 ? a.tab_gate : (wave == 1 ? a.tab_up : a.tab_down);
+    uint32_t* dst = dyn + (wave == 0 ? L.tabg : (wave == 1 ? L.tabu : L.tabd));
+    const char* src = reinterpret_cast<const char*>(tab);
+    dma_range([&](int c) { return src + 16 * c; }, E / 2, dst, lane);
+    if ((E & 1) && lane == 0)  // odd table length: the last pointer by a plain load
+      reinterpret_cast<unsigned long long*>(dst)[E - 1] =
+          reinterpret_cast<unsigned long long>(tab[E - 1]);
+  }
+
+  float lr[EPT];
+  if (a.logits) {
+    spec_select<EPT>(a, dyn, L, lr, tid, lane);
+    for (int i = tid; i < T * k; i += 256) ridx[i] = spec[(i / k) * L.m + (i % k)];
+  } else {
+    for (int i = tid; i < T * k; i += 256) ridx[i] = a.idx[(i / k) * stride + (i % k)];
+    for (int i = tid; i < T * stride; i += 256) rw[i] = a.weight[i];
+  }
+  __syncthreads();
+  // routing output is k distinct ids per token; the caller's may not be
+  bool direct = T == 1;
+  if (direct) {
+    if (a.logits)
+      for (int i = 0; i < k; ++i) direct &= ridx[i] >= 0;
+    else
+      direct = ids_distinct_valid(ridx, k, E);
+  }
+  if (direct)
+    plan_t1(dyn, L, k, a.has_shared, tid);
+  else
+    build_plan(dyn, L, T, k, E, a.has_shared, tid);
+  int n_groups = gbase + ctrl[1];
+
+  if (!publisher) {
+    if (wave < 2) wait_vm();  // pointer tables
+    __syncthreads();
+    if (g >= n_groups) return;
+    const int e = pexp[g];
+    const sg_block_q4k* wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
+    const sg_block_q4k* wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
+    const bool present = wg != nullptr && wu != nullptr;
+    if (present && nrw > 0) dma_gateup(wg, wu, row0, nrw, nbh, buf, lane);
+    quantize_x(a.x, T * nbh, xs, wave, lane);  // overlaps the weight stream
+    __syncthreads();
+    const int j0 = poff[g];
+    gateup_wave(present, row0, nrw, nbh, lpr, buf, xs,
+                [&](int j, int& t, int& sl) { t = ptok[j0 + j]; sl = pslot[j0 + j]; },
+                poff[g + 1] - j0, stride, a.n_ff, a.h, lane);
+    return;
+  }
+
+  // ---- publisher ------------------------------------------------------------------
+  // Exact routing: max, exp, the normalizer summed serially in index order,
+  // p = e / z.  p is a monotone function of the logit, so the logit order is
+  // the probability order unless two neighbours collide on one float; the
+  // check is p strictly decreasing across the k+1 leading candidates (or
+  // equal logits).  A collision, or a degenerate row (NaN, empty
+  // normalizer), selects on the probabilities themselves; slots whose
+  // expert differs from the compute workgroups' choice are recomputed into
+  // the fix buffer and flagged for the back kernel.
+  const int tw = L.tw, team = wave / tw, wit = wave - team * tw;
+  const int tt = tid - team * L.TT;
+  const int m = L.m;
+  if (a.logits) {
+    uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + L.keys) + team * L.npad;
+    float* lv = reinterpret_cast<float*>(dyn + L.lv) + team * L.e32;
+    float* ev = reinterpret_cast<float*>(dyn + L.ev) + team * L.e32;
+    uint64_t* cand = reinterpret_cast<uint64_t*>(dyn + L.cand) + team * L.ncp;
+    uint64_t* top = reinterpret_cast<uint64_t*>(dyn + L.top) + team * m;
+    float* red = reinterpret_cast<float*>(dyn + L.red) + team * 4;
+    float* zs = reinterpret_cast<float*>(dyn + L.zs);
+    if (tid == 0) ctrl[3] = 0;
+    for (int t0 = 0; t0 < T; t0 += L.nteams) {
+      const int t = t0 + team;
+      const bool ok = t < T;
+      if (T > L.nteams) {  // later passes: reload this token's logits
+        const float* lg = a.logits + static_cast<long long>(t) * E;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+          const int i = tt + L.TT * j;
+          lr[j] = (j < L.ept && i < E && ok) ? lg[i] : 0.f;
+          if (j < L.ept && i < L.e32) lv[i] = lr[j];
+        }
+      }
+      if (tid == 0) ctrl[2] = 0;
+      float mx = -1e30f;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j)
+        if (j < L.ept && tt + L.TT * j < E && ok) mx = fmaxf(mx, lr[j]);
+      mx = team_max(mx, red, wit, tw, lane);
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const int i = tt + L.TT * j;
+        if (j < L.ept && i < L.e32) ev[i] = (ok && i < E) ? expf_sg(lr[j] - mx) : 0.f;
+      }
+      __syncthreads();
+      if (tt == 0) zs[team] = serial_sum(ev, L.e32);
+      __syncthreads();
+      const float z = zs[team];
+      const bool degen = !(z == z) || z == 0.f;
+      bool fast = false;
+      float pk = -1.f;
+      int ik = -1;
+      if (wit == 0) {
+        ik = (ok && lane < m) ? spec[t * m + lane] : -1;
+        pk = (ik >= 0 && !degen) ? ev[ik] / z : -1.f;
+        const float lk = ik >= 0 ? lv[ik] : 0.f;
+        const float pn = __shfl(pk, lane + 1, 64);
+        const float ln = __shfl(lk, lane + 1, 64);
+        const int in = __shfl(ik, lane + 1, 64);
+        bool cond = true;
+        if (lane + 1 < k) cond = ik >= 0 && in >= 0 && (pk > pn || lk == ln);
+        else if (lane + 1 == k && E > k) cond = ik >= 0 && in >= 0 && pk > pn;
+        fast = ok && !degen && __ballot(!cond) == 0;
+        if (lane == 0) {
+          ctrl[4 + team] = ok && !degen && !fast;
+          if (ok && !degen && !fast) atomicOr(&ctrl[2], 1);
+        }
+      }
+      __syncthreads();
+      if (ctrl[2] != 0) {  // selection on the probabilities for the colliding rows
+        const bool slow_team = ctrl[4 + team] != 0;
+        uint64_t kr[EPT];
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+          const int i = tt + L.TT * j;
+          kr[j] = (j < L.ept && i < E && slow_team) ? sel_key(ev[i] / z, i) : 0;
+          if (j < L.ept && i < L.npad) keys[i] = kr[j];
+        }
+        team_select<EPT>(L, E, keys, kr, cand, top, tt);
+      }
+      if (wit == 0 && ok) {
+        int fi;
+        float pv;
+        if (degen) {
+          fi = lane % E;
+          pv = -1.f;
+        } else if (fast) {
+          fi = ik;
+          pv = pk;
+        } else {
+          fi = lane < m && top[lane] ? sel_idx(top[lane]) : 0;
+          pv = ev[fi] / z;
+        }
+        float wsum = 0.f;
+        for (int kk = 0; kk < k; ++kk) wsum += readlane_f(pv, kk);
+        const float wv = wsum > 0.f ? pv / wsum : pv;
+        if (lane < k) {
+          ctrl[8 + t * k + lane] = fi != ridx[t * k + lane];  // slot needs repair
+          if (fi != ridx[t * k + lane]) atomicOr(&ctrl[3], 1);
+          ridx[t * k + lane] = fi;
+          rw[t * stride + lane] = wv;
+        }
+        if (lane == 0) rw[t * stride + k] = a.shared_w;
+      }
+      __syncthreads();
+    }
+    if (ctrl[3]) {
+      if (T == 1)  // exact selections are k distinct valid ids
+        plan_t1(dyn, L, k, a.has_shared, tid);
+      else
+        build_plan(dyn, L, T, k, E, a.has_shared, tid);
+      n_groups = gbase + ctrl[1];
+    }
+  }
+  wait_vm();  // pointer tables
+  __syncthreads();
+
+  // publish idx, weight, plan, down pointers and the repair flags
+  const int* re = reinterpret_cast<const int*>(dyn + L.re);
+  const int nv = ctrl[0];
+  for (int t = tid; t < T; t += 256) {
+    bool bad = false;  // bounds-kill: a row with an invalid id loses all its weights
+    for (int kk = 0; kk < k; ++kk) bad |= re[t * k + kk] < 0;
+    for (int q = 0; q <= k; ++q) a.weight[t * stride + q] = bad ? 0.f : rw[t * stride + q];
+    if (a.logits)
+      for (int kk = 0; kk < k; ++kk) a.idx[t * stride + kk] = ridx[t * k + kk];
+  }
+  for (int i = tid; i < T * stride; i += 256) {
+    const int t = i / stride, s = i - t * stride;
+    a.plan.fix[i] = (a.logits && s < k && ctrl[3]) ? ctrl[8 + t * k + s] : 0;
+  }
+  for (int i = tid; i <= n_groups; i += 256) a.plan.off[i] = poff[i];
+  for (int i = tid; i < n_groups; i += 256) {
+    const int e = pexp[i];
+    a.plan.expert[i] = e;
+    const unsigned long long gp = e >= 0 ? tabg[e] : reinterpret_cast<unsigned long long>(a.sh_gate);
+    const unsigned long long up = e >= 0 ? tabu[e] : reinterpret_cast<unsigned long long>(a.sh_up);
+    const unsigned long long dp = e >= 0 ? tabd[e] : reinterpret_cast<unsigned long long>(a.sh_down);
+    a.plan.wdown[i] = (gp && up) ? dp : 0ull;
+  }
+  for (int i = tid; i < (a.has_shared ? T : 0) + nv; i += 256) {
+    a.plan.tok[i] = ptok[i];
+    a.plan.slot[i] = pslot[i];
+  }
+  if (tid == 0) {
+    a.plan.meta[0] = n_groups;
+    a.plan.meta[1] = a.has_shared;
+    a.plan.meta[2] = nv;
+  }
+  if (!(a.logits && ctrl[3])) return;
+
+  // repair: recompute h of every flagged slot with its final expert into
+  // the fix buffer (rare: a probability collision or a degenerate row)
+  quantize_x(a.x, T * nbh, xs, wave, lane);
+  __syncthreads();
+  for (int i = 0; i < T * k; ++i) {
+    if (!ctrl[8 + i]) continue;
+    const int t = i / k, s = i - t * k;
+    const int e = ridx[i];
+    const sg_block_q4k* wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
+    const sg_block_q4k* wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
+    const bool present = wg != nullptr && wu != nullptr;
+    for (int r0 = wave * rpw; r0 < a.n_ff; r0 += 4 * rpw) {
+      const int n = min(rpw, a.n_ff - r0);
+      wait_lds();
+      if (present) dma_gateup(wg, wu, r0, n, nbh, buf, lane);
+      gateup_wave(present, r0, n, nbh, lpr, buf, xs,
+                  [&](int, int& tt_, int& sl_) { tt_ = t; sl_ = s; }, 1, stride, a.n_ff,
+                  a.plan.hfix, lane);
+    }
   }
 }
 
@@ -614,7 +733,7 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
 // wave, and writes the slot outputs of the chunk into LDS.  Then the
 // workgroup combines: out = residual + sum_kk fma(w_kk, y_kk), slot order.
 struct BackLds {
-  int wbuf, hbuf, hq, ys, off, wdown, tok, slot, wt, ix, meta, total;
+  int wbuf, hbuf, hq, ys, off, wdown, tok, slot, wt, ix, fix, meta, total;
 };
 
 __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, int nbuf, int gmax,
@@ -638,6 +757,7 @@ __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, in
   L.slot = take(emax);
   L.wt = take(T * (k + 1));
   L.ix = take(T * (k + 1));
+  L.fix = take(T * (k + 1));
   L.meta = take(4);
   L.total = o;
   return L;
@@ -657,6 +777,7 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
   int* slot = reinterpret_cast<int*>(dyn + L.slot);
   float* wt = reinterpret_cast<float*>(dyn + L.wt);
   int* ix = reinterpret_cast<int*>(dyn + L.ix);
+  int* fix = reinterpret_cast<int*>(dyn + L.fix);
   int* meta = reinterpret_cast<int*>(dyn + L.meta);
   float* ys = reinterpret_cast<float*>(dyn + L.ys);
 
@@ -670,6 +791,7 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
   for (int i = tid; i < T * stride; i += 256) {
     wt[i] = a.weight[i];
     ix[i] = a.idx[i];
+    fix[i] = a.plan.fix[i];
   }
   if (tid < 2) meta[tid] = a.plan.meta[tid];
   for (int i = tid; i < T * stride * rows; i += 256) ys[i] = 0.f;
@@ -695,8 +817,9 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
         dma_chunks([&](int c) { return src + 16 * c; }, nr * nbf * 9, wb + b * rwords, lane);
       }
       const int j0 = off[gq];
-      const char* hsrc = reinterpret_cast<const char*>(
-          a.h + (static_cast<long long>(tok[j0]) * stride + slot[j0]) * a.n_ff);
+      const int hs0 = tok[j0] * stride + slot[j0];
+      const char* hsrc = reinterpret_cast<const char*>((fix[hs0] ? a.plan.hfix : a.h) +
+                                                       static_cast<long long>(hs0) * a.n_ff);
       dma_range([&](int c) { return hsrc + 16 * c; }, a.n_ff / 4,
                 reinterpret_cast<uint32_t*>(hb + b * a.n_ff), lane);
     }
@@ -716,8 +839,9 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
       for (int j = off[gq]; j < off[gq + 1]; ++j) {
         const float* hsrc = hb + b * a.n_ff;
         if (j != off[gq]) {  // a further token of this expert: fetch its h row
-          const char* hg = reinterpret_cast<const char*>(
-              a.h + (static_cast<long long>(tok[j]) * stride + slot[j]) * a.n_ff);
+          const int hs = tok[j] * stride + slot[j];
+          const char* hg = reinterpret_cast<const char*>((fix[hs] ? a.plan.hfix : a.h) +
+                                                         static_cast<long long>(hs) * a.n_ff);
           uint32_t* hd = reinterpret_cast<uint32_t*>(hb + b * a.n_ff);
           wait_lds();
           dma_range([&](int c) { return hg + 16 * c; }, a.n_ff / 4, hd, lane);
@@ -739,8 +863,8 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
           subblock_dots(w36 + 4, xr, ip);
           s = block_sum(w36[0], sm8, ip, xd, bsf);
         }
-        const float acc = row_sum_in_order(s, lane, lrow, nbf);
-        if (blk == 0 && rr < nr)
+        const float acc = row_sum_last(s, blk, nbf);
+        if (blk == nbf - 1 && rr < nr)
           ys[(tok[j] * stride + slot[j]) * rows + rr] = present ? acc : 0.f;
         __builtin_amdgcn_wave_barrier();
       }
@@ -848,7 +972,9 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   a.plan = LayerPlan{reinterpret_cast<int*>(base + ws.meta), reinterpret_cast<int*>(base + ws.off),
                      reinterpret_cast<int*>(base + ws.expert),
                      reinterpret_cast<int*>(base + ws.tok), reinterpret_cast<int*>(base + ws.slot),
-                     reinterpret_cast<unsigned long long*>(base + ws.wdown)};
+                     reinterpret_cast<unsigned long long*>(base + ws.wdown),
+                     reinterpret_cast<int*>(base + ws.fix),
+                     reinterpret_cast<float*>(base + ws.hfix)};
   a.h = reinterpret_cast<float*>(base + ws.h);
   a.T = n_tokens;
   a.hidden = hidden;
@@ -866,7 +992,8 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   if (stages & 1) {
     const int rows_wg = 4 * (32 / pow2_ceil(hidden / kQK));
     const FrontLds fl = front_lds(n_tokens, hidden / kQK, n_expert, k, true);
-    const dim3 grid((n_ff + rows_wg - 1) / rows_wg, ws.gmax);
+    // y < gmax: compute workgroups of group y; y == gmax: the publisher
+    const dim3 grid((n_ff + rows_wg - 1) / rows_wg, ws.gmax + 1);
     if (fl.ept <= 1)
       hipLaunchKernelGGL(layer_front_kernel<1>, grid, dim3(256), lds_f, s, a);
     else if (fl.ept <= 2)
