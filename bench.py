@@ -199,7 +199,7 @@ def main():
     # kernel (routing + gate/up + SiLU) and the back kernel (down + combine)
     log("[bench] per-kernel timing")
     S = 128
-    wss = [torch.empty_like(layers[0].workspace) for _ in range(S)]
+    wss = [torch.zeros_like(layers[0].workspace) for _ in range(S)]
     for j in range(S):
         step(j % n_in, stages=3, ws=wss[j])
     torch.cuda.synchronize()

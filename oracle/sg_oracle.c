@@ -231,20 +231,18 @@ float orc_expf(float xf) {
   const double kd = nearbyint(x * 1.4426950408889634);
   const double r = fma(-kd, 2.3190468138462996e-17, fma(-kd, 6.9314718055994529e-01, x));
   /* Taylor series of e^r to degree 13 (remainder < 5e-18 on |r| <= 0.35). */
-  double p = 1.0 / 6227020800.0;
-  p = fma(p, r, 1.0 / 479001600.0);
-  p = fma(p, r, 1.0 / 39916800.0);
-  p = fma(p, r, 1.0 / 3628800.0);
-  p = fma(p, r, 1.0 / 362880.0);
-  p = fma(p, r, 1.0 / 40320.0);
-  p = fma(p, r, 1.0 / 5040.0);
-  p = fma(p, r, 1.0 / 720.0);
-  p = fma(p, r, 1.0 / 120.0);
-  p = fma(p, r, 1.0 / 24.0);
-  p = fma(p, r, 1.0 / 6.0);
-  p = fma(p, r, 0.5);
-  p = fma(p, r, 1.0);
-  p = fma(p, r, 1.0);
+  /* Estrin evaluation (short dependency chain): pairs, then r^2, r^4, r^8. */
+  const double r2 = r * r, r4 = r2 * r2, r8 = r4 * r4;
+  const double q0 = fma(1.0, r, 1.0);
+  const double q1 = fma(1.0 / 6.0, r, 0.5);
+  const double q2 = fma(1.0 / 120.0, r, 1.0 / 24.0);
+  const double q3 = fma(1.0 / 5040.0, r, 1.0 / 720.0);
+  const double q4 = fma(1.0 / 362880.0, r, 1.0 / 40320.0);
+  const double q5 = fma(1.0 / 39916800.0, r, 1.0 / 3628800.0);
+  const double q6 = fma(1.0 / 6227020800.0, r, 1.0 / 479001600.0);
+  const double s0 = fma(q1, r2, q0), s1 = fma(q3, r2, q2), s2 = fma(q5, r2, q4);
+  const double u0 = fma(s1, r4, s0), u1 = fma(q6, r4, s2);
+  const double p = fma(u1, r8, u0);
   const int64_t k = (int64_t)kd;
   uint64_t sb = (uint64_t)(k + 1023) << 52;
   double scale;

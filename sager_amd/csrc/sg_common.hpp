@@ -161,20 +161,18 @@ __host__ __device__ __forceinline__ float expf_sg(float xf) {
   const double kd = __builtin_rint(x * 1.4426950408889634);
   double r = __builtin_fma(-kd, 6.9314718055994529e-01, x);
   r = __builtin_fma(-kd, 2.3190468138462996e-17, r);
-  double p = 1.0 / 6227020800.0;
-  p = __builtin_fma(p, r, 1.0 / 479001600.0);
-  p = __builtin_fma(p, r, 1.0 / 39916800.0);
-  p = __builtin_fma(p, r, 1.0 / 3628800.0);
-  p = __builtin_fma(p, r, 1.0 / 362880.0);
-  p = __builtin_fma(p, r, 1.0 / 40320.0);
-  p = __builtin_fma(p, r, 1.0 / 5040.0);
-  p = __builtin_fma(p, r, 1.0 / 720.0);
-  p = __builtin_fma(p, r, 1.0 / 120.0);
-  p = __builtin_fma(p, r, 1.0 / 24.0);
-  p = __builtin_fma(p, r, 1.0 / 6.0);
-  p = __builtin_fma(p, r, 0.5);
-  p = __builtin_fma(p, r, 1.0);
-  p = __builtin_fma(p, r, 1.0);
+  /* Estrin evaluation (short dependency chain): pairs, then r^2, r^4, r^8. */
+  const double r2 = r * r, r4 = r2 * r2, r8 = r4 * r4;
+  const double q0 = __builtin_fma(1.0, r, 1.0);
+  const double q1 = __builtin_fma(1.0 / 6.0, r, 0.5);
+  const double q2 = __builtin_fma(1.0 / 120.0, r, 1.0 / 24.0);
+  const double q3 = __builtin_fma(1.0 / 5040.0, r, 1.0 / 720.0);
+  const double q4 = __builtin_fma(1.0 / 362880.0, r, 1.0 / 40320.0);
+  const double q5 = __builtin_fma(1.0 / 39916800.0, r, 1.0 / 3628800.0);
+  const double q6 = __builtin_fma(1.0 / 6227020800.0, r, 1.0 / 479001600.0);
+  const double s0 = __builtin_fma(q1, r2, q0), s1 = __builtin_fma(q3, r2, q2), s2 = __builtin_fma(q5, r2, q4);
+  const double u0 = __builtin_fma(s1, r4, s0), u1 = __builtin_fma(q6, r4, s2);
+  const double p = __builtin_fma(u1, r8, u0);
   const long long k = static_cast<long long>(kd);
   const double scale = __builtin_bit_cast(double, static_cast<unsigned long long>(k + 1023) << 52);
   return static_cast<float>(p * scale);
@@ -363,6 +361,49 @@ __device__ __forceinline__ void quantize_block_wave_lds(const float v[4], uint32
   dst[lane] = packed;
   if (lane == 0) dst[64] = __builtin_bit_cast(uint32_t, d);
   if ((lane & 7) == 0) dst[65 + (lane >> 3)] = __builtin_bit_cast(uint32_t, static_cast<float>(s));
+}
+
+// N blocks at once with the calling wave (same arithmetic as
+// quantize_block_wave_lds, chains interleaved for latency); blocks b >=
+// n_act are computed but not stored.  v[b][0..3] = the lane's 4 values of
+// block b.
+template <int N>
+__device__ __forceinline__ void quantize_n_lds(const float (&v)[N][4], uint32_t* const (&dst)[N],
+                                               int n_act, int lane) {
+  float amax[N], d[N], id[N];
+#pragma unroll
+  for (int b = 0; b < N; ++b)
+    amax[b] = fmaxf(fmaxf(fabsf(v[b][0]), fabsf(v[b][1])), fmaxf(fabsf(v[b][2]), fabsf(v[b][3])));
+#pragma unroll
+  for (int b = 0; b < N; ++b) amax[b] = fmaxf(wave_max_dpp(amax[b]), 1e-30f);
+#pragma unroll
+  for (int b = 0; b < N; ++b) d[b] = amax[b] / 127.f;
+#pragma unroll
+  for (int b = 0; b < N; ++b) id[b] = d[b] > 0 ? 1.f / d[b] : 0.f;
+  uint32_t packed[N];
+  int qsum[N];
+#pragma unroll
+  for (int b = 0; b < N; ++b) {
+    packed[b] = 0;
+    qsum[b] = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = q8_code(v[b][i] * id[b]);
+      qsum[b] += q;
+      packed[b] |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * i);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < N; ++b) qsum[b] = sum8_dpp(qsum[b]);
+#pragma unroll
+  for (int b = 0; b < N; ++b) {
+    if (b < n_act) {
+      dst[b][lane] = packed[b];
+      if (lane == 0) dst[b][64] = __builtin_bit_cast(uint32_t, d[b]);
+      if ((lane & 7) == 0)
+        dst[b][65 + (lane >> 3)] = __builtin_bit_cast(uint32_t, static_cast<float>(qsum[b]));
+    }
+  }
 }
 
 // Stage the Q8_K rows of n tokens (token ids in `tok`, nb blocks per row)

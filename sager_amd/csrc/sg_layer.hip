@@ -29,7 +29,6 @@ constexpr int kLMaxExperts = 1024;
 constexpr int kLMaxK = 32;
 constexpr int kLMaxTokens = 16;
 constexpr int kMaxEpt = 16;        // experts per routing thread (1-wave teams, E = 1024)
-constexpr int kBackBufs = 3;       // down-row buffers per wave in the back kernel
 
 __host__ __device__ inline int pow2_ceil(int n) {
   int l = 1;
@@ -46,7 +45,7 @@ struct LayerPlan {
   int* tok;     // [emax] entry token
   int* slot;    // [emax] entry slot
   unsigned long long* wdown;  // [gmax] down matrix of the group, 0 = absent expert
-  int* fix;     // [T*(k+1)] 1 = take this slot's h from hfix
+  int* fix;     // [T*(k+1)] 1 = take this slot's h from the repair buffers
   float* hfix;  // [T*(k+1)][n_ff] repaired h rows
 };
 
@@ -93,7 +92,6 @@ struct LayerArgs {
   int T, hidden, n_ff, n_expert, k, has_shared, gmax, emax;
   float shared_w;
   int back_rows, back_lrow;  // rows per back workgroup, lanes per row there
-  int back_bufs;             // groups a back wave has in flight (<= kBackBufs)
 };
 
 // ---- front kernel LDS layout (dwords) -----------------------------------------------
@@ -363,13 +361,25 @@ __device__ __forceinline__ void dma_gateup(const sg_block_q4k* wg, const sg_bloc
              lane);
 }
 
-// Q8_K of every token's x into LDS (4 waves, one block per wave per step).
+// Q8_K of every token's x into LDS: wave w takes blocks w, w+4, ... four
+// at a time (interleaved chains).
 __device__ __forceinline__ void quantize_x(const float* x, int n_blocks, uint32_t* xs, int wave,
                                            int lane) {
-  for (int b = wave; b < n_blocks; b += 4) {
-    const float* xb = x + static_cast<long long>(b) * kQK + 4 * lane;
-    float v[4] = {xb[0], xb[1], xb[2], xb[3]};
-    quantize_block_wave_lds(v, xs + b * kXStride, lane);
+  for (int b0 = wave; b0 < n_blocks; b0 += 16) {
+    float v[4][4];
+    uint32_t* dst[4];
+    int n = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int b = b0 + 4 * u;
+      const int bb = b < n_blocks ? b : b0;
+      const float* xb = x + static_cast<long long>(bb) * kQK + 4 * lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[u][i] = xb[i];
+      dst[u] = xs + bb * kXStride;
+      n += b < n_blocks;
+    }
+    quantize_n_lds<4>(v, dst, n, lane);
   }
 }
 
@@ -513,6 +523,33 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
   }
 
   float lr[EPT];
+  if (!publisher && a.logits && T == 1) {
+    // one token: this workgroup's expert is the (g - gbase)-th smallest id of
+    // the logit-order top-k, its single entry (token 0, the slot it holds) -
+    // found by every wave on its own, no plan and no extra barrier
+    spec_select<EPT>(a, dyn, L, lr, tid, lane);
+    const int ej = lane < k ? spec[lane] : -1;
+    int r = 0;
+    for (int i = 0; i < k; ++i) {
+      const int ei = spec[i];
+      r += ei >= 0 && ei < ej;
+    }
+    const unsigned long long hit = __ballot(ej >= 0 && r == g - gbase);
+    if (wave < 2) wait_vm();  // pointer tables
+    __syncthreads();
+    if (hit == 0ull) return;
+    const int sl = __builtin_ctzll(hit);
+    const int e = __builtin_amdgcn_readlane(ej, sl);
+    const sg_block_q4k* wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
+    const sg_block_q4k* wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
+    const bool present = wg != nullptr && wu != nullptr;
+    if (present && nrw > 0) dma_gateup(wg, wu, row0, nrw, nbh, buf, lane);
+    quantize_x(a.x, nbh, xs, wave, lane);  // overlaps the weight stream
+    __syncthreads();
+    gateup_wave(present, row0, nrw, nbh, lpr, buf, xs,
+                [&](int, int& t, int& s_) { t = 0; s_ = sl; }, 1, stride, a.n_ff, a.h, lane);
+    return;
+  }
   if (a.logits) {
     spec_select<EPT>(a, dyn, L, lr, tid, lane);
     for (int i = tid; i < T * k; i += 256) ridx[i] = spec[(i / k) * L.m + (i % k)];
@@ -727,16 +764,17 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
 }
 
 // ---- back kernel ------------------------------------------------------------------------
-// One workgroup per chunk of `rows` output rows.  Wave w takes groups w,
-// w+4, w+8, ... (kBackBufs at a time): it streams the group's down rows for
-// the chunk and the group's h rows into LDS, quantizes h to Q8_K with the
-// wave, and writes the slot outputs of the chunk into LDS.  Then the
-// workgroup combines: out = residual + sum_kk fma(w_kk, y_kk), slot order.
+// One workgroup per chunk of `rows` output rows (hidden/rows >= 256 where the
+// shape allows).  A wave packs `gpw` groups side by side - lane = (group,
+// row, super-block) - and streams their down rows for the chunk into its LDS
+// buffer while all four waves quantize every entry's h row to Q8_K in LDS.
+// The slot outputs of the chunk go to LDS; then the workgroup combines
+// out = residual + sum_kk fma(w_kk, y_kk) in slot order.
 struct BackLds {
-  int wbuf, hbuf, hq, ys, off, wdown, tok, slot, wt, ix, fix, meta, total;
+  int hq, ys, off, wdown, tok, slot, wt, ok, fix, meta, total;
 };
 
-__host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, int nbuf, int gmax,
+__host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, int gmax,
                                             int emax) {
   BackLds L{};
   const int nbf = n_ff / kQK;
@@ -747,16 +785,14 @@ __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, in
     o += words;
     return at;
   };
-  L.wbuf = take(4 * nbuf * rows * nbf * 36);
-  L.hbuf = take(4 * nbuf * n_ff);
-  L.hq = take(4 * nbf * kXStride);
+  L.hq = take(emax * nbf * kXStride);
   L.ys = take(T * (k + 1) * rows);
   L.off = take(gmax + 1);
   L.wdown = take(gmax * 2);
   L.tok = take(emax);
   L.slot = take(emax);
   L.wt = take(T * (k + 1));
-  L.ix = take(T * (k + 1));
+  L.ok = take(T * (k + 1));
   L.fix = take(T * (k + 1));
   L.meta = take(4);
   L.total = o;
@@ -764,24 +800,27 @@ __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, in
 }
 
 __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, stride = k + 1;
   const int nbf = a.n_ff / kQK;
   const int rows = a.back_rows, lrow = a.back_lrow;
-  const int nbuf = a.back_bufs;
-  const BackLds L = back_lds(T, k, a.n_ff, rows, nbuf, a.gmax, a.emax);
+  const int gpw = 64 / (rows * lrow);  // groups per wave per pass
+  const BackLds L = back_lds(T, k, a.n_ff, rows, a.gmax, a.emax);
+  uint32_t* hq = dyn + L.hq;
+  float* ys = reinterpret_cast<float*>(dyn + L.ys);
   int* off = reinterpret_cast<int*>(dyn + L.off);
   unsigned long long* wdown = reinterpret_cast<unsigned long long*>(dyn + L.wdown);
   int* tok = reinterpret_cast<int*>(dyn + L.tok);
   int* slot = reinterpret_cast<int*>(dyn + L.slot);
   float* wt = reinterpret_cast<float*>(dyn + L.wt);
-  int* ix = reinterpret_cast<int*>(dyn + L.ix);
+  int* okf = reinterpret_cast<int*>(dyn + L.ok);
   int* fix = reinterpret_cast<int*>(dyn + L.fix);
   int* meta = reinterpret_cast<int*>(dyn + L.meta);
-  float* ys = reinterpret_cast<float*>(dyn + L.ys);
 
-  // the plan, routing and weights (one round of loads)
+  // the plan, routing weights and repair flags (one round of loads)
+  if (tid < 2) meta[tid] = a.plan.meta[tid];
   for (int i = tid; i <= a.gmax; i += 256) off[i] = a.plan.off[i];
   for (int i = tid; i < a.gmax; i += 256) wdown[i] = a.plan.wdown[i];
   for (int i = tid; i < a.emax; i += 256) {
@@ -790,114 +829,115 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
   }
   for (int i = tid; i < T * stride; i += 256) {
     wt[i] = a.weight[i];
-    ix[i] = a.idx[i];
     fix[i] = a.plan.fix[i];
+    const int kk = i % stride;
+    const int ee = a.idx[i];
+    okf[i] = kk < k ? (ee >= 0 && ee < a.n_expert) : -1;  // -1: shared slot
   }
-  if (tid < 2) meta[tid] = a.plan.meta[tid];
   for (int i = tid; i < T * stride * rows; i += 256) ys[i] = 0.f;
   __syncthreads();
-  const int G = meta[0];
+  const int G = __builtin_amdgcn_readfirstlane(meta[0]);
+  const int n_ent = __builtin_amdgcn_readfirstlane(off[G]);
   const int row0 = blockIdx.x * rows;
   const int nr = max(0, min(rows, a.hidden - row0));
-  const int rwords = rows * nbf * 36;
-  uint32_t* wb = dyn + L.wbuf + wave * nbuf * rwords;
-  float* hb = reinterpret_cast<float*>(dyn + L.hbuf) + wave * nbuf * a.n_ff;
-  uint32_t* hq = dyn + L.hq + wave * nbf * kXStride;
-  const int blk = lane & (lrow - 1), rr = lane / lrow;
+  const int gwords = rows * nbf * 36;  // one group's rows in the buffer
+  uint32_t* buf = wbuf[wave];
+  const int q = lane / (rows * lrow);  // this lane's group within the wave
+  const int rr = (lane / lrow) % rows, blk = lane & (lrow - 1);
 
-  for (int gb = 0; gb < G; gb += 4 * nbuf) {
-    // issue: down rows and the first entry's h of each of this wave's groups
-#pragma unroll
-    for (int b = 0; b < kBackBufs; ++b) {
-      const int gq = gb + wave + 4 * b;
-      if (b >= nbuf || gq >= G) break;
+  for (int gb = 0; gb < G; gb += 4 * gpw) {
+    // down rows of this wave's groups
+    for (int qq = 0; qq < gpw; ++qq) {
+      const int gq = gb + wave * gpw + qq;
+      if (gq >= G) break;
       const char* wd = reinterpret_cast<const char*>(wdown[gq]);
       if (wd && nr > 0) {
         const char* src = wd + static_cast<long long>(row0) * nbf * kQ4Bytes;
-        dma_chunks([&](int c) { return src + 16 * c; }, nr * nbf * 9, wb + b * rwords, lane);
+        dma_chunks([&](int c) { return src + 16 * c; }, nr * nbf * 9, buf + qq * gwords, lane);
       }
-      const int j0 = off[gq];
-      const int hs0 = tok[j0] * stride + slot[j0];
-      const char* hsrc = reinterpret_cast<const char*>((fix[hs0] ? a.plan.hfix : a.h) +
-                                                       static_cast<long long>(hs0) * a.n_ff);
-      dma_range([&](int c) { return hsrc + 16 * c; }, a.n_ff / 4,
-                reinterpret_cast<uint32_t*>(hb + b * a.n_ff), lane);
+    }
+    if (gb == 0) {  // Q8_K of every entry's h row, by all waves, while the rows stream in
+      const int nq = n_ent * nbf;
+      for (int e0 = wave; e0 < nq; e0 += 16) {
+        float v[4][4];
+        uint32_t* dst[4];
+        int n = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + 4 * u < nq ? e0 + 4 * u : e0;
+          const int j = e / nbf, b = e - j * nbf;
+          const int hs = tok[j] * stride + slot[j];
+          const float* hp = (fix[hs] ? a.plan.hfix : a.h) + static_cast<long long>(hs) * a.n_ff +
+                            b * kQK + 4 * lane;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[u][i] = hp[i];
+          dst[u] = hq + e * kXStride;
+          n += e0 + 4 * u < nq;
+        }
+        quantize_n_lds<4>(v, dst, n, lane);
+      }
+      __syncthreads();
     }
     wait_vm();
-#pragma unroll
-    for (int b = 0; b < kBackBufs; ++b) {
-      const int gq = gb + wave + 4 * b;
-      if (b >= nbuf || gq >= G) break;
-      const bool present = wdown[gq] != 0ull;
-      const bool live = present && blk < nbf && rr < nr;
-      uint32_t w36[36];
-      ScaleMins sm8{};
-      if (live) {
-        read_block_lds(wb + b * rwords + 36 * (rr * nbf + blk), w36);
-        sm8 = unpack_scales(w36[1], w36[2], w36[3]);
+    const int gq = gb + wave * gpw + q;
+    const bool has = gq < G;
+    const bool present = has && wdown[gq] != 0ull;
+    const bool live = present && blk < nbf && rr < nr;
+    uint32_t w36[36];
+    ScaleMins sm8{};
+    if (live) {
+      read_block_lds(buf + q * gwords + 36 * (rr * nbf + blk), w36);
+      sm8 = unpack_scales(w36[1], w36[2], w36[3]);
+    }
+    const int jb = has ? off[gq] : 0, je = has ? off[gq + 1] : 0;
+    int cnt = je - jb;
+    for (int o = 32; o > 0; o >>= 1) cnt = max(cnt, __shfl_xor(cnt, o, 64));
+    for (int ji = 0; ji < cnt; ++ji) {
+      const int j = jb + ji;
+      const bool ok = j < je;
+      float s = 0.f;
+      if (live && ok) {
+        int32_t xr[64], ip[8];
+        float xd, bsf[8];
+        load_x_regs(hq + (j * nbf + blk) * kXStride, xr, xd, bsf);
+        subblock_dots(w36 + 4, xr, ip);
+        s = block_sum(w36[0], sm8, ip, xd, bsf);
       }
-      for (int j = off[gq]; j < off[gq + 1]; ++j) {
-        const float* hsrc = hb + b * a.n_ff;
-        if (j != off[gq]) {  // a further token of this expert: fetch its h row
-          const int hs = tok[j] * stride + slot[j];
-          const char* hg = reinterpret_cast<const char*>((fix[hs] ? a.plan.hfix : a.h) +
-                                                         static_cast<long long>(hs) * a.n_ff);
-          uint32_t* hd = reinterpret_cast<uint32_t*>(hb + b * a.n_ff);
-          wait_lds();
-          dma_range([&](int c) { return hg + 16 * c; }, a.n_ff / 4, hd, lane);
-          wait_vm();
-        }
-        for (int bb = 0; bb < nbf; ++bb) {
-          const float* hp = hsrc + bb * kQK + 4 * lane;
-          float v[4] = {hp[0], hp[1], hp[2], hp[3]};
-          quantize_block_wave_lds(v, hq + bb * kXStride, lane);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        float s = 0.f;
-        if (live) {
-          int32_t xr[64], ip[8];
-          float xd, bsf[8];
-          load_x_regs(hq + blk * kXStride, xr, xd, bsf);
-          subblock_dots(w36 + 4, xr, ip);
-          s = block_sum(w36[0], sm8, ip, xd, bsf);
-        }
-        const float acc = row_sum_last(s, blk, nbf);
-        if (blk == nbf - 1 && rr < nr)
-          ys[(tok[j] * stride + slot[j]) * rows + rr] = present ? acc : 0.f;
-        __builtin_amdgcn_wave_barrier();
-      }
+      const float acc = row_sum_last(s, blk, nbf);
+      if (ok && blk == nbf - 1 && rr < nr)
+        ys[(tok[j] * stride + slot[j]) * rows + rr] = present ? acc : 0.f;
     }
     wait_lds();
   }
   __syncthreads();
   const int has_shared = meta[1];
-  for (int q = tid; q < T * nr; q += 256) {
-    const int t = q / nr, r = q - t * nr;
+  for (int qo = tid; qo < T * nr; qo += 256) {
+    const int t = qo / nr, r = qo - t * nr;
     const long long o = static_cast<long long>(t) * a.hidden + row0 + r;
     float acc = a.residual ? a.residual[o] : 0.f;
-    for (int kk = 0; kk <= k; ++kk) {
-      bool ok;
-      if (kk < k) {
-        const int ee = ix[t * stride + kk];
-        ok = ee >= 0 && ee < a.n_expert;
-      } else {
-        ok = has_shared != 0;
+    for (int k0 = 0; k0 <= k; k0 += 8) {  // gather 8 slots, then the ordered fma chain
+      float yv[8], wv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int kk = k0 + u;
+        const int i = t * stride + (kk <= k ? kk : k);
+        const bool ok = okf[i] < 0 ? has_shared != 0 : okf[i] != 0;
+        yv[u] = ok ? ys[i * rows + r] : 0.f;
+        wv[u] = wt[i];
       }
-      const float yv = ok ? ys[(t * stride + kk) * rows + r] : 0.f;
-      acc = __builtin_fmaf(wt[t * stride + kk], yv, acc);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u <= k) acc = __builtin_fmaf(wv[u], yv[u], acc);
     }
     a.out[o] = acc;
   }
 }
 
 static void back_geometry(int hidden, int n_ff, int& rows, int& lrow) {
-  const int lpr = pow2_ceil(n_ff / kQK);
-  int r = 64 / lpr;                  // rows a wave covers with every lane busy
+  lrow = pow2_ceil(n_ff / kQK);      // lanes per row: one per super-block
+  int r = 64 / lrow;                 // rows that fill a wave for one group
   while (r > 1 && hidden / r < 256) r >>= 1;  // at least 256 workgroups when possible
   rows = r;
-  lrow = 64 / r;
 }
 
 }  // namespace sg
@@ -946,13 +986,9 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   back_geometry(hidden, n_ff, rows, lrow);
   const size_t lds_f =
       static_cast<size_t>(front_lds(n_tokens, hidden / kQK, n_expert, k, true).total) * 4;
-  int nbuf = kBackBufs;
-  size_t lds_b = 0;
-  for (; nbuf >= 1; --nbuf) {
-    lds_b = static_cast<size_t>(back_lds(n_tokens, k, n_ff, rows, nbuf, ws.gmax, ws.emax).total) * 4;
-    if (lds_b <= 64 * 1024) break;
-  }
-  if (lds_f + 4 * 64 * 36 * 4 > 160 * 1024 || nbuf < 1)
+  const size_t lds_b =
+      static_cast<size_t>(back_lds(n_tokens, k, n_ff, rows, ws.gmax, ws.emax).total) * 4;
+  if (lds_f + 4 * 64 * 36 * 4 > 160 * 1024 || lds_b + 4 * 64 * 36 * 4 > 160 * 1024)
     return set_error(SG_ERR_UNSUPPORTED, "%s: this shape needs more LDS than a workgroup has",
                      nm);
   unsigned char* base = static_cast<unsigned char*>(workspace);
@@ -987,7 +1023,6 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   a.shared_w = shared_w;
   a.back_rows = rows;
   a.back_lrow = lrow;
-  a.back_bufs = nbuf;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (stages & 1) {
     const int rows_wg = 4 * (32 / pow2_ceil(hidden / kQK));

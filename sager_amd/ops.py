@@ -138,7 +138,8 @@ class MoeLayer:
         self.shared_w = float(shared_w)
         self.max_tokens = max_tokens
         nbytes = load().sg_moe_layer_workspace_bytes(max_tokens, hidden, n_ff, n_expert, k)
-        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=tab_gate.device)
+        # zero-filled once: the layer keeps its per-group arrival counters at zero
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=tab_gate.device)
 
     def forward(self, x, logits=None, residual=None, out=None, idx=None, weight=None,
                 stages=3, workspace=None):
