@@ -152,9 +152,8 @@ int sg_moe_combine(float* out, const float* residual, const float* expert_y,
  *   residual: fp32 [n_tokens][hidden] or NULL (zero); may alias out.
  *   out:      fp32 [n_tokens][hidden].
  *   idx, weight: [n_tokens][k+1] (slot k of weight = shared_w).
- *   workspace: device buffer of at least sg_moe_layer_workspace_bytes(),
- *             ZERO-FILLED before its first use (e.g. hipMemset once after
- *             allocation); the layer leaves it ready for the next call.
+ *   workspace: device buffer of at least sg_moe_layer_workspace_bytes()
+ *             (scratch: the plan and h between the two launches).
  * Routes with an id outside [0, n_expert) zero that token's whole weight row
  * (shared slot included), as moe_dispatch_scan does (moe.cu:385-396); a null
  * table entry is an absent expert and contributes zero (q4_k.cu:697-710).

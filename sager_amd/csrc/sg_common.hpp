@@ -135,6 +135,13 @@ __device__ __forceinline__ void wait_lds() {
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
 }
+// Workgroup barrier for LDS data: this wave's LDS operations complete,
+// then s_barrier.  Unlike __syncthreads it does not wait for outstanding
+// global loads - the LDS DMA included - so a weight stream issued before it
+// keeps flowing; a wave reads LDS it filled by DMA only after wait_vm().
+__device__ __forceinline__ void bar() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 // One 144-B block from LDS (16-B aligned) into 36 registers.
 __device__ __forceinline__ void read_block_lds(const uint32_t* b, uint32_t* w36) {
   const u32x4* p = reinterpret_cast<const u32x4*>(b);

@@ -2,9 +2,14 @@
 //
 // Two launches per layer, on one stream:
 //
-//   front  grid (row chunks of 16, groups): routing + the expert-major plan,
-//          then the gate and up rows of one (group, chunk) and
-//          h = SiLU(g) * u for every token of the group.
+//   front  grid (row chunks of 16, groups + 1): every routed workgroup finds
+//          its expert from the top-k by logit, starts streaming that
+//          expert's gate and up rows, and meanwhile derives the exact
+//          selection from the probabilities (a different expert only on a
+//          probability collision - then it streams the right one); then
+//          h = SiLU(g) * u for every token of its group.  The last row of the
+//          grid is one publisher workgroup that writes idx, weight and the
+//          expert-major plan for the back kernel.
 //   back   grid (row chunks of hidden/256 rows): every group's down rows for
 //          the chunk, the Q8_K of h done in the workgroup, and the combine of
 //          the chunk for every token in slot order - all inside one
@@ -15,6 +20,8 @@
 // 144-B super-block stride.  A group is the shared expert (group 0, tokens
 // 0..T-1 in slot k) or one distinct routed expert (ascending id) with its
 // (token, slot) routes; an expert shared by several tokens is streamed once.
+// Loads that do not depend on routing (x, h, residual) are issued at kernel
+// start so their latency overlaps the routing and the plan load.
 //
 // Stage order and semantics: Session::moe_dispatch_device
 // (session.cpp:2482-3030); router moe.cu:25-85 / 165-234; dispatch plan
@@ -45,12 +52,10 @@ struct LayerPlan {
   int* tok;     // [emax] entry token
   int* slot;    // [emax] entry slot
   unsigned long long* wdown;  // [gmax] down matrix of the group, 0 = absent expert
-  int* fix;     // [T*(k+1)] 1 = take this slot's h from the repair buffers
-  float* hfix;  // [T*(k+1)][n_ff] repaired h rows
 };
 
 struct LayerWs {
-  size_t meta, off, expert, tok, slot, wdown, fix, hfix, h, total;
+  size_t meta, off, expert, tok, slot, wdown, h, total;
   int gmax, emax;
 };
 
@@ -67,8 +72,6 @@ static LayerWs layer_ws(int T, int n_ff, int E, int k) {
   w.tok = o;    o = align256(o + w.emax * sizeof(int));
   w.slot = o;   o = align256(o + w.emax * sizeof(int));
   w.wdown = o;  o = align256(o + w.gmax * sizeof(unsigned long long));
-  w.fix = o;    o = align256(o + static_cast<size_t>(T) * (k + 1) * sizeof(int));
-  w.hfix = o;   o = align256(o + static_cast<size_t>(T) * (k + 1) * n_ff * sizeof(float));
   w.h = o;      o = align256(o + static_cast<size_t>(T) * (k + 1) * n_ff * sizeof(float));
   w.total = o;
   return w;
@@ -150,14 +153,17 @@ __host__ __device__ inline FrontLds front_lds(int T, int nbh, int E, int k, bool
 }
 
 // rank of `key` among 64 keys (16-B aligned): how many are larger.
+// All 32 reads are issued before the first compare (LDS latency paid once).
 __device__ __forceinline__ int rank64(const uint64_t* g, uint64_t key) {
   const u32x4* p = reinterpret_cast<const u32x4*>(g);
+  u32x4 v[32];
+#pragma unroll
+  for (int q = 0; q < 32; ++q) v[q] = p[q];
   int r = 0;
 #pragma unroll
   for (int q = 0; q < 32; ++q) {
-    const u32x4 v = p[q];
-    const uint64_t a = (static_cast<uint64_t>(v.y) << 32) | v.x;
-    const uint64_t b = (static_cast<uint64_t>(v.w) << 32) | v.z;
+    const uint64_t a = (static_cast<uint64_t>(v[q].y) << 32) | v[q].x;
+    const uint64_t b = (static_cast<uint64_t>(v[q].w) << 32) | v[q].z;
     r += (a > key) + (b > key);
   }
   return r;
@@ -166,8 +172,19 @@ __device__ __forceinline__ int rank64(const uint64_t* g, uint64_t key) {
 __device__ __forceinline__ int rank_n(const uint64_t* c, int n, uint64_t key) {
   const u32x4* p = reinterpret_cast<const u32x4*>(c);
   int r = 0;
-#pragma unroll 4
-  for (int q = 0; q < n / 2; ++q) {
+  int q = 0;
+  for (; q + 8 <= n / 2; q += 8) {  // eight reads in flight
+    u32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[q + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint64_t a = (static_cast<uint64_t>(v[u].y) << 32) | v[u].x;
+      const uint64_t b = (static_cast<uint64_t>(v[u].w) << 32) | v[u].z;
+      r += (a > key) + (b > key);
+    }
+  }
+  for (; q < n / 2; ++q) {
     const u32x4 v = p[q];
     const uint64_t a = (static_cast<uint64_t>(v.y) << 32) | v.x;
     const uint64_t b = (static_cast<uint64_t>(v.w) << 32) | v.z;
@@ -178,14 +195,14 @@ __device__ __forceinline__ int rank_n(const uint64_t* c, int n, uint64_t key) {
 
 // Top-m selection of a team over keys[0..npad) (own keys also in kr[]):
 // per 64-key group the m largest, then the m largest of those.  Three
-// workgroup barriers; every thread of the workgroup takes part.
+// barriers; every thread of the workgroup takes part.
 template <int EPT>
 __device__ void team_select(const FrontLds& L, int E, const uint64_t* keys, const uint64_t* kr,
                             uint64_t* cand, uint64_t* top, int tt) {
   const int m = L.m;
   for (int i = tt; i < L.ncp; i += L.TT) cand[i] = 0;
   for (int i = tt; i < m; i += L.TT) top[i] = 0;
-  __syncthreads();
+  bar();
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
     const int i = tt + L.TT * j;
@@ -194,14 +211,14 @@ __device__ void team_select(const FrontLds& L, int E, const uint64_t* keys, cons
       if (r < m) cand[(i >> 6) * m + r] = kr[j];
     }
   }
-  __syncthreads();
+  bar();
   for (int c = tt; c < L.ng * m; c += L.TT) {
     const uint64_t kc = cand[c];
     if (kc == 0) continue;
     const int r = rank_n(cand, L.ncp, kc);
     if (r < m) top[r] = kc;
   }
-  __syncthreads();
+  bar();
 }
 
 // Expert-major plan from ridx[T*k] (ids outside [0, E) skipped): group 0 =
@@ -264,7 +281,7 @@ __device__ void build_plan(uint32_t* dyn, const FrontLds& L, int T, int k, int E
         ctrl[1] = nf;
       }
     }
-    __syncthreads();
+    bar();
     return;
   }
   if (tid == 0) ctrl[0] = ctrl[1] = 0;
@@ -272,7 +289,7 @@ __device__ void build_plan(uint32_t* dyn, const FrontLds& L, int T, int k, int E
     const int e = ridx[i];
     re[i] = (e >= 0 && e < E) ? e : -1;
   }
-  __syncthreads();
+  bar();
   for (int i = tid; i < R; i += 256) {
     const int e = re[i];
     int first = e >= 0;
@@ -281,7 +298,7 @@ __device__ void build_plan(uint32_t* dyn, const FrontLds& L, int T, int k, int E
     if (e >= 0) atomicAdd(&ctrl[0], 1);
     if (first) atomicAdd(&ctrl[1], 1);
   }
-  __syncthreads();
+  bar();
   for (int i = tid; i < R; i += 256) {
     const int e = re[i];
     if (e < 0) continue;
@@ -303,13 +320,13 @@ __device__ void build_plan(uint32_t* dyn, const FrontLds& L, int T, int k, int E
     ptok[tid] = tid;
     pslot[tid] = k;
   }
-  __syncthreads();
+  bar();
   if (tid == 0) {
     poff[0] = 0;
     poff[gbase + ctrl[1]] = ebase + ctrl[0];
     if (has_shared) pexp[0] = -1;
   }
-  __syncthreads();
+  bar();
 }
 
 // ---- front kernel ---------------------------------------------------------------------
@@ -361,34 +378,59 @@ __device__ __forceinline__ void dma_gateup(const sg_block_q4k* wg, const sg_bloc
              lane);
 }
 
-// Q8_K of every token's x into LDS: wave w takes blocks w, w+4, ... four
-// at a time (interleaved chains).
-__device__ __forceinline__ void quantize_x(const float* x, int n_blocks, uint32_t* xs, int wave,
-                                           int lane) {
-  for (int b0 = wave; b0 < n_blocks; b0 += 16) {
+// x values of a wave's first quantization pass (blocks w + nw*u), loaded
+// at kernel start so their latency overlaps the routing.  Waves w < nw of
+// the workgroup take part.
+__device__ __forceinline__ void x_preload(const float* x, int n_blocks, int w, int nw, int lane,
+                                          float (&pre)[4][4]) {
+  if (w >= n_blocks || w >= nw) return;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int b = w + nw * u;
+    const int bb = b < n_blocks ? b : w;
+    const float* xb = x + static_cast<long long>(bb) * kQK + 4 * lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pre[u][i] = xb[i];
+  }
+}
+
+// Q8_K of every token's x into LDS by waves w < nw: wave w takes blocks
+// w, w+nw, ... up to four at a time (interleaved chains); the first pass
+// comes from x_preload.
+__device__ __forceinline__ void quantize_x(const float* x, int n_blocks, uint32_t* xs, int w,
+                                           int nw, int lane, const float (&pre)[4][4]) {
+  if (w >= nw) return;
+  for (int b0 = w; b0 < n_blocks; b0 += 4 * nw) {
     float v[4][4];
     uint32_t* dst[4];
     int n = 0;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int b = b0 + 4 * u;
+      const int b = b0 + nw * u;
       const int bb = b < n_blocks ? b : b0;
       const float* xb = x + static_cast<long long>(bb) * kQK + 4 * lane;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[u][i] = xb[i];
+      for (int i = 0; i < 4; ++i) v[u][i] = b0 == w ? pre[u][i] : xb[i];
       dst[u] = xs + bb * kXStride;
       n += b < n_blocks;
     }
-    quantize_n_lds<4>(v, dst, n, lane);
+    if (n <= 2) {  // fewer chains, fewer instructions
+      const float(&v2)[2][4] = *reinterpret_cast<const float(*)[2][4]>(&v[0][0]);
+      uint32_t* const d2[2] = {dst[0], dst[1]};
+      quantize_n_lds<2>(v2, d2, n, lane);
+    } else {
+      quantize_n_lds<4>(v, dst, n, lane);
+    }
   }
 }
 
 // Logit-order top-(k+1) of every token: spec[t*m + r] = r-th expert (or -1).
 // Teams of tw waves; each thread keeps its logits in lr[] (last pass's
-// token).  Workgroup-wide.
+// token).  Workgroup-wide; the last pass's top[] is readable on return,
+// spec[] only after the caller's next barrier.
 template <int EPT>
 __device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
-                            int tid, int lane) {
+                            int tid) {
   const int T = a.T, E = a.n_expert, m = L.m;
   const int wave = tid >> 6, team = wave / L.tw, tt = tid - team * L.TT;
   uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + L.keys) + team * L.npad;
@@ -412,15 +454,15 @@ __device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L
     }
     team_select<EPT>(L, E, keys, kr, cand, top, tt);
     if (ok && tt < m) spec[t * m + tt] = top[tt] ? sel_idx(top[tt]) : -1;
-    if (T > L.nteams) __syncthreads();
+    if (t0 + L.nteams < T) bar();  // the next pass reuses keys/cand/top
   }
-  __syncthreads();
 }
 
-// Plan for T == 1 straight from distinct, valid ids ridx[0..k): group
+// Plan for T == 1 straight from k distinct, valid ids id(0..k-1): group
 // gbase + r = the expert of rank r, its single entry (token 0, slot j).
-__device__ void plan_t1(uint32_t* dyn, const FrontLds& L, int k, int has_shared, int tid) {
-  const int* ridx = reinterpret_cast<const int*>(dyn + L.ridx);
+// Ends with a barrier.
+template <typename Id>
+__device__ void plan_t1(uint32_t* dyn, const FrontLds& L, int k, int has_shared, int tid, Id id) {
   int* re = reinterpret_cast<int*>(dyn + L.re);
   int* poff = reinterpret_cast<int*>(dyn + L.poff);
   int* pexp = reinterpret_cast<int*>(dyn + L.pexp);
@@ -429,9 +471,9 @@ __device__ void plan_t1(uint32_t* dyn, const FrontLds& L, int k, int has_shared,
   int* ctrl = reinterpret_cast<int*>(dyn + L.ctrl);
   const int gbase = has_shared, ebase = has_shared ? 1 : 0;
   if (tid < k) {
-    const int e = ridx[tid];
+    const int e = id(tid);
     int r = 0;
-    for (int j = 0; j < k; ++j) r += ridx[j] < e;
+    for (int j = 0; j < k; ++j) r += id(j) < e;
     re[tid] = e;
     poff[gbase + r] = ebase + r;
     pexp[gbase + r] = e;
@@ -449,11 +491,11 @@ __device__ void plan_t1(uint32_t* dyn, const FrontLds& L, int k, int has_shared,
     ctrl[0] = k;
     ctrl[1] = k;
   }
-  __syncthreads();
+  bar();
 }
 
-// True when ridx[0..T*k) are k distinct valid ids per token (what routing
-// produces); then the T == 1 plan needs no general build.
+// True when ridx[0..n) are distinct valid ids (what routing produces for
+// one token); then the T == 1 plan needs no general build.
 __device__ __forceinline__ bool ids_distinct_valid(const int* ridx, int n, int E) {
   bool ok = true;
   for (int i = 0; i < n; ++i) {
@@ -463,36 +505,262 @@ __device__ __forceinline__ bool ids_distinct_valid(const int* ridx, int n, int E
   return ok;
 }
 
-// Compute workgroups (blockIdx.y < gmax): one (group, chunk of 16 rows).
-// The shared expert's group streams at once; a routed group takes its
-// expert from the top-k by LOGIT (index tie rule) and writes h for the
-// (token, slot) entries of that expert.  The publisher workgroup
-// (blockIdx.y == gmax) derives the exact selection from the probabilities
-// and repairs any slot where the two differ (see the publisher below).
-template <int EPT>
-__global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
-  __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
-  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
+// The plan of ridx[0..T*k): the one-token form when the ids are distinct
+// and valid, else the general build.  Ends with a barrier.
+__device__ __forceinline__ void make_plan(uint32_t* dyn, const FrontLds& L, int T, int k, int E,
+                                          int has_shared, int tid) {
+  const int* ridx = reinterpret_cast<const int*>(dyn + L.ridx);
+  if (T == 1 && ids_distinct_valid(ridx, k, E))
+    plan_t1(dyn, L, k, has_shared, tid, [&](int j) { return ridx[j]; });
+  else
+    build_plan(dyn, L, T, k, E, has_shared, tid);
+}
 
+// Maximum of a 64-bit key over the wave (butterfly), same value in every lane.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), o, 64);
+    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), o, 64);
+    const uint64_t w = (static_cast<uint64_t>(hi) << 32) | lo;
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// Exact routing of ONE token by one wave, no workgroup barrier (moe.cu:25-85):
+// same arithmetic and checks as exact_route below.  Logits come from lv[]
+// (LDS, filled by spec_select), lane l holds experts l + 64j.  Writes ridx,
+// rw and ctrl[3] (1 when an id differs from the logit order).
+template <int EPL>
+__device__ void route_wave(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, int lane) {
+  const int E = a.n_expert, k = a.k, m = L.m;
+  const float* lv = reinterpret_cast<const float*>(dyn + L.lv);
+  float* ev = reinterpret_cast<float*>(dyn + L.ev);
+  const int* spec = reinterpret_cast<const int*>(dyn + L.spec);
+  int* ridx = reinterpret_cast<int*>(dyn + L.ridx);
+  float* rw = reinterpret_cast<float*>(dyn + L.rw);
+  int* ctrl = reinterpret_cast<int*>(dyn + L.ctrl);
+  float v[EPL];
+  float mx = -1e30f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int i = lane + 64 * j;
+    v[j] = i < E ? lv[i] : 0.f;
+    if (i < E) mx = fmaxf(mx, v[j]);
+  }
+  mx = wave_max_dpp(mx);
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int i = lane + 64 * j;
+    if (i < L.e32) ev[i] = i < E ? expf_sg(v[j] - mx) : 0.f;
+  }
+  // the wave's LDS writes complete in order before its own reads
+  const float z = readlane_f(lane == 0 ? serial_sum(ev, L.e32) : 0.f, 0);
+  const bool degen = !(z == z) || z == 0.f;
+  const int ik = lane < m ? spec[lane] : -1;
+  const float pk = (ik >= 0 && !degen) ? ev[ik] / z : -1.f;
+  const float lk = ik >= 0 ? lv[ik] : 0.f;
+  const float pn = __shfl(pk, lane + 1, 64);
+  const float ln = __shfl(lk, lane + 1, 64);
+  const int in = __shfl(ik, lane + 1, 64);
+  bool cond = true;
+  if (lane + 1 < k) cond = ik >= 0 && in >= 0 && (pk > pn || lk == ln);
+  else if (lane + 1 == k && E > k) cond = ik >= 0 && in >= 0 && pk > pn;
+  const bool fast = !degen && __ballot(!cond) == 0;
+  int fi;
+  float pv;
+  if (degen) {
+    fi = lane % E;
+    pv = -1.f;
+  } else if (fast) {
+    fi = ik;
+    pv = pk;
+  } else {  // a probability collision: k rounds of argmax on p itself
+    uint64_t kv[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int i = lane + 64 * j;
+      kv[j] = i < E ? sel_key(ev[i] / z, i) : 0ull;
+    }
+    fi = 0;
+    for (int kk = 0; kk < k; ++kk) {
+      uint64_t best = 0;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) best = kv[j] > best ? kv[j] : best;
+      best = wave_max_u64(best);
+      if (lane == kk) fi = best ? sel_idx(best) : 0;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        if (kv[j] == best) kv[j] = 0;
+    }
+    pv = ev[fi] / z;
+  }
+  float wsum = 0.f;
+  for (int kk = 0; kk < k; ++kk) wsum += readlane_f(pv, kk);
+  const float wv = wsum > 0.f ? pv / wsum : pv;
+  bool changed = false;
+  if (lane < k) {
+    changed = fi != ridx[lane];
+    ridx[lane] = fi;
+    rw[lane] = wv;
+  }
+  const bool any = __ballot(changed) != 0ull;
+  if (lane == 0) {
+    rw[k] = a.shared_w;
+    ctrl[3] = any;
+  }
+}
+
+// Exact routing of every token (moe.cu:25-85): max, exp, the normalizer
+// summed serially in index order, p = e / z.  p is a monotone function of
+// the logit, so the logit order (spec[]) is the probability order unless two
+// neighbours collide on one float; the check is p strictly decreasing
+// across the k+1 leading candidates (or equal logits).  A collision selects
+// on the probabilities themselves; a degenerate row (NaN, empty normalizer)
+// takes kk % E with weight -1.  Writes ridx (replacing the logit-order ids)
+// and rw; ctrl[3] = 1 when any id changed.  Workgroup-wide, barriers only
+// (no wait on the weight stream in flight).
+template <int EPT>
+__device__ void exact_route(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
+                            int tid) {
+  const int T = a.T, E = a.n_expert, k = a.k, stride = k + 1, m = L.m;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int tw = L.tw, team = wave / tw, wit = wave - team * tw;
+  const int tt = tid - team * L.TT;
+  uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + L.keys) + team * L.npad;
+  float* lv = reinterpret_cast<float*>(dyn + L.lv) + team * L.e32;
+  float* ev = reinterpret_cast<float*>(dyn + L.ev) + team * L.e32;
+  uint64_t* cand = reinterpret_cast<uint64_t*>(dyn + L.cand) + team * L.ncp;
+  uint64_t* top = reinterpret_cast<uint64_t*>(dyn + L.top) + team * m;
+  float* red = reinterpret_cast<float*>(dyn + L.red) + team * 4;
+  float* zs = reinterpret_cast<float*>(dyn + L.zs);
+  int* spec = reinterpret_cast<int*>(dyn + L.spec);
+  int* ridx = reinterpret_cast<int*>(dyn + L.ridx);
+  float* rw = reinterpret_cast<float*>(dyn + L.rw);
+  int* ctrl = reinterpret_cast<int*>(dyn + L.ctrl);
+  if (tid == 0) ctrl[3] = 0;
+  for (int t0 = 0; t0 < T; t0 += L.nteams) {
+    const int t = t0 + team;
+    const bool ok = t < T;
+    if (T > L.nteams) {  // several passes: (re)load this token's logits
+      const float* lg = a.logits + static_cast<long long>(t) * E;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const int i = tt + L.TT * j;
+        lr[j] = (j < L.ept && i < E && ok) ? lg[i] : 0.f;
+        if (j < L.ept && i < L.e32) lv[i] = lr[j];
+      }
+    }
+    if (tid == 0) ctrl[2] = 0;
+    float mx = -1e30f;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+      if (j < L.ept && tt + L.TT * j < E && ok) mx = fmaxf(mx, lr[j]);
+    mx = team_max(mx, red, wit, tw, lane);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int i = tt + L.TT * j;
+      if (j < L.ept && i < L.e32) ev[i] = (ok && i < E) ? expf_sg(lr[j] - mx) : 0.f;
+    }
+    bar();
+    if (tt == 0) zs[team] = serial_sum(ev, L.e32);
+    bar();
+    const float z = zs[team];
+    const bool degen = !(z == z) || z == 0.f;
+    bool fast = false;
+    float pk = -1.f;
+    int ik = -1;
+    if (wit == 0) {
+      ik = (ok && lane < m) ? spec[t * m + lane] : -1;
+      pk = (ik >= 0 && !degen) ? ev[ik] / z : -1.f;
+      const float lk = ik >= 0 ? lv[ik] : 0.f;
+      const float pn = __shfl(pk, lane + 1, 64);
+      const float ln = __shfl(lk, lane + 1, 64);
+      const int in = __shfl(ik, lane + 1, 64);
+      bool cond = true;
+      if (lane + 1 < k) cond = ik >= 0 && in >= 0 && (pk > pn || lk == ln);
+      else if (lane + 1 == k && E > k) cond = ik >= 0 && in >= 0 && pk > pn;
+      fast = ok && !degen && __ballot(!cond) == 0;
+      if (lane == 0) {
+        ctrl[4 + team] = ok && !degen && !fast;
+        if (ok && !degen && !fast) atomicOr(&ctrl[2], 1);
+      }
+    }
+    bar();
+    if (ctrl[2] != 0) {  // selection on the probabilities for the colliding rows
+      const bool slow_team = ctrl[4 + team] != 0;
+      uint64_t kr[EPT];
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const int i = tt + L.TT * j;
+        kr[j] = (j < L.ept && i < E && slow_team) ? sel_key(ev[i] / z, i) : 0;
+        if (j < L.ept && i < L.npad) keys[i] = kr[j];
+      }
+      team_select<EPT>(L, E, keys, kr, cand, top, tt);
+    }
+    if (wit == 0 && ok) {
+      int fi;
+      float pv;
+      if (degen) {
+        fi = lane % E;
+        pv = -1.f;
+      } else if (fast) {
+        fi = ik;
+        pv = pk;
+      } else {
+        fi = lane < m && top[lane] ? sel_idx(top[lane]) : 0;
+        pv = ev[fi] / z;
+      }
+      float wsum = 0.f;
+      for (int kk = 0; kk < k; ++kk) wsum += readlane_f(pv, kk);
+      const float wv = wsum > 0.f ? pv / wsum : pv;
+      if (lane < k) {
+        if (fi != ridx[t * k + lane]) atomicOr(&ctrl[3], 1);
+        ridx[t * k + lane] = fi;
+        rw[t * stride + lane] = wv;
+      }
+      if (lane == 0) rw[t * stride + k] = a.shared_w;
+    }
+    bar();
+  }
+}
+
+// Compute workgroups (blockIdx.y < gmax): one (group, chunk of 16 rows).
+// The shared expert's group streams at once; a routed group streams the
+// expert the logit order gives it, then checks that against the exact
+// routing (streaming the exact expert instead when they differ) and writes
+// h for the (token, slot) entries of its group in the exact plan.  The
+// publisher workgroup (blockIdx.y == gmax, x == 0) runs the same routing
+// and writes idx, weight and the plan.
+template <int EPT>
+__device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[64 * 36],
+                           uint32_t* dyn) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, E = a.n_expert, stride = k + 1;
-  const int g = blockIdx.y;
   const int nbh = a.hidden / kQK, lpr = pow2_ceil(nbh);
   const bool publisher = g == a.gmax;
-  if (publisher && blockIdx.x != 0) return;  // one publisher per launch
+  if (publisher && bx != 0) return;  // one publisher per launch
   const bool shared_grp = a.has_shared && g == 0;
   const FrontLds L = front_lds(T, nbh, E, k, !shared_grp);
   const int rpw = 32 / lpr;
-  const int row0 = blockIdx.x * 4 * rpw + wave * rpw;
+  const int row0 = bx * 4 * rpw + wave * rpw;
   const int nrw = max(0, min(rpw, a.n_ff - row0));
   const int gbase = a.has_shared;
   uint32_t* buf = wbuf[wave];
   uint32_t* xs = dyn + L.xs;
+  const int nxb = T * nbh;
+  // one token with router logits: wave 3 does the exact routing on its own
+  // while waves 0-2 issue the weight stream and quantize x
+  const bool t1w = T == 1 && a.logits != nullptr && !shared_grp;
+  const int nqw = t1w ? 3 : 4;
+  float xpre[4][4];
+  if (!publisher) x_preload(a.x, nxb, wave, nqw, lane, xpre);
 
   if (shared_grp) {
     if (nrw > 0) dma_gateup(a.sh_gate, a.sh_up, row0, nrw, nbh, buf, lane);
-    quantize_x(a.x, T * nbh, xs, wave, lane);
-    __syncthreads();
+    quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);
+    bar();
     // entries: tokens 0..T-1 in slot k, no plan needed
     gateup_wave(true, row0, nrw, nbh, lpr, buf, xs,
                 [&](int j, int& t, int& sl) { t = j; sl = k; }, T, stride, a.n_ff, a.h, lane);
@@ -511,8 +779,8 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
   const int* ptok = reinterpret_cast<const int*>(dyn + L.ptok);
   const int* pslot = reinterpret_cast<const int*>(dyn + L.pslot);
 
-  // expert pointer tables into LDS (waves 0-2, one table each)
-  if (wave < 3 && (wave < 2 || publisher)) {
+  // expert pointer tables into LDS (gate and up; down for the publisher)
+  if (wave < 2 || (wave == 2 && publisher)) {
     const sg_block_q4k* const* tab = wave == 0 ? a.tab_gate : (wave == 1 ? a.tab_up : a.tab_down);
     uint32_t* dst = dyn + (wave == 0 ? L.tabg : (wave == 1 ? L.tabu : L.tabd));
     const char* src = reinterpret_cast<const char*>(tab);
@@ -522,256 +790,159 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
           reinterpret_cast<unsigned long long>(tab[E - 1]);
   }
 
-  float lr[EPT];
-  if (!publisher && a.logits && T == 1) {
-    // one token: this workgroup's expert is the (g - gbase)-th smallest id of
-    // the logit-order top-k, its single entry (token 0, the slot it holds) -
-    // found by every wave on its own, no plan and no extra barrier
-    spec_select<EPT>(a, dyn, L, lr, tid, lane);
-    const int ej = lane < k ? spec[lane] : -1;
-    int r = 0;
-    for (int i = 0; i < k; ++i) {
-      const int ei = spec[i];
-      r += ei >= 0 && ei < ej;
-    }
-    const unsigned long long hit = __ballot(ej >= 0 && r == g - gbase);
-    if (wave < 2) wait_vm();  // pointer tables
-    __syncthreads();
-    if (hit == 0ull) return;
-    const int sl = __builtin_ctzll(hit);
-    const int e = __builtin_amdgcn_readlane(ej, sl);
+  // stream the gate/up rows of expert e (none when e < 0 or it is absent)
+  // for wave w's rows into wave w's buffer
+  auto stream_rows = [&](int e, int w) {
+    const int r0 = bx * 4 * rpw + w * rpw;
+    const int n = min(rpw, a.n_ff - r0);
+    if (e < 0 || n <= 0) return;
     const sg_block_q4k* wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
     const sg_block_q4k* wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
-    const bool present = wg != nullptr && wu != nullptr;
-    if (present && nrw > 0) dma_gateup(wg, wu, row0, nrw, nbh, buf, lane);
-    quantize_x(a.x, nbh, xs, wave, lane);  // overlaps the weight stream
-    __syncthreads();
-    gateup_wave(present, row0, nrw, nbh, lpr, buf, xs,
-                [&](int, int& t, int& s_) { t = 0; s_ = sl; }, 1, stride, a.n_ff, a.h, lane);
-    return;
-  }
+    if (wg && wu) dma_gateup(wg, wu, r0, n, nbh, wbuf[w], lane);
+  };
+
+  float lr[EPT];
+  int e_mine = -1;
+  int n_groups;
   if (a.logits) {
-    spec_select<EPT>(a, dyn, L, lr, tid, lane);
-    for (int i = tid; i < T * k; i += 256) ridx[i] = spec[(i / k) * L.m + (i % k)];
+    spec_select<EPT>(a, dyn, L, lr, tid);
+    if (T == 1) {
+      // top[] of the single token is readable now: with k valid ids the
+      // plan is made here, in the same phase as spec[] and ridx[]
+      const uint64_t* top = reinterpret_cast<const uint64_t*>(dyn + L.top);
+      bool valid = true;
+      for (int j = 0; j < k; ++j) valid &= top[j] != 0ull;
+      if (valid) {
+        if (tid < k) ridx[tid] = sel_idx(top[tid]);
+        plan_t1(dyn, L, k, a.has_shared, tid, [&](int j) { return sel_idx(top[j]); });
+      } else {
+        if (tid < k) ridx[tid] = top[tid] ? sel_idx(top[tid]) : -1;
+        bar();
+        build_plan(dyn, L, T, k, E, a.has_shared, tid);
+      }
+    } else {
+      bar();
+      for (int i = tid; i < T * k; i += 256) ridx[i] = spec[(i / k) * L.m + (i % k)];
+      bar();
+      build_plan(dyn, L, T, k, E, a.has_shared, tid);
+    }
+    if (!publisher) {
+      if (wave < 2) wait_vm();  // pointer tables
+      bar();
+      e_mine = g < gbase + ctrl[1] ? pexp[g] : -1;
+      // speculative: the logit-order expert.  One token: waves 0-2 issue
+      // the stream (wave 0 also wave 3's rows) so wave 3 routes unblocked.
+      if (!t1w) {
+        stream_rows(e_mine, wave);
+      } else if (wave < 3) {
+        stream_rows(e_mine, wave);
+        if (wave == 0) stream_rows(e_mine, 3);
+      }
+    }
+    if (t1w) {
+      if (wave == 3) {
+        route_wave<4 * EPT>(a, dyn, L, lane);
+      } else if (!publisher) {
+        quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);  // overlaps the weight stream
+        if (wave == 0) wait_vm();  // wave 3's rows
+      }
+      bar();
+    } else {
+      exact_route<EPT>(a, dyn, L, lr, tid);
+    }
+    if (ctrl[3]) make_plan(dyn, L, T, k, E, a.has_shared, tid);
+    n_groups = gbase + ctrl[1];
+    if (!publisher) {
+      const int e_x = g < n_groups ? pexp[g] : -1;
+      if (e_x != e_mine) {  // a collision moved this group to another expert
+        wait_vm();          // the speculative stream has landed; reuse the buffers
+        bar();
+        stream_rows(e_x, wave);
+        e_mine = e_x;
+      }
+    }
   } else {
     for (int i = tid; i < T * k; i += 256) ridx[i] = a.idx[(i / k) * stride + (i % k)];
     for (int i = tid; i < T * stride; i += 256) rw[i] = a.weight[i];
+    bar();
+    make_plan(dyn, L, T, k, E, a.has_shared, tid);
+    n_groups = gbase + ctrl[1];
+    if (!publisher) {
+      if (wave < 2) wait_vm();  // pointer tables
+      bar();
+      e_mine = g < n_groups ? pexp[g] : -1;
+      stream_rows(e_mine, wave);
+    }
   }
-  __syncthreads();
-  // routing output is k distinct ids per token; the caller's may not be
-  bool direct = T == 1;
-  if (direct) {
-    if (a.logits)
-      for (int i = 0; i < k; ++i) direct &= ridx[i] >= 0;
-    else
-      direct = ids_distinct_valid(ridx, k, E);
-  }
-  if (direct)
-    plan_t1(dyn, L, k, a.has_shared, tid);
-  else
-    build_plan(dyn, L, T, k, E, a.has_shared, tid);
-  int n_groups = gbase + ctrl[1];
 
-  if (!publisher) {
-    if (wave < 2) wait_vm();  // pointer tables
-    __syncthreads();
-    if (g >= n_groups) return;
-    const int e = pexp[g];
-    const sg_block_q4k* wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
-    const sg_block_q4k* wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
-    const bool present = wg != nullptr && wu != nullptr;
-    if (present && nrw > 0) dma_gateup(wg, wu, row0, nrw, nbh, buf, lane);
-    quantize_x(a.x, T * nbh, xs, wave, lane);  // overlaps the weight stream
-    __syncthreads();
-    const int j0 = poff[g];
-    gateup_wave(present, row0, nrw, nbh, lpr, buf, xs,
-                [&](int j, int& t, int& sl) { t = ptok[j0 + j]; sl = pslot[j0 + j]; },
-                poff[g + 1] - j0, stride, a.n_ff, a.h, lane);
+  if (publisher) {
+    // publish idx, weight, plan and down pointers
+    wait_vm();  // pointer tables
+    bar();
+    const int* re = reinterpret_cast<const int*>(dyn + L.re);
+    const int nv = ctrl[0];
+    for (int t = tid; t < T; t += 256) {
+      bool bad = false;  // bounds-kill: a row with an invalid id loses all its weights
+      for (int kk = 0; kk < k; ++kk) bad |= re[t * k + kk] < 0;
+      for (int q = 0; q <= k; ++q) a.weight[t * stride + q] = bad ? 0.f : rw[t * stride + q];
+      if (a.logits)
+        for (int kk = 0; kk < k; ++kk) a.idx[t * stride + kk] = ridx[t * k + kk];
+    }
+    for (int i = tid; i <= n_groups; i += 256) a.plan.off[i] = poff[i];
+    for (int i = tid; i < n_groups; i += 256) {
+      const int e = pexp[i];
+      a.plan.expert[i] = e;
+      const unsigned long long gp =
+          e >= 0 ? tabg[e] : reinterpret_cast<unsigned long long>(a.sh_gate);
+      const unsigned long long up = e >= 0 ? tabu[e] : reinterpret_cast<unsigned long long>(a.sh_up);
+      const unsigned long long dp =
+          e >= 0 ? tabd[e] : reinterpret_cast<unsigned long long>(a.sh_down);
+      a.plan.wdown[i] = (gp && up) ? dp : 0ull;
+    }
+    for (int i = tid; i < (a.has_shared ? T : 0) + nv; i += 256) {
+      a.plan.tok[i] = ptok[i];
+      a.plan.slot[i] = pslot[i];
+    }
+    if (tid == 0) {
+      a.plan.meta[0] = n_groups;
+      a.plan.meta[1] = a.has_shared;
+      a.plan.meta[2] = nv;
+    }
     return;
   }
+  if (g >= n_groups) {
+    wait_vm();  // a stream may still be landing in this LDS
+    return;
+  }
+  const int e = pexp[g];
+  const bool present = tabg[e] != 0ull && tabu[e] != 0ull;
+  if (!t1w) {
+    quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);  // overlaps the weight stream
+    bar();
+  }
+  const int j0 = poff[g];
+  gateup_wave(present, row0, nrw, nbh, lpr, buf, xs,
+              [&](int j, int& t, int& sl) { t = ptok[j0 + j]; sl = pslot[j0 + j]; },
+              poff[g + 1] - j0, stride, a.n_ff, a.h, lane);
+}
 
-  // ---- publisher ------------------------------------------------------------------
-  // Exact routing: max, exp, the normalizer summed serially in index order,
-  // p = e / z.  p is a monotone function of the logit, so the logit order is
-  // the probability order unless two neighbours collide on one float; the
-  // check is p strictly decreasing across the k+1 leading candidates (or
-  // equal logits).  A collision, or a degenerate row (NaN, empty
-  // normalizer), selects on the probabilities themselves; slots whose
-  // expert differs from the compute workgroups' choice are recomputed into
-  // the fix buffer and flagged for the back kernel.
-  const int tw = L.tw, team = wave / tw, wit = wave - team * tw;
-  const int tt = tid - team * L.TT;
-  const int m = L.m;
-  if (a.logits) {
-    uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + L.keys) + team * L.npad;
-    float* lv = reinterpret_cast<float*>(dyn + L.lv) + team * L.e32;
-    float* ev = reinterpret_cast<float*>(dyn + L.ev) + team * L.e32;
-    uint64_t* cand = reinterpret_cast<uint64_t*>(dyn + L.cand) + team * L.ncp;
-    uint64_t* top = reinterpret_cast<uint64_t*>(dyn + L.top) + team * m;
-    float* red = reinterpret_cast<float*>(dyn + L.red) + team * 4;
-    float* zs = reinterpret_cast<float*>(dyn + L.zs);
-    if (tid == 0) ctrl[3] = 0;
-    for (int t0 = 0; t0 < T; t0 += L.nteams) {
-      const int t = t0 + team;
-      const bool ok = t < T;
-      if (T > L.nteams) {  // later passes: reload this token's logits
-        const float* lg = a.logits + static_cast<long long>(t) * E;
-#pragma unroll
-        for (int j = 0; j < EPT; ++j) {
-          const int i = tt + L.TT * j;
-          lr[j] = (j < L.ept && i < E && ok) ? lg[i] : 0.f;
-          if (j < L.ept && i < L.e32) lv[i] = lr[j];
-        }
-      }
-      if (tid == 0) ctrl[2] = 0;
-      float mx = -1e30f;
-#pragma unroll
-      for (int j = 0; j < EPT; ++j)
-        if (j < L.ept && tt + L.TT * j < E && ok) mx = fmaxf(mx, lr[j]);
-      mx = team_max(mx, red, wit, tw, lane);
-#pragma unroll
-      for (int j = 0; j < EPT; ++j) {
-        const int i = tt + L.TT * j;
-        if (j < L.ept && i < L.e32) ev[i] = (ok && i < E) ? expf_sg(lr[j] - mx) : 0.f;
-      }
-      __syncthreads();
-      if (tt == 0) zs[team] = serial_sum(ev, L.e32);
-      __syncthreads();
-      const float z = zs[team];
-      const bool degen = !(z == z) || z == 0.f;
-      bool fast = false;
-      float pk = -1.f;
-      int ik = -1;
-      if (wit == 0) {
-        ik = (ok && lane < m) ? spec[t * m + lane] : -1;
-        pk = (ik >= 0 && !degen) ? ev[ik] / z : -1.f;
-        const float lk = ik >= 0 ? lv[ik] : 0.f;
-        const float pn = __shfl(pk, lane + 1, 64);
-        const float ln = __shfl(lk, lane + 1, 64);
-        const int in = __shfl(ik, lane + 1, 64);
-        bool cond = true;
-        if (lane + 1 < k) cond = ik >= 0 && in >= 0 && (pk > pn || lk == ln);
-        else if (lane + 1 == k && E > k) cond = ik >= 0 && in >= 0 && pk > pn;
-        fast = ok && !degen && __ballot(!cond) == 0;
-        if (lane == 0) {
-          ctrl[4 + team] = ok && !degen && !fast;
-          if (ok && !degen && !fast) atomicOr(&ctrl[2], 1);
-        }
-      }
-      __syncthreads();
-      if (ctrl[2] != 0) {  // selection on the probabilities for the colliding rows
-        const bool slow_team = ctrl[4 + team] != 0;
-        uint64_t kr[EPT];
-#pragma unroll
-        for (int j = 0; j < EPT; ++j) {
-          const int i = tt + L.TT * j;
-          kr[j] = (j < L.ept && i < E && slow_team) ? sel_key(ev[i] / z, i) : 0;
-          if (j < L.ept && i < L.npad) keys[i] = kr[j];
-        }
-        team_select<EPT>(L, E, keys, kr, cand, top, tt);
-      }
-      if (wit == 0 && ok) {
-        int fi;
-        float pv;
-        if (degen) {
-          fi = lane % E;
-          pv = -1.f;
-        } else if (fast) {
-          fi = ik;
-          pv = pk;
-        } else {
-          fi = lane < m && top[lane] ? sel_idx(top[lane]) : 0;
-          pv = ev[fi] / z;
-        }
-        float wsum = 0.f;
-        for (int kk = 0; kk < k; ++kk) wsum += readlane_f(pv, kk);
-        const float wv = wsum > 0.f ? pv / wsum : pv;
-        if (lane < k) {
-          ctrl[8 + t * k + lane] = fi != ridx[t * k + lane];  // slot needs repair
-          if (fi != ridx[t * k + lane]) atomicOr(&ctrl[3], 1);
-          ridx[t * k + lane] = fi;
-          rw[t * stride + lane] = wv;
-        }
-        if (lane == 0) rw[t * stride + k] = a.shared_w;
-      }
-      __syncthreads();
-    }
-    if (ctrl[3]) {
-      if (T == 1)  // exact selections are k distinct valid ids
-        plan_t1(dyn, L, k, a.has_shared, tid);
-      else
-        build_plan(dyn, L, T, k, E, a.has_shared, tid);
-      n_groups = gbase + ctrl[1];
-    }
-  }
-  wait_vm();  // pointer tables
-  __syncthreads();
-
-  // publish idx, weight, plan, down pointers and the repair flags
-  const int* re = reinterpret_cast<const int*>(dyn + L.re);
-  const int nv = ctrl[0];
-  for (int t = tid; t < T; t += 256) {
-    bool bad = false;  // bounds-kill: a row with an invalid id loses all its weights
-    for (int kk = 0; kk < k; ++kk) bad |= re[t * k + kk] < 0;
-    for (int q = 0; q <= k; ++q) a.weight[t * stride + q] = bad ? 0.f : rw[t * stride + q];
-    if (a.logits)
-      for (int kk = 0; kk < k; ++kk) a.idx[t * stride + kk] = ridx[t * k + kk];
-  }
-  for (int i = tid; i < T * stride; i += 256) {
-    const int t = i / stride, s = i - t * stride;
-    a.plan.fix[i] = (a.logits && s < k && ctrl[3]) ? ctrl[8 + t * k + s] : 0;
-  }
-  for (int i = tid; i <= n_groups; i += 256) a.plan.off[i] = poff[i];
-  for (int i = tid; i < n_groups; i += 256) {
-    const int e = pexp[i];
-    a.plan.expert[i] = e;
-    const unsigned long long gp = e >= 0 ? tabg[e] : reinterpret_cast<unsigned long long>(a.sh_gate);
-    const unsigned long long up = e >= 0 ? tabu[e] : reinterpret_cast<unsigned long long>(a.sh_up);
-    const unsigned long long dp = e >= 0 ? tabd[e] : reinterpret_cast<unsigned long long>(a.sh_down);
-    a.plan.wdown[i] = (gp && up) ? dp : 0ull;
-  }
-  for (int i = tid; i < (a.has_shared ? T : 0) + nv; i += 256) {
-    a.plan.tok[i] = ptok[i];
-    a.plan.slot[i] = pslot[i];
-  }
-  if (tid == 0) {
-    a.plan.meta[0] = n_groups;
-    a.plan.meta[1] = a.has_shared;
-    a.plan.meta[2] = nv;
-  }
-  if (!(a.logits && ctrl[3])) return;
-
-  // repair: recompute h of every flagged slot with its final expert into
-  // the fix buffer (rare: a probability collision or a degenerate row)
-  quantize_x(a.x, T * nbh, xs, wave, lane);
-  __syncthreads();
-  for (int i = 0; i < T * k; ++i) {
-    if (!ctrl[8 + i]) continue;
-    const int t = i / k, s = i - t * k;
-    const int e = ridx[i];
-    const sg_block_q4k* wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
-    const sg_block_q4k* wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
-    const bool present = wg != nullptr && wu != nullptr;
-    for (int r0 = wave * rpw; r0 < a.n_ff; r0 += 4 * rpw) {
-      const int n = min(rpw, a.n_ff - r0);
-      wait_lds();
-      if (present) dma_gateup(wg, wu, r0, n, nbh, buf, lane);
-      gateup_wave(present, r0, n, nbh, lpr, buf, xs,
-                  [&](int, int& tt_, int& sl_) { tt_ = t; sl_ = s; }, 1, stride, a.n_ff,
-                  a.plan.hfix, lane);
-    }
-  }
+template <int EPT>
+__global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
+  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
+  front_body<EPT>(a, blockIdx.x, blockIdx.y, wbuf, dyn);
 }
 
 // ---- back kernel ------------------------------------------------------------------------
 // One workgroup per chunk of `rows` output rows (hidden/rows >= 256 where the
 // shape allows).  A wave packs `gpw` groups side by side - lane = (group,
 // row, super-block) - and streams their down rows for the chunk into its LDS
-// buffer while all four waves quantize every entry's h row to Q8_K in LDS.
-// The slot outputs of the chunk go to LDS; then the workgroup combines
+// buffer while all four waves quantize every (token, slot) h row to Q8_K in
+// LDS (h was loaded at kernel start, beside the plan).  The slot outputs of
+// the chunk go to LDS; then the workgroup combines
 // out = residual + sum_kk fma(w_kk, y_kk) in slot order.
 struct BackLds {
-  int hq, ys, off, wdown, tok, slot, wt, ok, fix, meta, total;
+  int hq, ys, off, wdown, tok, slot, wt, ok, meta, total;
 };
 
 __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, int gmax,
@@ -785,7 +956,7 @@ __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, in
     o += words;
     return at;
   };
-  L.hq = take(emax * nbf * kXStride);
+  L.hq = take(T * (k + 1) * nbf * kXStride);
   L.ys = take(T * (k + 1) * rows);
   L.off = take(gmax + 1);
   L.wdown = take(gmax * 2);
@@ -793,53 +964,36 @@ __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, in
   L.slot = take(emax);
   L.wt = take(T * (k + 1));
   L.ok = take(T * (k + 1));
-  L.fix = take(T * (k + 1));
   L.meta = take(4);
   L.total = o;
   return L;
 }
 
-__global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
-  __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
-  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
+// The down rows, Q8_K of h and combine of one chunk of `rows` output rows,
+// with the plan in LDS (off, wdown, tok, slot, wt, ok, meta).  before_h()
+// runs after the first down rows are issued and before h is read;
+// hblock(pass_first, u, e, v) yields the lane's 4 values of h block e.
+template <typename BeforeH, typename HBlock>
+__device__ void back_core(const LayerArgs& a, const BackLds& L, uint32_t* bd,
+                          uint32_t (*wbuf)[64 * 36], int row0, int nr, float res0,
+                          BeforeH before_h, HBlock hblock) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, stride = k + 1;
   const int nbf = a.n_ff / kQK;
   const int rows = a.back_rows, lrow = a.back_lrow;
   const int gpw = 64 / (rows * lrow);  // groups per wave per pass
-  const BackLds L = back_lds(T, k, a.n_ff, rows, a.gmax, a.emax);
-  uint32_t* hq = dyn + L.hq;
-  float* ys = reinterpret_cast<float*>(dyn + L.ys);
-  int* off = reinterpret_cast<int*>(dyn + L.off);
-  unsigned long long* wdown = reinterpret_cast<unsigned long long*>(dyn + L.wdown);
-  int* tok = reinterpret_cast<int*>(dyn + L.tok);
-  int* slot = reinterpret_cast<int*>(dyn + L.slot);
-  float* wt = reinterpret_cast<float*>(dyn + L.wt);
-  int* okf = reinterpret_cast<int*>(dyn + L.ok);
-  int* fix = reinterpret_cast<int*>(dyn + L.fix);
-  int* meta = reinterpret_cast<int*>(dyn + L.meta);
-
-  // the plan, routing weights and repair flags (one round of loads)
-  if (tid < 2) meta[tid] = a.plan.meta[tid];
-  for (int i = tid; i <= a.gmax; i += 256) off[i] = a.plan.off[i];
-  for (int i = tid; i < a.gmax; i += 256) wdown[i] = a.plan.wdown[i];
-  for (int i = tid; i < a.emax; i += 256) {
-    tok[i] = a.plan.tok[i];
-    slot[i] = a.plan.slot[i];
-  }
-  for (int i = tid; i < T * stride; i += 256) {
-    wt[i] = a.weight[i];
-    fix[i] = a.plan.fix[i];
-    const int kk = i % stride;
-    const int ee = a.idx[i];
-    okf[i] = kk < k ? (ee >= 0 && ee < a.n_expert) : -1;  // -1: shared slot
-  }
-  for (int i = tid; i < T * stride * rows; i += 256) ys[i] = 0.f;
-  __syncthreads();
+  uint32_t* hq = bd + L.hq;
+  float* ys = reinterpret_cast<float*>(bd + L.ys);
+  const int* off = reinterpret_cast<const int*>(bd + L.off);
+  const unsigned long long* wdown = reinterpret_cast<const unsigned long long*>(bd + L.wdown);
+  const int* tok = reinterpret_cast<const int*>(bd + L.tok);
+  const int* slot = reinterpret_cast<const int*>(bd + L.slot);
+  const float* wt = reinterpret_cast<const float*>(bd + L.wt);
+  const int* okf = reinterpret_cast<const int*>(bd + L.ok);
+  const int* meta = reinterpret_cast<const int*>(bd + L.meta);
+  const int nq = T * stride * nbf;
+  const int n_out = T * nr;
   const int G = __builtin_amdgcn_readfirstlane(meta[0]);
-  const int n_ent = __builtin_amdgcn_readfirstlane(off[G]);
-  const int row0 = blockIdx.x * rows;
-  const int nr = max(0, min(rows, a.hidden - row0));
   const int gwords = rows * nbf * 36;  // one group's rows in the buffer
   uint32_t* buf = wbuf[wave];
   const int q = lane / (rows * lrow);  // this lane's group within the wave
@@ -856,8 +1010,8 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
         dma_chunks([&](int c) { return src + 16 * c; }, nr * nbf * 9, buf + qq * gwords, lane);
       }
     }
-    if (gb == 0) {  // Q8_K of every entry's h row, by all waves, while the rows stream in
-      const int nq = n_ent * nbf;
+    if (gb == 0) {  // Q8_K of every (token, slot) h row while the rows stream in
+      before_h();
       for (int e0 = wave; e0 < nq; e0 += 16) {
         float v[4][4];
         uint32_t* dst[4];
@@ -865,18 +1019,13 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int e = e0 + 4 * u < nq ? e0 + 4 * u : e0;
-          const int j = e / nbf, b = e - j * nbf;
-          const int hs = tok[j] * stride + slot[j];
-          const float* hp = (fix[hs] ? a.plan.hfix : a.h) + static_cast<long long>(hs) * a.n_ff +
-                            b * kQK + 4 * lane;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[u][i] = hp[i];
+          hblock(e0 == wave, u, e, v[u]);
           dst[u] = hq + e * kXStride;
           n += e0 + 4 * u < nq;
         }
         quantize_n_lds<4>(v, dst, n, lane);
       }
-      __syncthreads();
+      bar();
     }
     wait_vm();
     const int gq = gb + wave * gpw + q;
@@ -895,26 +1044,26 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
     for (int ji = 0; ji < cnt; ++ji) {
       const int j = jb + ji;
       const bool ok = j < je;
+      const int hs = ok ? tok[j] * stride + slot[j] : 0;
       float s = 0.f;
       if (live && ok) {
         int32_t xr[64], ip[8];
         float xd, bsf[8];
-        load_x_regs(hq + (j * nbf + blk) * kXStride, xr, xd, bsf);
+        load_x_regs(hq + (hs * nbf + blk) * kXStride, xr, xd, bsf);
         subblock_dots(w36 + 4, xr, ip);
         s = block_sum(w36[0], sm8, ip, xd, bsf);
       }
       const float acc = row_sum_last(s, blk, nbf);
-      if (ok && blk == nbf - 1 && rr < nr)
-        ys[(tok[j] * stride + slot[j]) * rows + rr] = present ? acc : 0.f;
+      if (ok && blk == nbf - 1 && rr < nr) ys[hs * rows + rr] = present ? acc : 0.f;
     }
     wait_lds();
   }
-  __syncthreads();
+  bar();
   const int has_shared = meta[1];
-  for (int qo = tid; qo < T * nr; qo += 256) {
+  for (int qo = tid; qo < n_out; qo += 256) {
     const int t = qo / nr, r = qo - t * nr;
     const long long o = static_cast<long long>(t) * a.hidden + row0 + r;
-    float acc = a.residual ? a.residual[o] : 0.f;
+    float acc = a.residual ? (qo == tid ? res0 : a.residual[o]) : 0.f;
     for (int k0 = 0; k0 <= k; k0 += 8) {  // gather 8 slots, then the ordered fma chain
       float yv[8], wv[8];
 #pragma unroll
@@ -931,6 +1080,72 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
     }
     a.out[o] = acc;
   }
+}
+
+// residual of the first combine pass (qo = tid), loaded early
+__device__ __forceinline__ float residual_pre(const LayerArgs& a, int row0, int nr) {
+  const int tid = threadIdx.x;
+  if (!a.residual || tid >= a.T * nr) return 0.f;
+  const int t = tid / nr, r = tid - t * nr;
+  return a.residual[static_cast<long long>(t) * a.hidden + row0 + r];
+}
+
+__global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
+  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = a.T, k = a.k, stride = k + 1;
+  const int nbf = a.n_ff / kQK;
+  const int rows = a.back_rows;
+  const BackLds L = back_lds(T, k, a.n_ff, rows, a.gmax, a.emax);
+  int* off = reinterpret_cast<int*>(dyn + L.off);
+  unsigned long long* wdown = reinterpret_cast<unsigned long long*>(dyn + L.wdown);
+  int* tok = reinterpret_cast<int*>(dyn + L.tok);
+  int* slot = reinterpret_cast<int*>(dyn + L.slot);
+  float* wt = reinterpret_cast<float*>(dyn + L.wt);
+  int* okf = reinterpret_cast<int*>(dyn + L.ok);
+  int* meta = reinterpret_cast<int*>(dyn + L.meta);
+  float* ys = reinterpret_cast<float*>(dyn + L.ys);
+  const int row0 = blockIdx.x * rows;
+  const int nr = max(0, min(rows, a.hidden - row0));
+
+  // loads that do not depend on the plan: this wave's first pass of h
+  // blocks (every (token, slot) row, 4 blocks per wave) and the residual
+  const int nq = T * stride * nbf;
+  float hpre[4][4];
+  if (wave < nq) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = wave + 4 * u < nq ? wave + 4 * u : wave;
+      const float* hp = a.h + static_cast<long long>(e) * kQK + 4 * lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hpre[u][i] = hp[i];
+    }
+  }
+  const float res0 = residual_pre(a, row0, nr);
+
+  // the plan and routing weights (one round of loads)
+  if (tid < 2) meta[tid] = a.plan.meta[tid];
+  for (int i = tid; i <= a.gmax; i += 256) off[i] = a.plan.off[i];
+  for (int i = tid; i < a.gmax; i += 256) wdown[i] = a.plan.wdown[i];
+  for (int i = tid; i < a.emax; i += 256) {
+    tok[i] = a.plan.tok[i];
+    slot[i] = a.plan.slot[i];
+  }
+  for (int i = tid; i < T * stride; i += 256) {
+    wt[i] = a.weight[i];
+    const int kk = i % stride;
+    const int ee = a.idx[i];
+    okf[i] = kk < k ? (ee >= 0 && ee < a.n_expert) : -1;  // -1: shared slot
+  }
+  for (int i = tid; i < T * stride * rows; i += 256) ys[i] = 0.f;
+  bar();
+  back_core(a, L, dyn, wbuf, row0, nr, res0, [] {},
+            [&](bool first, int u, int e, float* v) {
+              const float* hp = a.h + static_cast<long long>(e) * kQK + 4 * lane;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) v[i] = first ? hpre[u][i] : hp[i];
+            });
 }
 
 static void back_geometry(int hidden, int n_ff, int& rows, int& lrow) {
@@ -978,12 +1193,12 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   if (k <= 0 || k > kLMaxK || n_expert < k || n_expert > kLMaxExperts)
     return set_error(SG_ERR_GEOMETRY, "%s: k=%d (<=%d) n_expert=%d (k..%d)", nm, k, kLMaxK,
                      n_expert, kLMaxExperts);
+  int rows = 1, lrow = 64;
+  back_geometry(hidden, n_ff, rows, lrow);
   const LayerWs ws = layer_ws(n_tokens, n_ff, n_expert, k);
   if (workspace_bytes < ws.total)
     return set_error(SG_ERR_INVALID_ARGUMENT, "%s: workspace %zu < %zu bytes", nm,
                      workspace_bytes, ws.total);
-  int rows = 1, lrow = 64;
-  back_geometry(hidden, n_ff, rows, lrow);
   const size_t lds_f =
       static_cast<size_t>(front_lds(n_tokens, hidden / kQK, n_expert, k, true).total) * 4;
   const size_t lds_b =
@@ -1008,9 +1223,7 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   a.plan = LayerPlan{reinterpret_cast<int*>(base + ws.meta), reinterpret_cast<int*>(base + ws.off),
                      reinterpret_cast<int*>(base + ws.expert),
                      reinterpret_cast<int*>(base + ws.tok), reinterpret_cast<int*>(base + ws.slot),
-                     reinterpret_cast<unsigned long long*>(base + ws.wdown),
-                     reinterpret_cast<int*>(base + ws.fix),
-                     reinterpret_cast<float*>(base + ws.hfix)};
+                     reinterpret_cast<unsigned long long*>(base + ws.wdown)};
   a.h = reinterpret_cast<float*>(base + ws.h);
   a.T = n_tokens;
   a.hidden = hidden;
@@ -1024,9 +1237,9 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   a.back_rows = rows;
   a.back_lrow = lrow;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rows_wg = 4 * (32 / pow2_ceil(hidden / kQK));
+  const FrontLds fl = front_lds(n_tokens, hidden / kQK, n_expert, k, true);
   if (stages & 1) {
-    const int rows_wg = 4 * (32 / pow2_ceil(hidden / kQK));
-    const FrontLds fl = front_lds(n_tokens, hidden / kQK, n_expert, k, true);
     // y < gmax: compute workgroups of group y; y == gmax: the publisher
     const dim3 grid((n_ff + rows_wg - 1) / rows_wg, ws.gmax + 1);
     if (fl.ept <= 1)

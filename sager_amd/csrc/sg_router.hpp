@@ -26,13 +26,13 @@ __device__ __forceinline__ int sel_idx(uint64_t key) {
 // inside the group), then the top m of those candidates.  Results in
 // top[0..m) in selection order (0 = missing).  cand holds ceil(n/64)*m keys.
 // Every thread of the workgroup must call this together: it contains three
-// workgroup barriers.
+// barriers.
 __device__ void team_top_m(const uint64_t* keys, int n, int m, uint64_t* cand, uint64_t* top,
                            int tt, int nthr) {
   const int ng = (n + 63) >> 6;
   for (int i = tt; i < ng * m; i += nthr) cand[i] = 0;
   for (int i = tt; i < m; i += nthr) top[i] = 0;
-  __syncthreads();
+  bar();
   for (int i = tt; i < n; i += nthr) {
     const uint64_t ki = keys[i];
     const int g0 = i & ~63, g1 = min(n, g0 + 64);
@@ -40,7 +40,7 @@ __device__ void team_top_m(const uint64_t* keys, int n, int m, uint64_t* cand, u
     for (int j = g0; j < g1; ++j) r += keys[j] > ki;
     if (r < m && ki != 0) cand[(g0 >> 6) * m + r] = ki;
   }
-  __syncthreads();
+  bar();
   const int nc = ng * m;
   for (int c = tt; c < nc; c += nthr) {
     const uint64_t kc = cand[c];
@@ -49,7 +49,7 @@ __device__ void team_top_m(const uint64_t* keys, int n, int m, uint64_t* cand, u
     for (int d = 0; d < nc; ++d) r += cand[d] > kc;
     if (r < m) top[r] = kc;
   }
-  __syncthreads();
+  bar();
 }
 
 // Maximum of v over a team of nw waves (fmaxf semantics); `red` holds nw
@@ -57,7 +57,7 @@ __device__ void team_top_m(const uint64_t* keys, int n, int m, uint64_t* cand, u
 __device__ __forceinline__ float team_max(float v, float* red, int wave_in_team, int nw, int lane) {
   v = wave_max_dpp(v);
   if (lane == 0) red[wave_in_team] = v;
-  __syncthreads();
+  bar();
   float m = red[0];
   for (int w = 1; w < nw; ++w) m = fmaxf(m, red[w]);
   return m;

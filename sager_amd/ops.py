@@ -128,7 +128,8 @@ def moe_combine_batched(expert_y, weight, residual=None, out=None):
 class MoeLayer:
     """One MoE layer's device-side pointer tables and workspace; ``forward``
     is the device-path dispatch of Session::moe_dispatch_device
-    (session.cpp:2482-3030) as one fused call."""
+    (session.cpp:2482-3030) as one call.  ``stages``: 3 = front and back (the
+    whole layer), 1 / 2 = one of the two launches."""
 
     def __init__(self, tab_gate, tab_up, tab_down, shared=None, hidden=2048, n_ff=512,
                  n_expert=256, k=8, max_tokens=1, shared_w=1.0):
@@ -138,7 +139,6 @@ class MoeLayer:
         self.shared_w = float(shared_w)
         self.max_tokens = max_tokens
         nbytes = load().sg_moe_layer_workspace_bytes(max_tokens, hidden, n_ff, n_expert, k)
-        # zero-filled once: the layer keeps its per-group arrival counters at zero
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=tab_gate.device)
 
     def forward(self, x, logits=None, residual=None, out=None, idx=None, weight=None,

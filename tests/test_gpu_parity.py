@@ -219,6 +219,23 @@ def test_moe_layer_small_pool(T, sigma):
     np.testing.assert_array_equal(host(out2), host(out))
 
 
+def test_moe_layer_workspace_shared_by_sizes():
+    """One workspace, calls of 4, 1, 3, 1 and 4 tokens in a row, the last
+    split into its two launches: every call matches the oracle."""
+    rng = np.random.default_rng(4242)
+    H, F, E, K = 1024, 512, 32, 8
+    g, u, d = _expert_pool(rng, E + 1, H, F)
+    shared = (g.pop(), u.pop(), d.pop())
+    layer = _layer(g, u, d, shared, H, F, K, 4)
+    for T, stages in [(4, 3), (1, 3), (3, 3), (1, 3), (4, None)]:
+        x = rng.normal(0, 1, (T, H)).astype(np.float32)
+        lg = rng.normal(0, 1.5, (T, E)).astype(np.float32)
+        out, idx, w = layer.forward(dev(x), dev(lg))
+        ref, ri, rw = orc.moe_layer(g, u, d, shared, x, logits=lg, hidden=H, n_ff=F, k=K)
+        np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K])
+        np.testing.assert_array_equal(host(out).view(np.uint32), ref.view(np.uint32))
+
+
 def test_moe_layer_config2_full_pool():
     """Config 2: 256 experts x (gate, up [512x2048], down [2048x512]) resident,
     top-8 from N(0,1) logits, shared expert, residual 0."""
