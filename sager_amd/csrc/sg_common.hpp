@@ -130,6 +130,24 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+// Wait until at most n (0..9) of this wave's vector memory operations are
+// outstanding: with two weight streams in flight, the older has landed once
+// only the newer one's instructions remain.
+__device__ __forceinline__ void wait_vm_n(int n) {
+  switch (n) {
+    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;  // vmcnt(9)
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 // Wait for this wave's LDS reads, so the buffer can be refilled.
 __device__ __forceinline__ void wait_lds() {
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
