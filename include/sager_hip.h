@@ -190,6 +190,46 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate,
                         int n_ff, int n_expert, int k, float shared_w,
                         int stages, void* stream);
 
+/* ---- prefill chunk (many tokens): device plan + int8-MFMA grouped GEMMs -- */
+
+/* Expert-major plan of n_rows tokens x k routes, on the device, in one
+ * launch.  Replaces cuda::moe_dispatch_scan (cuda_ops.hpp:219-222,
+ * moe.cu:366-444) with the same outputs - off[E+1] row prefix, toff[E+1]
+ * tile prefix (tok_per rows per tile), meta = {R, tiles, bad routes},
+ * gslot[n_rows*k] (-1 for an invalid id), grows[R] (the token of each
+ * grouped position) - and the same bounds-kill (an invalid id zeroes its
+ * row of `weight`, stride k+1).  Unlike the reference, the order inside an
+ * expert is deterministic: token order, then slot.  No mailbox: absent
+ * experts are handled by the grouped kernels themselves.  off needs E+2
+ * entries (off[E+1] = off[E]).  n_expert <= 1024 and
+ * n_expert * ceil(n_rows/32) <= 37,888 (the plan is built in LDS). */
+int sg_moe_dispatch_scan(const int* idx, float* weight, int* gslot, int* grows,
+                         int* off, int* toff, int* meta, int n_rows, int k,
+                         int n_expert, int tok_per, void* stream);
+
+/* A whole MoE layer for a prefill chunk of n_tokens tokens (up to the scan
+ * limit above), same arguments and semantics as sg_moe_layer: Q8_K(x),
+ * router top-k (logits != NULL) or caller routing, the device plan, gate/up
+ * + SiLU and down as grouped int8-MFMA contractions over every routed expert
+ * (the shared expert as one more group), combine in slot order.  Replaces
+ * the reference's prefill MoE (session.cpp:2643-2840: the TC dequant+GEMM
+ * path and its dp4a grouped twin, cuda_ops.hpp:190-250).  Sub-block dots are
+ * exact int32 (one MFMA per Q4_K sub-block); the fp32 epilogue is the
+ * integer-first super-block order (t = fma(d, sum sc*ip, -(dmin * sum
+ * mn*bsum)), acc = fma(xd, t, acc)).  workspace: at least
+ * sg_moe_prefill_workspace_bytes(). */
+size_t sg_moe_prefill_workspace_bytes(int n_tokens, int hidden, int n_ff,
+                                      int n_expert, int k);
+int sg_moe_prefill(const sg_block_q4k* const* tab_gate,
+                   const sg_block_q4k* const* tab_up,
+                   const sg_block_q4k* const* tab_down,
+                   const sg_block_q4k* sh_gate, const sg_block_q4k* sh_up,
+                   const sg_block_q4k* sh_down, const float* x,
+                   const float* logits, const float* residual, float* out,
+                   int* idx, float* weight, void* workspace,
+                   size_t workspace_bytes, int n_tokens, int hidden, int n_ff,
+                   int n_expert, int k, float shared_w, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -68,6 +68,14 @@ def gemv(w, xq, n_rows, k, n_tokens=1):
     return y
 
 
+def gemv_int(w, xq, n_rows, k, n_tokens=1):
+    """The GEMV with the prefill path's integer-first super-block epilogue."""
+    w, xq = _c(w, np.uint8), _c(xq, np.uint8)
+    y = np.zeros((n_tokens, n_rows), np.float32)
+    lib().orc_gemv_q4k_q8_int(P(w), P(xq), P(y), n_rows, k, n_tokens)
+    return y
+
+
 def dequant(w, n):
     w = _c(w, np.uint8)
     out = np.zeros(n, np.float32)
@@ -118,9 +126,11 @@ def _ptr_table(mats):
 
 
 def moe_layer(gate, up, down, shared, x, logits=None, idx=None, weight=None, residual=None,
-              hidden=2048, n_ff=512, k=8, shared_w=1.0, n_threads=1):
+              hidden=2048, n_ff=512, k=8, shared_w=1.0, n_threads=1, prefill=False):
     """gate/up/down: lists of per-expert uint8 arrays (None = absent);
-    shared: (g, u, d) or None.  Returns out [T, hidden], idx, weight."""
+    shared: (g, u, d) or None.  Returns out [T, hidden], idx, weight.
+    prefill=True: every GEMV in the integer-first epilogue order of the
+    MFMA prefill path (orc_moe_prefill)."""
     x = _c(np.atleast_2d(x), np.float32)
     T = x.shape[0]
     n_expert = len(gate)
@@ -135,7 +145,21 @@ def moe_layer(gate, up, down, shared, x, logits=None, idx=None, weight=None, res
         sg, su, sd = (m.ctypes.data for m in shared)
     out = np.zeros((T, hidden), np.float32)
     res = _c(residual, np.float32) if residual is not None else None
-    if logits is not None:
+    if prefill:
+        if logits is not None:
+            logits = _c(np.atleast_2d(logits), np.float32)
+            idx = np.full((T, k + 1), -1, np.int32)
+            weight = np.zeros((T, k + 1), np.float32)
+        else:
+            idx, weight = _c(idx, np.int32), _c(weight, np.float32).copy()
+        lib().orc_moe_prefill(tg, tu, td, ctypes.c_void_p(sg), ctypes.c_void_p(su),
+                              ctypes.c_void_p(sd), P(x),
+                              P(logits) if logits is not None else None,
+                              P(res) if res is not None else None, P(out), P(idx), P(weight), T,
+                              hidden, n_ff, n_expert, k, ctypes.c_float(shared_w), n_threads)
+        bad = ((idx[:, :k] < 0) | (idx[:, :k] >= n_expert)).any(axis=1)
+        weight[bad] = 0.0
+    elif logits is not None:
         logits = _c(np.atleast_2d(logits), np.float32)
         idx = np.full((T, k + 1), -1, np.int32)
         weight = np.zeros((T, k + 1), np.float32)

@@ -220,6 +220,44 @@ void orc_gemv_q4k_q8(const void* w, const void* xq, float* y, int n_rows, int k,
       y[t * n_rows + r] = row_dot(W + r * nb, X + t * nb, nb);
 }
 
+/* ---- fp32 GEMV, integer-first super-block epilogue (prefill path) -------
+ * The reference's grouped prefill kernels compute the same exact integer
+ * sub-block dots as every other path (q4_k.cu:733-741, dp4a_subblock) and
+ * differ from the AVX2 path only in fp32 order.  The MFMA prefill kernels
+ * here fix one order that maps onto integer matrix cores: per super-block
+ * the exact integers I = sum_s sc_s * ip_s and M = sum_s mn_s * bsum_s
+ * (|I| < 2^25, |M| < 2^21), then
+ *   t = fma(d, (float)I, -(dmin * (float)M));  acc = fma(xd, t, acc)
+ * over the super-blocks in order.  Same quantities as q4_avx2.cpp:30-39 and
+ * q4_k.cpp:195-203; within ~1e-6 relative of the AVX2 order. */
+static float row_dot_int(const orc_q4k* row, const orc_q8k* x, int nb) {
+  float acc = 0.f;
+  for (int b = 0; b < nb; ++b) {
+    const orc_q4k* blk = row + b;
+    int32_t I = 0, M = 0;
+    for (int s = 0; s < 8; ++s) {
+      uint8_t sc, mn;
+      orc_get_scale_min(s, blk->scales, &sc, &mn);
+      I += (int32_t)sc * sub_dot(blk->qs + (s >> 1) * 32, x[b].qs + s * 32, s & 1);
+      M += (int32_t)mn * (int32_t)x[b].bsums[s];
+    }
+    const float t = fmaf(orc_half_to_float(blk->d), (float)I,
+                         -(orc_half_to_float(blk->dmin) * (float)M));
+    acc = fmaf(x[b].d, t, acc);
+  }
+  return acc;
+}
+
+void orc_gemv_q4k_q8_int(const void* w, const void* xq, float* y, int n_rows, int k,
+                         int n_tokens) {
+  const int nb = k / 256;
+  const orc_q4k* W = (const orc_q4k*)w;
+  const orc_q8k* X = (const orc_q8k*)xq;
+  for (int64_t t = 0; t < n_tokens; ++t)
+    for (int64_t r = 0; r < n_rows; ++r)
+      y[t * n_rows + r] = row_dot_int(W + r * nb, X + t * nb, nb);
+}
+
 /* ---- exp (double evaluation, one final rounding) ----------------------- */
 
 float orc_expf(float xf) {
@@ -260,16 +298,18 @@ void orc_silu_mul(const float* g, const float* u, float* h, int n) {
 /* ---- expert FFN (q4_avx2.cpp:175-196) ---------------------------------- */
 
 static void ffn_q8(const void* wg, const void* wu, const void* wd,
-                   const orc_q8k* xq, float* y, int hidden, int n_ff) {
+                   const orc_q8k* xq, float* y, int hidden, int n_ff, int int_first) {
   float* g = (float*)malloc(sizeof(float) * 3 * (size_t)n_ff);
   float* u = g + n_ff;
   float* h = u + n_ff;
   orc_q8k* hq = (orc_q8k*)malloc(sizeof(orc_q8k) * (size_t)(n_ff / 256));
-  orc_gemv_q4k_q8(wg, xq, g, n_ff, hidden, 1);
-  orc_gemv_q4k_q8(wu, xq, u, n_ff, hidden, 1);
+  void (*gemv)(const void*, const void*, float*, int, int, int) =
+      int_first ? orc_gemv_q4k_q8_int : orc_gemv_q4k_q8;
+  gemv(wg, xq, g, n_ff, hidden, 1);
+  gemv(wu, xq, u, n_ff, hidden, 1);
   orc_silu_mul(g, u, h, n_ff);
   orc_quantize_q8_k(h, hq, n_ff, 1);
-  orc_gemv_q4k_q8(wd, hq, y, hidden, n_ff, 1);
+  gemv(wd, hq, y, hidden, n_ff, 1);
   free(hq);
   free(g);
 }
@@ -278,7 +318,7 @@ void orc_expert_ffn(const void* wg, const void* wu, const void* wd,
                     const float* x, float* y, int hidden, int n_ff) {
   orc_q8k* xq = (orc_q8k*)malloc(sizeof(orc_q8k) * (size_t)(hidden / 256));
   orc_quantize_q8_k(x, xq, hidden, 1);
-  ffn_q8(wg, wu, wd, xq, y, hidden, n_ff);
+  ffn_q8(wg, wu, wd, xq, y, hidden, n_ff, 0);
   free(xq);
 }
 
@@ -340,7 +380,7 @@ typedef struct {
   const void *wg, *wu, *wd;
   const orc_q8k* xq;
   float* y;
-  int hidden, n_ff;
+  int hidden, n_ff, int_first;
 } ffn_job;
 
 typedef struct {
@@ -360,7 +400,7 @@ static void run_job(const ffn_job* j) {
     memset(j->y, 0, sizeof(float) * (size_t)j->hidden);
     return;
   }
-  ffn_q8(j->wg, j->wu, j->wd, j->xq, j->y, j->hidden, j->n_ff);
+  ffn_q8(j->wg, j->wu, j->wd, j->xq, j->y, j->hidden, j->n_ff, j->int_first);
 }
 
 static void* worker(void* arg) {
@@ -404,14 +444,12 @@ static void pool_run(ffn_job* jobs, int n_jobs, int n_threads) {
 
 /* ---- MoE layer (session.cpp:2482-3030 stage order) --------------------- */
 
-void orc_moe_layer_routed(const void* const* tab_gate,
-                          const void* const* tab_up,
-                          const void* const* tab_down, const void* sh_gate,
-                          const void* sh_up, const void* sh_down,
-                          const float* x, const int* idx, const float* weight,
-                          const float* residual, float* out, int n_tokens,
-                          int hidden, int n_ff, int n_expert, int k,
-                          int n_threads) {
+static void moe_layer_routed(const void* const* tab_gate, const void* const* tab_up,
+                             const void* const* tab_down, const void* sh_gate,
+                             const void* sh_up, const void* sh_down, const float* x,
+                             const int* idx, const float* weight, const float* residual,
+                             float* out, int n_tokens, int hidden, int n_ff, int n_expert,
+                             int k, int n_threads, int int_first) {
   const int nbh = hidden / 256;
   const int slots = k + 1;
   orc_q8k* xq = (orc_q8k*)malloc(sizeof(orc_q8k) * (size_t)nbh * n_tokens);
@@ -428,6 +466,7 @@ void orc_moe_layer_routed(const void* const* tab_gate,
       j->y = ys + ((size_t)t * slots + kk) * hidden;
       j->hidden = hidden;
       j->n_ff = n_ff;
+      j->int_first = int_first;
       if (kk < k) {
         const int e = idx[t * slots + kk];
         if (e < 0 || e >= n_expert) {
@@ -451,6 +490,30 @@ void orc_moe_layer_routed(const void* const* tab_gate,
   free(jobs);
   free(ys);
   free(xq);
+}
+
+void orc_moe_layer_routed(const void* const* tab_gate, const void* const* tab_up,
+                          const void* const* tab_down, const void* sh_gate, const void* sh_up,
+                          const void* sh_down, const float* x, const int* idx,
+                          const float* weight, const float* residual, float* out,
+                          int n_tokens, int hidden, int n_ff, int n_expert, int k,
+                          int n_threads) {
+  moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, x, idx, weight,
+                   residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads, 0);
+}
+
+/* The prefill layer: the same routing, experts and combine as
+ * orc_moe_layer, with every GEMV in the integer-first epilogue order of
+ * orc_gemv_q4k_q8_int (what the MFMA prefill kernels compute). */
+void orc_moe_prefill(const void* const* tab_gate, const void* const* tab_up,
+                     const void* const* tab_down, const void* sh_gate, const void* sh_up,
+                     const void* sh_down, const float* x, const float* logits,
+                     const float* residual, float* out, int* idx, float* weight, int n_tokens,
+                     int hidden, int n_ff, int n_expert, int k, float shared_w,
+                     int n_threads) {
+  if (logits) orc_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w);
+  moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, x, idx, weight,
+                   residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads, 1);
 }
 
 void orc_moe_layer(const void* const* tab_gate, const void* const* tab_up,

@@ -47,6 +47,12 @@ void orc_subblock_dots(const void* w, const void* xq, int32_t* dots, int n_rows,
 
 /* y[tok][r] = W[r] . xq[tok], fp32 in the AVX2 order (q4_avx2.cpp:124-145):
  * per super-block sum_s xd*(sd*ip - sm*bsum), then acc += block sum. */
+/* Same GEMV with the integer-first super-block epilogue of the prefill
+ * path: t = fma(d, (float)sum_s sc*ip, -(dmin * (float)sum_s mn*bsum)),
+ * acc = fma(xd, t, acc) per super-block. */
+void orc_gemv_q4k_q8_int(const void* w, const void* xq, float* y, int n_rows, int k,
+                         int n_tokens);
+
 void orc_gemv_q4k_q8(const void* w, const void* xq, float* y, int n_rows, int k,
                      int n_tokens);
 
@@ -84,6 +90,16 @@ void orc_moe_layer(const void* const* tab_gate, const void* const* tab_up,
                    const float* logits, const float* residual, float* out,
                    int* idx, float* weight, int n_tokens, int hidden, int n_ff,
                    int n_expert, int k, float shared_w, int n_threads);
+
+/* Prefill layer: orc_moe_layer's routing/experts/combine with every GEMV
+ * in the integer-first order (orc_gemv_q4k_q8_int).  logits may be NULL
+ * (idx/weight then inputs). */
+void orc_moe_prefill(const void* const* tab_gate, const void* const* tab_up,
+                     const void* const* tab_down, const void* sh_gate, const void* sh_up,
+                     const void* sh_down, const float* x, const float* logits,
+                     const float* residual, float* out, int* idx, float* weight, int n_tokens,
+                     int hidden, int n_ff, int n_expert, int k, float shared_w,
+                     int n_threads);
 
 /* Same as orc_moe_layer but with routing given (idx/weight [n_tokens][k+1]
  * already filled, e.g. sampled routing); no softmax. */

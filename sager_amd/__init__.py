@@ -41,6 +41,10 @@ SIGNATURES = {
                           _VP, _SZ, _I, _I, _I, _I, _I, _F, _VP]),
     "sg_moe_layer_stages": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                  _VP, _SZ, _I, _I, _I, _I, _I, _F, _I, _VP]),
+    "sg_moe_dispatch_scan": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
+    "sg_moe_prefill_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "sg_moe_prefill": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                            _VP, _SZ, _I, _I, _I, _I, _I, _F, _VP]),
 }
 
 

@@ -1,0 +1,499 @@
+// sg_prefill.hip - the multi-token (prefill chunk) MoE layer on gfx950 with
+// int8 matrix cores.
+//
+// Stage order of the reference's grouped device path
+// (Session::moe_dispatch_device, session.cpp:2643-2840):
+//   Q8_K(x) -> router top-k (batched) -> dispatch scan into an expert-major
+//   plan (moe.cu:366-444) -> grouped gate/up + SiLU -> Q8_K(h) -> grouped
+//   down -> combine in slot order (moe.cu:265-280).
+//
+// The grouped contractions run on v_mfma_i32_16x16x32_i8: one MFMA is one
+// Q4_K sub-block (32 weights) for 16 tokens x 16 weight rows, so every
+// int32 sub-block dot is exact.  Per super-block each output keeps
+// I = sum_s sc_s * ip_s and M = sum_s mn_s * bsum_s as exact integers; the
+// fp32 epilogue is t = fma(d, I, -(dmin * M)), acc = fma(xd, t, acc) over
+// the super-blocks in order (the integer-first order; the CPU oracle's
+// orc_gemv_q4k_q8_int is the same arithmetic).
+//
+// Workgroup tile: 64 tokens x 128 weight rows (gate/up: 64 h rows of gate
+// and the same 64 of up; down: 128 output rows), eight waves of 16 tokens x
+// 64 rows each (gate/up: 32 h rows of gate and their up rows, so SiLU pairs
+// meet in one lane), K streamed one super-block at a time through two LDS
+// buffers (weights by global_load_lds, token rows gathered through
+// registers).
+#include "sg_common.hpp"
+
+namespace sg {
+
+// ---- dispatch scan --------------------------------------------------------------
+// One workgroup of 1024 threads.  Pass 1: per-expert route counts and a
+// [expert][token] bitmap in LDS; invalid ids zero their row's weights
+// (bounds-kill, moe.cu:385-396).  The exclusive scans give off/toff/meta.
+// Pass 2 places every route at off[e] + (its rank among the expert's routes
+// in token order) - a popcount over the bitmap - so the plan is
+// deterministic (the reference's atomic placement is not).  A token routed
+// twice to one expert (caller-supplied ids) takes a serial placement.
+// With shared_tail > 0, positions off[E] .. off[E] + shared_tail - 1 are the
+// shared expert's (token t at off[E] + t) and off[E+1] closes them.
+__global__ void __launch_bounds__(1024) dispatch_scan_kernel(
+    const int* __restrict__ idx, float* __restrict__ weight, int* __restrict__ gslot,
+    int* __restrict__ grows, int* __restrict__ off, int* __restrict__ toff,
+    int* __restrict__ meta, int n_rows, int k, int n_expert, int tok_per, int shared_tail) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  __shared__ int s_bad, s_dup, s_total;
+  const int E = n_expert, W = (n_rows + 31) / 32;
+  int* hist = reinterpret_cast<int*>(lds);       // [E]
+  int* offl = hist + E;                          // [E]
+  int* part = offl + E;                          // [1024]
+  uint32_t* bm = reinterpret_cast<uint32_t*>(part + 1024);  // [E][W]
+  const int tid = threadIdx.x, nth = blockDim.x;
+  for (int i = tid; i < E; i += nth) hist[i] = 0;
+  for (int i = tid; i < E * W; i += nth) bm[i] = 0u;
+  if (tid == 0) {
+    s_bad = 0;
+    s_dup = 0;
+  }
+  __syncthreads();
+  const int total = n_rows * k;
+  for (int i = tid; i < total; i += nth) {
+    const int r = i / k, kk = i - r * k;
+    const int e = idx[static_cast<long long>(r) * (k + 1) + kk];
+    if (e < 0 || e >= E) {
+      for (int q = 0; q <= k; ++q) weight[static_cast<long long>(r) * (k + 1) + q] = 0.f;
+      gslot[i] = -1;
+      atomicAdd(&s_bad, 1);
+      continue;
+    }
+    atomicAdd(&hist[e], 1);
+    const uint32_t bit = 1u << (r & 31);
+    if (atomicOr(&bm[e * W + (r >> 5)], bit) & bit) s_dup = 1;
+  }
+  __syncthreads();
+  if (tid == 0) {  // E <= 1024: one thread, in order
+    int acc = 0, tacc = 0;
+    for (int e = 0; e < E; ++e) {
+      off[e] = acc;
+      offl[e] = acc;
+      toff[e] = tacc;
+      acc += hist[e];
+      tacc += (hist[e] + tok_per - 1) / tok_per;
+    }
+    off[E] = acc;
+    toff[E] = tacc;
+    off[E + 1] = acc + shared_tail;
+    meta[0] = acc;
+    meta[1] = tacc;
+    meta[2] = s_bad;
+    s_total = acc;
+  }
+  __syncthreads();
+  if (!s_dup) {
+    const int tpe = max(1, nth / E);  // threads per expert
+    const int e = tid / tpe, q = tid - e * tpe;
+    const int wpt = (W + tpe - 1) / tpe;
+    const int w0 = min(W, q * wpt), w1 = min(W, w0 + wpt);
+    int c = 0;
+    if (e < E)
+      for (int w = w0; w < w1; ++w) c += __popc(bm[e * W + w]);
+    part[tid] = c;
+    __syncthreads();
+    if (e < E) {
+      int pos = offl[e];
+      for (int j = 0; j < q; ++j) pos += part[e * tpe + j];
+      for (int w = w0; w < w1; ++w) {
+        uint32_t bits = bm[e * W + w];
+        while (bits) {
+          const int r = 32 * w + __builtin_ctz(bits);
+          bits &= bits - 1u;
+          int kk = 0;
+          while (kk < k && idx[static_cast<long long>(r) * (k + 1) + kk] != e) ++kk;
+          gslot[r * k + kk] = pos;
+          grows[pos] = r;
+          ++pos;
+        }
+      }
+    }
+  } else if (tid == 0) {  // duplicated ids in a row: serial placement in (token, slot) order
+    for (int e = 0; e < E; ++e) hist[e] = offl[e];
+    for (int i = 0; i < total; ++i) {
+      const int r = i / k, kk = i - r * k;
+      const int e = idx[static_cast<long long>(r) * (k + 1) + kk];
+      if (e < 0 || e >= E) continue;
+      const int pos = hist[e]++;
+      gslot[i] = pos;
+      grows[pos] = r;
+    }
+  }
+  for (int t = tid; t < shared_tail; t += nth) grows[s_total + t] = t;
+}
+
+// ---- grouped int8-MFMA contraction ------------------------------------------------
+constexpr int kTokTile = 64;
+constexpr int kRowsWg = 128;                 // weight rows per workgroup
+constexpr int kWRowWords = 36;               // one 144-B block
+constexpr int kWBufWords = kRowsWg * kWRowWords;   // 18 KB
+constexpr int kXBufWords = kTokTile * 69;          // 17.25 KB, packed Q8_K blocks
+constexpr int kThreads = 512;                 // eight waves
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct GroupedArgs {
+  const sg_block_q4k* const* tab_a;  // gate (gate/up pass) or down
+  const sg_block_q4k* const* tab_b;  // up (gate/up pass)
+  const sg_block_q4k* const* tab_c;  // the third matrix: an expert is absent if any is null
+  const sg_block_q4k* sh_a;          // shared expert (group E)
+  const sg_block_q4k* sh_b;
+  const sg_block_q4k* sh_c;
+  const unsigned char* xq;  // Q8_K rows: x [T][nb] (gate/up) or h [P][nb] (down)
+  const int* off;           // [G+1] position range of each group
+  const int* grows;         // [P] token of each position (gate/up only)
+  float* out;               // h [P][n_out] (gate/up) or y [P][n_out] (down)
+  int nb, n_out, n_expert, n_groups;
+};
+
+__device__ __forceinline__ int sbyte(uint32_t w, int i) { return (w >> (8 * i)) & 0xFF; }
+
+template <bool kGateUp>
+__global__ void __launch_bounds__(kThreads) grouped_mfma_kernel(GroupedArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[2][kWBufWords];
+  __shared__ __attribute__((aligned(16))) uint32_t xbuf[2][kXBufWords];
+  __shared__ int trow[kTokTile];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.y;
+  if (g >= a.n_groups) return;
+  static_assert(kThreads == 512, "eight waves: 4 token blocks x 2 row halves");
+  const int p0 = a.off[g], p1 = a.off[g + 1];
+  if (p0 >= p1) return;
+  const bool shared = g >= a.n_expert;
+  const sg_block_q4k* ma = shared ? a.sh_a : a.tab_a[g];
+  const sg_block_q4k* mb = kGateUp ? (shared ? a.sh_b : a.tab_b[g]) : ma;
+  const sg_block_q4k* mc = shared ? a.sh_c : a.tab_c[g];
+  const int nb = a.nb;
+  const int rows_out = kGateUp ? kRowsWg / 2 : kRowsWg;
+  const int r0 = blockIdx.x * rows_out;
+  const int lr = lane & 15, lq = lane >> 4;  // MFMA: row/column in the tile, K quarter
+  const int tb = wave & 3, rh = wave >> 2;   // the wave's token block and row half
+  // the wave's four row blocks: gate/up -> gate 2rh, 2rh+1 and up 4+2rh, 4+2rh+1
+  // (h rows 32rh .. 32rh+31); down -> 4rh .. 4rh+3
+  auto rblk = [&](int j) { return kGateUp ? (j < 2 ? 2 * rh + j : 4 + 2 * rh + (j - 2)) : 4 * rh + j; };
+
+  if (!ma || !mb || !mc) {  // absent expert: its outputs are zero
+    for (long long p = p0; p < p1; ++p)
+      for (int r = tid; r < rows_out; r += kThreads) a.out[p * a.n_out + r0 + r] = 0.f;
+    return;
+  }
+
+  // weight rows of super-block b into wbuf[s]: gate/up -> 64 gate rows then
+  // the same 64 up rows; down -> 128 rows.  Chunk c (16 B) of row c/9.
+  auto stage_w = [&](int b, int s) {
+    const int c0 = wave * (kRowsWg * 9 / 8);  // 144 chunks per wave
+    dma_chunks(
+        [&](int c) {
+          const int cc = c0 + c;
+          const int row = cc / 9, part = cc - row * 9;
+          const sg_block_q4k* m = (kGateUp && row >= 64) ? mb : ma;
+          const int rr = kGateUp ? (row & 63) : row;
+          const unsigned off = (static_cast<unsigned>(r0 + rr) * nb + b) * kQ4Bytes + 16 * part;
+          return reinterpret_cast<const char*>(m) + off;
+        },
+        kRowsWg * 9 / 8, wbuf[s] + 4 * c0, lane);
+  };
+  // the tile's token blocks of super-block b into xbuf[s], packed 69 words
+  // per token (d, 64 qs words, 4 words of int16 bsums): dword chunk c is
+  // word c % 69 of token c / 69, so lane-consecutive chunks land
+  // LDS-consecutive (global_load_lds_dword)
+  auto stage_x = [&](int b, int s) {
+    for (int c0 = wave * 64; c0 < kTokTile * 69; c0 += kThreads) {
+      const int c = c0 + lane;
+      const int cc = c < kTokTile * 69 ? c : kTokTile * 69 - 1;
+      const int t = cc / 69, w = cc - t * 69;
+      const char* src = reinterpret_cast<const char*>(a.xq) +
+                        static_cast<long long>(trow[t] + b) * kQ8Bytes + 4 * w;
+      if (c0 + 64 <= kTokTile * 69 || c < kTokTile * 69)
+        __builtin_amdgcn_global_load_lds((glb_void_p)src, (lds_void_p)(xbuf[s] + c0), 4, 0, 0);
+    }
+  };
+
+  for (int t0 = p0; t0 < p1; t0 += kTokTile) {
+    const int nt = min(kTokTile, p1 - t0);
+    if (tid < kTokTile) {  // block index of each token row (tokens past nt repeat the first)
+      const int t = tid < nt ? tid : 0;
+      trow[tid] = (kGateUp ? a.grows[t0 + t] : t0 + t) * nb;
+    }
+    bar();
+    float acc[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[j][i] = 0.f;
+
+    stage_w(0, 0);
+    stage_x(0, 0);
+    for (int b = 0; b < nb; ++b) {
+      const int s = b & 1;
+      wait_vm();  // this wave's copies of block b have landed
+      bar();      // ... and every wave's
+      if (b + 1 < nb) {  // the next block streams in while this one computes
+        stage_w(b + 1, s ^ 1);
+        stage_x(b + 1, s ^ 1);
+      }
+      const uint32_t* W = wbuf[s];
+      const uint32_t* X = xbuf[s];
+      // the lane's four output tokens are the MFMA result rows tx .. tx+3;
+      // its weight row in row block j is 16j + lr
+      const int tx = 16 * tb + 4 * lq;
+      int I[4][4], M[4][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) I[j][i] = M[j][i] = 0;
+      const uint32_t* xa = X + (16 * tb + lr) * 69 + 1;  // the lane's A row (qs words)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {  // sub-blocks 0-3 (low scale words), 4-7 (high)
+        uint32_t scw[4], mnw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t* wr = W + (16 * rblk(j) + lr) * kWRowWords;
+          const ScaleMins sm = unpack_scales(wr[1], wr[2], wr[3]);
+          scw[j] = hf ? sm.sc_hi : sm.sc_lo;
+          mnw[j] = hf ? sm.mn_hi : sm.mn_lo;
+        }
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2) {
+          const int gq = 2 * hf + g2;  // sub-blocks 2gq (low nibbles) and 2gq+1 (high)
+          const long a0 = static_cast<long>(xa[16 * gq + 2 * lq]) |
+                          (static_cast<long>(xa[16 * gq + 2 * lq + 1]) << 32);
+          const long a1 = static_cast<long>(xa[16 * gq + 8 + 2 * lq]) |
+                          (static_cast<long>(xa[16 * gq + 8 + 2 * lq + 1]) << 32);
+          int bs0[4], bs1[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {  // bsums of sub-blocks 2gq, 2gq+1: one word
+            const uint32_t bw = X[(tx + i) * 69 + 65 + gq];
+            bs0[i] = static_cast<int16_t>(bw & 0xFFFFu);
+            bs1[i] = static_cast<int16_t>(bw >> 16);
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t* wr = W + (16 * rblk(j) + lr) * kWRowWords + 4 + 8 * gq + 2 * lq;
+            const uint32_t q0 = wr[0], q1 = wr[1];
+            const long b0 = static_cast<long>(q0 & 0x0F0F0F0Fu) |
+                            (static_cast<long>(q1 & 0x0F0F0F0Fu) << 32);
+            const long b1 = static_cast<long>((q0 >> 4) & 0x0F0F0F0Fu) |
+                            (static_cast<long>((q1 >> 4) & 0x0F0F0F0Fu) << 32);
+            const v4i z = {0, 0, 0, 0};
+            const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, z, 0, 0, 0);
+            const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, z, 0, 0, 0);
+            const int sc0 = sbyte(scw[j], 2 * g2), sc1 = sbyte(scw[j], 2 * g2 + 1);
+            const int mn0 = sbyte(mnw[j], 2 * g2), mn1 = sbyte(mnw[j], 2 * g2 + 1);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              I[j][i] += sc0 * c0[i] + sc1 * c1[i];
+              M[j][i] += mn0 * bs0[i] + mn1 * bs1[i];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t dd = W[(16 * rblk(j) + lr) * kWRowWords];
+        const float d = half_bits_to_float(dd & 0xFFFFu);
+        const float dmin = half_bits_to_float(dd >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float xd = __builtin_bit_cast(float, X[(tx + i) * 69]);
+          const float t = __builtin_fmaf(d, static_cast<float>(I[j][i]),
+                                         -(dmin * static_cast<float>(M[j][i])));
+          acc[j][i] = __builtin_fmaf(xd, t, acc[j][i]);
+        }
+      }
+    }
+    // outputs of the lane's four tokens
+    const int tx = 16 * tb + 4 * lq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (tx + i >= nt) continue;
+      float* orow = a.out + static_cast<long long>(t0 + tx + i) * a.n_out + r0;
+      if (kGateUp) {  // gate blocks j = 0, 1 pair with up blocks j = 2, 3
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          orow[16 * (2 * rh + j) + lr] = silu_mul(acc[j][i], acc[j + 2][i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) orow[16 * (4 * rh + j) + lr] = acc[j][i];
+      }
+    }
+    bar();  // the next token tile reuses both buffers and trow
+  }
+}
+
+// out[t] = residual[t] + sum_kk fma(w[t][kk], y[pos(t, kk)]) in slot order;
+// pos(t, k) = the shared expert's position off[E] + t when present.
+__global__ void __launch_bounds__(256) prefill_combine_kernel(
+    float* __restrict__ out, const float* __restrict__ residual, const float* __restrict__ y,
+    const float* __restrict__ weight, const int* __restrict__ gslot, const int* __restrict__ off,
+    int n_expert, int k, int hidden, int has_shared) {
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= hidden) return;
+  const long long o = static_cast<long long>(t) * hidden + i;
+  float acc = residual ? residual[o] : 0.f;
+  const int shared_pos = off[n_expert] + t;
+  for (int kk = 0; kk <= k; ++kk) {
+    const int pos = kk < k ? gslot[t * k + kk] : (has_shared ? shared_pos : -1);
+    const float yv = pos >= 0 ? y[static_cast<long long>(pos) * hidden + i] : 0.f;
+    acc = __builtin_fmaf(weight[t * (k + 1) + kk], yv, acc);
+  }
+  out[o] = acc;
+}
+
+// ---- workspace ------------------------------------------------------------------
+struct PrefillWs {
+  size_t xq, gslot, grows, off, toff, meta, h, hq, y, total;
+  int P;  // positions: T*k routes + T shared
+};
+
+static size_t al256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
+  PrefillWs w{};
+  w.P = T * k + T;
+  size_t o = 0;
+  w.xq = o;    o = al256(o + static_cast<size_t>(T) * (hidden / kQK) * kQ8Bytes);
+  w.gslot = o; o = al256(o + static_cast<size_t>(T) * k * 4);
+  w.grows = o; o = al256(o + static_cast<size_t>(w.P) * 4);
+  w.off = o;   o = al256(o + static_cast<size_t>(E + 2) * 4);
+  w.toff = o;  o = al256(o + static_cast<size_t>(E + 2) * 4);
+  w.meta = o;  o = al256(o + 4 * 4);
+  w.h = o;     o = al256(o + static_cast<size_t>(w.P) * n_ff * 4);
+  w.hq = o;    o = al256(o + static_cast<size_t>(w.P) * (n_ff / kQK) * kQ8Bytes);
+  w.y = o;     o = al256(o + static_cast<size_t>(w.P) * hidden * 4);
+  w.total = o;
+  return w;
+}
+
+constexpr int kScanLdsWords = 38 * 1024;  // dispatch scan: hist, offsets, parts, bitmap
+
+static int scan_lds_words(int n_rows, int E) { return 2 * E + 1024 + E * ((n_rows + 31) / 32); }
+
+static int scan_launch(const int* idx, float* weight, int* gslot, int* grows, int* off, int* toff,
+                       int* meta, int n_rows, int k, int E, int tok_per, int shared_tail,
+                       hipStream_t s, const char* nm) {
+  const int words = scan_lds_words(n_rows, E);
+  if (words > kScanLdsWords)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows=%d x n_expert=%d too large for one scan",
+                     nm, n_rows, E);
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), words * 4, s, idx, weight, gslot,
+                     grows, off, toff, meta, n_rows, k, E, tok_per, shared_tail);
+  return check_launch(nm);
+}
+
+}  // namespace sg
+
+using namespace sg;
+
+extern "C" {
+
+int sg_moe_dispatch_scan(const int* idx, float* weight, int* gslot, int* grows, int* off,
+                         int* toff, int* meta, int n_rows, int k, int n_expert, int tok_per,
+                         void* stream) {
+  const char* nm = "sg_moe_dispatch_scan";
+  if (!idx || !weight || !gslot || !grows || !off || !toff || !meta)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  if (n_rows <= 0 || k <= 0 || n_expert <= 0 || n_expert > 1024 || tok_per <= 0)
+    return set_error(SG_ERR_GEOMETRY, "%s: n_rows=%d k=%d n_expert=%d (<=1024) tok_per=%d", nm,
+                     n_rows, k, n_expert, tok_per);
+  return scan_launch(idx, weight, gslot, grows, off, toff, meta, n_rows, k, n_expert, tok_per, 0,
+                     static_cast<hipStream_t>(stream), nm);
+}
+
+size_t sg_moe_prefill_workspace_bytes(int n_tokens, int hidden, int n_ff, int n_expert, int k) {
+  if (n_tokens <= 0 || hidden <= 0 || n_ff <= 0 || n_expert <= 0 || k <= 0) return 0;
+  return prefill_ws(n_tokens, hidden, n_ff, n_expert, k).total;
+}
+
+int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
+                   const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
+                   const sg_block_q4k* sh_up, const sg_block_q4k* sh_down, const float* x,
+                   const float* logits, const float* residual, float* out, int* idx,
+                   float* weight, void* workspace, size_t workspace_bytes, int n_tokens,
+                   int hidden, int n_ff, int n_expert, int k, float shared_w, void* stream) {
+  const char* nm = "sg_moe_prefill";
+  if (!tab_gate || !tab_up || !tab_down || !x || !out || !idx || !weight || !workspace)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  const int n_sh = (sh_gate != nullptr) + (sh_up != nullptr) + (sh_down != nullptr);
+  if (n_sh != 0 && n_sh != 3)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: shared expert needs gate, up and down", nm);
+  if (n_tokens <= 0 || hidden <= 0 || hidden % kQK || n_ff <= 0 || n_ff % kQK)
+    return set_error(SG_ERR_GEOMETRY, "%s: n_tokens=%d hidden=%d n_ff=%d (multiples of 256)", nm,
+                     n_tokens, hidden, n_ff);
+  if (k <= 0 || k > 32 || n_expert < k || n_expert > 1024)
+    return set_error(SG_ERR_GEOMETRY, "%s: k=%d n_expert=%d", nm, k, n_expert);
+  const PrefillWs ws = prefill_ws(n_tokens, hidden, n_ff, n_expert, k);
+  if (workspace_bytes < ws.total)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: workspace %zu < %zu bytes", nm,
+                     workspace_bytes, ws.total);
+  if (scan_lds_words(n_tokens, n_expert) > kScanLdsWords)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: n_tokens=%d x n_expert=%d too large", nm, n_tokens,
+                     n_expert);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  unsigned char* base = static_cast<unsigned char*>(workspace);
+  auto* xq = reinterpret_cast<sg_block_q8k*>(base + ws.xq);
+  int* gslot = reinterpret_cast<int*>(base + ws.gslot);
+  int* grows = reinterpret_cast<int*>(base + ws.grows);
+  int* off = reinterpret_cast<int*>(base + ws.off);
+  int* toff = reinterpret_cast<int*>(base + ws.toff);
+  int* meta = reinterpret_cast<int*>(base + ws.meta);
+  float* h = reinterpret_cast<float*>(base + ws.h);
+  auto* hq = reinterpret_cast<sg_block_q8k*>(base + ws.hq);
+  float* y = reinterpret_cast<float*>(base + ws.y);
+  const int has_shared = n_sh == 3;
+
+  if (int st = sg_quantize_q8_k(x, xq, hidden, n_tokens, stream)) return st;
+  if (logits)
+    if (int st = sg_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w,
+                                stream))
+      return st;
+  if (int st = scan_launch(idx, weight, gslot, grows, off, toff, meta, n_tokens, k, n_expert,
+                           kTokTile, has_shared ? n_tokens : 0, s, nm))
+    return st;
+  const int G = n_expert + has_shared;
+  GroupedArgs ga{};
+  ga.tab_a = tab_gate;
+  ga.tab_b = tab_up;
+  ga.tab_c = tab_down;
+  ga.sh_a = sh_gate;
+  ga.sh_b = sh_up;
+  ga.sh_c = sh_down;
+  ga.xq = reinterpret_cast<const unsigned char*>(xq);
+  ga.off = off;
+  ga.grows = grows;
+  ga.out = h;
+  ga.nb = hidden / kQK;
+  ga.n_out = n_ff;
+  ga.n_expert = n_expert;
+  ga.n_groups = G;
+  hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(n_ff / (kRowsWg / 2), G), dim3(kThreads), 0,
+                     s, ga);
+  if (int st = check_launch("sg_moe_prefill/gate_up")) return st;
+  if (int st = sg_quantize_q8_k(h, hq, n_ff, ws.P, stream)) return st;
+  GroupedArgs gd = ga;
+  gd.tab_a = tab_down;
+  gd.tab_b = tab_down;
+  gd.tab_c = tab_gate;  // an expert without gate/up contributes zero
+  gd.sh_a = sh_down;
+  gd.sh_b = sh_down;
+  gd.sh_c = sh_gate;
+  gd.xq = reinterpret_cast<const unsigned char*>(hq);
+  gd.grows = nullptr;
+  gd.out = y;
+  gd.nb = n_ff / kQK;
+  gd.n_out = hidden;
+  hipLaunchKernelGGL(grouped_mfma_kernel<false>, dim3(hidden / kRowsWg, G), dim3(kThreads), 0, s,
+                     gd);
+  if (int st = check_launch("sg_moe_prefill/down")) return st;
+  hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 255) / 256, n_tokens), dim3(256), 0, s,
+                     out, residual, y, weight, gslot, off, n_expert, k, hidden, has_shared);
+  return check_launch("sg_moe_prefill/combine");
+}
+
+}  // extern "C"

@@ -161,3 +161,55 @@ class MoeLayer:
             _ptr(ws), ws.numel(), T, self.hidden, self.n_ff, self.n_expert, self.k,
             self.shared_w, stages, _stream()))
         return out, idx, weight
+
+
+def moe_dispatch_scan(idx, weight, n_expert, k, tok_per=64):
+    """cuda::moe_dispatch_scan (cuda_ops.hpp:219-222) on the device: returns
+    dict(gslot, grows, off, toff, meta); `weight` is bounds-killed in place."""
+    n_rows = idx.shape[0]
+    dev = idx.device
+    gslot = torch.empty(n_rows * k, dtype=torch.int32, device=dev)
+    grows = torch.empty(n_rows * k, dtype=torch.int32, device=dev)
+    off = torch.empty(n_expert + 2, dtype=torch.int32, device=dev)
+    toff = torch.empty(n_expert + 2, dtype=torch.int32, device=dev)
+    meta = torch.zeros(4, dtype=torch.int32, device=dev)
+    _check(load().sg_moe_dispatch_scan(_ptr(idx), _ptr(weight), _ptr(gslot), _ptr(grows),
+                                       _ptr(off), _ptr(toff), _ptr(meta), n_rows, k, n_expert,
+                                       tok_per, _stream()))
+    return dict(gslot=gslot, grows=grows, off=off, toff=toff, meta=meta)
+
+
+class MoePrefill(MoeLayer):
+    """The same layer for a prefill chunk of up to max_tokens tokens: the
+    device plan and int8-MFMA grouped contractions (sg_moe_prefill)."""
+
+    def __init__(self, tab_gate, tab_up, tab_down, shared=None, hidden=2048, n_ff=512,
+                 n_expert=256, k=8, max_tokens=2048, shared_w=1.0):
+        self.tab_gate, self.tab_up, self.tab_down = tab_gate, tab_up, tab_down
+        self.shared = shared
+        self.hidden, self.n_ff, self.n_expert, self.k = hidden, n_ff, n_expert, k
+        self.shared_w = float(shared_w)
+        self.max_tokens = max_tokens
+        nbytes = load().sg_moe_prefill_workspace_bytes(max_tokens, hidden, n_ff, n_expert, k)
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=tab_gate.device)
+
+    def forward(self, x, logits=None, residual=None, out=None, idx=None, weight=None,
+                workspace=None):
+        T = x.shape[0]
+        if T > self.max_tokens:
+            raise SagerError(f"{T} tokens > max_tokens={self.max_tokens}")
+        dev = x.device
+        if out is None:
+            out = torch.empty((T, self.hidden), dtype=torch.float32, device=dev)
+        if idx is None:
+            idx = torch.full((T, self.k + 1), -1, dtype=torch.int32, device=dev)
+        if weight is None:
+            weight = torch.zeros((T, self.k + 1), dtype=torch.float32, device=dev)
+        sg, su, sd = self.shared if self.shared is not None else (None, None, None)
+        ws = self.workspace if workspace is None else workspace
+        _check(load().sg_moe_prefill(
+            _ptr(self.tab_gate), _ptr(self.tab_up), _ptr(self.tab_down), _ptr(sg), _ptr(su),
+            _ptr(sd), _ptr(x), _ptr(logits), _ptr(residual), _ptr(out), _ptr(idx), _ptr(weight),
+            _ptr(ws), ws.numel(), T, self.hidden, self.n_ff, self.n_expert, self.k,
+            self.shared_w, _stream()))
+        return out, idx, weight

@@ -351,3 +351,111 @@ def test_moe_layer_near_collision_probabilities():
     np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K])
     np.testing.assert_array_equal(host(w).view(np.uint32), rw.view(np.uint32))
     np.testing.assert_array_equal(host(out).view(np.uint32), ref.view(np.uint32))
+
+
+# ---- prefill chunk: device plan + int8-MFMA grouped contractions ----------
+
+@pytest.mark.parametrize("n_rows,n_expert,k", [(64, 32, 8), (2048, 256, 8), (300, 1024, 4)])
+def test_dispatch_scan_matches_oracle(n_rows, n_expert, k):
+    rng = np.random.default_rng(n_rows + n_expert)
+    idx = np.stack([rng.choice(n_expert, k, replace=False) for _ in range(n_rows)]).astype(
+        np.int32)
+    idx = np.concatenate([idx, np.full((n_rows, 1), -1, np.int32)], axis=1)
+    idx[3, 1] = n_expert + 5           # invalid ids: bounds-kill of rows 3 and 7
+    idx[7, 0] = -2
+    w = rng.uniform(0, 1, (n_rows, k + 1)).astype(np.float32)
+    ref = orc.dispatch_scan(idx, w, k, n_expert, tok_per=64)
+    wd = dev(w)
+    got = ops.moe_dispatch_scan(dev(idx), wd, n_expert, k, tok_per=64)
+    R = int(ref["meta"][0])
+    np.testing.assert_array_equal(host(got["meta"])[:3], ref["meta"][:3])
+    np.testing.assert_array_equal(host(got["off"])[:n_expert + 1], ref["off"])
+    np.testing.assert_array_equal(host(got["toff"])[:n_expert + 1], ref["toff"])
+    np.testing.assert_array_equal(host(got["gslot"]), ref["gslot"])
+    np.testing.assert_array_equal(host(got["grows"])[:R], ref["grows"][:R])
+    np.testing.assert_array_equal(host(wd), ref["weight"])
+
+
+def test_dispatch_scan_duplicate_ids():
+    """Caller routing may name one expert twice in a row: the serial
+    placement keeps (token, slot) order."""
+    idx = np.array([[1, 1, 2, -1], [2, 0, 2, -1], [0, 1, 2, -1]], np.int32)
+    w = np.ones((3, 4), np.float32)
+    ref = orc.dispatch_scan(idx, w, 3, 4, tok_per=2)
+    got = ops.moe_dispatch_scan(dev(idx), dev(w), 4, 3, tok_per=2)
+    np.testing.assert_array_equal(host(got["gslot"]), ref["gslot"])
+    np.testing.assert_array_equal(host(got["grows"])[:9], ref["grows"][:9])
+
+
+def _prefill(g, u, d, shared, hidden, n_ff, k, max_tokens):
+    tg, kg = _tables(g)
+    tu, ku = _tables(u)
+    td, kd = _tables(d)
+    sh = tuple(dev(m) for m in shared) if shared is not None else None
+    layer = ops.MoePrefill(tg, tu, td, sh, hidden=hidden, n_ff=n_ff, n_expert=len(g), k=k,
+                           max_tokens=max_tokens)
+    layer._keep = (kg, ku, kd)
+    return layer
+
+
+@pytest.mark.parametrize("T,shared", [(1, True), (7, False), (64, True), (200, True)])
+def test_moe_prefill_small_pool(T, shared):
+    """hidden 2048, n_ff 512, top-8 of 32 experts: the MFMA path bit-exact
+    against the integer-first oracle (routing, plan, grouped GEMMs, combine)."""
+    rng = np.random.default_rng(700 + T)
+    H, F, E, K = 2048, 512, 32, 8
+    g, u, d = _expert_pool(rng, E + 1, H, F)
+    sh = (g.pop(), u.pop(), d.pop())
+    if not shared:
+        sh = None
+    x = rng.normal(0, 1, (T, H)).astype(np.float32)
+    lg = rng.normal(0, 1, (T, E)).astype(np.float32)
+    res = rng.normal(0, 1, (T, H)).astype(np.float32)
+    layer = _prefill(g, u, d, sh, H, F, K, max(T, 16))
+    out, idx, w = layer.forward(dev(x), dev(lg), residual=dev(res))
+    ref, ri, rw = orc.moe_layer(g, u, d, sh, x, logits=lg, residual=res, hidden=H, n_ff=F, k=K,
+                                prefill=True, n_threads=8)
+    np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K])
+    np.testing.assert_array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+    assert_fp32_parity(host(out), ref)
+
+
+def test_moe_prefill_routed_edge_cases():
+    """Caller routing: an out-of-range id (bounds-kill), an absent expert,
+    a token routed twice to one expert, no shared expert, residual = out."""
+    rng = np.random.default_rng(78)
+    H, F, E, K, T = 512, 256, 8, 2, 5
+    g, u, d = _expert_pool(rng, E, H, F)
+    g[3] = None
+    x = rng.normal(0, 1, (T, H)).astype(np.float32)
+    idx = np.array([[1, 99, -1], [2, 3, -1], [3, 5, -1], [4, 4, -1], [0, 7, -1]], np.int32)
+    w = rng.uniform(0.1, 1, (T, K + 1)).astype(np.float32)
+    res = rng.normal(0, 1, (T, H)).astype(np.float32)
+    layer = _prefill(g, u, d, None, H, F, K, T)
+    io = dev(res)
+    wd = dev(w)
+    out, _, wgt = layer.forward(dev(x), None, residual=io, out=io, idx=dev(idx), weight=wd)
+    ref, _, rw = orc.moe_layer(g, u, d, None, x, idx=idx, weight=w, residual=res, hidden=H,
+                               n_ff=F, k=K, prefill=True)
+    np.testing.assert_array_equal(host(wgt), rw)
+    assert_fp32_parity(host(out), ref)
+
+
+def test_moe_prefill_vs_decode_path():
+    """The prefill path and the decode path agree on indices and weights and,
+    through their different fp32 epilogue orders, on the outputs to within
+    what one flipped Q8_K code of h can move (both are checked bit-exact
+    against their own oracle elsewhere)."""
+    rng = np.random.default_rng(4321)
+    H, F, E, K, T = 2048, 512, 32, 8, 16
+    g, u, d = _expert_pool(rng, E + 1, H, F)
+    sh = (g.pop(), u.pop(), d.pop())
+    x = rng.normal(0, 1, (T, H)).astype(np.float32)
+    lg = rng.normal(0, 1, (T, E)).astype(np.float32)
+    pre = _prefill(g, u, d, sh, H, F, K, T)
+    dec = _layer(g, u, d, sh, H, F, K, T)
+    o1, i1, w1 = pre.forward(dev(x), dev(lg))
+    o2, i2, w2 = dec.forward(dev(x), dev(lg))
+    np.testing.assert_array_equal(host(i1), host(i2))
+    np.testing.assert_array_equal(host(w1), host(w2))
+    assert rel_err(host(o1), host(o2)) < 5e-3

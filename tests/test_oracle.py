@@ -148,6 +148,64 @@ def test_gemv_vs_fp64_dequant_dot(gold, case):
     assert np.abs(gold[case + "_vecdot"] - ref).max() <= 1e-5 * scale
 
 
+@pytest.mark.parametrize("case", ["gemv_a", "gemv_c"])
+def test_gemv_int_first_vs_fp64(gold, case):
+    """The prefill GEMV (integer-first epilogue: exact I = sum sc*ip and
+    M = sum mn*bsum per super-block, then two fmas) against the same float64
+    evaluation; it is at least as close as the AVX2 order."""
+    n_rows, k = (int(v) for v in gold[case + "_shape"])
+    w, xq = gold[case + "_w"], gold[case + "_xq"][0]
+    nb = k // 256
+    dots = _brute_dots(w, xq, n_rows, k).astype(np.int64)
+    wb = w.reshape(n_rows, nb, 144)
+    d = wb[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+    dm = wb[:, :, 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+    s12 = wb[:, :, 4:16].astype(np.int64)
+    sc = np.zeros((n_rows, nb, 8), np.int64); mn = np.zeros((n_rows, nb, 8), np.int64)
+    for j in range(8):
+        if j < 4:
+            sc[..., j] = s12[..., j] & 63
+            mn[..., j] = s12[..., j + 4] & 63
+        else:
+            sc[..., j] = (s12[..., j + 4] & 15) | ((s12[..., j - 4] >> 6) << 4)
+            mn[..., j] = (s12[..., j + 4] >> 4) | ((s12[..., j] >> 6) << 4)
+    xd, _, bs = _q8_fields(xq)
+    I = (sc * dots).sum(axis=2)                       # exact integers per super-block
+    M = (mn * bs[None].astype(np.int64)).sum(axis=2)
+    ref = (xd[None, :] * (d * I - dm * M)).sum(axis=1)
+    y = orc.gemv_int(w, xq, n_rows, k)[0].astype(np.float64)
+    y_avx = orc.gemv(w, xq, n_rows, k)[0].astype(np.float64)
+    scale = np.abs(ref).max()
+    assert np.abs(y - ref).max() <= 1e-5 * scale
+    assert np.abs(y - ref).max() <= np.abs(y_avx - ref).max() * 1.5 + 1e-7 * scale
+
+
+def test_moe_prefill_is_router_ffn_int_combine():
+    """orc_moe_prefill = router + per-route expert FFN with the integer-first
+    GEMV (each stage by its own oracle function) + slot-order combine."""
+    rng = np.random.default_rng(31)
+    H, F, E, K, T = 512, 256, 8, 2, 3
+    g = [q4k_random_np(rng, F * H // 256) for _ in range(E)]
+    u = [q4k_random_np(rng, F * H // 256) for _ in range(E)]
+    d = [q4k_random_np(rng, H * F // 256) for _ in range(E)]
+    x = rng.normal(0, 1, (T, H)).astype(np.float32)
+    lg = rng.normal(0, 1, (T, E)).astype(np.float32)
+    out, idx, w = orc.moe_layer(g, u, d, None, x, logits=lg, hidden=H, n_ff=F, k=K, prefill=True)
+    ri, rw = orc.router_topk(lg, K)
+    np.testing.assert_array_equal(idx, ri)
+    ys = np.zeros((T, K + 1, H), np.float32)
+    for t in range(T):
+        xq = orc.quantize_q8_k(x[t])
+        for kk in range(K):
+            e = ri[t, kk]
+            gg = orc.gemv_int(g[e], xq, F, H)[0]
+            uu = orc.gemv_int(u[e], xq, F, H)[0]
+            hq = orc.quantize_q8_k(orc.silu_mul(gg, uu))
+            ys[t, kk] = orc.gemv_int(d[e], hq, H, F)[0]
+    ref = orc.moe_combine(ys, rw)
+    np.testing.assert_array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
 # ---- exp, SiLU, expert FFN ------------------------------------------------
 
 def test_expf_correctly_rounded_sample():
