@@ -202,7 +202,8 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate,
  * expert is deterministic: token order, then slot.  No mailbox: absent
  * experts are handled by the grouped kernels themselves.  off needs E+2
  * entries (off[E+1] = off[E]).  n_expert <= 1024 and
- * n_expert * ceil(n_rows/32) <= 37,888 (the plan is built in LDS). */
+ * 2 * n_expert * (ceil(n_rows/32) + 1) + 1024 <= 38,912 (the plan is built in
+ * LDS; 2048 tokens x 256 experts fit). */
 int sg_moe_dispatch_scan(const int* idx, float* weight, int* gslot, int* grows,
                          int* off, int* toff, int* meta, int n_rows, int k,
                          int n_expert, int tok_per, void* stream);

@@ -26,15 +26,39 @@
 namespace sg {
 
 // ---- dispatch scan --------------------------------------------------------------
+constexpr int kScanPerThread = 32;  // routes per thread: n_rows * k <= 32768
 // One workgroup of 1024 threads.  Pass 1: per-expert route counts and a
 // [expert][token] bitmap in LDS; invalid ids zero their row's weights
 // (bounds-kill, moe.cu:385-396).  The exclusive scans give off/toff/meta.
 // Pass 2 places every route at off[e] + (its rank among the expert's routes
-// in token order) - a popcount over the bitmap - so the plan is
-// deterministic (the reference's atomic placement is not).  A token routed
+// in token order) - a per-word prefix plus a popcount over the bitmap - so
+// the plan is deterministic (the reference's atomic placement is not).  A token routed
 // twice to one expert (caller-supplied ids) takes a serial placement.
 // With shared_tail > 0, positions off[E] .. off[E] + shared_tail - 1 are the
 // shared expert's (token t at off[E] + t) and off[E+1] closes them.
+// Exclusive prefix sum of v over a 1024-thread workgroup (thread order);
+// *total gets the sum.  tmp: 16 ints of LDS.  Contains three barriers.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;  // inclusive scan inside the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) tmp[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int w = 0; w < 16; ++w) {
+    const int t = tmp[w];
+    before += w < wave ? t : 0;
+    all += t;
+  }
+  __syncthreads();  // tmp is reused by the caller's next scan
+  *total = all;
+  return before + x - v;
+}
+
 __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
     const int* __restrict__ idx, float* __restrict__ weight, int* __restrict__ gslot,
     int* __restrict__ grows, int* __restrict__ off, int* __restrict__ toff,
@@ -45,7 +69,8 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
   int* hist = reinterpret_cast<int*>(lds);       // [E]
   int* offl = hist + E;                          // [E]
   int* part = offl + E;                          // [1024]
-  uint32_t* bm = reinterpret_cast<uint32_t*>(part + 1024);  // [E][W]
+  uint32_t* bm = reinterpret_cast<uint32_t*>(part + 1024);  // [E][W] token bitmap
+  int* pre = reinterpret_cast<int*>(bm + E * W);            // [E][W] routes before each word
   const int tid = threadIdx.x, nth = blockDim.x;
   for (int i = tid; i < E; i += nth) hist[i] = 0;
   for (int i = tid; i < E * W; i += nth) bm[i] = 0u;
@@ -55,9 +80,21 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
   }
   __syncthreads();
   const int total = n_rows * k;
-  for (int i = tid; i < total; i += nth) {
+  // every route id this thread handles, loaded up front (independent loads
+  // in flight together; route i = tid + 1024 j)
+  int ids[kScanPerThread];
+#pragma unroll
+  for (int j = 0; j < kScanPerThread; ++j) {
+    const int i = tid + nth * j;
     const int r = i / k, kk = i - r * k;
-    const int e = idx[static_cast<long long>(r) * (k + 1) + kk];
+    ids[j] = i < total ? idx[static_cast<long long>(r) * (k + 1) + kk] : -1;
+  }
+#pragma unroll
+  for (int j = 0; j < kScanPerThread; ++j) {
+    const int i = tid + nth * j;
+    if (i >= total) break;
+    const int r = i / k;
+    const int e = ids[j];
     if (e < 0 || e >= E) {
       for (int q = 0; q <= k; ++q) weight[static_cast<long long>(r) * (k + 1) + q] = 0.f;
       gslot[i] = -1;
@@ -69,25 +106,31 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
     if (atomicOr(&bm[e * W + (r >> 5)], bit) & bit) s_dup = 1;
   }
   __syncthreads();
-  if (tid == 0) {  // E <= 1024: one thread, in order
-    int acc = 0, tacc = 0;
-    for (int e = 0; e < E; ++e) {
-      off[e] = acc;
-      offl[e] = acc;
-      toff[e] = tacc;
-      acc += hist[e];
-      tacc += (hist[e] + tok_per - 1) / tok_per;
+  {  // exclusive prefix sums over the experts (E <= 1024: one per thread)
+    const int h = tid < E ? hist[tid] : 0;
+    const int tl = (h + tok_per - 1) / tok_per;
+    int tot_h, tot_t;
+    const int ph = block_exclusive_scan(h, part, &tot_h);
+    const int pt = block_exclusive_scan(tl, part, &tot_t);
+    if (tid < E) {
+      off[tid] = ph;
+      offl[tid] = ph;
+      toff[tid] = pt;
     }
-    off[E] = acc;
-    toff[E] = tacc;
-    off[E + 1] = acc + shared_tail;
-    meta[0] = acc;
-    meta[1] = tacc;
-    meta[2] = s_bad;
-    s_total = acc;
+    if (tid == 0) {
+      off[E] = tot_h;
+      toff[E] = tot_t;
+      off[E + 1] = tot_h + shared_tail;
+      meta[0] = tot_h;
+      meta[1] = tot_t;
+      meta[2] = s_bad;
+      s_total = tot_h;
+    }
   }
   __syncthreads();
   if (!s_dup) {
+    // per-(expert, word) prefix of route counts, in place of the bitmap's
+    // companion array pre[]: thread group of expert e scans its words
     const int tpe = max(1, nth / E);  // threads per expert
     const int e = tid / tpe, q = tid - e * tpe;
     const int wpt = (W + tpe - 1) / tpe;
@@ -98,20 +141,27 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
     part[tid] = c;
     __syncthreads();
     if (e < E) {
-      int pos = offl[e];
-      for (int j = 0; j < q; ++j) pos += part[e * tpe + j];
+      int run = offl[e];
+      for (int j = 0; j < q; ++j) run += part[e * tpe + j];
       for (int w = w0; w < w1; ++w) {
-        uint32_t bits = bm[e * W + w];
-        while (bits) {
-          const int r = 32 * w + __builtin_ctz(bits);
-          bits &= bits - 1u;
-          int kk = 0;
-          while (kk < k && idx[static_cast<long long>(r) * (k + 1) + kk] != e) ++kk;
-          gslot[r * k + kk] = pos;
-          grows[pos] = r;
-          ++pos;
-        }
+        pre[e * W + w] = run;
+        run += __popc(bm[e * W + w]);
       }
+    }
+    __syncthreads();
+    // every route independently: its position is the expert's offset plus
+    // the routes of lower tokens (a popcount of the word's lower bits)
+#pragma unroll
+    for (int j = 0; j < kScanPerThread; ++j) {
+      const int i = tid + nth * j;
+      if (i >= total) break;
+      const int r = i / k;
+      const int ee = ids[j];
+      if (ee < 0 || ee >= E) continue;
+      const uint32_t word = bm[ee * W + (r >> 5)];
+      const int pos = pre[ee * W + (r >> 5)] + __popc(word & ((1u << (r & 31)) - 1u));
+      gslot[i] = pos;
+      grows[pos] = r;
     }
   } else if (tid == 0) {  // duplicated ids in a row: serial placement in (token, slot) order
     for (int e = 0; e < E; ++e) hist[e] = offl[e];
@@ -132,7 +182,8 @@ constexpr int kTokTile = 64;
 constexpr int kRowsWg = 128;                 // weight rows per workgroup
 constexpr int kWRowWords = 36;               // one 144-B block
 constexpr int kWBufWords = kRowsWg * kWRowWords;   // 18 KB
-constexpr int kXBufWords = kTokTile * 69;          // 17.25 KB, packed Q8_K blocks
+constexpr int kXRow = 72;                           // staged Q8_K block: qs, bsums, d, pad
+constexpr int kXBufWords = kTokTile * kXRow;        // 17.5 KB
 constexpr int kThreads = 512;                 // eight waves
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -184,33 +235,58 @@ __global__ void __launch_bounds__(kThreads) grouped_mfma_kernel(GroupedArgs a) {
   }
 
   // weight rows of super-block b into wbuf[s]: gate/up -> 64 gate rows then
-  // the same 64 up rows; down -> 128 rows.  Chunk c (16 B) of row c/9.
+  // the same 64 up rows; down -> 128 rows.  Wave w copies chunks
+  // [144w, 144w+144) (16 B each, chunk c = part c%9 of row c/9), all from one
+  // matrix; the per-lane offsets are fixed for the kernel, the block's
+  // offset b*144 goes in the scalar offset (buffer_load ... lds).
+  constexpr int kWChunks = kRowsWg * 9 / 8;  // 144 per wave
+  const sg_block_q4k* mw = (kGateUp && wave >= 4) ? mb : ma;
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<sg_block_q4k*>(mw), 0, a.n_out * nb * kQ4Bytes, 0x00020000);
+  uint32_t wofs[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int cc = min(wave * kWChunks + lane + 64 * i, kRowsWg * 9 - 1);
+    const int row = cc / 9, part = cc - row * 9;
+    const int rr = kGateUp ? (row & 63) : row;
+    wofs[i] = static_cast<uint32_t>((r0 + rr) * nb) * kQ4Bytes + 16 * part;
+  }
   auto stage_w = [&](int b, int s) {
-    const int c0 = wave * (kRowsWg * 9 / 8);  // 144 chunks per wave
-    dma_chunks(
-        [&](int c) {
-          const int cc = c0 + c;
-          const int row = cc / 9, part = cc - row * 9;
-          const sg_block_q4k* m = (kGateUp && row >= 64) ? mb : ma;
-          const int rr = kGateUp ? (row & 63) : row;
-          const unsigned off = (static_cast<unsigned>(r0 + rr) * nb + b) * kQ4Bytes + 16 * part;
-          return reinterpret_cast<const char*>(m) + off;
-        },
-        kRowsWg * 9 / 8, wbuf[s] + 4 * c0, lane);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      if (64 * i + lane < kWChunks)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rw, (lds_void_p)(wbuf[s] + 4 * (wave * kWChunks + 64 * i)), 16, wofs[i],
+            b * kQ4Bytes, 0, 0);
   };
-  // the tile's token blocks of super-block b into xbuf[s], packed 69 words
-  // per token (d, 64 qs words, 4 words of int16 bsums): dword chunk c is
-  // word c % 69 of token c / 69, so lane-consecutive chunks land
-  // LDS-consecutive (global_load_lds_dword)
+  // the tile's token blocks of super-block b into xbuf[s], 72 words per
+  // token in 16-B chunks: chunks 0-15 the 64 qs words (64-bit aligned for
+  // the MFMA operand reads), 16 the 4 words of int16 bsums, 17 d and three
+  // pad words.  LDS chunk c = 18t + j is filled from the matching 16 B of
+  // token t's block (buffer_load_dwordx4 ... lds: lane-consecutive chunks
+  // land LDS-consecutive); offsets are set per token tile, b*276 is the
+  // scalar offset.
+  constexpr int kXChunks = kTokTile * kXRow / 4;                 // 1152
+  constexpr int kXInstr = (kXChunks / 64 + 7) / 8;               // per wave: 3
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<unsigned char*>(a.xq), 0, 0x7FFFFFFF, 0x00020000);
+  uint32_t xofs[kXInstr];
+  auto set_x_offsets = [&]() {
+#pragma unroll
+    for (int i = 0; i < kXInstr; ++i) {
+      const int c = min(64 * (wave + 8 * i) + lane, kXChunks - 1);
+      const int t = c / 18, j = c - t * 18;
+      const int gw = j < 16 ? 1 + 4 * j : (j == 16 ? 65 : 0);  // qs, bsums, then d
+      xofs[i] = static_cast<uint32_t>(trow[t]) * kQ8Bytes + 4 * gw;
+    }
+  };
   auto stage_x = [&](int b, int s) {
-    for (int c0 = wave * 64; c0 < kTokTile * 69; c0 += kThreads) {
-      const int c = c0 + lane;
-      const int cc = c < kTokTile * 69 ? c : kTokTile * 69 - 1;
-      const int t = cc / 69, w = cc - t * 69;
-      const char* src = reinterpret_cast<const char*>(a.xq) +
-                        static_cast<long long>(trow[t] + b) * kQ8Bytes + 4 * w;
-      if (c0 + 64 <= kTokTile * 69 || c < kTokTile * 69)
-        __builtin_amdgcn_global_load_lds((glb_void_p)src, (lds_void_p)(xbuf[s] + c0), 4, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kXInstr; ++i) {
+      const int q = wave + 8 * i;  // the instruction's 64-chunk slice
+      if (64 * q < kXChunks)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_p)(xbuf[s] + 256 * q), 16, xofs[i],
+                                                 b * kQ8Bytes, 0, 0);
     }
   };
 
@@ -221,6 +297,7 @@ __global__ void __launch_bounds__(kThreads) grouped_mfma_kernel(GroupedArgs a) {
       trow[tid] = (kGateUp ? a.grows[t0 + t] : t0 + t) * nb;
     }
     bar();
+    set_x_offsets();
     float acc[4][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -240,56 +317,70 @@ __global__ void __launch_bounds__(kThreads) grouped_mfma_kernel(GroupedArgs a) {
       const uint32_t* W = wbuf[s];
       const uint32_t* X = xbuf[s];
       // the lane's four output tokens are the MFMA result rows tx .. tx+3;
-      // its weight row in row block j is 16j + lr
+      // its weight row in row block j is 16 rblk(j) + lr
       const int tx = 16 * tb + 4 * lq;
+      // M = sum_s mn_s * bsum_s by MFMA: A = the wave's 16 tokens' eight
+      // bsums split exactly as 128*hi + lo (both int8), B = the rows' eight
+      // 6-bit mins; K = the 8 sub-blocks in the first K quarter, zeros in
+      // the other three.  M = 128 * C(hi) + C(lo).
+      long am_lo = 0, am_hi = 0;
+      if (lq == 0) {
+        const uint32_t* brow = X + (16 * tb + lr) * kXRow + 64;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t bw = brow[q];
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int bsv = static_cast<int16_t>(h2 ? (bw >> 16) : (bw & 0xFFFFu));
+            const int hi = bsv >> 7, lo = bsv - 128 * hi;  // hi in [-32, 31], lo in [0, 127]
+            am_hi |= static_cast<long>(hi & 0xFF) << (8 * (2 * q + h2));
+            am_lo |= static_cast<long>(lo) << (8 * (2 * q + h2));
+          }
+        }
+      }
+      ScaleMins smj[4];
       int I[4][4], M[4][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t* wr = W + (16 * rblk(j) + lr) * kWRowWords;
+        smj[j] = unpack_scales(wr[1], wr[2], wr[3]);
+        const long bmn =
+            lq == 0 ? static_cast<long>(smj[j].mn_lo) | (static_cast<long>(smj[j].mn_hi) << 32)
+                    : 0l;
+        const v4i z = {0, 0, 0, 0};
+        const v4i ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(am_hi, bmn, z, 0, 0, 0);
+        const v4i cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(am_lo, bmn, z, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) I[j][i] = M[j][i] = 0;
-      const uint32_t* xa = X + (16 * tb + lr) * 69 + 1;  // the lane's A row (qs words)
+        for (int i = 0; i < 4; ++i) {
+          M[j][i] = ch[i] * 128 + cl[i];
+          I[j][i] = 0;
+        }
+      }
+      // the lane's A row: 8 qs bytes per sub-block, 64-bit aligned
+      const long* xa = reinterpret_cast<const long*>(X + (16 * tb + lr) * kXRow) + lq;
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {  // sub-blocks 0-3 (low scale words), 4-7 (high)
-        uint32_t scw[4], mnw[4];
+      for (int gq = 0; gq < 4; ++gq) {  // sub-blocks 2gq (low nibbles) and 2gq+1 (high)
+        const long a0 = xa[8 * gq];
+        const long a1 = xa[8 * gq + 4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t* wr = W + (16 * rblk(j) + lr) * kWRowWords;
-          const ScaleMins sm = unpack_scales(wr[1], wr[2], wr[3]);
-          scw[j] = hf ? sm.sc_hi : sm.sc_lo;
-          mnw[j] = hf ? sm.mn_hi : sm.mn_lo;
-        }
+          const unsigned long q = *reinterpret_cast<const unsigned long*>(
+              W + (16 * rblk(j) + lr) * kWRowWords + 4 + 8 * gq + 2 * lq);
+          const long b0 = static_cast<long>(q & 0x0F0F0F0F0F0F0F0Ful);
+          const long b1 = static_cast<long>((q >> 4) & 0x0F0F0F0F0F0F0F0Ful);
+          const v4i z = {0, 0, 0, 0};
+          const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, z, 0, 0, 0);
+          const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, z, 0, 0, 0);
+          const uint32_t scw = gq < 2 ? smj[j].sc_lo : smj[j].sc_hi;
+          const int sc0 = sbyte(scw, (2 * gq) & 3), sc1 = sbyte(scw, (2 * gq + 1) & 3);
+          // |ip| <= 32*15*127 and sc <= 63: 24-bit multiplies are exact
 #pragma unroll
-        for (int g2 = 0; g2 < 2; ++g2) {
-          const int gq = 2 * hf + g2;  // sub-blocks 2gq (low nibbles) and 2gq+1 (high)
-          const long a0 = static_cast<long>(xa[16 * gq + 2 * lq]) |
-                          (static_cast<long>(xa[16 * gq + 2 * lq + 1]) << 32);
-          const long a1 = static_cast<long>(xa[16 * gq + 8 + 2 * lq]) |
-                          (static_cast<long>(xa[16 * gq + 8 + 2 * lq + 1]) << 32);
-          int bs0[4], bs1[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {  // bsums of sub-blocks 2gq, 2gq+1: one word
-            const uint32_t bw = X[(tx + i) * 69 + 65 + gq];
-            bs0[i] = static_cast<int16_t>(bw & 0xFFFFu);
-            bs1[i] = static_cast<int16_t>(bw >> 16);
-          }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t* wr = W + (16 * rblk(j) + lr) * kWRowWords + 4 + 8 * gq + 2 * lq;
-            const uint32_t q0 = wr[0], q1 = wr[1];
-            const long b0 = static_cast<long>(q0 & 0x0F0F0F0Fu) |
-                            (static_cast<long>(q1 & 0x0F0F0F0Fu) << 32);
-            const long b1 = static_cast<long>((q0 >> 4) & 0x0F0F0F0Fu) |
-                            (static_cast<long>((q1 >> 4) & 0x0F0F0F0Fu) << 32);
-            const v4i z = {0, 0, 0, 0};
-            const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, z, 0, 0, 0);
-            const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, z, 0, 0, 0);
-            const int sc0 = sbyte(scw[j], 2 * g2), sc1 = sbyte(scw[j], 2 * g2 + 1);
-            const int mn0 = sbyte(mnw[j], 2 * g2), mn1 = sbyte(mnw[j], 2 * g2 + 1);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              I[j][i] += sc0 * c0[i] + sc1 * c1[i];
-              M[j][i] += mn0 * bs0[i] + mn1 * bs1[i];
-            }
+          for (int i = 0; i < 4; ++i) {
+            // sign-extension from 24 bits tells the compiler the dots fit
+            // v_mad_i32_i24 (it drops the shifts: the op ignores bits 24+)
+            const int d0 = (c0[i] << 8) >> 8, d1 = (c1[i] << 8) >> 8;
+            I[j][i] += sc0 * d0;
+            I[j][i] += sc1 * d1;
           }
         }
       }
@@ -300,7 +391,7 @@ __global__ void __launch_bounds__(kThreads) grouped_mfma_kernel(GroupedArgs a) {
         const float dmin = half_bits_to_float(dd >> 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float xd = __builtin_bit_cast(float, X[(tx + i) * 69]);
+          const float xd = __builtin_bit_cast(float, X[(tx + i) * kXRow + 68]);  // chunk 17
           const float t = __builtin_fmaf(d, static_cast<float>(I[j][i]),
                                          -(dmin * static_cast<float>(M[j][i])));
           acc[j][i] = __builtin_fmaf(xd, t, acc[j][i]);
@@ -373,7 +464,9 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
 
 constexpr int kScanLdsWords = 38 * 1024;  // dispatch scan: hist, offsets, parts, bitmap
 
-static int scan_lds_words(int n_rows, int E) { return 2 * E + 1024 + E * ((n_rows + 31) / 32); }
+static int scan_lds_words(int n_rows, int E) {
+  return 2 * E + 1024 + 2 * E * ((n_rows + 31) / 32);
+}
 
 static int scan_launch(const int* idx, float* weight, int* gslot, int* grows, int* off, int* toff,
                        int* meta, int n_rows, int k, int E, int tok_per, int shared_tail,
@@ -402,6 +495,9 @@ int sg_moe_dispatch_scan(const int* idx, float* weight, int* gslot, int* grows, 
   if (n_rows <= 0 || k <= 0 || n_expert <= 0 || n_expert > 1024 || tok_per <= 0)
     return set_error(SG_ERR_GEOMETRY, "%s: n_rows=%d k=%d n_expert=%d (<=1024) tok_per=%d", nm,
                      n_rows, k, n_expert, tok_per);
+  if (n_rows * k > 1024 * kScanPerThread)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows*k=%d > %d", nm, n_rows * k,
+                     1024 * kScanPerThread);
   return scan_launch(idx, weight, gslot, grows, off, toff, meta, n_rows, k, n_expert, tok_per, 0,
                      static_cast<hipStream_t>(stream), nm);
 }
@@ -432,7 +528,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   if (workspace_bytes < ws.total)
     return set_error(SG_ERR_INVALID_ARGUMENT, "%s: workspace %zu < %zu bytes", nm,
                      workspace_bytes, ws.total);
-  if (scan_lds_words(n_tokens, n_expert) > kScanLdsWords)
+  if (scan_lds_words(n_tokens, n_expert) > kScanLdsWords || n_tokens * k > 1024 * kScanPerThread)
     return set_error(SG_ERR_UNSUPPORTED, "%s: n_tokens=%d x n_expert=%d too large", nm, n_tokens,
                      n_expert);
   hipStream_t s = static_cast<hipStream_t>(stream);
