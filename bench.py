@@ -122,12 +122,66 @@ def cpu_baseline(pool_l0, xs, lgs, budget_s=8.0):
                       f"median; nproc={os.cpu_count()}, cpu={model}"}, outs
 
 
+def run_config5(torch, np, ops, gen, orc, q4k_random_dev, reps=10):
+    """Config 5: prefill chunk of 2048 tokens through the int8-MFMA path."""
+    log("[bench] config-5 prefill chunk")
+    T5 = 2048
+    pool5 = torch.empty((3, E, F * H // 256, 144), dtype=torch.uint8, device="cuda")
+    q4k_random_dev(3 * E * F * H // 256, gen, out=pool5.view(-1, 144))
+    tabs5 = [torch.tensor([pool5[m, e].data_ptr() for e in range(E)], dtype=torch.int64,
+                          device="cuda") for m in range(3)]
+    pre = ops.MoePrefill(*tabs5, None, hidden=H, n_ff=F, n_expert=E, k=K, max_tokens=T5)
+    rng5 = np.random.default_rng(5)
+    x5_h = rng5.normal(0, 1, (T5, H)).astype(np.float32)
+    l5_h = rng5.uniform(0, 1, (T5, E)).astype(np.float32)
+    x5, l5 = torch.from_numpy(x5_h).cuda(), torch.from_numpy(l5_h).cuda()
+    o5 = torch.empty((T5, H), dtype=torch.float32, device="cuda")
+    i5 = torch.empty((T5, K + 1), dtype=torch.int32, device="cuda")
+    w5 = torch.empty((T5, K + 1), dtype=torch.float32, device="cuda")
+    pre.forward(x5, l5, out=o5, idx=i5, weight=w5)
+    torch.cuda.synchronize()
+    ms5, _ = time_graph(torch, lambda: pre.forward(x5, l5, out=o5, idx=i5, weight=w5), reps)
+    # parity: the first 64 tokens against the integer-first oracle (tokens are
+    # independent once routed)
+    n_chk = 64
+    p5 = pool5.cpu().numpy()
+    ref5, ri5, _ = orc.moe_layer([p5[0, e] for e in range(E)], [p5[1, e] for e in range(E)],
+                                 [p5[2, e] for e in range(E)], None, x5_h[:n_chk],
+                                 logits=l5_h[:n_chk], hidden=H, n_ff=F, k=K, prefill=True,
+                                 n_threads=max(1, (os.cpu_count() or 2) // 2))
+    o5_h = o5[:n_chk].cpu().numpy()
+    floor = 1e-3 * np.abs(ref5).max()
+    rel5 = float((np.abs(o5_h - ref5) / np.maximum(np.abs(ref5), floor)).max())
+    exact5 = bool((o5_h == ref5).all()) and bool((i5[:n_chk, :K].cpu().numpy()
+                                                  == ri5[:, :K]).all())
+    routes5 = T5 * K
+    bytes5 = E * 3 * MAT_BYTES + T5 * (H // 256) * 276 + T5 * H * 4 + T5 * E * 4
+    ops5 = routes5 * 3 * F * H * 2
+    us5 = ms5 * 1e3
+    config5 = {"us_per_chunk": round(us5, 1), "tokens": T5,
+               "hbm": {"gbs": round(bytes5 / (us5 * 1e-6) / 1e9, 1),
+                       "frac": round(bytes5 / (us5 * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                       "algorithmic_bytes": bytes5},
+               "mfma_int8": {"tops": round(ops5 / (us5 * 1e-6) / 1e12, 2),
+                             "frac": round(ops5 / (us5 * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4),
+                             "ops": ops5},
+               "parity_first_64_tokens": {"bit_exact": exact5, "max_rel_err": rel5},
+               "workload": "2048 tokens x hidden 2048, U(0,1) logits, top-8 of 256 Q4_K experts "
+                           "(all touched), no shared expert; Q8_K(x), router, device plan, "
+                           "grouped int8-MFMA gate/up+SiLU and down, combine; one HIP graph"}
+    del pre, pool5
+    torch.cuda.synchronize()
+    return config5
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["5"], default=None,
+                    help="run one leg alone (5: the config-5 prefill chunk) and print its JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -143,6 +197,11 @@ def main():
     sager_amd.load()
     torch.cuda.init()
     gen = torch.Generator(device="cuda").manual_seed(1)
+    if args.only == "5":
+        from oracle import oracle as orc
+        print(json.dumps({"config5_prefill": run_config5(torch, np, ops, gen, orc,
+                                                          q4k_random_dev)}), flush=True)
+        return 0
     log(f"[bench] building {N_LAYERS} layers x {E + 1} experts "
         f"({N_LAYERS * 3 * (E + 1) * MAT_BYTES / 1e9:.1f} GB)")
     pool = build_pool(torch, N_LAYERS, gen)
@@ -361,55 +420,8 @@ def main():
     del stack, pool4, head
     torch.cuda.synchronize()
 
-    # config 5: prefill chunk of 2048 tokens, N(0,1) x, U(0,1) logits, top-8
-    # of 256 experts (no shared expert), the int8-MFMA grouped path
-    log("[bench] config-5 prefill chunk")
-    T5 = 2048
-    pool5 = torch.empty((3, E, F * H // 256, 144), dtype=torch.uint8, device="cuda")
-    q4k_random_dev(3 * E * F * H // 256, gen, out=pool5.view(-1, 144))
-    tabs5 = [torch.tensor([pool5[m, e].data_ptr() for e in range(E)], dtype=torch.int64,
-                          device="cuda") for m in range(3)]
-    pre = ops.MoePrefill(*tabs5, None, hidden=H, n_ff=F, n_expert=E, k=K, max_tokens=T5)
-    rng5 = np.random.default_rng(5)
-    x5_h = rng5.normal(0, 1, (T5, H)).astype(np.float32)
-    l5_h = rng5.uniform(0, 1, (T5, E)).astype(np.float32)
-    x5, l5 = torch.from_numpy(x5_h).cuda(), torch.from_numpy(l5_h).cuda()
-    o5 = torch.empty((T5, H), dtype=torch.float32, device="cuda")
-    i5 = torch.empty((T5, K + 1), dtype=torch.int32, device="cuda")
-    w5 = torch.empty((T5, K + 1), dtype=torch.float32, device="cuda")
-    pre.forward(x5, l5, out=o5, idx=i5, weight=w5)
-    torch.cuda.synchronize()
-    ms5, _ = time_graph(torch, lambda: pre.forward(x5, l5, out=o5, idx=i5, weight=w5), 10)
-    # parity: the first 64 tokens against the integer-first oracle (tokens are
-    # independent once routed)
-    n_chk = 64
-    p5 = pool5.cpu().numpy()
-    ref5, ri5, _ = orc.moe_layer([p5[0, e] for e in range(E)], [p5[1, e] for e in range(E)],
-                                 [p5[2, e] for e in range(E)], None, x5_h[:n_chk],
-                                 logits=l5_h[:n_chk], hidden=H, n_ff=F, k=K, prefill=True,
-                                 n_threads=max(1, (os.cpu_count() or 2) // 2))
-    o5_h = o5[:n_chk].cpu().numpy()
-    floor = 1e-3 * np.abs(ref5).max()
-    rel5 = float((np.abs(o5_h - ref5) / np.maximum(np.abs(ref5), floor)).max())
-    exact5 = bool((o5_h == ref5).all()) and bool((i5[:n_chk, :K].cpu().numpy()
-                                                  == ri5[:, :K]).all())
-    routes5 = T5 * K
-    bytes5 = E * 3 * MAT_BYTES + T5 * (H // 256) * 276 + T5 * H * 4 + T5 * E * 4
-    ops5 = routes5 * 3 * F * H * 2
-    us5 = ms5 * 1e3
-    config5 = {"us_per_chunk": round(us5, 1), "tokens": T5,
-               "hbm": {"gbs": round(bytes5 / (us5 * 1e-6) / 1e9, 1),
-                       "frac": round(bytes5 / (us5 * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-                       "algorithmic_bytes": bytes5},
-               "mfma_int8": {"tops": round(ops5 / (us5 * 1e-6) / 1e12, 2),
-                             "frac": round(ops5 / (us5 * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4),
-                             "ops": ops5},
-               "parity_first_64_tokens": {"bit_exact": exact5, "max_rel_err": rel5},
-               "workload": "2048 tokens x hidden 2048, U(0,1) logits, top-8 of 256 Q4_K experts "
-                           "(all touched), no shared expert; Q8_K(x), router, device plan, "
-                           "grouped int8-MFMA gate/up+SiLU and down, combine; one HIP graph"}
-    del pre, pool5
-    torch.cuda.synchronize()
+    config5 = run_config5(torch, np, ops, gen, orc, q4k_random_dev)
+
 
     cpu = None
     if not args.no_cpu:

@@ -205,7 +205,8 @@ struct GroupedArgs {
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (w >> (8 * i)) & 0xFF; }
 
 template <bool kGateUp>
-__global__ void __launch_bounds__(kThreads) grouped_mfma_kernel(GroupedArgs a) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
+grouped_mfma_kernel(GroupedArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[2][kWBufWords];
   __shared__ __attribute__((aligned(16))) uint32_t xbuf[2][kXBufWords];
   __shared__ int trow[kTokTile];
@@ -223,10 +224,14 @@ __global__ void __launch_bounds__(kThreads) grouped_mfma_kernel(GroupedArgs a) {
   const int rows_out = kGateUp ? kRowsWg / 2 : kRowsWg;
   const int r0 = blockIdx.x * rows_out;
   const int lr = lane & 15, lq = lane >> 4;  // MFMA: row/column in the tile, K quarter
-  const int tb = wave & 3, rh = wave >> 2;   // the wave's token block and row half
-  // the wave's four row blocks: gate/up -> gate 2rh, 2rh+1 and up 4+2rh, 4+2rh+1
-  // (h rows 32rh .. 32rh+31); down -> 4rh .. 4rh+3
-  auto rblk = [&](int j) { return kGateUp ? (j < 2 ? 2 * rh + j : 4 + 2 * rh + (j - 2)) : 4 * rh + j; };
+  // the wave's MFMA tiles: NT token blocks (16 tokens) x NR row blocks (16
+  // weight rows).  gate/up: h row block hb = w&3 - gate block hb and up block
+  // 4+hb, so SiLU pairs meet in one lane - for token blocks 2(w>>2), +1;
+  // down: row block w for all four token blocks.  Weight-side work (nibble
+  // unpack, scales) is shared by the NT token blocks.
+  constexpr int NT = kGateUp ? 2 : 4, NR = kGateUp ? 2 : 1;
+  auto tblk = [&](int ti) { return kGateUp ? 2 * (wave >> 2) + ti : ti; };
+  auto rblk = [&](int ri) { return kGateUp ? (ri ? 4 + (wave & 3) : (wave & 3)) : wave; };
 
   if (!ma || !mb || !mc) {  // absent expert: its outputs are zero
     for (long long p = p0; p < p1; ++p)
@@ -298,11 +303,13 @@ __global__ void __launch_bounds__(kThreads) grouped_mfma_kernel(GroupedArgs a) {
     }
     bar();
     set_x_offsets();
-    float acc[4][4];
+    float acc[NT][NR][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int ti = 0; ti < NT; ++ti)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[j][i] = 0.f;
+      for (int ri = 0; ri < NR; ++ri)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[ti][ri][i] = 0.f;
 
     stage_w(0, 0);
     stage_x(0, 0);
@@ -316,101 +323,116 @@ __global__ void __launch_bounds__(kThreads) grouped_mfma_kernel(GroupedArgs a) {
       }
       const uint32_t* W = wbuf[s];
       const uint32_t* X = xbuf[s];
-      // the lane's four output tokens are the MFMA result rows tx .. tx+3;
-      // its weight row in row block j is 16 rblk(j) + lr
-      const int tx = 16 * tb + 4 * lq;
-      // M = sum_s mn_s * bsum_s by MFMA: A = the wave's 16 tokens' eight
-      // bsums split exactly as 128*hi + lo (both int8), B = the rows' eight
-      // 6-bit mins; K = the 8 sub-blocks in the first K quarter, zeros in
-      // the other three.  M = 128 * C(hi) + C(lo).
-      long am_lo = 0, am_hi = 0;
-      if (lq == 0) {
-        const uint32_t* brow = X + (16 * tb + lr) * kXRow + 64;
+      // tile (ti, ri): the lane's four output tokens are the MFMA result rows
+      // 16 tblk(ti) + 4lq + i, its weight row is 16 rblk(ri) + lr.
+      // M = sum_s mn_s * bsum_s by MFMA: A = a token block's eight bsums
+      // split exactly as 128*hi + lo (both int8), B = the rows' eight 6-bit
+      // mins; K = the 8 sub-blocks in the first K quarter, zeros elsewhere.
+      // M = 128 * C(hi) + C(lo).
+      long am_lo[NT], am_hi[NT];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t bw = brow[q];
+      for (int ti = 0; ti < NT; ++ti) {
+        am_lo[ti] = 0;
+        am_hi[ti] = 0;
+        if (lq == 0) {
+          const uint32_t* brow = X + (16 * tblk(ti) + lr) * kXRow + 64;
 #pragma unroll
-          for (int h2 = 0; h2 < 2; ++h2) {
-            const int bsv = static_cast<int16_t>(h2 ? (bw >> 16) : (bw & 0xFFFFu));
-            const int hi = bsv >> 7, lo = bsv - 128 * hi;  // hi in [-32, 31], lo in [0, 127]
-            am_hi |= static_cast<long>(hi & 0xFF) << (8 * (2 * q + h2));
-            am_lo |= static_cast<long>(lo) << (8 * (2 * q + h2));
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t bw = brow[q];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int bsv = static_cast<int16_t>(h2 ? (bw >> 16) : (bw & 0xFFFFu));
+              const int hi = bsv >> 7, lo = bsv - 128 * hi;  // hi in [-32, 31], lo in [0, 127]
+              am_hi[ti] |= static_cast<long>(hi & 0xFF) << (8 * (2 * q + h2));
+              am_lo[ti] |= static_cast<long>(lo) << (8 * (2 * q + h2));
+            }
           }
         }
       }
-      ScaleMins smj[4];
-      int I[4][4], M[4][4];
+      ScaleMins smr[NR];
+      int I[NT][NR][4], M[NT][NR][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t* wr = W + (16 * rblk(j) + lr) * kWRowWords;
-        smj[j] = unpack_scales(wr[1], wr[2], wr[3]);
+      for (int ri = 0; ri < NR; ++ri) {
+        const uint32_t* wr = W + (16 * rblk(ri) + lr) * kWRowWords;
+        smr[ri] = unpack_scales(wr[1], wr[2], wr[3]);
         const long bmn =
-            lq == 0 ? static_cast<long>(smj[j].mn_lo) | (static_cast<long>(smj[j].mn_hi) << 32)
+            lq == 0 ? static_cast<long>(smr[ri].mn_lo) | (static_cast<long>(smr[ri].mn_hi) << 32)
                     : 0l;
-        const v4i z = {0, 0, 0, 0};
-        const v4i ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(am_hi, bmn, z, 0, 0, 0);
-        const v4i cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(am_lo, bmn, z, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          M[j][i] = ch[i] * 128 + cl[i];
-          I[j][i] = 0;
-        }
-      }
-      // the lane's A row: 8 qs bytes per sub-block, 64-bit aligned
-      const long* xa = reinterpret_cast<const long*>(X + (16 * tb + lr) * kXRow) + lq;
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {  // sub-blocks 2gq (low nibbles) and 2gq+1 (high)
-        const long a0 = xa[8 * gq];
-        const long a1 = xa[8 * gq + 4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const unsigned long q = *reinterpret_cast<const unsigned long*>(
-              W + (16 * rblk(j) + lr) * kWRowWords + 4 + 8 * gq + 2 * lq);
-          const long b0 = static_cast<long>(q & 0x0F0F0F0F0F0F0F0Ful);
-          const long b1 = static_cast<long>((q >> 4) & 0x0F0F0F0F0F0F0F0Ful);
+        for (int ti = 0; ti < NT; ++ti) {
           const v4i z = {0, 0, 0, 0};
-          const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, z, 0, 0, 0);
-          const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, z, 0, 0, 0);
-          const uint32_t scw = gq < 2 ? smj[j].sc_lo : smj[j].sc_hi;
-          const int sc0 = sbyte(scw, (2 * gq) & 3), sc1 = sbyte(scw, (2 * gq + 1) & 3);
-          // |ip| <= 32*15*127 and sc <= 63: 24-bit multiplies are exact
+          const v4i ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(am_hi[ti], bmn, z, 0, 0, 0);
+          const v4i cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(am_lo[ti], bmn, z, 0, 0, 0);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            // sign-extension from 24 bits tells the compiler the dots fit
-            // v_mad_i32_i24 (it drops the shifts: the op ignores bits 24+)
-            const int d0 = (c0[i] << 8) >> 8, d1 = (c1[i] << 8) >> 8;
-            I[j][i] += sc0 * d0;
-            I[j][i] += sc1 * d1;
+            M[ti][ri][i] = ch[i] * 128 + cl[i];
+            I[ti][ri][i] = 0;
           }
         }
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t dd = W[(16 * rblk(j) + lr) * kWRowWords];
+      for (int gq = 0; gq < 4; ++gq) {  // sub-blocks 2gq (low nibbles) and 2gq+1 (high)
+        long a0[NT], a1[NT];
+#pragma unroll
+        for (int ti = 0; ti < NT; ++ti) {  // the lane's A rows: 8 qs bytes per sub-block
+          const long* xa = reinterpret_cast<const long*>(X + (16 * tblk(ti) + lr) * kXRow) + lq;
+          a0[ti] = xa[8 * gq];
+          a1[ti] = xa[8 * gq + 4];
+        }
+#pragma unroll
+        for (int ri = 0; ri < NR; ++ri) {
+          const unsigned long q = *reinterpret_cast<const unsigned long*>(
+              W + (16 * rblk(ri) + lr) * kWRowWords + 4 + 8 * gq + 2 * lq);
+          const long b0 = static_cast<long>(q & 0x0F0F0F0F0F0F0F0Ful);
+          const long b1 = static_cast<long>((q >> 4) & 0x0F0F0F0F0F0F0F0Ful);
+          const uint32_t scw = gq < 2 ? smr[ri].sc_lo : smr[ri].sc_hi;
+          const int sc0 = sbyte(scw, (2 * gq) & 3), sc1 = sbyte(scw, (2 * gq + 1) & 3);
+#pragma unroll
+          for (int ti = 0; ti < NT; ++ti) {
+            const v4i z = {0, 0, 0, 0};
+            const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0[ti], b0, z, 0, 0, 0);
+            const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1[ti], b1, z, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              // |ip| <= 32*15*127 fits 24 bits: sign-extending from bit 23
+              // lets the compiler use the 24-bit multiply (it drops the shifts)
+              const int d0 = (c0[i] << 8) >> 8, d1 = (c1[i] << 8) >> 8;
+              I[ti][ri][i] += sc0 * d0;
+              I[ti][ri][i] += sc1 * d1;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int ri = 0; ri < NR; ++ri) {
+        const uint32_t dd = W[(16 * rblk(ri) + lr) * kWRowWords];
         const float d = half_bits_to_float(dd & 0xFFFFu);
         const float dmin = half_bits_to_float(dd >> 16);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float xd = __builtin_bit_cast(float, X[(tx + i) * kXRow + 68]);  // chunk 17
-          const float t = __builtin_fmaf(d, static_cast<float>(I[j][i]),
-                                         -(dmin * static_cast<float>(M[j][i])));
-          acc[j][i] = __builtin_fmaf(xd, t, acc[j][i]);
+        for (int ti = 0; ti < NT; ++ti) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float xd =
+                __builtin_bit_cast(float, X[(16 * tblk(ti) + 4 * lq + i) * kXRow + 68]);
+            const float t = __builtin_fmaf(d, static_cast<float>(I[ti][ri][i]),
+                                           -(dmin * static_cast<float>(M[ti][ri][i])));
+            acc[ti][ri][i] = __builtin_fmaf(xd, t, acc[ti][ri][i]);
+          }
         }
       }
     }
-    // outputs of the lane's four tokens
-    const int tx = 16 * tb + 4 * lq;
+    // outputs of the lane's tokens
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (tx + i >= nt) continue;
-      float* orow = a.out + static_cast<long long>(t0 + tx + i) * a.n_out + r0;
-      if (kGateUp) {  // gate blocks j = 0, 1 pair with up blocks j = 2, 3
+    for (int ti = 0; ti < NT; ++ti) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          orow[16 * (2 * rh + j) + lr] = silu_mul(acc[j][i], acc[j + 2][i]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) orow[16 * (4 * rh + j) + lr] = acc[j][i];
+      for (int i = 0; i < 4; ++i) {
+        const int tt = 16 * tblk(ti) + 4 * lq + i;
+        if (tt >= nt) continue;
+        float* orow = a.out + static_cast<long long>(t0 + tt) * a.n_out + r0;
+        if (kGateUp)  // gate block wave&3 pairs with up block 4 + wave&3: h row block wave&3
+          orow[16 * (wave & 3) + lr] = silu_mul(acc[ti][0][i], acc[ti][NR - 1][i]);
+        else
+          orow[16 * wave + lr] = acc[ti][0][i];
       }
     }
     bar();  // the next token tile reuses both buffers and trow
