@@ -174,14 +174,41 @@ def run_config5(torch, np, ops, gen, orc, q4k_random_dev, reps=10):
     return config5
 
 
+def traffic_run(torch, np, layers, n_steps=32):
+    """Dispatches for the HBM-traffic passes: a plain 256 MiB device copy
+    (the scale reference: it reads and writes exactly 256 MiB), then n_steps
+    config-2 decode steps on rotated layers as separate front and back
+    launches."""
+    src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    rng = np.random.default_rng(9)
+    xs = torch.from_numpy(rng.normal(0, 1, (n_steps, H)).astype(np.float32)).cuda()
+    lgs = torch.from_numpy(rng.normal(0, 1, (n_steps, E)).astype(np.float32)).cuda()
+    out = torch.empty((n_steps, H), dtype=torch.float32, device="cuda")
+    idx = torch.empty((n_steps, K + 1), dtype=torch.int32, device="cuda")
+    wgt = torch.empty((n_steps, K + 1), dtype=torch.float32, device="cuda")
+    for i in range(n_steps):
+        for st in (1, 2):
+            layers[i % N_LAYERS].forward(xs[i:i + 1], lgs[i:i + 1], out=out[i:i + 1],
+                                         idx=idx[i:i + 1], weight=wgt[i:i + 1], stages=st)
+    torch.cuda.synchronize()
+    print(json.dumps({"traffic_run": {"copy_bytes": 2 * src.numel() * 4, "steps": n_steps}}),
+          flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["5"], default=None,
-                    help="run one leg alone (5: the config-5 prefill chunk) and print its JSON")
+    ap.add_argument("--only", choices=["5", "traffic"], default=None,
+                    help="run one leg alone and print its JSON: 5 = the config-5 prefill "
+                         "chunk; traffic = eager config-2 front/back launches beside a plain "
+                         "256 MiB copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -206,6 +233,8 @@ def main():
         f"({N_LAYERS * 3 * (E + 1) * MAT_BYTES / 1e9:.1f} GB)")
     pool = build_pool(torch, N_LAYERS, gen)
     layers = make_layers(torch, ops, pool)
+    if args.only == "traffic":
+        return traffic_run(torch, np, layers)
 
     n_in = args.steps + args.warmup
     rng = np.random.default_rng(2)
@@ -429,6 +458,15 @@ def main():
         cpu, _ = cpu_baseline(l0, xs, lgs)
 
     fr_gbs = front_bytes / (front_us * 1e-6) / 1e9
+    # HBM bytes per front launch from the two rocprofv3 counter passes over
+    # `bench.py --only traffic` (FETCH_SIZE, WRITE_SIZE, scaled by a 256 MiB
+    # copy), committed under profiles/
+    traffic = None
+    try:
+        with open(os.path.join(ROOT, "profiles", "moe_layer_config2_traffic.json")) as fh:
+            traffic = json.load(fh)["layer_front_kernel"]["hbm_bytes"]
+    except (OSError, KeyError, ValueError):
+        traffic = None
     res = {
         "metric": "MoE layer decode us/token at top-8/256 (Q4_K experts, batch 1)",
         "value": round(us_per_token, 3),
@@ -447,7 +485,7 @@ def main():
                    "layers_rotated": N_LAYERS, "timing": "HIP graph of K steps"},
         "roofline": {"kernel": "layer_front_kernel (routing + 9 experts x gate/up + SiLU)",
                      "bound": "hbm", "achieved": round(fr_gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(fr_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(fr_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": front_bytes, "avg_us": round(front_us, 3)},
         "cpu_baseline": cpu,
         "parity": {"checked_steps": len(chk), "max_rel_err": max_rel, "bit_exact": bit_exact},
