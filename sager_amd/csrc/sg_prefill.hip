@@ -360,6 +360,7 @@ grouped_mfma_kernel(GroupedArgs a) {
                     : 0l;
 #pragma unroll
         for (int ti = 0; ti < NT; ++ti) {
+          if (16 * tblk(ti) >= nt) continue;
           const v4i z = {0, 0, 0, 0};
           const v4i ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(am_hi[ti], bmn, z, 0, 0, 0);
           const v4i cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(am_lo[ti], bmn, z, 0, 0, 0);
@@ -389,6 +390,7 @@ grouped_mfma_kernel(GroupedArgs a) {
           const int sc0 = sbyte(scw, (2 * gq) & 3), sc1 = sbyte(scw, (2 * gq + 1) & 3);
 #pragma unroll
           for (int ti = 0; ti < NT; ++ti) {
+            if (16 * tblk(ti) >= nt) continue;  // wave-uniform: a token block past the tile's end
             const v4i z = {0, 0, 0, 0};
             const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0[ti], b0, z, 0, 0, 0);
             const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1[ti], b1, z, 0, 0, 0);
@@ -410,6 +412,7 @@ grouped_mfma_kernel(GroupedArgs a) {
         const float dmin = half_bits_to_float(dd >> 16);
 #pragma unroll
         for (int ti = 0; ti < NT; ++ti) {
+          if (16 * tblk(ti) >= nt) continue;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float xd =
