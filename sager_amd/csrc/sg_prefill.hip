@@ -62,7 +62,8 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total)
 __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
     const int* __restrict__ idx, float* __restrict__ weight, int* __restrict__ gslot,
     int* __restrict__ grows, int* __restrict__ off, int* __restrict__ toff,
-    int* __restrict__ meta, int n_rows, int k, int n_expert, int tok_per, int shared_tail) {
+    int* __restrict__ meta, int* __restrict__ tiles, int n_rows, int k, int n_expert, int tok_per,
+    int shared_tail) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   __shared__ int s_bad, s_dup, s_total;
   const int E = n_expert, W = (n_rows + 31) / 32;
@@ -126,6 +127,13 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
       meta[2] = s_bad;
       s_total = tot_h;
     }
+    if (tiles) {  // the work list: tiles[0] = count, then (group << 16 | tile) in group order
+      if (tid < E)
+        for (int j = 0; j < tl; ++j) tiles[1 + pt + j] = (tid << 16) | j;
+      const int sh_t = (shared_tail + tok_per - 1) / tok_per;
+      for (int j = tid; j < sh_t; j += nth) tiles[1 + tot_t + j] = (E << 16) | j;
+      if (tid == 0) tiles[0] = tot_t + sh_t;
+    }
   }
   __syncthreads();
   if (!s_dup) {
@@ -182,8 +190,11 @@ constexpr int kTokTile = 64;
 constexpr int kRowsWg = 128;                 // weight rows per workgroup
 constexpr int kWRowWords = 36;               // one 144-B block
 constexpr int kWBufWords = kRowsWg * kWRowWords;   // 18 KB
-constexpr int kXRow = 72;                           // staged Q8_K block: qs, bsums, d, pad
-constexpr int kXBufWords = kTokTile * kXRow;        // 17.5 KB
+// staged Q8_K block: qs, bsums, d, pad.  76 words = 19 16-B chunks: the
+// stride is 12 banks mod 32, so eight lanes reading 16 B of eight
+// consecutive rows (one ds_read_b128 pass) touch every bank once.
+constexpr int kXRow = 76;
+constexpr int kXBufWords = kTokTile * kXRow;        // 19 KB
 constexpr int kThreads = 512;                 // eight waves
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -198,11 +209,23 @@ struct GroupedArgs {
   const unsigned char* xq;  // Q8_K rows: x [T][nb] (gate/up) or h [P][nb] (down)
   const int* off;           // [G+1] position range of each group
   const int* grows;         // [P] token of each position (gate/up only)
-  float* out;               // h [P][n_out] (gate/up) or y [P][n_out] (down)
-  int nb, n_out, n_expert, n_groups;
+  const int* tiles;         // work list: [0] = count, then group << 16 | tile index
+  float* out;               // [P][n_out]: gate|up (gate/up pass) or y (down)
+  int nb;                   // super-blocks per weight row
+  int n_rows;               // rows of each weight matrix
+  int n_out;                // output row stride: 2 n_rows (gate/up) or n_rows (down)
+  int n_expert, n_groups;
 };
 
-__device__ __forceinline__ int sbyte(uint32_t w, int i) { return (w >> (8 * i)) & 0xFF; }
+// a pointer the caller knows to be wave-uniform, moved to scalar registers
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uintptr_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 
 template <bool kGateUp>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
@@ -211,50 +234,46 @@ grouped_mfma_kernel(GroupedArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t xbuf[2][kXBufWords];
   __shared__ int trow[kTokTile];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = blockIdx.y;
-  if (g >= a.n_groups) return;
-  static_assert(kThreads == 512, "eight waves: 4 token blocks x 2 row halves");
-  const int p0 = a.off[g], p1 = a.off[g + 1];
-  if (p0 >= p1) return;
+  static_assert(kThreads == 512, "eight waves, one 16-row block each");
+  // one tile (up to kTokTile positions of one group) per workgroup row
+  if (static_cast<int>(blockIdx.y) >= a.tiles[0]) return;
+  const int item = a.tiles[1 + blockIdx.y];
+  const int g = item >> 16;
+  const int p0 = a.off[g] + kTokTile * (item & 0xFFFF);
+  const int p1 = min(a.off[g + 1], p0 + kTokTile);
+  if (g >= a.n_groups || p0 >= p1) return;
   const bool shared = g >= a.n_expert;
   const sg_block_q4k* ma = shared ? a.sh_a : a.tab_a[g];
   const sg_block_q4k* mb = kGateUp ? (shared ? a.sh_b : a.tab_b[g]) : ma;
   const sg_block_q4k* mc = shared ? a.sh_c : a.tab_c[g];
   const int nb = a.nb;
-  const int rows_out = kGateUp ? kRowsWg / 2 : kRowsWg;
-  const int r0 = blockIdx.x * rows_out;
-  const int lr = lane & 15, lq = lane >> 4;  // MFMA: row/column in the tile, K quarter
-  // the wave's MFMA tiles: NT token blocks (16 tokens) x NR row blocks (16
-  // weight rows).  gate/up: h row block hb = w&3 - gate block hb and up block
-  // 4+hb, so SiLU pairs meet in one lane - for token blocks 2(w>>2), +1;
-  // down: row block w for all four token blocks.  Weight-side work (nibble
-  // unpack, scales) is shared by the NT token blocks.
-  constexpr int NT = kGateUp ? 2 : 4, NR = kGateUp ? 2 : 1;
-  auto tblk = [&](int ti) { return kGateUp ? 2 * (wave >> 2) + ti : ti; };
-  auto rblk = [&](int ri) { return kGateUp ? (ri ? 4 + (wave & 3) : (wave & 3)) : wave; };
+  // output columns [c0, c0 + 128); gate/up: the gate rows fill columns
+  // [0, n_rows) and the up rows [n_rows, 2 n_rows)
+  const int c0 = blockIdx.x * kRowsWg;
+  const bool second = kGateUp && c0 >= a.n_rows;
+  const int r0 = second ? c0 - a.n_rows : c0;  // first weight row of the matrix
+  const int lr = lane & 15, lq = lane >> 4;     // MFMA: row/column in the tile, K quarter
 
   if (!ma || !mb || !mc) {  // absent expert: its outputs are zero
     for (long long p = p0; p < p1; ++p)
-      for (int r = tid; r < rows_out; r += kThreads) a.out[p * a.n_out + r0 + r] = 0.f;
+      for (int r = tid; r < kRowsWg; r += kThreads) a.out[p * a.n_out + c0 + r] = 0.f;
     return;
   }
 
-  // weight rows of super-block b into wbuf[s]: gate/up -> 64 gate rows then
-  // the same 64 up rows; down -> 128 rows.  Wave w copies chunks
-  // [144w, 144w+144) (16 B each, chunk c = part c%9 of row c/9), all from one
-  // matrix; the per-lane offsets are fixed for the kernel, the block's
-  // offset b*144 goes in the scalar offset (buffer_load ... lds).
+  // weight rows r0 .. r0+127 of super-block b into wbuf[s].  Wave w copies
+  // chunks [144w, 144w+144) (16 B each, chunk c = part c%9 of row c/9); the
+  // per-lane offsets are fixed for the kernel, the block's offset b*144 goes
+  // in the scalar offset (buffer_load ... lds).
   constexpr int kWChunks = kRowsWg * 9 / 8;  // 144 per wave
-  const sg_block_q4k* mw = (kGateUp && wave >= 4) ? mb : ma;
+  const sg_block_q4k* mw = uniform_ptr(second ? mb : ma);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<sg_block_q4k*>(mw), 0, a.n_out * nb * kQ4Bytes, 0x00020000);
+      const_cast<sg_block_q4k*>(mw), 0, a.n_rows * nb * kQ4Bytes, 0x00020000);
   uint32_t wofs[3];
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
     const int cc = min(wave * kWChunks + lane + 64 * i, kRowsWg * 9 - 1);
     const int row = cc / 9, part = cc - row * 9;
-    const int rr = kGateUp ? (row & 63) : row;
-    wofs[i] = static_cast<uint32_t>((r0 + rr) * nb) * kQ4Bytes + 16 * part;
+    wofs[i] = static_cast<uint32_t>((r0 + row) * nb) * kQ4Bytes + 16 * part;
   }
   auto stage_w = [&](int b, int s) {
 #pragma unroll
@@ -264,27 +283,19 @@ grouped_mfma_kernel(GroupedArgs a) {
             rw, (lds_void_p)(wbuf[s] + 4 * (wave * kWChunks + 64 * i)), 16, wofs[i],
             b * kQ4Bytes, 0, 0);
   };
-  // the tile's token blocks of super-block b into xbuf[s], 72 words per
-  // token in 16-B chunks: chunks 0-15 the 64 qs words (64-bit aligned for
-  // the MFMA operand reads), 16 the 4 words of int16 bsums, 17 d and three
-  // pad words.  LDS chunk c = 18t + j is filled from the matching 16 B of
-  // token t's block (buffer_load_dwordx4 ... lds: lane-consecutive chunks
-  // land LDS-consecutive); offsets are set per token tile, b*276 is the
-  // scalar offset.
-  constexpr int kXChunks = kTokTile * kXRow / 4;                 // 1152
-  constexpr int kXInstr = (kXChunks / 64 + 7) / 8;               // per wave: 3
+  // the tile's token rows of super-block b into xbuf[s], 76 words per token
+  // in 16-B chunks: chunks 0-15 the 64 qs words, 16 the split bsums (eight
+  // lo bytes, eight hi bytes), 17 d and three pad words, 18 padding (a copy
+  // of chunk 17).  LDS chunk c = 19t + j is filled from
+  // the matching 16 B of token t's block (buffer_load_dwordx4 ... lds:
+  // lane-consecutive chunks land LDS-consecutive); offsets are set per
+  // token tile, b*276 is the scalar offset.
+  constexpr int kXChunks = kTokTile * kXRow / 4;    // 1216 = 19 instructions
+  static_assert(kXChunks % 64 == 0, "whole instructions");
+  constexpr int kXInstr = (kXChunks / 64 + 7) / 8;  // per wave: 3
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<unsigned char*>(a.xq), 0, 0x7FFFFFFF, 0x00020000);
   uint32_t xofs[kXInstr];
-  auto set_x_offsets = [&]() {
-#pragma unroll
-    for (int i = 0; i < kXInstr; ++i) {
-      const int c = min(64 * (wave + 8 * i) + lane, kXChunks - 1);
-      const int t = c / 18, j = c - t * 18;
-      const int gw = j < 16 ? 1 + 4 * j : (j == 16 ? 65 : 0);  // qs, bsums, then d
-      xofs[i] = static_cast<uint32_t>(trow[t]) * kQ8Bytes + 4 * gw;
-    }
-  };
   auto stage_x = [&](int b, int s) {
 #pragma unroll
     for (int i = 0; i < kXInstr; ++i) {
@@ -295,151 +306,151 @@ grouped_mfma_kernel(GroupedArgs a) {
     }
   };
 
-  for (int t0 = p0; t0 < p1; t0 += kTokTile) {
-    const int nt = min(kTokTile, p1 - t0);
-    if (tid < kTokTile) {  // block index of each token row (tokens past nt repeat the first)
-      const int t = tid < nt ? tid : 0;
-      trow[tid] = (kGateUp ? a.grows[t0 + t] : t0 + t) * nb;
-    }
-    bar();
-    set_x_offsets();
-    float acc[NT][NR][4];
+  const int t0 = p0, nt = p1 - p0;
+  if (tid < kTokTile) {  // block index of each token row (rows past nt repeat the first)
+    const int t = tid < nt ? tid : 0;
+    trow[tid] = (kGateUp ? a.grows[t0 + t] : t0 + t) * nb;
+  }
+  bar();
 #pragma unroll
-    for (int ti = 0; ti < NT; ++ti)
+  for (int i = 0; i < kXInstr; ++i) {
+    const int c = min(64 * (wave + 8 * i) + lane, kXChunks - 1);
+    const int t = c / 19, j = c - t * 19;
+    const int gw = j < 16 ? 1 + 4 * j : (j == 16 ? 65 : 0);  // qs, bsums, then d
+    xofs[i] = static_cast<uint32_t>(trow[t]) * kQ8Bytes + 4 * gw;
+  }
+  // the wave's MFMA tiles: token blocks ti = 0..3 (16 tokens each) of weight
+  // row block `wave`; the lane's four output tokens of block ti are the MFMA
+  // result rows 16ti + 4lq + i, its weight row is 16 wave + lr.  The
+  // weight-side work (nibble unpack, scales) is shared by the four blocks.
+  constexpr int NT = 4;
+  const int ntb = (nt + 15) >> 4;  // token blocks holding tokens (wave-uniform)
+  float acc[NT][4];
 #pragma unroll
-      for (int ri = 0; ri < NR; ++ri)
+  for (int ti = 0; ti < NT; ++ti)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[ti][ri][i] = 0.f;
+    for (int i = 0; i < 4; ++i) acc[ti][i] = 0.f;
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  auto pmul = [](uint32_t q, uint32_t s2) -> int {  // 4 bytes x s2 (the same 16 bits twice)
+    return __builtin_bit_cast(int, __builtin_bit_cast(u16x2, q) * __builtin_bit_cast(u16x2, s2));
+  };
 
-    stage_w(0, 0);
-    stage_x(0, 0);
-    for (int b = 0; b < nb; ++b) {
-      const int s = b & 1;
-      wait_vm();  // this wave's copies of block b have landed
-      bar();      // ... and every wave's
-      if (b + 1 < nb) {  // the next block streams in while this one computes
-        stage_w(b + 1, s ^ 1);
-        stage_x(b + 1, s ^ 1);
-      }
-      const uint32_t* W = wbuf[s];
-      const uint32_t* X = xbuf[s];
-      // tile (ti, ri): the lane's four output tokens are the MFMA result rows
-      // 16 tblk(ti) + 4lq + i, its weight row is 16 rblk(ri) + lr.
-      // M = sum_s mn_s * bsum_s by MFMA: A = a token block's eight bsums
-      // split exactly as 128*hi + lo (both int8), B = the rows' eight 6-bit
-      // mins; K = the 8 sub-blocks in the first K quarter, zeros elsewhere.
-      // M = 128 * C(hi) + C(lo).
-      long am_lo[NT], am_hi[NT];
+  stage_w(0, 0);
+  stage_x(0, 0);
+  for (int b = 0; b < nb; ++b) {
+    const int s = b & 1;
+    wait_vm();  // this wave's copies of block b have landed
+    bar();      // ... and every wave's
+    if (b + 1 < nb) {  // the next block streams in while this one computes
+      stage_w(b + 1, s ^ 1);
+      stage_x(b + 1, s ^ 1);
+    }
+    const uint32_t* W = wbuf[s] + (16 * wave + lr) * kWRowWords;
+    const uint32_t* X = xbuf[s];
+    // I = sum_s sc_s * ip_s with the 6-bit scale split as sc = 8*sh + sl
+    // (sh, sl in [0, 7]) and folded into the weight operand: nibble * sl
+    // and nibble * sh are at most 105, so each byte of the packed product
+    // stays an exact int8 and the products of four nibbles come from one
+    // packed 16-bit multiply (no carry crosses a byte).  Then
+    // I = 8 * C(sh) + C(sl), where each chain accumulates all eight
+    // sub-blocks inside the MFMA (16x16x64, four K groups of 64; a lane's
+    // A and B bytes only need to agree on the K order).  |C(sl)|, |C(sh)|
+    // <= 8*7*32*15*127 fit int32, so I is exact.
+    // The lane's 16 K bytes of group gq (64 weights) are 16 consecutive
+    // ones: k = 64gq + 16lq + j, i.e. sub-block 2gq + (lq >> 1), the low
+    // (lq < 2) or high nibbles of qs bytes 32gq + 16(lq & 1) + j - one
+    // ds_read_b128 on each side.
+    const ScaleMins sm = unpack_scales(W[1], W[2], W[3]);
+    const uint32_t scl[2] = {sm.sc_lo & 0x07070707u, sm.sc_hi & 0x07070707u};
+    const uint32_t sch[2] = {(sm.sc_lo >> 3) & 0x07070707u, (sm.sc_hi >> 3) & 0x07070707u};
+    const uint32_t nsh = 4 * (lq >> 1);                          // nibble of this lane
+    const uint32_t sel_l = 0x0C000C00u + 0x00010001u * (lq >> 1);  // its sub-block's byte
+    v4i cl[NT], ch[NT];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const uint4 q = *reinterpret_cast<const uint4*>(W + 4 + 8 * gq + 4 * (lq & 1));
+      // sl and sh of sub-block 2gq + (lq >> 1), spread to both 16-bit halves
+      const uint32_t sel = sel_l + 0x00010001u * ((2 * gq) & 3);
+      const uint32_t sl = __builtin_amdgcn_perm(0u, scl[gq >> 1], sel);
+      const uint32_t sh = __builtin_amdgcn_perm(0u, sch[gq >> 1], sel);
+      const uint32_t n0 = (q.x >> nsh) & 0x0F0F0F0Fu, n1 = (q.y >> nsh) & 0x0F0F0F0Fu;
+      const uint32_t n2 = (q.z >> nsh) & 0x0F0F0F0Fu, n3 = (q.w >> nsh) & 0x0F0F0F0Fu;
+      const v4i bl = {pmul(n0, sl), pmul(n1, sl), pmul(n2, sl), pmul(n3, sl)};
+      const v4i bh = {pmul(n0, sh), pmul(n1, sh), pmul(n2, sh), pmul(n3, sh)};
 #pragma unroll
       for (int ti = 0; ti < NT; ++ti) {
-        am_lo[ti] = 0;
-        am_hi[ti] = 0;
-        if (lq == 0) {
-          const uint32_t* brow = X + (16 * tblk(ti) + lr) * kXRow + 64;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t bw = brow[q];
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-              const int bsv = static_cast<int16_t>(h2 ? (bw >> 16) : (bw & 0xFFFFu));
-              const int hi = bsv >> 7, lo = bsv - 128 * hi;  // hi in [-32, 31], lo in [0, 127]
-              am_hi[ti] |= static_cast<long>(hi & 0xFF) << (8 * (2 * q + h2));
-              am_lo[ti] |= static_cast<long>(lo) << (8 * (2 * q + h2));
-            }
-          }
-        }
-      }
-      ScaleMins smr[NR];
-      int I[NT][NR][4], M[NT][NR][4];
-#pragma unroll
-      for (int ri = 0; ri < NR; ++ri) {
-        const uint32_t* wr = W + (16 * rblk(ri) + lr) * kWRowWords;
-        smr[ri] = unpack_scales(wr[1], wr[2], wr[3]);
-        const long bmn =
-            lq == 0 ? static_cast<long>(smr[ri].mn_lo) | (static_cast<long>(smr[ri].mn_hi) << 32)
-                    : 0l;
-#pragma unroll
-        for (int ti = 0; ti < NT; ++ti) {
-          if (16 * tblk(ti) >= nt) continue;
-          const v4i z = {0, 0, 0, 0};
-          const v4i ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(am_hi[ti], bmn, z, 0, 0, 0);
-          const v4i cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(am_lo[ti], bmn, z, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            M[ti][ri][i] = ch[i] * 128 + cl[i];
-            I[ti][ri][i] = 0;
-          }
-        }
-      }
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {  // sub-blocks 2gq (low nibbles) and 2gq+1 (high)
-        long a0[NT], a1[NT];
-#pragma unroll
-        for (int ti = 0; ti < NT; ++ti) {  // the lane's A rows: 8 qs bytes per sub-block
-          const long* xa = reinterpret_cast<const long*>(X + (16 * tblk(ti) + lr) * kXRow) + lq;
-          a0[ti] = xa[8 * gq];
-          a1[ti] = xa[8 * gq + 4];
-        }
-#pragma unroll
-        for (int ri = 0; ri < NR; ++ri) {
-          const unsigned long q = *reinterpret_cast<const unsigned long*>(
-              W + (16 * rblk(ri) + lr) * kWRowWords + 4 + 8 * gq + 2 * lq);
-          const long b0 = static_cast<long>(q & 0x0F0F0F0F0F0F0F0Ful);
-          const long b1 = static_cast<long>((q >> 4) & 0x0F0F0F0F0F0F0F0Ful);
-          const uint32_t scw = gq < 2 ? smr[ri].sc_lo : smr[ri].sc_hi;
-          const int sc0 = sbyte(scw, (2 * gq) & 3), sc1 = sbyte(scw, (2 * gq + 1) & 3);
-#pragma unroll
-          for (int ti = 0; ti < NT; ++ti) {
-            if (16 * tblk(ti) >= nt) continue;  // wave-uniform: a token block past the tile's end
-            const v4i z = {0, 0, 0, 0};
-            const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0[ti], b0, z, 0, 0, 0);
-            const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1[ti], b1, z, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              // |ip| <= 32*15*127 fits 24 bits: sign-extending from bit 23
-              // lets the compiler use the 24-bit multiply (it drops the shifts)
-              const int d0 = (c0[i] << 8) >> 8, d1 = (c1[i] << 8) >> 8;
-              I[ti][ri][i] += sc0 * d0;
-              I[ti][ri][i] += sc1 * d1;
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int ri = 0; ri < NR; ++ri) {
-        const uint32_t dd = W[(16 * rblk(ri) + lr) * kWRowWords];
-        const float d = half_bits_to_float(dd & 0xFFFFu);
-        const float dmin = half_bits_to_float(dd >> 16);
-#pragma unroll
-        for (int ti = 0; ti < NT; ++ti) {
-          if (16 * tblk(ti) >= nt) continue;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float xd =
-                __builtin_bit_cast(float, X[(16 * tblk(ti) + 4 * lq + i) * kXRow + 68]);
-            const float t = __builtin_fmaf(d, static_cast<float>(I[ti][ri][i]),
-                                           -(dmin * static_cast<float>(M[ti][ri][i])));
-            acc[ti][ri][i] = __builtin_fmaf(xd, t, acc[ti][ri][i]);
-          }
-        }
+        const uint4 xv = *reinterpret_cast<const uint4*>(X + (16 * ti + lr) * kXRow + 16 * gq + 4 * lq);
+        const v4i av = {static_cast<int>(xv.x), static_cast<int>(xv.y), static_cast<int>(xv.z),
+                        static_cast<int>(xv.w)};
+        const v4i z = {0, 0, 0, 0};
+        cl[ti] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bl, gq ? cl[ti] : z, 0, 0, 0);
+        ch[ti] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bh, gq ? ch[ti] : z, 0, 0, 0);
       }
     }
-    // outputs of the lane's tokens
+    // M = sum_s mn_s * bsum_s by MFMA: A = a token row's eight bsums split
+    // exactly as 128*hi + lo (hi in [-32, 31], lo in [0, 127], both int8,
+    // written so by the quantizer), B = the row's eight 6-bit mins in the
+    // first K quarter (lanes 0-15) and zeros elsewhere, so the other lanes'
+    // A bytes do not count.  M = 128 * C(hi) + C(lo).
+    const uint32_t dd = W[0];
+    const long bmn =
+        lq == 0 ? static_cast<long>(sm.mn_lo) | (static_cast<long>(sm.mn_hi) << 32) : 0l;
+    const float d = half_bits_to_float(dd & 0xFFFFu);
+    const float dmin = half_bits_to_float(dd >> 16);
 #pragma unroll
     for (int ti = 0; ti < NT; ++ti) {
+      if (ti >= ntb) continue;  // wave-uniform: a token block past the tile's end
+      const long* bs = reinterpret_cast<const long*>(X + (16 * ti + lr) * kXRow + 64);
+      const v4i z = {0, 0, 0, 0};
+      const v4i mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(bs[1], bmn, z, 0, 0, 0);
+      const v4i ml = __builtin_amdgcn_mfma_i32_16x16x32_i8(bs[0], bmn, z, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int tt = 16 * tblk(ti) + 4 * lq + i;
-        if (tt >= nt) continue;
-        float* orow = a.out + static_cast<long long>(t0 + tt) * a.n_out + r0;
-        if (kGateUp)  // gate block wave&3 pairs with up block 4 + wave&3: h row block wave&3
-          orow[16 * (wave & 3) + lr] = silu_mul(acc[ti][0][i], acc[ti][NR - 1][i]);
-        else
-          orow[16 * wave + lr] = acc[ti][0][i];
+        const int I = ch[ti][i] * 8 + cl[ti][i];
+        const int M = mh[i] * 128 + ml[i];
+        const float xd = __builtin_bit_cast(float, X[(16 * ti + 4 * lq + i) * kXRow + 68]);
+        const float t =
+            __builtin_fmaf(d, static_cast<float>(I), -(dmin * static_cast<float>(M)));
+        acc[ti][i] = __builtin_fmaf(xd, t, acc[ti][i]);
       }
     }
-    bar();  // the next token tile reuses both buffers and trow
   }
+  // outputs of the lane's tokens
+#pragma unroll
+  for (int ti = 0; ti < NT; ++ti) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tt = 16 * ti + 4 * lq + i;
+      if (tt < nt)
+        a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * wave + lr] = acc[ti][i];
+    }
+  }
+}
+
+// Q8_K blocks for the grouped kernels: the standard block except that the
+// 16-byte bsums field holds each sub-block sum s split as s = 128*hi + lo,
+// lo = s & 127 in bytes 0-7 and hi = s >> 7 (two's complement) in bytes
+// 8-15.  kSilu: the input row is [gate | up] of width 2n and the value
+// quantized is silu_mul(gate, up) (h of the reference's gate/up stage).
+template <bool kSilu>
+__global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __restrict__ in,
+                                                               unsigned char* __restrict__ out,
+                                                               long long n_blocks, int nb_row) {
+  const long long blk = static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (blk >= n_blocks) return;
+  float v[4];
+  if (kSilu) {
+    const long long row = blk / nb_row, j = blk - row * nb_row;
+    const float* gp = in + row * (2LL * nb_row * kQK) + j * kQK + 4 * lane;
+    const float* up = gp + static_cast<long long>(nb_row) * kQK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = silu_mul(gp[i], up[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = in[blk * kQK + 4 * lane + i];
+  }
+  quantize_block_wave<true>(v, out + blk * kQ8Bytes, lane);
 }
 
 // out[t] = residual[t] + sum_kk fma(w[t][kk], y[pos(t, kk)]) in slot order;
@@ -464,8 +475,9 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(
 
 // ---- workspace ------------------------------------------------------------------
 struct PrefillWs {
-  size_t xq, gslot, grows, off, toff, meta, h, hq, y, total;
-  int P;  // positions: T*k routes + T shared
+  size_t xq, gslot, grows, off, toff, meta, tiles, h, hq, y, total;
+  int P;          // positions: T*k routes + T shared
+  int max_tiles;  // bound on the work list: every group's last tile may be partial
 };
 
 static size_t al256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
@@ -480,11 +492,28 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
   w.off = o;   o = al256(o + static_cast<size_t>(E + 2) * 4);
   w.toff = o;  o = al256(o + static_cast<size_t>(E + 2) * 4);
   w.meta = o;  o = al256(o + 4 * 4);
-  w.h = o;     o = al256(o + static_cast<size_t>(w.P) * n_ff * 4);
+  w.max_tiles = (T * k + kTokTile - 1) / kTokTile + E + (T + kTokTile - 1) / kTokTile;
+  w.tiles = o; o = al256(o + static_cast<size_t>(1 + w.max_tiles) * 4);
+  w.h = o;     o = al256(o + static_cast<size_t>(w.P) * 2 * n_ff * 4);  // gate | up
   w.hq = o;    o = al256(o + static_cast<size_t>(w.P) * (n_ff / kQK) * kQ8Bytes);
   w.y = o;     o = al256(o + static_cast<size_t>(w.P) * hidden * 4);
   w.total = o;
   return w;
+}
+
+// the grouped kernels' Q8_K input (split bsums); kSilu: from [gate | up] rows
+static int quantize_split(const float* in, sg_block_q8k* out, int nb_row, int n_rows, bool silu,
+                          hipStream_t s, const char* nm) {
+  const long long n_blocks = static_cast<long long>(nb_row) * n_rows;
+  const unsigned grid = static_cast<unsigned>((n_blocks + 3) / 4);
+  unsigned char* o = reinterpret_cast<unsigned char*>(out);
+  if (silu)
+    hipLaunchKernelGGL(prefill_quantize_kernel<true>, dim3(grid), dim3(256), 0, s, in, o, n_blocks,
+                       nb_row);
+  else
+    hipLaunchKernelGGL(prefill_quantize_kernel<false>, dim3(grid), dim3(256), 0, s, in, o,
+                       n_blocks, nb_row);
+  return check_launch(nm);
 }
 
 constexpr int kScanLdsWords = 38 * 1024;  // dispatch scan: hist, offsets, parts, bitmap
@@ -494,14 +523,14 @@ static int scan_lds_words(int n_rows, int E) {
 }
 
 static int scan_launch(const int* idx, float* weight, int* gslot, int* grows, int* off, int* toff,
-                       int* meta, int n_rows, int k, int E, int tok_per, int shared_tail,
-                       hipStream_t s, const char* nm) {
+                       int* meta, int* tiles, int n_rows, int k, int E, int tok_per,
+                       int shared_tail, hipStream_t s, const char* nm) {
   const int words = scan_lds_words(n_rows, E);
   if (words > kScanLdsWords)
     return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows=%d x n_expert=%d too large for one scan",
                      nm, n_rows, E);
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), words * 4, s, idx, weight, gslot,
-                     grows, off, toff, meta, n_rows, k, E, tok_per, shared_tail);
+                     grows, off, toff, meta, tiles, n_rows, k, E, tok_per, shared_tail);
   return check_launch(nm);
 }
 
@@ -523,7 +552,8 @@ int sg_moe_dispatch_scan(const int* idx, float* weight, int* gslot, int* grows, 
   if (n_rows * k > 1024 * kScanPerThread)
     return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows*k=%d > %d", nm, n_rows * k,
                      1024 * kScanPerThread);
-  return scan_launch(idx, weight, gslot, grows, off, toff, meta, n_rows, k, n_expert, tok_per, 0,
+  return scan_launch(idx, weight, gslot, grows, off, toff, meta, nullptr, n_rows, k, n_expert,
+                     tok_per, 0,
                      static_cast<hipStream_t>(stream), nm);
 }
 
@@ -564,17 +594,18 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   int* off = reinterpret_cast<int*>(base + ws.off);
   int* toff = reinterpret_cast<int*>(base + ws.toff);
   int* meta = reinterpret_cast<int*>(base + ws.meta);
+  int* tiles = reinterpret_cast<int*>(base + ws.tiles);
   float* h = reinterpret_cast<float*>(base + ws.h);
   auto* hq = reinterpret_cast<sg_block_q8k*>(base + ws.hq);
   float* y = reinterpret_cast<float*>(base + ws.y);
   const int has_shared = n_sh == 3;
 
-  if (int st = sg_quantize_q8_k(x, xq, hidden, n_tokens, stream)) return st;
+  if (int st = quantize_split(x, xq, hidden / kQK, n_tokens, false, s, nm)) return st;
   if (logits)
     if (int st = sg_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w,
                                 stream))
       return st;
-  if (int st = scan_launch(idx, weight, gslot, grows, off, toff, meta, n_tokens, k, n_expert,
+  if (int st = scan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, n_tokens, k, n_expert,
                            kTokTile, has_shared ? n_tokens : 0, s, nm))
     return st;
   const int G = n_expert + has_shared;
@@ -588,15 +619,17 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   ga.xq = reinterpret_cast<const unsigned char*>(xq);
   ga.off = off;
   ga.grows = grows;
+  ga.tiles = tiles;
   ga.out = h;
   ga.nb = hidden / kQK;
-  ga.n_out = n_ff;
+  ga.n_rows = n_ff;
+  ga.n_out = 2 * n_ff;
   ga.n_expert = n_expert;
   ga.n_groups = G;
-  hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(n_ff / (kRowsWg / 2), G), dim3(kThreads), 0,
-                     s, ga);
+  hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(2 * n_ff / kRowsWg, ws.max_tiles),
+                     dim3(kThreads), 0, s, ga);
   if (int st = check_launch("sg_moe_prefill/gate_up")) return st;
-  if (int st = sg_quantize_q8_k(h, hq, n_ff, ws.P, stream)) return st;
+  if (int st = quantize_split(h, hq, n_ff / kQK, ws.P, true, s, nm)) return st;
   GroupedArgs gd = ga;
   gd.tab_a = tab_down;
   gd.tab_b = tab_down;
@@ -608,9 +641,10 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   gd.grows = nullptr;
   gd.out = y;
   gd.nb = n_ff / kQK;
+  gd.n_rows = hidden;
   gd.n_out = hidden;
-  hipLaunchKernelGGL(grouped_mfma_kernel<false>, dim3(hidden / kRowsWg, G), dim3(kThreads), 0, s,
-                     gd);
+  hipLaunchKernelGGL(grouped_mfma_kernel<false>, dim3(hidden / kRowsWg, ws.max_tiles),
+                     dim3(kThreads), 0, s, gd);
   if (int st = check_launch("sg_moe_prefill/down")) return st;
   hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 255) / 256, n_tokens), dim3(256), 0, s,
                      out, residual, y, weight, gslot, off, n_expert, k, hidden, has_shared);
