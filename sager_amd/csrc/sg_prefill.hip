@@ -66,15 +66,18 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
     int shared_tail) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   __shared__ int s_bad, s_dup, s_total;
-  const int E = n_expert, W = (n_rows + 31) / 32;
+  // W bitmap words per expert, stored at an odd stride WS: a wave's routes
+  // share a token word, and an even stride would put all their experts' words
+  // in one LDS bank
+  const int E = n_expert, W = (n_rows + 31) / 32, WS = W | 1;
   int* hist = reinterpret_cast<int*>(lds);       // [E]
   int* offl = hist + E;                          // [E]
   int* part = offl + E;                          // [1024]
   uint32_t* bm = reinterpret_cast<uint32_t*>(part + 1024);  // [E][W] token bitmap
-  int* pre = reinterpret_cast<int*>(bm + E * W);            // [E][W] routes before each word
+  int* pre = reinterpret_cast<int*>(bm + E * WS);           // [E][W] routes before each word
   const int tid = threadIdx.x, nth = blockDim.x;
   for (int i = tid; i < E; i += nth) hist[i] = 0;
-  for (int i = tid; i < E * W; i += nth) bm[i] = 0u;
+  for (int i = tid; i < E * WS; i += nth) bm[i] = 0u;
   if (tid == 0) {
     s_bad = 0;
     s_dup = 0;
@@ -104,7 +107,7 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
     }
     atomicAdd(&hist[e], 1);
     const uint32_t bit = 1u << (r & 31);
-    if (atomicOr(&bm[e * W + (r >> 5)], bit) & bit) s_dup = 1;
+    if (atomicOr(&bm[e * WS + (r >> 5)], bit) & bit) s_dup = 1;
   }
   __syncthreads();
   {  // exclusive prefix sums over the experts (E <= 1024: one per thread)
@@ -145,15 +148,15 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
     const int w0 = min(W, q * wpt), w1 = min(W, w0 + wpt);
     int c = 0;
     if (e < E)
-      for (int w = w0; w < w1; ++w) c += __popc(bm[e * W + w]);
+      for (int w = w0; w < w1; ++w) c += __popc(bm[e * WS + w]);
     part[tid] = c;
     __syncthreads();
     if (e < E) {
       int run = offl[e];
       for (int j = 0; j < q; ++j) run += part[e * tpe + j];
       for (int w = w0; w < w1; ++w) {
-        pre[e * W + w] = run;
-        run += __popc(bm[e * W + w]);
+        pre[e * WS + w] = run;
+        run += __popc(bm[e * WS + w]);
       }
     }
     __syncthreads();
@@ -166,8 +169,8 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
       const int r = i / k;
       const int ee = ids[j];
       if (ee < 0 || ee >= E) continue;
-      const uint32_t word = bm[ee * W + (r >> 5)];
-      const int pos = pre[ee * W + (r >> 5)] + __popc(word & ((1u << (r & 31)) - 1u));
+      const uint32_t word = bm[ee * WS + (r >> 5)];
+      const int pos = pre[ee * WS + (r >> 5)] + __popc(word & ((1u << (r & 31)) - 1u));
       gslot[i] = pos;
       grows[pos] = r;
     }
@@ -210,10 +213,10 @@ struct GroupedArgs {
   const int* off;           // [G+1] position range of each group
   const int* grows;         // [P] token of each position (gate/up only)
   const int* tiles;         // work list: [0] = count, then group << 16 | tile index
-  float* out;               // [P][n_out]: gate|up (gate/up pass) or y (down)
+  float* out;               // [P][n_out]: h (gate/up pass) or y (down)
   int nb;                   // super-blocks per weight row
   int n_rows;               // rows of each weight matrix
-  int n_out;                // output row stride: 2 n_rows (gate/up) or n_rows (down)
+  int n_out;                // output row stride (= n_rows)
   int n_expert, n_groups;
 };
 
@@ -247,25 +250,26 @@ grouped_mfma_kernel(GroupedArgs a) {
   const sg_block_q4k* mb = kGateUp ? (shared ? a.sh_b : a.tab_b[g]) : ma;
   const sg_block_q4k* mc = shared ? a.sh_c : a.tab_c[g];
   const int nb = a.nb;
-  // output columns [c0, c0 + 128); gate/up: the gate rows fill columns
-  // [0, n_rows) and the up rows [n_rows, 2 n_rows)
-  const int c0 = blockIdx.x * kRowsWg;
-  const bool second = kGateUp && c0 >= a.n_rows;
-  const int r0 = second ? c0 - a.n_rows : c0;  // first weight row of the matrix
+  // down: output columns [c0, c0 + 128) from weight rows c0 ..; gate/up:
+  // h columns [c0, c0 + 64) from gate rows c0 .. (waves 0-3) and the same
+  // up rows (waves 4-7)
+  const int c0 = blockIdx.x * (kGateUp ? kRowsWg / 2 : kRowsWg);
   const int lr = lane & 15, lq = lane >> 4;     // MFMA: row/column in the tile, K quarter
 
   if (!ma || !mb || !mc) {  // absent expert: its outputs are zero
     for (long long p = p0; p < p1; ++p)
-      for (int r = tid; r < kRowsWg; r += kThreads) a.out[p * a.n_out + c0 + r] = 0.f;
+      for (int r = tid; r < (kGateUp ? kRowsWg / 2 : kRowsWg); r += kThreads)
+        a.out[p * a.n_out + c0 + r] = 0.f;
     return;
   }
 
-  // weight rows r0 .. r0+127 of super-block b into wbuf[s].  Wave w copies
-  // chunks [144w, 144w+144) (16 B each, chunk c = part c%9 of row c/9); the
+  // the 128 weight rows of super-block b into wbuf[s] (gate/up: 64 gate
+  // rows, then the same 64 up rows).  Wave w copies chunks [144w, 144w+144)
+  // (16 B each, chunk c = part c%9 of row c/9), rows of one matrix; the
   // per-lane offsets are fixed for the kernel, the block's offset b*144 goes
   // in the scalar offset (buffer_load ... lds).
   constexpr int kWChunks = kRowsWg * 9 / 8;  // 144 per wave
-  const sg_block_q4k* mw = uniform_ptr(second ? mb : ma);
+  const sg_block_q4k* mw = uniform_ptr((kGateUp && wave >= 4) ? mb : ma);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<sg_block_q4k*>(mw), 0, a.n_rows * nb * kQ4Bytes, 0x00020000);
   uint32_t wofs[3];
@@ -273,7 +277,8 @@ grouped_mfma_kernel(GroupedArgs a) {
   for (int i = 0; i < 3; ++i) {
     const int cc = min(wave * kWChunks + lane + 64 * i, kRowsWg * 9 - 1);
     const int row = cc / 9, part = cc - row * 9;
-    wofs[i] = static_cast<uint32_t>((r0 + row) * nb) * kQ4Bytes + 16 * part;
+    const int rr = kGateUp ? (row & 63) : row;
+    wofs[i] = static_cast<uint32_t>((c0 + rr) * nb) * kQ4Bytes + 16 * part;
   }
   auto stage_w = [&](int b, int s) {
 #pragma unroll
@@ -416,13 +421,41 @@ grouped_mfma_kernel(GroupedArgs a) {
     }
   }
   // outputs of the lane's tokens
+  if (kGateUp) {  // h = silu(gate) * up; wave w (gate) and w + 4 (up) hold the same h
+    // positions and each takes half of them: token blocks 0-1 in the gate
+    // wave, 2-3 in the up wave, swapping the other half through LDS
+    bar();  // every wave is done with xbuf
+    float* pair = reinterpret_cast<float*>(xbuf);  // [8 waves][2 blocks * 4][64 lanes]
+    const bool up_wave = wave >= 4;
 #pragma unroll
-  for (int ti = 0; ti < NT; ++ti) {
+    for (int tj = 0; tj < 2; ++tj)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tt = 16 * ti + 4 * lq + i;
-      if (tt < nt)
-        a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * wave + lr] = acc[ti][i];
+      for (int i = 0; i < 4; ++i)
+        pair[(wave * 8 + 4 * tj + i) * 64 + lane] = acc[up_wave ? tj : 2 + tj][i];
+    bar();
+    const int partner = wave ^ 4;
+#pragma unroll
+    for (int tj = 0; tj < 2; ++tj) {
+      const int ti = up_wave ? 2 + tj : tj;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tt = 16 * ti + 4 * lq + i;
+        const float other = pair[(partner * 8 + 4 * tj + i) * 64 + lane];
+        const float gv = up_wave ? other : acc[ti][i], uv = up_wave ? acc[ti][i] : other;
+        if (tt < nt)
+          a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * (wave & 3) + lr] =
+              silu_mul(gv, uv);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int ti = 0; ti < NT; ++ti) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tt = 16 * ti + 4 * lq + i;
+        if (tt < nt)
+          a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * wave + lr] = acc[ti][i];
+      }
     }
   }
 }
@@ -430,26 +463,15 @@ grouped_mfma_kernel(GroupedArgs a) {
 // Q8_K blocks for the grouped kernels: the standard block except that the
 // 16-byte bsums field holds each sub-block sum s split as s = 128*hi + lo,
 // lo = s & 127 in bytes 0-7 and hi = s >> 7 (two's complement) in bytes
-// 8-15.  kSilu: the input row is [gate | up] of width 2n and the value
-// quantized is silu_mul(gate, up) (h of the reference's gate/up stage).
-template <bool kSilu>
+// 8-15.
 __global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __restrict__ in,
                                                                unsigned char* __restrict__ out,
-                                                               long long n_blocks, int nb_row) {
+                                                               long long n_blocks) {
   const long long blk = static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (blk >= n_blocks) return;
-  float v[4];
-  if (kSilu) {
-    const long long row = blk / nb_row, j = blk - row * nb_row;
-    const float* gp = in + row * (2LL * nb_row * kQK) + j * kQK + 4 * lane;
-    const float* up = gp + static_cast<long long>(nb_row) * kQK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = silu_mul(gp[i], up[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = in[blk * kQK + 4 * lane + i];
-  }
+  const float4 v4 = *reinterpret_cast<const float4*>(in + blk * kQK + 4 * lane);
+  const float v[4] = {v4.x, v4.y, v4.z, v4.w};
   quantize_block_wave<true>(v, out + blk * kQ8Bytes, lane);
 }
 
@@ -494,32 +516,27 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
   w.meta = o;  o = al256(o + 4 * 4);
   w.max_tiles = (T * k + kTokTile - 1) / kTokTile + E + (T + kTokTile - 1) / kTokTile;
   w.tiles = o; o = al256(o + static_cast<size_t>(1 + w.max_tiles) * 4);
-  w.h = o;     o = al256(o + static_cast<size_t>(w.P) * 2 * n_ff * 4);  // gate | up
+  w.h = o;     o = al256(o + static_cast<size_t>(w.P) * n_ff * 4);
   w.hq = o;    o = al256(o + static_cast<size_t>(w.P) * (n_ff / kQK) * kQ8Bytes);
   w.y = o;     o = al256(o + static_cast<size_t>(w.P) * hidden * 4);
   w.total = o;
   return w;
 }
 
-// the grouped kernels' Q8_K input (split bsums); kSilu: from [gate | up] rows
-static int quantize_split(const float* in, sg_block_q8k* out, int nb_row, int n_rows, bool silu,
+// the grouped kernels' Q8_K input (split bsums)
+static int quantize_split(const float* in, sg_block_q8k* out, int nb_row, int n_rows,
                           hipStream_t s, const char* nm) {
   const long long n_blocks = static_cast<long long>(nb_row) * n_rows;
   const unsigned grid = static_cast<unsigned>((n_blocks + 3) / 4);
-  unsigned char* o = reinterpret_cast<unsigned char*>(out);
-  if (silu)
-    hipLaunchKernelGGL(prefill_quantize_kernel<true>, dim3(grid), dim3(256), 0, s, in, o, n_blocks,
-                       nb_row);
-  else
-    hipLaunchKernelGGL(prefill_quantize_kernel<false>, dim3(grid), dim3(256), 0, s, in, o,
-                       n_blocks, nb_row);
+  hipLaunchKernelGGL(prefill_quantize_kernel, dim3(grid), dim3(256), 0, s, in,
+                     reinterpret_cast<unsigned char*>(out), n_blocks);
   return check_launch(nm);
 }
 
 constexpr int kScanLdsWords = 38 * 1024;  // dispatch scan: hist, offsets, parts, bitmap
 
 static int scan_lds_words(int n_rows, int E) {
-  return 2 * E + 1024 + 2 * E * ((n_rows + 31) / 32);
+  return 2 * E + 1024 + 2 * E * (((n_rows + 31) / 32) | 1);
 }
 
 static int scan_launch(const int* idx, float* weight, int* gslot, int* grows, int* off, int* toff,
@@ -600,7 +617,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   float* y = reinterpret_cast<float*>(base + ws.y);
   const int has_shared = n_sh == 3;
 
-  if (int st = quantize_split(x, xq, hidden / kQK, n_tokens, false, s, nm)) return st;
+  if (int st = quantize_split(x, xq, hidden / kQK, n_tokens, s, nm)) return st;
   if (logits)
     if (int st = sg_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w,
                                 stream))
@@ -623,13 +640,13 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   ga.out = h;
   ga.nb = hidden / kQK;
   ga.n_rows = n_ff;
-  ga.n_out = 2 * n_ff;
+  ga.n_out = n_ff;
   ga.n_expert = n_expert;
   ga.n_groups = G;
-  hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(2 * n_ff / kRowsWg, ws.max_tiles),
+  hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(n_ff / (kRowsWg / 2), ws.max_tiles),
                      dim3(kThreads), 0, s, ga);
   if (int st = check_launch("sg_moe_prefill/gate_up")) return st;
-  if (int st = quantize_split(h, hq, n_ff / kQK, ws.P, true, s, nm)) return st;
+  if (int st = quantize_split(h, hq, n_ff / kQK, ws.P, s, nm)) return st;
   GroupedArgs gd = ga;
   gd.tab_a = tab_down;
   gd.tab_b = tab_down;
