@@ -10,7 +10,6 @@ namespace sg {
 
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxK = 32;
-constexpr int kPerLane = kMaxExperts / 64;
 
 __host__ __device__ inline int round4(int n) { return (n + 3) & ~3; }
 __host__ __device__ inline int lpr_of(int nb) {
@@ -24,9 +23,12 @@ __host__ __device__ inline int lpr_of(int nb) {
 // of (value desc, index asc) argmax over non-NaN probabilities, degenerate
 // rounds pick kk % n_expert, weights renormalized by their k-order sum,
 // slot k = shared_w.  oi/ow may point to LDS or global memory; lane 0
-// writes them.  All 64 lanes must be active.
+// writes them.  All 64 lanes must be active.  PL = experts per lane
+// (n_expert <= 64 PL).
+template <int PL>
 __device__ void router_wave(const float* __restrict__ lg, int n_expert, int k, float shared_w,
                             int* oi, float* ow, float* ev, int lane) {
+  constexpr int kPerLane = PL;
   float p[kPerLane];
   float mx = -1e30f;
 #pragma unroll
@@ -83,14 +85,15 @@ __device__ void router_wave(const float* __restrict__ lg, int n_expert, int k, f
   }
 }
 
+template <int PL>
 __global__ void __launch_bounds__(64) router_kernel(const float* __restrict__ logits,
                                                     int* __restrict__ idx,
                                                     float* __restrict__ weight, int n_expert,
                                                     int k, int stride, float shared_w) {
-  __shared__ __attribute__((aligned(16))) float ev[kMaxExperts];
+  __shared__ __attribute__((aligned(16))) float ev[64 * PL];
   const long long row = blockIdx.x;
-  router_wave(logits + row * n_expert, n_expert, k, shared_w, idx + row * stride,
-              weight + row * stride, ev, threadIdx.x);
+  router_wave<PL>(logits + row * n_expert, n_expert, k, shared_w, idx + row * stride,
+                  weight + row * stride, ev, threadIdx.x);
 }
 
 __global__ void __launch_bounds__(256) silu_kernel(float* __restrict__ out,
@@ -130,9 +133,17 @@ int sg_router_topk(const float* logits, int* idx, float* weight, int n_expert, i
     return set_error(SG_ERR_GEOMETRY,
                      "sg_router_topk: n_expert=%d (<=%d) n_expert_used=%d idx_stride=%d n_rows=%d",
                      n_expert, kMaxExperts, n_expert_used, idx_stride, n_rows);
-  hipLaunchKernelGGL(router_kernel, dim3(n_rows), dim3(64), 0,
-                     static_cast<hipStream_t>(stream), logits, idx, weight, n_expert,
-                     n_expert_used, idx_stride, shared_w);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // experts per lane: the smallest power of two that covers n_expert
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(n_rows), dim3(64), 0, s, logits, idx, weight, n_expert,
+                       n_expert_used, idx_stride, shared_w);
+  };
+  if (n_expert <= 64) launch(router_kernel<1>);
+  else if (n_expert <= 128) launch(router_kernel<2>);
+  else if (n_expert <= 256) launch(router_kernel<4>);
+  else if (n_expert <= 512) launch(router_kernel<8>);
+  else launch(router_kernel<16>);
   return check_launch("sg_router_topk");
 }
 

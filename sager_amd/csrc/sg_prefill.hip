@@ -220,6 +220,32 @@ struct GroupedArgs {
   int n_expert, n_groups;
 };
 
+// raw buffer descriptor: base address, stride 0, size in bytes, dword format
+// (wave-uniform arguments; the words are moved to scalar registers)
+__device__ __forceinline__ u32x4 buffer_desc(const void* base, uint32_t bytes) {
+  const uint64_t v = reinterpret_cast<uintptr_t>(base);
+  auto rfl = [](uint32_t x) { return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(x)); };
+  return (u32x4){rfl(static_cast<uint32_t>(v)), rfl(static_cast<uint32_t>(v >> 32) & 0xFFFFu),
+                 rfl(bytes), 0x00020000u};
+}
+
+// 16 B per lane from buffer rsrc at voff + soff into LDS at lds + 16 * lane
+// (buffer_load_dwordx4 ... lds).  Inline asm on purpose: the compiler then
+// does not treat it as an LDS store in flight, which would make it wait for
+// every outstanding copy before each LDS read; the kernels order these
+// copies themselves (vmcnt waits and barriers).  Sets M0, which the
+// compiler uses for nothing else in these kernels.
+__device__ __forceinline__ void dma16(const uint32_t* lds, uint32_t voff, u32x4 rsrc,
+                                      uint32_t soff) {
+  const uint32_t l =
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  soff = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(soff));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(l), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory");
+}
+
 // a pointer the caller knows to be wave-uniform, moved to scalar registers
 template <typename T>
 __device__ __forceinline__ T* uniform_ptr(T* p) {
@@ -270,8 +296,7 @@ grouped_mfma_kernel(GroupedArgs a) {
   // in the scalar offset (buffer_load ... lds).
   constexpr int kWChunks = kRowsWg * 9 / 8;  // 144 per wave
   const sg_block_q4k* mw = uniform_ptr((kGateUp && wave >= 4) ? mb : ma);
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<sg_block_q4k*>(mw), 0, a.n_rows * nb * kQ4Bytes, 0x00020000);
+  const u32x4 rw4 = buffer_desc(mw, a.n_rows * nb * kQ4Bytes);
   uint32_t wofs[3];
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
@@ -284,9 +309,7 @@ grouped_mfma_kernel(GroupedArgs a) {
 #pragma unroll
     for (int i = 0; i < 3; ++i)
       if (64 * i + lane < kWChunks)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rw, (lds_void_p)(wbuf[s] + 4 * (wave * kWChunks + 64 * i)), 16, wofs[i],
-            b * kQ4Bytes, 0, 0);
+        dma16(wbuf[s] + 4 * (wave * kWChunks + 64 * i), wofs[i], rw4, b * kQ4Bytes);
   };
   // the tile's token rows of super-block b into xbuf[s], 76 words per token
   // in 16-B chunks: chunks 0-15 the 64 qs words, 16 the split bsums (eight
@@ -298,16 +321,14 @@ grouped_mfma_kernel(GroupedArgs a) {
   constexpr int kXChunks = kTokTile * kXRow / 4;    // 1216 = 19 instructions
   static_assert(kXChunks % 64 == 0, "whole instructions");
   constexpr int kXInstr = (kXChunks / 64 + 7) / 8;  // per wave: 3
-  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<unsigned char*>(a.xq), 0, 0x7FFFFFFF, 0x00020000);
+  const u32x4 rx4 = buffer_desc(a.xq, 0x7FFFFFFFu);
   uint32_t xofs[kXInstr];
   auto stage_x = [&](int b, int s) {
 #pragma unroll
     for (int i = 0; i < kXInstr; ++i) {
       const int q = wave + 8 * i;  // the instruction's 64-chunk slice
       if (64 * q < kXChunks)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_p)(xbuf[s] + 256 * q), 16, xofs[i],
-                                                 b * kQ8Bytes, 0, 0);
+        dma16(xbuf[s] + 256 * q, xofs[i], rx4, b * kQ8Bytes);
     }
   };
 
