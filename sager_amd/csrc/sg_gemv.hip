@@ -117,7 +117,7 @@ __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned ch
   bar();
   rows.attach(tab);
   if (kDepth > 1 && g + n_waves < n_groups)
-    dma_rows(rows, (g + n_waves) * rpw, rows_of(g + n_waves), nb, wbuf[wv][1], lane);
+    dma_rows(rows, (g + n_waves) * rpw, rows_of(g + n_waves), nb, wbuf[wv][kDepth - 1], lane);
 
   const int blk = lane & (lpr - 1);
   const int rr = lane / lpr;
@@ -133,7 +133,7 @@ __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned ch
     wait_vm_n(kDepth > 1 && gn < n_groups ? dma_instrs(rows_of(gn), nb) : 0);  // group g has landed
     uint32_t w36[36];
     const bool live = active && rr < n;
-    if (live) read_block_lds(wbuf[wv][cur] + (rr * nb + blk) * 36, w36);
+    if (live) read_block_lds(wbuf[wv][kDepth > 1 ? cur : 0] + (rr * nb + blk) * 36, w36);
     wait_lds();
     const int g2 = g + kDepth * n_waves;
     if (g2 < n_groups) dma_rows(rows, g2 * rpw, rows_of(g2), nb, wbuf[wv][kDepth > 1 ? cur : 0], lane);

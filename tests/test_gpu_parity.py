@@ -101,6 +101,32 @@ def test_gemv_shapes(n_rows, k):
     assert_fp32_parity(y, orc.gemv(w, xq, n_rows, k)[0])
 
 
+@pytest.mark.parametrize("n_rows,k", [(65536, 2048), (20000, 4096)])
+def test_gemv_many_groups_per_wave(n_rows, k):
+    """More row groups than waves in the grid: every wave loops over several
+    groups through its LDS buffer (the LM-head regime).  Bit-identical across
+    runs and within the fp32 bar against the oracle."""
+    rng = np.random.default_rng(n_rows + 3 * k)
+    w, xq = _case(rng, n_rows, k)
+    wd, xd = dev(w), dev(xq)
+    ys = [host(ops.gemv_q4_k_q8(wd, xd, n_rows, k)) for _ in range(3)]
+    for y in ys[1:]:
+        np.testing.assert_array_equal(y, ys[0])
+    assert_fp32_parity(ys[0], orc.gemv(w, xq, n_rows, k)[0])
+
+
+def test_gemv_ptrs_many_groups_per_wave():
+    rng = np.random.default_rng(32)
+    n_ptrs, rows_per, k = 40, 2048, 2048
+    mats = [dev(q4k_random_np(rng, rows_per * k // 256)) for _ in range(n_ptrs)]
+    ptrs = torch.tensor([m.data_ptr() for m in mats], dtype=torch.int64, device="cuda")
+    xq = orc.quantize_q8_k(rng.normal(0, 1, k).astype(np.float32))
+    ys = [host(ops.gemv_ptrs_q4_k_q8(ptrs, dev(xq), n_ptrs, rows_per, k)) for _ in range(2)]
+    np.testing.assert_array_equal(ys[1], ys[0])
+    ref = np.concatenate([orc.gemv(m.cpu().numpy(), xq, rows_per, k)[0] for m in mats])
+    assert_fp32_parity(ys[0], ref)
+
+
 @pytest.mark.parametrize("n_tokens", [1, 2, 4, 5, 16])
 def test_gemv_batched(n_tokens):
     rng = np.random.default_rng(100 + n_tokens)
