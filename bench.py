@@ -438,11 +438,19 @@ def main():
         exact4 &= bool((acts_h[L] == ref).all())
         floor = 1e-3 * np.abs(ref).max()
         rel4 = max(rel4, float((np.abs(acts_h[L] - ref) / np.maximum(np.abs(ref), floor)).max()))
+    # and of the LM head on the last layer's quantized output
+    yref4 = orc.gemv(head.cpu().numpy(), xq4.cpu().numpy(), head_rows, 2048)[0]
+    y4_h = y4.cpu().numpy()
+    head_floor = 1e-3 * np.abs(yref4).max()
+    head_parity = {"bit_exact": bool((y4_h == yref4).all()),
+                   "max_rel_err": float((np.abs(y4_h - yref4) /
+                                         np.maximum(np.abs(yref4), head_floor)).max())}
     config4 = {"us_per_token": round(ms4 * 1e3, 2),
                "gbs": round(stack_bytes / (ms4 * 1e-3) / 1e9, 1),
                "frac": round(stack_bytes / (ms4 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                "algorithmic_bytes": stack_bytes,
                "parity_all_layers": {"bit_exact": exact4, "max_rel_err": rel4},
+               "parity_lm_head": head_parity,
                "workload": "40 x 256 Q4_K experts (18.1 GB) resident, Zipf(1.1) top-8 per "
                            "layer, no shared expert, 1 token, then Q8_K + 248320x2048 LM head; "
                            "one HIP graph per token; each layer its own N(0,1) input"}

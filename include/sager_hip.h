@@ -92,6 +92,17 @@ int sg_gemv_q4_k_q8_batched(const sg_block_q4k* w, const sg_block_q8k* x,
                             float* y, int n_rows, int k, int n_tokens,
                             void* stream);
 
+/* Q6_K x Q8_K GEMV (the real model's LM head).  w6 points at raw
+ * block_q6_K bytes (210 per 256 weights: ql[128] | qh[64] | int8 sc[16] |
+ * fp16 d, weights.cpp:168-209); y[r] fp32 for r < n_rows.  The fp32 order
+ * is the reference kernel's (q4_k.cu:1578-1652): per row 32 lanes, lane l
+ * accumulating sub-groups l, l+32, ... as fma((xd*d)*sc, (float)isum, acc),
+ * then the shfl_down tree.  k <= 8192; the matrix must be under 2 GiB.  Replaces
+ * cuda::gemv_q6_k_q8 (cuda_ops.hpp:44-48) and its x-in-shared twin
+ * gemv_q6_k_q8_smx (cuda_ops.hpp:179-182). */
+int sg_gemv_q6_k_q8(const void* w6, const sg_block_q8k* x, float* y, int n_rows,
+                    int k, void* stream);
+
 /* Pointer-table GEMV: row r is row (r % rows_per) of matrix ptrs[r/rows_per]
  * (ptrs is a DEVICE array of n_ptrs device pointers); y[r] fp32 for
  * r < n_ptrs*rows_per.  Replaces cuda::gemv_ptrs_q4_k_q8_f16out

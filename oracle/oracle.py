@@ -33,6 +33,7 @@ def lib():
         L.orc_count_expf_mismatch.argtypes = [ctypes.c_int64, ctypes.c_uint64, ctypes.c_float,
                                               ctypes.c_float]
         L.orc_dequant.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.orc_dequant_q6k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
         _lib = L
     return _lib
 
@@ -65,6 +66,30 @@ def gemv(w, xq, n_rows, k, n_tokens=1):
     w, xq = _c(w, np.uint8), _c(xq, np.uint8)
     y = np.zeros((n_tokens, n_rows), np.float32)
     lib().orc_gemv_q4k_q8(P(w), P(xq), P(y), n_rows, k, n_tokens)
+    return y
+
+
+def dequant_q6k(w6, n):
+    """Q6_K bytes (210 per 256 weights) -> fp32 [n]."""
+    w6 = _c(w6, np.uint8)
+    out = np.zeros(n, np.float32)
+    lib().orc_dequant_q6k(P(w6), P(out), n)
+    return out
+
+
+def q6k_subgroup_dots(w6, xq, n_rows, k):
+    """int32 [n_rows, k/256, 16]: sum over each 16-weight sub-group of (q6 - 32) * xq."""
+    w6, xq = _c(w6, np.uint8), _c(xq, np.uint8)
+    d = np.zeros((n_rows, k // 256, 16), np.int32)
+    lib().orc_q6k_subgroup_dots(P(w6), P(xq), P(d), n_rows, k)
+    return d
+
+
+def gemv_q6k(w6, xq, n_rows, k):
+    """y fp32 [n_rows] = W6 . xq (one token), the reference GPU kernel's order."""
+    w6, xq = _c(w6, np.uint8), _c(xq, np.uint8)
+    y = np.zeros(n_rows, np.float32)
+    lib().orc_gemv_q6k_q8(P(w6), P(xq), P(y), n_rows, k)
     return y
 
 

@@ -22,6 +22,10 @@
  *                                            duplicated logits, NaN rows
  *   orc_moe_combine                        - fp64 closed form
  *   orc_dispatch_scan                      - counting invariants
+ *   orc_dequant_q6k                        - closed form per field (numpy)
+ *   orc_q6k_subgroup_dots                  - brute force from the dequant
+ *   orc_gemv_q6k_q8                        - fp64 dequant-dot tolerance,
+ *                                            32-lane order replayed in numpy
  */
 #include "sg_oracle.h"
 
@@ -259,6 +263,83 @@ void orc_gemv_q4k_q8_int(const void* w, const void* xq, float* y, int n_rows, in
 }
 
 /* ---- exp (double evaluation, one final rounding) ----------------------- */
+
+/* ---- Q6_K (the LM head) -----------------------------------------------
+ * block_q6_K, 210 B per 256 weights (weights.cpp:168-209):
+ *   u8 ql[128] | u8 qh[64] | i8 scales[16] | u16 d (bytes 208-209).
+ * Weight n*128 + q*32 + l (half n, quarter q, l < 32) is
+ *   ((ql[n*64 + (q&1)*32 + l] >> 4*(q>>1)) & 15) | ((qh[n*32 + l] >> 2q) & 3) << 4,
+ * minus 32, with scale sc[n*8 + 2q + l/16]. */
+void orc_dequant_q6k(const void* w6, float* out, int64_t n) {
+  const uint8_t* b = (const uint8_t*)w6;
+  for (int64_t blk = 0; blk < n / ORC_QK_K; ++blk, b += ORC_Q6K_BYTES) {
+    const int8_t* sc = (const int8_t*)(b + 192);
+    uint16_t dh;
+    memcpy(&dh, b + 208, 2);
+    const float d = orc_half_to_float(dh);
+    for (int i = 0; i < ORC_QK_K; ++i) {
+      const int nh = i >> 7, q = (i >> 5) & 3, l = i & 31;
+      const int lo = (b[nh * 64 + (q & 1) * 32 + l] >> (4 * (q >> 1))) & 15;
+      const int hi = (b[128 + nh * 32 + l] >> (2 * q)) & 3;
+      out[blk * ORC_QK_K + i] = d * (float)sc[nh * 8 + 2 * q + l / 16] * (float)((lo | hi << 4) - 32);
+    }
+  }
+}
+
+/* int32 sum over sub-group t (16 weights) of block b: sum (q6 - 32) * xq.
+ * Sub-group t: half n = t>>3, quarter q = (t&7)>>1, is = t&1 covers weights
+ * n*128 + q*32 + is*16 + j (j < 16) with scale sc[t] (q4_k.cu:1595-1613). */
+static int32_t q6_subgroup_dot(const uint8_t* blk6, const int8_t* x256, int t) {
+  const int n = t >> 3, q = (t & 7) >> 1, is = t & 1;
+  const uint8_t* ql = blk6 + n * 64 + (q & 1) * 32 + is * 16;
+  const uint8_t* qh = blk6 + 128 + n * 32 + is * 16;
+  const int8_t* x = x256 + n * 128 + q * 32 + is * 16;
+  int32_t s = 0;
+  for (int j = 0; j < 16; ++j) {
+    const int v = (((ql[j] >> (4 * (q >> 1))) & 15) | (((qh[j] >> (2 * q)) & 3) << 4)) - 32;
+    s += v * (int32_t)x[j];
+  }
+  return s;
+}
+
+void orc_q6k_subgroup_dots(const void* w6, const void* xq, int32_t* dots, int n_rows, int k) {
+  const int nb = k / ORC_QK_K;
+  const uint8_t* w = (const uint8_t*)w6;
+  const orc_q8k* x = (const orc_q8k*)xq;
+  for (int r = 0; r < n_rows; ++r)
+    for (int b = 0; b < nb; ++b)
+      for (int t = 0; t < 16; ++t)
+        dots[((int64_t)r * nb + b) * 16 + t] =
+            q6_subgroup_dot(w + ((int64_t)r * nb + b) * ORC_Q6K_BYTES, x[b].qs, t);
+}
+
+/* y[r] = W6[r] . xq in the reference GPU kernel's fp32 order
+ * (gemv_q6_k_q8_kernel, q4_k.cu:1578-1652): 32 lanes per row, lane l takes
+ * sub-groups sg = l, l+32, ... (block sg>>4, sub-group sg&15) in order,
+ * acc = fma((xd*d)*sc, (float)isum, acc) - nvcc's default contraction of
+ * acc += xd*d*sc*isum - then the shfl_down tree over offsets 16..1. */
+void orc_gemv_q6k_q8(const void* w6, const void* xq, float* y, int n_rows, int k) {
+  const int nb = k / ORC_QK_K;
+  const uint8_t* w = (const uint8_t*)w6;
+  const orc_q8k* x = (const orc_q8k*)xq;
+  for (int r = 0; r < n_rows; ++r) {
+    float lane[32] = {0};
+    const uint8_t* row = w + (int64_t)r * nb * ORC_Q6K_BYTES;
+    for (int sg = 0; sg < nb * 16; ++sg) {
+      const int b = sg >> 4, t = sg & 15;
+      const uint8_t* blk6 = row + (int64_t)b * ORC_Q6K_BYTES;
+      uint16_t dh;
+      memcpy(&dh, blk6 + 208, 2);
+      const float d = orc_half_to_float(dh);
+      const float sc = (float)((const int8_t*)(blk6 + 192))[t];
+      const int32_t is = q6_subgroup_dot(blk6, x[b].qs, t);
+      lane[sg & 31] = fmaf(x[b].d * d * sc, (float)is, lane[sg & 31]);
+    }
+    for (int off = 16; off > 0; off >>= 1)
+      for (int l = 0; l < off; ++l) lane[l] = lane[l] + lane[l + off];
+    y[r] = lane[0];
+  }
+}
 
 float orc_expf(float xf) {
   if (xf != xf) return xf;

@@ -9,6 +9,8 @@
  *   - Q8_K activation quantization     src/kernels/q4_k.cpp:44-61
  *   - int32 sub-block dots             src/kernels/q4_k.cpp:195-199
  *   - the fp32 Q4_K x Q8_K GEMV        src/kernels/cpu/q4_avx2.cpp:124-145
+ *   - the Q6_K format and head GEMV    src/core/weights.cpp:168-209,
+ *                                      src/kernels/cuda/q4_k.cu:1578-1652
  *   - the fp32 expert FFN              src/kernels/cpu/q4_avx2.cpp:175-196
  *   - router softmax/top-k/renorm      src/kernels/cuda/moe.cu:25-85
  *   - the fp32 combine                 src/kernels/cuda/moe.cu:265-280
@@ -30,6 +32,7 @@ extern "C" {
 #define ORC_QK_K 256
 #define ORC_Q4K_BYTES 144
 #define ORC_Q8K_BYTES 276
+#define ORC_Q6K_BYTES 210
 
 /* fp16 bits -> fp32 (exact). q4_k.hpp:66-88 */
 float orc_half_to_float(uint16_t h);
@@ -55,6 +58,15 @@ void orc_gemv_q4k_q8_int(const void* w, const void* xq, float* y, int n_rows, in
 
 void orc_gemv_q4k_q8(const void* w, const void* xq, float* y, int n_rows, int k,
                      int n_tokens);
+
+/* Q6_K (210 B per 256 weights, weights.cpp:168-209) -> fp32 weights. */
+void orc_dequant_q6k(const void* w6, float* out, int64_t n);
+/* int32 sum_j (q6 - 32) * xq over each 16-weight sub-group:
+ * dots[r][b*16 + t] (q4_k.cu:1595-1640). */
+void orc_q6k_subgroup_dots(const void* w6, const void* xq, int32_t* dots, int n_rows, int k);
+/* y[r] = W6[r] . xq (one token) in the order of gemv_q6_k_q8_kernel
+ * (q4_k.cu:1578-1652): 32-lane strided sub-groups, fma accumulate, shfl_down tree. */
+void orc_gemv_q6k_q8(const void* w6, const void* xq, float* y, int n_rows, int k);
 
 /* exp for float arguments, evaluated in double and rounded once (stands in
  * for std::exp(float) of q4_avx2.cpp:189 and expf of moe.cu:38-43). */

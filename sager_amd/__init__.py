@@ -32,6 +32,7 @@ SIGNATURES = {
     "sg_gemv_q4_k_q8": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
     "sg_gemv_q4_k_q8_batched": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
     "sg_gemv_ptrs_q4_k_q8": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
+    "sg_gemv_q6_k_q8": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
     "sg_q4k_subblock_dots": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
     "sg_router_topk": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _F, _VP]),
     "sg_silu_mul": (_I, [_VP, _VP, _VP, _I, _VP]),

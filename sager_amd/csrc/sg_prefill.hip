@@ -220,40 +220,6 @@ struct GroupedArgs {
   int n_expert, n_groups;
 };
 
-// raw buffer descriptor: base address, stride 0, size in bytes, dword format
-// (wave-uniform arguments; the words are moved to scalar registers)
-__device__ __forceinline__ u32x4 buffer_desc(const void* base, uint32_t bytes) {
-  const uint64_t v = reinterpret_cast<uintptr_t>(base);
-  auto rfl = [](uint32_t x) { return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(x)); };
-  return (u32x4){rfl(static_cast<uint32_t>(v)), rfl(static_cast<uint32_t>(v >> 32) & 0xFFFFu),
-                 rfl(bytes), 0x00020000u};
-}
-
-// 16 B per lane from buffer rsrc at voff + soff into LDS at lds + 16 * lane
-// (buffer_load_dwordx4 ... lds).  Inline asm on purpose: the compiler then
-// does not treat it as an LDS store in flight, which would make it wait for
-// every outstanding copy before each LDS read; the kernels order these
-// copies themselves (vmcnt waits and barriers).  Sets M0, which the
-// compiler uses for nothing else in these kernels.
-__device__ __forceinline__ void dma16(const uint32_t* lds, uint32_t voff, u32x4 rsrc,
-                                      uint32_t soff) {
-  const uint32_t l =
-      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
-  soff = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(soff));
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(l), "v"(voff), "s"(rsrc), "s"(soff)
-               : "memory");
-}
-
-// a pointer the caller knows to be wave-uniform, moved to scalar registers
-template <typename T>
-__device__ __forceinline__ T* uniform_ptr(T* p) {
-  const uint64_t v = reinterpret_cast<uintptr_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-  return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
 
 
 template <bool kGateUp>

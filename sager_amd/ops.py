@@ -62,6 +62,15 @@ def gemv_q4_k_q8(w, x_q8, n_rows, k, y=None):
     return y
 
 
+def gemv_q6_k_q8(w6, x_q8, n_rows, k, y=None):
+    """cuda::gemv_q6_k_q8 (cuda_ops.hpp:44-48): y[n_rows] fp32 = W6 . x, W6 raw
+    block_q6_K bytes (210 per 256 weights)."""
+    if y is None:
+        y = torch.empty(n_rows, dtype=torch.float32, device=w6.device)
+    _check(load().sg_gemv_q6_k_q8(_ptr(w6), _ptr(x_q8), _ptr(y), n_rows, k, _stream()))
+    return y
+
+
 def gemv_q4_k_q8_batched(w, x_q8, n_rows, k, n_tokens, y=None):
     """cuda::gemv_q4_k_q8_batched (cuda_ops.hpp:72-74): y[n_tokens, n_rows]."""
     if y is None:

@@ -32,6 +32,30 @@ def q4k_random_dev(n_blocks, gen, device="cuda", out=None):
     return out
 
 
+def q6k_random_np(rng, n_blocks):
+    """Q6_K blocks: uniform ql/qh bytes, int8 scales uniform in [-128, 127],
+    d = fp16(|N(0, 0.002)|)."""
+    b = rng.integers(0, 256, size=(n_blocks, 210), dtype=np.uint8)
+    d = np.abs(rng.normal(0.0, 0.002, size=(n_blocks, 1))).astype(np.float16)
+    b[:, 208:210] = d.view(np.uint8).reshape(n_blocks, 2)
+    return b
+
+
+def q6k_random_dev(n_blocks, gen, device="cuda", out=None):
+    import torch
+    if out is None:
+        out = torch.empty((n_blocks, 210), dtype=torch.uint8, device=device)
+    step = 1 << 22
+    for s in range(0, n_blocks, step):
+        e = min(n_blocks, s + step)
+        v = out[s:e]
+        v.copy_(torch.randint(0, 256, (e - s, 210), dtype=torch.uint8, device=device,
+                              generator=gen))
+        d = (torch.randn((e - s, 1), device=device, generator=gen) * 0.002).abs().half()
+        v[:, 208:210] = d.view(torch.uint8).reshape(e - s, 2)
+    return out
+
+
 def zipf_routes(rng, n_layers, n_expert, k, s=1.1):
     """Per layer, k distinct experts sampled without replacement from a
     Zipf(s) popularity over a seeded permutation of the experts (Gumbel

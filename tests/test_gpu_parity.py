@@ -127,6 +127,22 @@ def test_gemv_ptrs_many_groups_per_wave():
     assert_fp32_parity(ys[0], ref)
 
 
+@pytest.mark.parametrize("n_rows,k", [(64, 2048), (1, 256), (7, 768), (33, 4096),
+                                      (3, 8192), (50000, 2048), (9001, 1280)])
+def test_gemv_q6k_bit_exact(n_rows, k):
+    """Q6_K head GEMV against the oracle's restatement of the reference
+    kernel's order: bit-identical, including shapes where every wave loops
+    over several row groups and rows that start off 16-B boundaries."""
+    from sager_amd.synth import q6k_random_np
+    rng = np.random.default_rng(n_rows * 7 + k)
+    w6 = q6k_random_np(rng, n_rows * k // 256)
+    xq = orc.quantize_q8_k(rng.normal(0, 1, k).astype(np.float32))
+    wd = dev(w6)
+    y = host(ops.gemv_q6_k_q8(wd, dev(xq), n_rows, k))
+    np.testing.assert_array_equal(y, orc.gemv_q6k(w6, xq[0], n_rows, k))
+    np.testing.assert_array_equal(host(ops.gemv_q6_k_q8(wd, dev(xq), n_rows, k)), y)
+
+
 @pytest.mark.parametrize("n_tokens", [1, 2, 4, 5, 16])
 def test_gemv_batched(n_tokens):
     rng = np.random.default_rng(100 + n_tokens)

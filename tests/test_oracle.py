@@ -385,3 +385,84 @@ def test_dispatch_scan_invariants():
                 assert r["off"][e] <= gs < r["off"][e + 1] and r["grows"][gs] == rr
             else:
                 assert gs == -1
+
+
+# ---- Q6_K head GEMV ----------------------------------------------------------
+
+def _q6_codes_by_subgroup(w6, n_blocks):
+    """q6 - 32 per weight, decoded through the GPU kernel's sub-group view
+    (q4_k.cu:1595-1613: sub-group t = half*8 + 2*quarter + is, 16 weights
+    each) - a different indexing from the dequant loops of weights.cpp."""
+    b = w6.reshape(n_blocks, 210).astype(np.int64)
+    out = np.zeros((n_blocks, 256), np.int64)
+    scale = np.zeros((n_blocks, 256), np.int64)
+    sc = b[:, 192:208].astype(np.uint8).view(np.int8).astype(np.int64)
+    for t in range(16):
+        n, q, is_ = t >> 3, (t & 7) >> 1, t & 1
+        for j in range(16):
+            lo = (b[:, n * 64 + (q & 1) * 32 + is_ * 16 + j] >> (4 if q & 2 else 0)) & 15
+            hi = (b[:, 128 + n * 32 + is_ * 16 + j] >> (2 * q)) & 3
+            col = n * 128 + q * 32 + is_ * 16 + j
+            out[:, col] = (lo | (hi << 4)) - 32
+            scale[:, col] = sc[:, t]
+    return out, scale
+
+
+def test_q6k_dequant_matches_subgroup_view():
+    rng = np.random.default_rng(61)
+    from sager_amd.synth import q6k_random_np
+    w6 = q6k_random_np(rng, 40)
+    codes, scale = _q6_codes_by_subgroup(w6, 40)
+    d = w6[:, 208:210].copy().view(np.float16)[:, 0].astype(np.float32)
+    ref = (d[:, None] * scale.astype(np.float32)) * codes.astype(np.float32)
+    np.testing.assert_array_equal(orc.dequant_q6k(w6, 40 * 256), ref.reshape(-1))
+
+
+def test_q6k_dequant_hand_block():
+    """One block built by hand: weight 0 = ql[0] low nibble | qh[0] bits 0-1,
+    weight 64 = ql[0] high nibble | qh[0] bits 4-5, weight 160 (second half,
+    quarter 1) = ql[64+32] low | qh[32] bits 2-3; scales sc[0], sc[4], sc[10]."""
+    blk = np.zeros(210, np.uint8)
+    blk[0] = 0x5A            # low 0xA, high 0x5
+    blk[128] = 0b00_10_00_11  # bits 0-1 = 3, bits 4-5 = 2
+    blk[96] = 0x07
+    blk[160] = 0b0000_01_00  # bits 2-3 = 1
+    sc = np.zeros(16, np.int8)
+    sc[0], sc[4], sc[10] = 3, -2, 5
+    blk[192:208] = sc.view(np.uint8)
+    blk[208:210] = np.array([1.0], np.float16).view(np.uint8)
+    y = orc.dequant_q6k(blk, 256)
+    assert y[0] == 3 * ((0xA | 3 << 4) - 32)
+    assert y[64] == -2 * ((0x5 | 2 << 4) - 32)
+    assert y[160] == 5 * ((0x7 | 1 << 4) - 32)
+    assert y[1] == 3 * (0 - 32)
+
+
+def test_q6k_subgroup_dots_brute_force():
+    rng = np.random.default_rng(62)
+    from sager_amd.synth import q6k_random_np
+    n_rows, k = 7, 768
+    w6 = q6k_random_np(rng, n_rows * k // 256)
+    xq = orc.quantize_q8_k(rng.normal(0, 1, k).astype(np.float32))[0]
+    codes, _ = _q6_codes_by_subgroup(w6, n_rows * k // 256)
+    x = np.concatenate([_q8_fields(xq)[1][b] for b in range(k // 256)]).astype(np.int64)
+    ref = (codes.reshape(n_rows, k) * x[None]).reshape(n_rows, k // 256, 16, 16).sum(-1)
+    np.testing.assert_array_equal(orc.q6k_subgroup_dots(w6, xq, n_rows, k), ref)
+
+
+@pytest.mark.parametrize("n_rows,k", [(64, 2048), (5, 256), (3, 4096)])
+def test_q6k_gemv_vs_fp64(n_rows, k):
+    """Float64 dequant-dot of the same quantized operands: the 32-lane fp32
+    order stays within 1e-5 of the row scale."""
+    rng = np.random.default_rng(n_rows + k)
+    from sager_amd.synth import q6k_random_np
+    w6 = q6k_random_np(rng, n_rows * k // 256)
+    xq = orc.quantize_q8_k(rng.normal(0, 1, k).astype(np.float32))[0]
+    codes, scale = _q6_codes_by_subgroup(w6, n_rows * k // 256)
+    d = w6[:, 208:210].copy().view(np.float16)[:, 0].astype(np.float64)
+    wf = (d[:, None] * scale * codes).reshape(n_rows, k)
+    xd = np.repeat(_q8_fields(xq)[0].astype(np.float64), 256)
+    xv = np.concatenate([_q8_fields(xq)[1][b] for b in range(k // 256)]).astype(np.float64)
+    ref = wf @ (xd * xv)
+    y = orc.gemv_q6k(w6, xq, n_rows, k).astype(np.float64)
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
