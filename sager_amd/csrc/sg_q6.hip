@@ -14,11 +14,11 @@
 // 16, 8, 4, 2, 1.  Here one wave holds two rows (a half-wave each, lane l of
 // the half = reference lane l).
 //
-// Memory: each wave streams row groups (R rows, about 8 KB) into its two LDS
+// Memory: each wave streams row groups (R rows, about 4 KB) into its two LDS
 // buffers with buffer_load_dwordx4 ... lds (the copy of the next group is in
-// flight while the current one is computed); the 210-B blocks sit at 2-byte
-// alignment in LDS, so 16-B fields are read as five dwords and byte-aligned
-// (v_alignbyte).  The activation (Q8_K) is staged once per workgroup with
+// flight while the current one is computed), each 210-B block into a 224-B
+// slot so that its 16-B fields are aligned (the copy reads from 2-byte
+// aligned offsets).  The activation (Q8_K) is staged once per workgroup with
 // the per-16 sums the zero point needs: I = sum code'*x - 32 * sum x.
 #include "sg_common.hpp"
 
@@ -26,60 +26,70 @@ namespace sg {
 
 constexpr int kQ6Bytes = 210;
 constexpr int kQ6Waves = 4;
-constexpr int kQ6GroupBytes = 8192;  // target bytes per row group
+constexpr int kQ6GroupBytes = 4096;  // target bytes per row group
+constexpr int kQ6WgPerCu = 3;        // grid cap (LDS allows three at K = 2048)
 constexpr int kQ6XWords = 84;        // staged Q8_K block: 64 qs words, d, 16 sums, pad
 
-static int q6_rows_per_group(int nb) {
-  const int r = (kQ6GroupBytes / (nb * kQ6Bytes)) & ~1;
-  return r < 2 ? 2 : r;
+__host__ __device__ constexpr int q6_rows_per_group(int nb) {
+  return ((kQ6GroupBytes / (nb * kQ6Bytes)) & ~1) < 2 ? 2
+                                                    : ((kQ6GroupBytes / (nb * kQ6Bytes)) & ~1);
 }
-// words per LDS buffer: the group's bytes, its start offset (< 16) and the
-// over-read of the last 16-B field (one dword), rounded to 16 B
-static int q6_buf_words(int nb) {
-  const int bytes = q6_rows_per_group(nb) * nb * kQ6Bytes + 16 + 16;
-  return (bytes + 15) / 16 * 4;
-}
+// words per LDS buffer: one 224-B slot per block of the group
+static int q6_buf_words(int nb) { return q6_rows_per_group(nb) * nb * 224 / 4; }
 
-// 16 bytes at byte offset off (2-byte aligned) of LDS
-__device__ __forceinline__ u32x4 lds_read16(const uint32_t* base, uint32_t off) {
-  const uint32_t* p = base + (off >> 2);
-  const uint32_t sh = off & 3;
-  const uint32_t w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3], w4 = p[4];
-  return (u32x4){__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
-                 __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh)};
-}
+// LDS slot of one block: its 210 bytes copied as 14 16-B chunks (the last
+// one runs 14 bytes into the next block), so every 16-B field is aligned
+constexpr int kQ6Slot = 224;
+constexpr int kQ6SlotChunks = kQ6Slot / 16;
 
+// kNb > 0: the super-blocks per row fixed at compile time (the head's
+// K = 2048); 0: taken from nb_arg.  kQ6Depth: row groups in flight per
+// wave (the LDS ring's slots).
+template <int kNb, int kQ6Depth>
 __global__ void __launch_bounds__(256) gemv_q6_kernel(const unsigned char* __restrict__ w6,
                                                       const unsigned char* __restrict__ xq,
-                                                      float* __restrict__ y, int n_rows, int nb,
-                                                      int R, int buf_words) {
+                                                      float* __restrict__ y, int n_rows, int nb_arg,
+                                                      int R_arg, int buf_words, int gpw) {
+  const int nb = kNb > 0 ? kNb : nb_arg;
+  const int R = kNb > 0 ? q6_rows_per_group(kNb) : R_arg;
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   uint32_t* xs = lds;  // nb * kQ6XWords
-  uint32_t* bufs[2] = {lds + nb * kQ6XWords + wv * 2 * buf_words,
-                       lds + nb * kQ6XWords + wv * 2 * buf_words + buf_words};
+  uint32_t* ring = lds + nb * kQ6XWords + wv * kQ6Depth * buf_words;
+  // the wave's results, written out once at the end: a global store between
+  // the copies would join the vmcnt queue that the copies are waited on with
+  float* ys = reinterpret_cast<float*>(lds + nb * kQ6XWords + kQ6Waves * kQ6Depth * buf_words) +
+              wv * gpw * R;
   const uint32_t row_bytes = static_cast<uint32_t>(nb) * kQ6Bytes;
   const int n_groups = (n_rows + R - 1) / R;
-  const int n_waves = gridDim.x * kQ6Waves;
+  // wave W takes the contiguous groups [W * gpw, (W + 1) * gpw)
+  const int g_begin = (blockIdx.x * kQ6Waves + wv) * gpw;
+  const int g_end = min(n_groups, g_begin + gpw);
   const u32x4 rw = buffer_desc(w6, static_cast<uint32_t>(n_rows) * row_bytes);
   const uint32_t last_blk = static_cast<uint32_t>(n_rows) * nb - 1;
 
-  // copy of row group gg into buf: bytes [start & ~15, end) in 16-B chunks
-  // (dwords past the matrix end - the buffer's size - read as zeros)
-  auto n_chunks = [&](int gg) {
-    const uint32_t start = static_cast<uint32_t>(gg) * R * row_bytes;
-    const int nr = min(R, n_rows - gg * R);
-    return static_cast<int>(((start & 15u) + nr * row_bytes + 15) / 16);
-  };
+  // copy of row group gg: block slot s (row s / nb, block s % nb) from the
+  // group's byte offset + 210 s, chunk by chunk; the per-lane part of the
+  // offset is fixed, the group's goes in the scalar offset.  Bytes past the
+  // matrix end (the buffer's size) read as zeros.
+  const int n_slots = R * nb;
+  const int n_instr = (n_slots * kQ6SlotChunks + 63) / 64;
   auto issue = [&](int gg, uint32_t* buf) {
-    const uint32_t a0 = (static_cast<uint32_t>(gg) * R * row_bytes) & ~15u;
-    const int nch = n_chunks(gg);
-    for (int c0 = 0; c0 < nch; c0 += 64)
-      if (c0 + lane < nch) dma16(buf + 4 * c0, a0 + 16 * (c0 + lane), rw, 0);
+    const int nr = min(R, n_rows - gg * R);
+    const int nch = nr * nb * kQ6SlotChunks;
+    const uint32_t base = static_cast<uint32_t>(gg) * R * row_bytes;
+    for (int i = 0; i < n_instr; ++i) {
+      const int c = 64 * i + lane;
+      const int slot = c / kQ6SlotChunks, j = c - slot * kQ6SlotChunks;
+      if (64 * i < nch && c < nch)
+        dma16(buf + 256 * i, slot * kQ6Bytes + 16 * j, rw, base);
+    }
   };
-  int g = blockIdx.x * kQ6Waves + wv;
-  if (g < n_groups) issue(g, bufs[0]);
-  if (g + n_waves < n_groups) issue(g + n_waves, bufs[1]);
+  // instructions a copy of group gg issues (for the vmcnt waits)
+  auto instrs = [&](int gg) { return (min(R, n_rows - gg * R) * nb * kQ6SlotChunks + 63) / 64; };
+  int g = g_begin;
+  for (int j = 0; j < kQ6Depth - 1; ++j)
+    if (g + j < g_end) issue(g + j, ring + j * buf_words);
 
   // stage x: qs words, d, and the 16 sums of 16 codes per block
   for (int i = threadIdx.x; i < nb * 65; i += blockDim.x) {
@@ -102,44 +112,54 @@ __global__ void __launch_bounds__(256) gemv_q6_kernel(const unsigned char* __res
   // the lane's fixed sub-group position (sg & 15 == l & 15 for every sg of the lane)
   const int half = lane >> 5, l = lane & 31;
   const int t = l & 15, qn = t >> 3, qq = (t & 7) >> 1, is = t & 1;
-  const uint32_t ql_off = qn * 64 + (qq & 1) * 32 + is * 16, qh_off = 128 + qn * 32 + is * 16;
+  const int ql_w = (qn * 64 + (qq & 1) * 32 + is * 16) / 4, qh_w = (128 + qn * 32 + is * 16) / 4;
   const uint32_t nib = (qq & 2) ? 4 : 0, hsh = 2 * qq;
   const int xw = (qn * 128 + qq * 32 + is * 16) / 4;  // first qs word of the sub-group
-  const int8_t* lds8 = nullptr;
 
-  for (int cur = 0; g < n_groups; g += n_waves, cur ^= 1) {
-    const int gn = g + n_waves;
-    // group g has landed: only the next group's copy may still be in flight
-    wait_vm_n(gn < n_groups ? (n_chunks(gn) + 63) / 64 : 0);
-    const uint32_t* buf = bufs[cur];
-    lds8 = reinterpret_cast<const int8_t*>(buf);
+  for (int cur = 0; g < g_end; ++g, cur = cur + 1 == kQ6Depth ? 0 : cur + 1) {
+    // group g has landed: only the copies of the next kQ6Depth - 2 groups may
+    // still be in flight
+    int younger = 0;
+#pragma unroll
+    for (int j = 1; j < kQ6Depth - 1; ++j)
+      if (g + j < g_end) younger += instrs(g + j);
+    wait_vm_n(younger);
+    // refill the slot of group g - 1 (read in the previous iteration) with
+    // g + depth - 1 before computing on g
+    const int g2 = g + kQ6Depth - 1;
+    if (g2 < g_end) {
+      wait_lds();  // every read of the ring so far has returned
+      issue(g2, ring + (cur == 0 ? kQ6Depth - 1 : cur - 1) * buf_words);
+    }
+    const uint32_t* buf = ring + cur * buf_words;
     const int r0 = g * R, nr = min(R, n_rows - r0);
-    const uint32_t o0 = (static_cast<uint32_t>(r0) * row_bytes) & 15u;
     for (int p = 0; p < nr; p += 2) {
       const int row = p + half;
       float acc = 0.f;
       if (row < nr) {
-        const uint32_t rb = o0 + static_cast<uint32_t>(row) * row_bytes;
+#pragma unroll 4
         for (int sg = l; sg < nb * 16; sg += 32) {
           const int blk = sg >> 4;
-          const uint32_t bb = rb + blk * kQ6Bytes;
-          const u32x4 ql = lds_read16(buf, bb + ql_off);
-          const u32x4 qh = lds_read16(buf, bb + qh_off);
-          const float sc = static_cast<float>(lds8[bb + 192 + t]);
+          const uint32_t* sl = buf + (row * nb + blk) * (kQ6Slot / 4);
+          const u32x4 ql = *reinterpret_cast<const u32x4*>(sl + ql_w);
+          const u32x4 qh = *reinterpret_cast<const u32x4*>(sl + qh_w);
+          const float sc = static_cast<float>(reinterpret_cast<const int8_t*>(sl)[192 + t]);
           // the matrix's last d sits in a dword that ends past the buffer's
           // size when the size is 2 mod 4 (the copy then returns zeros for
           // it): read that one from memory
           const uint32_t gblk = static_cast<uint32_t>(r0 + row) * nb + blk;
           const uint32_t dh = gblk == last_blk
                                   ? *reinterpret_cast<const uint16_t*>(w6 + static_cast<size_t>(gblk) * kQ6Bytes + 208)
-                                  : reinterpret_cast<const uint16_t*>(buf)[(bb + 208) >> 1];
+                                  : reinterpret_cast<const uint16_t*>(sl)[104];
           const uint32_t* xb = xs + blk * kQ6XWords;
           const u32x4 xv = *reinterpret_cast<const u32x4*>(xb + xw);
           int isum = 0;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const uint32_t code = ((ql[j] >> nib) & 0x0F0F0F0Fu) | (((qh[j] >> hsh) & 0x03030303u) << 4);
-            isum = __builtin_amdgcn_sdot4(static_cast<int>(code), static_cast<int>(xv[j]), isum, false);
+            const uint32_t code =
+                ((ql[j] >> nib) & 0x0F0F0F0Fu) | (((qh[j] >> hsh) & 0x03030303u) << 4);
+            isum = __builtin_amdgcn_sdot4(static_cast<int>(code), static_cast<int>(xv[j]), isum,
+                                          false);
           }
           isum -= 32 * static_cast<int>(xb[65 + t]);
           const float xd = __builtin_bit_cast(float, xb[64]);
@@ -147,16 +167,19 @@ __global__ void __launch_bounds__(256) gemv_q6_kernel(const unsigned char* __res
           acc = __builtin_fmaf(xd * d * sc, static_cast<float>(isum), acc);
         }
       }
-#pragma unroll
-      for (int off = 16; off > 0; off >>= 1) acc += __shfl_down(acc, off, 32);
-      if (l == 0 && row < nr) y[r0 + row] = acc;
-    }
-    const int g2 = g + 2 * n_waves;
-    if (g2 < n_groups) {
-      wait_lds();  // every read of this buffer has returned
-      issue(g2, bufs[cur]);
+      // shfl_down tree over the half's 32 lanes (offsets 16, 8, 4, 2, 1; only
+      // lane 0's sum is used): xor-16 swizzle, then DPP row shifts
+      acc += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, acc), 0x401F));
+      acc += dpp_f<0x108>(acc);  // row_shl:8
+      acc += dpp_f<0x104>(acc);
+      acc += dpp_f<0x102>(acc);
+      acc += dpp_f<0x101>(acc);
+      if (l == 0 && row < nr) ys[r0 - g_begin * R + row] = acc;
     }
   }
+  wait_lds();  // this wave's result writes (read back by its own lanes)
+  const int w_rows = max(0, min(n_rows, g_end * R) - g_begin * R);
+  for (int i = lane; i < w_rows; i += 64) y[g_begin * R + i] = ys[i];
 }
 
 }  // namespace sg
@@ -181,11 +204,19 @@ int sg_gemv_q6_k_q8(const void* w6, const sg_block_q8k* x, float* y, int n_rows,
   const int R = q6_rows_per_group(nb), bw = q6_buf_words(nb);
   const long long n_groups = (n_rows + R - 1) / R;
   const long long wgs = (n_groups + kQ6Waves - 1) / kQ6Waves;
-  const unsigned grid = static_cast<unsigned>(wgs < 512 ? wgs : 512);  // two per CU
-  const size_t lds_bytes = (static_cast<size_t>(nb) * kQ6XWords + kQ6Waves * 2 * bw) * 4;
-  hipLaunchKernelGGL(gemv_q6_kernel, dim3(grid), dim3(256), lds_bytes,
-                     static_cast<hipStream_t>(stream), static_cast<const unsigned char*>(w6),
-                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, R, bw);
+  const long long cap = 256LL * kQ6WgPerCu;
+  const unsigned grid = static_cast<unsigned>(wgs < cap ? wgs : cap);
+  // three groups in flight at K = 2048; two otherwise (the ring must fit LDS)
+  const int depth = nb == 8 ? 3 : 2;
+  const int gpw = static_cast<int>((n_groups + grid * kQ6Waves - 1) / (grid * kQ6Waves));
+  const size_t lds_bytes =
+      (static_cast<size_t>(nb) * kQ6XWords + kQ6Waves * depth * bw + kQ6Waves * gpw * R) * 4;
+  if (lds_bytes > 160 * 1024)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows=%d needs %zu B of LDS", nm, n_rows, lds_bytes);
+  auto kern = nb == 8 ? gemv_q6_kernel<8, 3> : gemv_q6_kernel<0, 2>;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds_bytes, static_cast<hipStream_t>(stream),
+                     static_cast<const unsigned char*>(w6),
+                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, R, bw, gpw);
   return check_launch(nm);
 }
 
