@@ -174,6 +174,26 @@ def run_config5(torch, np, ops, gen, orc, q4k_random_dev, reps=10):
     return config5
 
 
+def run_q6_head(torch, np, ops, gen, orc, head_rows, xq):
+    """The real model's LM head format: Q6_K 248320 x 2048 (417 MB), one
+    token; parity of every row against the oracle."""
+    from sager_amd.synth import q6k_random_dev
+    log("[bench] Q6_K LM head")
+    w6 = q6k_random_dev(head_rows * 8, gen)
+    y6 = torch.empty(head_rows, dtype=torch.float32, device="cuda")
+    ms6, _ = time_graph(torch, lambda: ops.gemv_q6_k_q8(w6, xq, head_rows, 2048, y=y6), 20)
+    q6_bytes = head_rows * 8 * 210 + 8 * 276 + head_rows * 4
+    ref = orc.gemv_q6k(w6.cpu().numpy(), xq.cpu().numpy()[0], head_rows, 2048)
+    out = {"shape": f"{head_rows}x2048 Q6_K", "us": round(ms6 * 1e3, 2),
+           "gbs": round(q6_bytes / (ms6 * 1e-3) / 1e9, 1),
+           "frac": round(q6_bytes / (ms6 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+           "algorithmic_bytes": q6_bytes,
+           "parity": {"bit_exact": bool((y6.cpu().numpy() == ref).all())}}
+    del w6
+    torch.cuda.empty_cache()
+    return out
+
+
 def traffic_run(torch, np, layers, n_steps=32):
     """Dispatches for the HBM-traffic passes: a plain 256 MiB device copy
     (the scale reference: it reads and writes exactly 256 MiB), then n_steps
@@ -205,10 +225,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["5", "traffic"], default=None,
+    ap.add_argument("--only", choices=["5", "q6", "traffic"], default=None,
                     help="run one leg alone and print its JSON: 5 = the config-5 prefill "
-                         "chunk; traffic = eager config-2 front/back launches beside a plain "
-                         "256 MiB copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+                         "chunk; q6 = the Q6_K LM head; traffic = eager config-2 front/back "
+                         "launches beside a plain 256 MiB copy, for rocprofv3 --pmc "
+                         "FETCH_SIZE / WRITE_SIZE passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -228,6 +249,12 @@ def main():
         from oracle import oracle as orc
         print(json.dumps({"config5_prefill": run_config5(torch, np, ops, gen, orc,
                                                           q4k_random_dev)}), flush=True)
+        return 0
+    if args.only == "q6":
+        from oracle import oracle as orc
+        xq = ops.quantize_q8_k(torch.randn((1, 2048), device="cuda", generator=gen))
+        print(json.dumps({"lm_head_q6k_gemv": run_q6_head(torch, np, ops, gen, orc, 248320, xq)}),
+              flush=True)
         return 0
     log(f"[bench] building {N_LAYERS} layers x {E + 1} experts "
         f"({N_LAYERS * 3 * (E + 1) * MAT_BYTES / 1e9:.1f} GB)")
@@ -379,6 +406,7 @@ def main():
     yh = torch.empty(head_rows, dtype=torch.float32, device="cuda")
     ms_head, _ = time_graph(torch, lambda: ops.gemv_q4_k_q8(head, xq, head_rows, 2048, y=yh), 20)
     head_bytes = head_rows * 8 * 144 + 8 * 276 + head_rows * 4
+    q6_head = run_q6_head(torch, np, ops, gen, orc, head_rows, xq)
 
     # config 4: 40 layers x 256 experts (18.1 GB) resident behind the device
     # pointer tables, Zipf(1.1) routing per layer (sampled, so idx/weight are
@@ -511,6 +539,7 @@ def main():
                          "gbs": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1),
                          "frac": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                          "rotation": f"{n_rot} distinct 2048x2048 matrices, graph-replayed"},
+        "lm_head_q6k_gemv": q6_head,
         "lm_head_gemv": {"shape": "248320x2048", "us": round(ms_head * 1e3, 2),
                          "gbs": round(head_bytes / (ms_head * 1e-3) / 1e9, 1),
                          "frac": round(head_bytes / (ms_head * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
