@@ -24,7 +24,6 @@ constexpr int kMaxNb = 64;       // k <= 16384
 constexpr int kMaxTokens = 16;   // batched GEMV token tile
 constexpr int kWaves = 4;        // waves per workgroup
 constexpr int kBufWords = 64 * 36;  // one wave's 9216-B weight buffer
-constexpr int kDepth = 1;          // row groups in flight per wave (1 or 2)
 constexpr int kWgPerCu = 2;        // grid cap: workgroups per CU
 
 struct PlainRows {
@@ -36,6 +35,7 @@ struct PlainRows {
   __device__ void stage(uint32_t*, int, int) {}
   __device__ void attach(const uint32_t*) {}
   __device__ bool contiguous(int, int) const { return true; }
+  __device__ int table_words() const { return 0; }
 };
 
 // Rows of n_ptrs matrices of rows_per rows each, matrix e at ptrs[e].  With
@@ -64,6 +64,8 @@ struct TableRows {
     if (n_ptrs <= kMaxLdsPtrs) lds = reinterpret_cast<const unsigned long long*>(src);
   }
   __device__ bool contiguous(int r0, int n) const { return r0 / rows_per == (r0 + n - 1) / rows_per; }
+  // LDS words the staged table occupies (2 per pointer, when it is staged)
+  __device__ int table_words() const { return n_ptrs <= kMaxLdsPtrs ? 2 * n_ptrs : 0; }
 };
 
 __host__ __device__ inline int lanes_per_row(int nb) {
@@ -89,35 +91,33 @@ __device__ __forceinline__ void dma_rows(const Rows& rows, int r0, int n, int nb
   }
 }
 
-// Instructions dma_rows issues for a group of n rows.
-__device__ __forceinline__ int dma_instrs(int n, int nb) { return (n * nb * 9 + 63) / 64; }
-
-// y[r] = W[r] . x, one token; grid-stride over row groups.  Each wave keeps
-// kDepth row groups in flight (kDepth 9 KB buffers) and refills the buffer
-// it just read before computing on it.  On MI355X one group per wave with
-// two workgroups per CU streams fastest (5.4-5.6 TB/s on the 286 MB LM
-// head); two groups per wave or four workgroups per CU measured slower.
+// y[r] = W[r] . x, one token.  Wave W takes the contiguous row groups
+// [W*gpw, (W+1)*gpw) (a group = 64/lpr rows, one 9 KB buffer): it issues the
+// next group's copy as soon as the current one has been read into
+// registers, so one group is always in flight while it computes.  The row
+// results stay in LDS until the wave's last group and are then written
+// together: a global store between the copies would sit in the vmcnt queue
+// that each copy is waited on with.  Two workgroups per CU.
 template <typename Rows>
 __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned char* __restrict__ xq,
                                                     float* __restrict__ y, int n_rows, int nb,
-                                                    int lpr) {
-  __shared__ __attribute__((aligned(16))) uint32_t wbuf[kWaves][kDepth][kBufWords];
-  extern __shared__ __attribute__((aligned(16))) uint32_t xs_dyn[];  // nb * kXStride
+                                                    int lpr, int gpw) {
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[kWaves][kBufWords];
+  extern __shared__ __attribute__((aligned(16))) uint32_t xs_dyn[];  // nb * kXStride, table, results
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int rpw = 64 / lpr;
   const int n_groups = (n_rows + rpw - 1) / rpw;
-  const int n_waves = gridDim.x * kWaves;
-  int g = blockIdx.x * kWaves + wv;
+  const int g_begin = (blockIdx.x * kWaves + wv) * gpw;
+  const int g_end = min(n_groups, g_begin + gpw);
   auto rows_of = [&](int gg) { return min(rpw, n_rows - gg * rpw); };
   // the first group's weights first: their HBM latency overlaps the staging
-  if (g < n_groups) dma_rows(rows, g * rpw, rows_of(g), nb, wbuf[wv][0], lane);
+  if (g_begin < g_end) dma_rows(rows, g_begin * rpw, rows_of(g_begin), nb, wbuf[wv], lane);
   stage_q8k(xq, nb, xs_dyn, threadIdx.x, blockDim.x);
   uint32_t* tab = xs_dyn + nb * kXStride;  // row table, when the rows have one
   rows.stage(tab, threadIdx.x, blockDim.x);
+  float* res = reinterpret_cast<float*>(tab + rows.table_words()) + wv * gpw * rpw;
   bar();
   rows.attach(tab);
-  if (kDepth > 1 && g + n_waves < n_groups)
-    dma_rows(rows, (g + n_waves) * rpw, rows_of(g + n_waves), nb, wbuf[wv][kDepth - 1], lane);
 
   const int blk = lane & (lpr - 1);
   const int rr = lane / lpr;
@@ -126,21 +126,21 @@ __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned ch
   float xd = 0.f, bsf[8];
   load_x_regs(xs_dyn + (active ? blk : 0) * kXStride, xr, xd, bsf);
 
-  for (int cur = 0; g < n_groups; g += n_waves, cur ^= 1) {
-    const int r0 = g * rpw;
+  for (int g = g_begin; g < g_end; ++g) {
     const int n = rows_of(g);
-    const int gn = g + n_waves;
-    wait_vm_n(kDepth > 1 && gn < n_groups ? dma_instrs(rows_of(gn), nb) : 0);  // group g has landed
+    wait_vm();  // group g has landed
     uint32_t w36[36];
     const bool live = active && rr < n;
-    if (live) read_block_lds(wbuf[wv][kDepth > 1 ? cur : 0] + (rr * nb + blk) * 36, w36);
+    if (live) read_block_lds(wbuf[wv] + (rr * nb + blk) * 36, w36);
     wait_lds();
-    const int g2 = g + kDepth * n_waves;
-    if (g2 < n_groups) dma_rows(rows, g2 * rpw, rows_of(g2), nb, wbuf[wv][kDepth > 1 ? cur : 0], lane);
+    if (g + 1 < g_end) dma_rows(rows, (g + 1) * rpw, rows_of(g + 1), nb, wbuf[wv], lane);
     const float s = live ? q4k_block_dot(w36, xr, xd, bsf) : 0.f;
     const float acc = row_sum_last(s, blk, nb);
-    if (blk == nb - 1 && rr < n) y[r0 + rr] = acc;
+    if (blk == nb - 1 && rr < n) res[(g - g_begin) * rpw + rr] = acc;
   }
+  wait_lds();  // this wave's result writes (read back by its own lanes)
+  const int w_rows = max(0, min(n_rows, g_end * rpw) - g_begin * rpw);
+  for (int i = lane; i < w_rows; i += 64) y[g_begin * rpw + i] = res[i];
 }
 
 // y[t*n_rows + r] = W[r] . x[t] for t < n_tokens; weights read once.
@@ -233,6 +233,22 @@ static unsigned gemv_grid(long long n_groups) {
   return static_cast<unsigned>(wgs < cap ? (wgs > 0 ? wgs : 1) : cap);
 }
 
+// gemv1_kernel's launch: grid, contiguous groups per wave and the LDS its
+// per-wave results take
+struct Gemv1Launch {
+  unsigned grid;
+  int gpw;
+  size_t res_bytes;
+};
+static Gemv1Launch gemv1_launch(long long n_groups, int rpw) {
+  Gemv1Launch l{};
+  l.grid = gemv_grid(n_groups);
+  const long long waves = static_cast<long long>(l.grid) * kWaves;
+  l.gpw = static_cast<int>((n_groups + waves - 1) / waves);
+  l.res_bytes = static_cast<size_t>(kWaves) * l.gpw * rpw * 4;
+  return l;
+}
+
 static int check_gemv_geometry(const char* name, int n_rows, int k) {
   if (n_rows <= 0 || k <= 0 || k % kQK != 0)
     return set_error(SG_ERR_GEOMETRY, "%s: n_rows=%d k=%d (k must be a positive multiple of 256)",
@@ -254,9 +270,14 @@ int sg_gemv_q4_k_q8(const sg_block_q4k* w, const sg_block_q8k* x, float* y, int 
   if (int st = check_gemv_geometry("sg_gemv_q4_k_q8", n_rows, k)) return st;
   const int nb = k / kQK, lpr = lanes_per_row(nb);
   const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
-  hipLaunchKernelGGL(gemv1_kernel<PlainRows>, dim3(gemv_grid(n_groups)), dim3(256),
-                     nb * kXStride * 4, static_cast<hipStream_t>(stream), PlainRows{w, nb},
-                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr);
+  const Gemv1Launch L = gemv1_launch(n_groups, 64 / lpr);
+  const size_t lds = static_cast<size_t>(nb) * kXStride * 4 + L.res_bytes;
+  if (lds > 96 * 1024)
+    return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_q4_k_q8: n_rows=%d k=%d needs %zu B of LDS",
+                     n_rows, k, lds);
+  hipLaunchKernelGGL(gemv1_kernel<PlainRows>, dim3(L.grid), dim3(256), lds,
+                     static_cast<hipStream_t>(stream), PlainRows{w, nb},
+                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr, L.gpw);
   return check_launch("sg_gemv_q4_k_q8");
 }
 
@@ -271,11 +292,15 @@ int sg_gemv_ptrs_q4_k_q8(const sg_block_q4k* const* ptrs, const sg_block_q8k* x,
   if (int st = check_gemv_geometry("sg_gemv_ptrs_q4_k_q8", n_rows, k)) return st;
   const int nb = k / kQK, lpr = lanes_per_row(nb);
   const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
+  const Gemv1Launch L = gemv1_launch(n_groups, 64 / lpr);
   const size_t lds = static_cast<size_t>(nb) * kXStride * 4 +
-                     (n_ptrs <= kMaxLdsPtrs ? static_cast<size_t>(n_ptrs) * 8 : 0);
-  hipLaunchKernelGGL(gemv1_kernel<TableRows>, dim3(gemv_grid(n_groups)), dim3(256), lds,
+                     (n_ptrs <= kMaxLdsPtrs ? static_cast<size_t>(n_ptrs) * 8 : 0) + L.res_bytes;
+  if (lds > 96 * 1024)
+    return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_ptrs_q4_k_q8: n_rows=%d k=%d needs %zu B of LDS",
+                     n_rows, k, lds);
+  hipLaunchKernelGGL(gemv1_kernel<TableRows>, dim3(L.grid), dim3(256), lds,
                      static_cast<hipStream_t>(stream), TableRows{ptrs, rows_per, nb, n_ptrs},
-                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr);
+                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr, L.gpw);
   return check_launch("sg_gemv_ptrs_q4_k_q8");
 }
 
