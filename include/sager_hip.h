@@ -53,7 +53,10 @@ typedef struct sg_block_q8k {
 enum {
   SG_OK = 0,
   SG_ERR_INVALID_ARGUMENT = 1,
+  SG_ERR_FILE_NOT_FOUND = 2,
+  SG_ERR_GGUF_PARSE = 3,
   SG_ERR_GEOMETRY = 4,
+  SG_ERR_OOM_VRAM = 5,
   SG_ERR_HIP = 7,
   SG_ERR_UNSUPPORTED = 8
 };
@@ -241,6 +244,36 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate,
                    int* idx, float* weight, void* workspace,
                    size_t workspace_bytes, int n_tokens, int hidden, int n_ff,
                    int n_expert, int k, float shared_w, void* stream);
+
+/* ---- GGUF expert pool (load time, host + HBM) ------------------------
+ * Replaces Weights::load_expert_pool (weights.cpp:800-870, over the GGUF v3
+ * reader of gguf.hpp/gguf.cpp) and the device pointer table the session
+ * uploads (session.cpp:2787-2796, 3596-3597).  Every blk.L.ffn_{gate,up,
+ * down}_exps (stacked [n_expert][rows][cols]; gate/up Q4_K, down Q4_K or
+ * Q6_K) of L = 0, 1, ... is copied once into one HBM allocation laid out
+ * [layer][expert][gate | up | down]; a Q6_K down projection is requantized to
+ * Q4_K per row on the host first, as the reference does (weights.cpp:841-857).
+ * The table is [gate|up|down][layer][expert] device pointers: layer l's three
+ * slices are table + (m*L + l)*E, m = 0, 1, 2 - the tab_gate/tab_up/tab_down
+ * arguments of sg_moe_layer and sg_moe_prefill.  Synchronous; not for the
+ * hot path. */
+typedef struct sg_expert_pool sg_expert_pool;
+
+/* Parse a GGUF v3 file's header and expert tensors without touching the GPU. */
+int sg_gguf_expert_dims(const char* path, int* n_layers, int* n_expert, int* hidden,
+                        int* n_ff, int* q6_down_layers);
+/* Load the expert pool of a GGUF v3 file onto the current device. */
+int sg_expert_pool_load_gguf(const char* path, sg_expert_pool** out);
+int sg_expert_pool_dims(const sg_expert_pool* p, int* n_layers, int* n_expert, int* hidden,
+                        int* n_ff);
+/* Device pointer table [3][n_layers][n_expert] (a device address). */
+const sg_block_q4k* const* sg_expert_pool_table(const sg_expert_pool* p);
+void sg_expert_pool_free(sg_expert_pool* p);
+
+/* Host Q4_K quantizer of one fp32 row (n a multiple of 256): the
+ * reference's quantize_row (q4_k.cpp:62-174), used to requantize Q6_K
+ * expert tensors at load time. */
+int sg_q4k_quantize_row(const float* x, sg_block_q4k* out, int n);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,12 @@ SIGNATURES = {
     "sg_moe_prefill_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "sg_moe_prefill": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                             _VP, _SZ, _I, _I, _I, _I, _I, _F, _VP]),
+    "sg_gguf_expert_dims": (_I, [ctypes.c_char_p, _VP, _VP, _VP, _VP, _VP]),
+    "sg_expert_pool_load_gguf": (_I, [ctypes.c_char_p, _VP]),
+    "sg_expert_pool_dims": (_I, [_VP, _VP, _VP, _VP, _VP]),
+    "sg_expert_pool_table": (_VP, [_VP]),
+    "sg_expert_pool_free": (None, [_VP]),
+    "sg_q4k_quantize_row": (_I, [_VP, _VP, _I]),
 }
 
 

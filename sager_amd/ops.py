@@ -8,6 +8,9 @@ message (the reference's launchers return void and surface failures through
 cudaGetLastError).  Block tensors are uint8 views of the packed formats:
 Q4_K ``[..., 144]`` per 256 weights, Q8_K ``[..., 276]`` per 256 values.
 """
+import ctypes
+
+import numpy as np
 import torch
 
 from . import Q4K_BYTES, Q8K_BYTES, QK, load
@@ -19,6 +22,21 @@ class SagerError(RuntimeError):
 
 def _stream():
     return torch.cuda.current_stream().cuda_stream
+
+
+class DeviceAddress:
+    """A raw device address the library owns (e.g. an expert pool's pointer
+    table), usable wherever a device tensor argument is expected."""
+
+    def __init__(self, addr, device):
+        self.addr, self.device = int(addr), torch.device(device)
+        self.is_cuda = True
+
+    def data_ptr(self):
+        return self.addr
+
+    def is_contiguous(self):
+        return True
 
 
 def _ptr(t):
@@ -222,3 +240,57 @@ class MoePrefill(MoeLayer):
             _ptr(ws), ws.numel(), T, self.hidden, self.n_ff, self.n_expert, self.k,
             self.shared_w, _stream()))
         return out, idx, weight
+
+
+def q4k_quantize_row(x):
+    """Host Q4_K quantizer (the reference's quantize_row, q4_k.cpp:62-174):
+    fp32 numpy [n] (n a multiple of 256) -> uint8 [n/256, 144]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros((x.size // QK, Q4K_BYTES), np.uint8)
+    _check(load().sg_q4k_quantize_row(x.ctypes.data_as(ctypes.c_void_p),
+                                      out.ctypes.data_as(ctypes.c_void_p), x.size))
+    return out
+
+
+def gguf_expert_dims(path):
+    """(n_layers, n_expert, hidden, n_ff, q6_down_layers) of a GGUF v3 file's
+    blk.L.ffn_{gate,up,down}_exps tensors; host only."""
+    v = [ctypes.c_int(0) for _ in range(5)]
+    _check(load().sg_gguf_expert_dims(str(path).encode(), *[ctypes.byref(c) for c in v]))
+    return tuple(c.value for c in v)
+
+
+class ExpertPool:
+    """Every MoE layer's experts of a GGUF v3 file resident in HBM, with the
+    device pointer table [gate|up|down][layer][expert] (replaces
+    Weights::load_expert_pool, weights.cpp:800-870, and the session's table
+    upload, session.cpp:3596-3597)."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p(0)
+        _check(load().sg_expert_pool_load_gguf(str(path).encode(), ctypes.byref(h)))
+        self._h = h
+        v = [ctypes.c_int(0) for _ in range(4)]
+        _check(load().sg_expert_pool_dims(h, *[ctypes.byref(c) for c in v]))
+        self.n_layers, self.n_expert, self.hidden, self.n_ff = (c.value for c in v)
+        self.table = load().sg_expert_pool_table(h)
+        self.device = torch.device("cuda", torch.cuda.current_device())
+
+    def layer_tables(self, layer):
+        """(tab_gate, tab_up, tab_down) of one layer: device arrays of n_expert pointers."""
+        if not 0 <= layer < self.n_layers:
+            raise SagerError(f"layer {layer} not in [0, {self.n_layers})")
+        step = self.n_layers * self.n_expert * 8
+        base = self.table + layer * self.n_expert * 8
+        return tuple(DeviceAddress(base + m * step, self.device) for m in range(3))
+
+    def close(self):
+        if self._h:
+            load().sg_expert_pool_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -37,6 +37,13 @@ def P(a):
     return a.ctypes.data_as(ctypes.c_void_p)
 
 
+def orc_dequant_q6k(w6, n):
+    """Q6_K -> fp32 through the repository's oracle (input generation only)."""
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", ".."))
+    from oracle import oracle as orc
+    return orc.dequant_q6k(w6, n)
+
+
 def random_q4k(rng, n_blocks):
     """Synthetic Q4_K blocks as the configs specify: fp16 d, dmin from
     |N(0, 0.02)|, 12 uniform random scale bytes, 128 uniform random qs bytes."""
@@ -157,6 +164,31 @@ def main():
     g["ffn_wg"], g["ffn_wu"], g["ffn_wd"] = wg, wu, wd
     g["ffn_x"], g["ffn_y"] = xs, ys
     g["ffn_shape"] = np.array([H, F], np.int32)
+
+    # Q4_K requantization (the GGUF loader's path for Q6_K expert tensors):
+    # fp32 rows -> quantize_row.  Its own seed, so the cases above keep their
+    # values.  Rows: gaussian weights, weights dequantized from random Q6_K
+    # blocks, and edge rows (constant sub-blocks, zeros, one spike, a
+    # one-sided range, large magnitudes).
+    rq = np.random.default_rng(20261202)
+    gauss = (rq.normal(0, 1, 16 * 2048) * 0.05).astype(np.float32)
+    q6 = rq.integers(0, 256, size=(64, 210), dtype=np.uint8)
+    q6[:, 208:210] = np.abs(rq.normal(0, 0.002, (64, 1))).astype(np.float16).view(np.uint8)
+    from_q6 = orc_dequant_q6k(q6, 64 * 256)
+    edge = np.zeros(8 * 256, np.float32)
+    edge[0:32] = 0.25                                         # constant sub-block
+    edge[256:512] = rq.normal(0, 1, 256).astype(np.float32)
+    edge[300] = 40.0                                          # spike
+    edge[512:768] = np.abs(rq.normal(0, 1, 256)).astype(np.float32) + 3.0  # positive only
+    edge[768:1024] = -np.abs(rq.normal(0, 1, 256)).astype(np.float32)     # negative only
+    edge[1024:1280] = (rq.normal(0, 1, 256) * 1e4).astype(np.float32)     # large
+    edge[1280:1536] = (rq.normal(0, 1, 256) * 1e-6).astype(np.float32)    # tiny
+    # 1536..2047 stay zero (an all-zero super-block)
+    for name, x in (("gauss", gauss), ("q6", from_q6), ("edge", edge)):
+        x = np.ascontiguousarray(x, np.float32)
+        q = np.zeros((x.size // 256, 144), np.uint8)
+        ref.ref_quantize_row_q4k(P(x), P(q), x.size)
+        g["requant_" + name + "_x"], g["requant_" + name + "_q"] = x, q
 
     np.savez_compressed(OUT, **g)
     print("wrote", OUT, os.path.getsize(OUT), "bytes")
