@@ -95,6 +95,30 @@ int sg_gemv_q4_k_q8_batched(const sg_block_q4k* w, const sg_block_q8k* x,
                             float* y, int n_rows, int k, int n_tokens,
                             void* stream);
 
+/* ---- dense-projection GEMVs (fp16 outputs) ---------------------------
+ * The same Q4_K x Q8_K row dot (bit-identical to sg_gemv_q4_k_q8), rounded
+ * to fp16 (nearest even).  Replaces cuda::gemv_q4_k_q8_f16out
+ * (cuda_ops.hpp:53-54). */
+int sg_gemv_q4_k_q8_f16out(const sg_block_q4k* w, const sg_block_q8k* x, uint16_t* y,
+                           int n_rows, int k, void* stream);
+/* The layer's two (GDN qkvz | ba) or three (GQA q | k | v) projections of
+ * one x in ONE launch: y_m[r] = f16(W_m[r] . x), rows_m rows each.  Replaces
+ * cuda::gemv2m / gemv3m_q4_k_q8_f16out (cuda_ops.hpp:156-164); the
+ * reference's graph-parameter `slot` has no counterpart (nothing is stored
+ * per layer). */
+int sg_gemv2m_q4_k_q8_f16out(const sg_block_q4k* w1, const sg_block_q4k* w2,
+                             const sg_block_q8k* x, uint16_t* y1, uint16_t* y2, int rows1,
+                             int rows2, int k, void* stream);
+int sg_gemv3m_q4_k_q8_f16out(const sg_block_q4k* w1, const sg_block_q4k* w2,
+                             const sg_block_q4k* w3, const sg_block_q8k* x, uint16_t* y1,
+                             uint16_t* y2, uint16_t* y3, int rows1, int rows2, int rows3,
+                             int k, void* stream);
+/* y[r] = f16(W[r] . x) and res_inout[r] = f16(f32(res_inout[r]) + f32(y[r]))
+ * (add_kernel's semantics) in one launch.  Replaces
+ * cuda::gemv_q4_k_q8_f16out_resadd (cuda_ops.hpp:166-171). */
+int sg_gemv_q4_k_q8_f16out_resadd(const sg_block_q4k* w, const sg_block_q8k* x, uint16_t* y,
+                                  uint16_t* res_inout, int n_rows, int k, void* stream);
+
 /* Q6_K x Q8_K GEMV (the real model's LM head).  w6 points at raw
  * block_q6_K bytes (210 per 256 weights: ql[128] | qh[64] | int8 sc[16] |
  * fp16 d, weights.cpp:168-209); y[r] fp32 for r < n_rows.  The fp32 order

@@ -33,6 +33,10 @@ SIGNATURES = {
     "sg_gemv_q4_k_q8_batched": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
     "sg_gemv_ptrs_q4_k_q8": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
     "sg_gemv_q6_k_q8": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
+    "sg_gemv_q4_k_q8_f16out": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
+    "sg_gemv2m_q4_k_q8_f16out": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP]),
+    "sg_gemv3m_q4_k_q8_f16out": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
+    "sg_gemv_q4_k_q8_f16out_resadd": (_I, [_VP, _VP, _VP, _VP, _I, _I, _VP]),
     "sg_q4k_subblock_dots": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
     "sg_router_topk": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _F, _VP]),
     "sg_silu_mul": (_I, [_VP, _VP, _VP, _I, _VP]),

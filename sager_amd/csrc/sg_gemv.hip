@@ -43,6 +43,24 @@ struct PlainRows {
 // the address of a row group costs an LDS read instead of a dependent
 // global load in front of every weight stream.
 constexpr int kMaxLdsPtrs = 2048;
+// Up to three matrices of the same K stacked: rows [0, end[0]) of w[0],
+// [end[0], end[1]) of w[1], [end[1], end[2]) of w[2] (the layer's q|k|v or
+// qkvz|ba projections, gemv2m/gemv3m).
+struct SegRows {
+  const sg_block_q4k* w[3];
+  int end[3];
+  int nb;
+  __device__ int seg(int r) const { return r < end[0] ? 0 : (r < end[1] ? 1 : 2); }
+  __device__ const char* row(int r) const {
+    const int m = seg(r);
+    const int lr = r - (m ? end[m - 1] : 0);
+    return reinterpret_cast<const char*>(w[m] + static_cast<long long>(lr) * nb);
+  }
+  __device__ void stage(uint32_t*, int, int) {}
+  __device__ void attach(const uint32_t*) {}
+  __device__ bool contiguous(int r0, int n) const { return seg(r0) == seg(r0 + n - 1); }
+  __device__ int table_words() const { return 0; }
+};
 struct TableRows {
   const sg_block_q4k* const* ptrs;
   int rows_per, nb, n_ptrs;
@@ -98,10 +116,42 @@ __device__ __forceinline__ void dma_rows(const Rows& rows, int r0, int n, int nb
 // results stay in LDS until the wave's last group and are then written
 // together: a global store between the copies would sit in the vmcnt queue
 // that each copy is waited on with.  Two workgroups per CU.
-template <typename Rows>
+// Where a row result goes: fp32 y[r] (F32Out); fp16 into the row's segment
+// output (F16SegOut, gemv2m/3m); fp16 y[r] and the residual add
+// res[r] = f16(f32(res[r]) + f32(y[r])) (F16ResAddOut, add_kernel's
+// semantics).  fp16 conversions round to nearest even (__float2half).
+struct F32Out {
+  float* y;
+  __device__ void store(int r, float v) const { y[r] = v; }
+};
+__device__ __forceinline__ uint16_t f16_bits(float v) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+__device__ __forceinline__ float f16_value(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+struct F16SegOut {
+  uint16_t* y[3];
+  int end[3];
+  __device__ void store(int r, float v) const {
+    const int m = r < end[0] ? 0 : (r < end[1] ? 1 : 2);
+    y[m][r - (m ? end[m - 1] : 0)] = f16_bits(v);
+  }
+};
+struct F16ResAddOut {
+  uint16_t* y;
+  uint16_t* res;
+  __device__ void store(int r, float v) const {
+    const uint16_t h = f16_bits(v);
+    y[r] = h;
+    res[r] = f16_bits(f16_value(res[r]) + f16_value(h));
+  }
+};
+
+template <typename Rows, typename Out>
 __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned char* __restrict__ xq,
-                                                    float* __restrict__ y, int n_rows, int nb,
-                                                    int lpr, int gpw) {
+                                                    Out out, int n_rows, int nb, int lpr,
+                                                    int gpw) {
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[kWaves][kBufWords];
   extern __shared__ __attribute__((aligned(16))) uint32_t xs_dyn[];  // nb * kXStride, table, results
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -140,7 +190,7 @@ __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned ch
   }
   wait_lds();  // this wave's result writes (read back by its own lanes)
   const int w_rows = max(0, min(n_rows, g_end * rpw) - g_begin * rpw);
-  for (int i = lane; i < w_rows; i += 64) y[g_begin * rpw + i] = res[i];
+  for (int i = lane; i < w_rows; i += 64) out.store(g_begin * rpw + i, res[i]);
 }
 
 // y[t*n_rows + r] = W[r] . x[t] for t < n_tokens; weights read once.
@@ -258,6 +308,24 @@ static int check_gemv_geometry(const char* name, int n_rows, int k) {
   return SG_OK;
 }
 
+// one gemv1 launch over a row source and an output policy (shared by the
+// fp16-output entry points)
+template <typename Rows, typename Out>
+static int launch_gemv1(Rows rows, const sg_block_q8k* x, Out out, int n_rows, int k,
+                        hipStream_t s, const char* nm) {
+  if (int st = check_gemv_geometry(nm, n_rows, k)) return st;
+  const int nb = k / kQK, lpr = lanes_per_row(nb);
+  const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
+  const Gemv1Launch L = gemv1_launch(n_groups, 64 / lpr);
+  const size_t lds = static_cast<size_t>(nb) * kXStride * 4 + L.res_bytes;
+  if (lds > 96 * 1024)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows=%d k=%d needs %zu B of LDS", nm, n_rows, k,
+                     lds);
+  hipLaunchKernelGGL((gemv1_kernel<Rows, Out>), dim3(L.grid), dim3(256), lds, s, rows,
+                     reinterpret_cast<const unsigned char*>(x), out, n_rows, nb, lpr, L.gpw);
+  return check_launch(nm);
+}
+
 }  // namespace sg
 
 using namespace sg;
@@ -275,9 +343,9 @@ int sg_gemv_q4_k_q8(const sg_block_q4k* w, const sg_block_q8k* x, float* y, int 
   if (lds > 96 * 1024)
     return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_q4_k_q8: n_rows=%d k=%d needs %zu B of LDS",
                      n_rows, k, lds);
-  hipLaunchKernelGGL(gemv1_kernel<PlainRows>, dim3(L.grid), dim3(256), lds,
+  hipLaunchKernelGGL((gemv1_kernel<PlainRows, F32Out>), dim3(L.grid), dim3(256), lds,
                      static_cast<hipStream_t>(stream), PlainRows{w, nb},
-                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr, L.gpw);
+                     reinterpret_cast<const unsigned char*>(x), F32Out{y}, n_rows, nb, lpr, L.gpw);
   return check_launch("sg_gemv_q4_k_q8");
 }
 
@@ -298,9 +366,10 @@ int sg_gemv_ptrs_q4_k_q8(const sg_block_q4k* const* ptrs, const sg_block_q8k* x,
   if (lds > 96 * 1024)
     return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_ptrs_q4_k_q8: n_rows=%d k=%d needs %zu B of LDS",
                      n_rows, k, lds);
-  hipLaunchKernelGGL(gemv1_kernel<TableRows>, dim3(L.grid), dim3(256), lds,
+  hipLaunchKernelGGL((gemv1_kernel<TableRows, F32Out>), dim3(L.grid), dim3(256), lds,
                      static_cast<hipStream_t>(stream), TableRows{ptrs, rows_per, nb, n_ptrs},
-                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr, L.gpw);
+                     reinterpret_cast<const unsigned char*>(x), F32Out{y}, n_rows, nb, lpr,
+                     L.gpw);
   return check_launch("sg_gemv_ptrs_q4_k_q8");
 }
 
@@ -334,6 +403,46 @@ int sg_q4k_subblock_dots(const sg_block_q4k* w, const sg_block_q8k* x, int32_t* 
                      dim3(256), nb * kXStride * 4, static_cast<hipStream_t>(stream), w,
                      reinterpret_cast<const unsigned char*>(x), dots, n_rows, nb, lpr);
   return check_launch("sg_q4k_subblock_dots");
+}
+
+int sg_gemv_q4_k_q8_f16out(const sg_block_q4k* w, const sg_block_q8k* x, uint16_t* y, int n_rows,
+                           int k, void* stream) {
+  const char* nm = "sg_gemv_q4_k_q8_f16out";
+  if (!w || !x || !y) return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  F16SegOut o{{y, y, y}, {n_rows, n_rows, n_rows}};
+  return launch_gemv1(PlainRows{w, k / kQK}, x, o, n_rows, k, static_cast<hipStream_t>(stream),
+                      nm);
+}
+
+int sg_gemv3m_q4_k_q8_f16out(const sg_block_q4k* w1, const sg_block_q4k* w2,
+                             const sg_block_q4k* w3, const sg_block_q8k* x, uint16_t* y1,
+                             uint16_t* y2, uint16_t* y3, int rows1, int rows2, int rows3, int k,
+                             void* stream) {
+  const char* nm = "sg_gemv3m_q4_k_q8_f16out";
+  if (!w1 || !w2 || !x || !y1 || !y2 || (rows3 > 0 && (!w3 || !y3)))
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  if (rows1 <= 0 || rows2 <= 0 || rows3 < 0 ||
+      static_cast<long long>(rows1) + rows2 + rows3 > 0x7fffffffLL)
+    return set_error(SG_ERR_GEOMETRY, "%s: rows %d/%d/%d", nm, rows1, rows2, rows3);
+  const int e0 = rows1, e1 = rows1 + rows2, e2 = e1 + rows3;
+  SegRows rs{{w1, w2, rows3 > 0 ? w3 : w2}, {e0, e1, e2}, k / kQK};
+  F16SegOut o{{y1, y2, rows3 > 0 ? y3 : y2}, {e0, e1, e2}};
+  return launch_gemv1(rs, x, o, e2, k, static_cast<hipStream_t>(stream), nm);
+}
+
+int sg_gemv2m_q4_k_q8_f16out(const sg_block_q4k* w1, const sg_block_q4k* w2,
+                             const sg_block_q8k* x, uint16_t* y1, uint16_t* y2, int rows1,
+                             int rows2, int k, void* stream) {
+  return sg_gemv3m_q4_k_q8_f16out(w1, w2, nullptr, x, y1, y2, nullptr, rows1, rows2, 0, k,
+                                  stream);
+}
+
+int sg_gemv_q4_k_q8_f16out_resadd(const sg_block_q4k* w, const sg_block_q8k* x, uint16_t* y,
+                                  uint16_t* res_inout, int n_rows, int k, void* stream) {
+  const char* nm = "sg_gemv_q4_k_q8_f16out_resadd";
+  if (!w || !x || !y || !res_inout) return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  return launch_gemv1(PlainRows{w, k / kQK}, x, F16ResAddOut{y, res_inout}, n_rows, k,
+                      static_cast<hipStream_t>(stream), nm);
 }
 
 }  // extern "C"

@@ -80,6 +80,41 @@ def gemv_q4_k_q8(w, x_q8, n_rows, k, y=None):
     return y
 
 
+def gemv_q4_k_q8_f16out(w, x_q8, n_rows, k, y=None):
+    """cuda::gemv_q4_k_q8_f16out (cuda_ops.hpp:53-54): y fp16 [n_rows]."""
+    if y is None:
+        y = torch.empty(n_rows, dtype=torch.float16, device=w.device)
+    _check(load().sg_gemv_q4_k_q8_f16out(_ptr(w), _ptr(x_q8), _ptr(y), n_rows, k, _stream()))
+    return y
+
+
+def gemv_nm_q4_k_q8_f16out(ws, x_q8, rows, k, ys=None):
+    """cuda::gemv2m / gemv3m_q4_k_q8_f16out (cuda_ops.hpp:156-164): the two or
+    three projections of one x in one launch; returns the fp16 outputs."""
+    if len(ws) not in (2, 3) or len(rows) != len(ws):
+        raise SagerError("two or three matrices")
+    if ys is None:
+        ys = [torch.empty(r, dtype=torch.float16, device=x_q8.device) for r in rows]
+    if len(ws) == 2:
+        _check(load().sg_gemv2m_q4_k_q8_f16out(_ptr(ws[0]), _ptr(ws[1]), _ptr(x_q8), _ptr(ys[0]),
+                                               _ptr(ys[1]), rows[0], rows[1], k, _stream()))
+    else:
+        _check(load().sg_gemv3m_q4_k_q8_f16out(_ptr(ws[0]), _ptr(ws[1]), _ptr(ws[2]), _ptr(x_q8),
+                                               _ptr(ys[0]), _ptr(ys[1]), _ptr(ys[2]), rows[0],
+                                               rows[1], rows[2], k, _stream()))
+    return ys
+
+
+def gemv_q4_k_q8_f16out_resadd(w, x_q8, res_inout, n_rows, k, y=None):
+    """cuda::gemv_q4_k_q8_f16out_resadd (cuda_ops.hpp:166-171): y = f16(W.x),
+    res_inout += y in fp16 (in place)."""
+    if y is None:
+        y = torch.empty(n_rows, dtype=torch.float16, device=w.device)
+    _check(load().sg_gemv_q4_k_q8_f16out_resadd(_ptr(w), _ptr(x_q8), _ptr(y), _ptr(res_inout),
+                                                n_rows, k, _stream()))
+    return y
+
+
 def gemv_q6_k_q8(w6, x_q8, n_rows, k, y=None):
     """cuda::gemv_q6_k_q8 (cuda_ops.hpp:44-48): y[n_rows] fp32 = W6 . x, W6 raw
     block_q6_K bytes (210 per 256 weights)."""

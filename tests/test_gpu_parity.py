@@ -143,6 +143,38 @@ def test_gemv_q6k_bit_exact(n_rows, k):
     np.testing.assert_array_equal(host(ops.gemv_q6_k_q8(wd, dev(xq), n_rows, k)), y)
 
 
+@pytest.mark.parametrize("rows,k", [((4096, 512, 512), 2048), ((8192, 64), 2048),
+                                    ((33, 7, 250), 768), ((60000, 4000, 1), 2048)])
+def test_gemv_nm_f16out(rows, k):
+    """gemv2m / gemv3m: each projection equals the fp32 GEMV (AVX2 order)
+    rounded to fp16 (nearest even), including segments that start inside a
+    row group and a 1-row segment."""
+    rng = np.random.default_rng(sum(rows) + k)
+    ws = [q4k_random_np(rng, r * k // 256) for r in rows]
+    xq = orc.quantize_q8_k(rng.normal(0, 1, k).astype(np.float32))
+    ys = ops.gemv_nm_q4_k_q8_f16out([dev(w) for w in ws], dev(xq), list(rows), k)
+    for w, r, y in zip(ws, rows, ys):
+        ref = orc.gemv(w, xq, r, k)[0].astype(np.float16)
+        np.testing.assert_array_equal(host(y).view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("n_rows,k", [(2048, 4096), (777, 512), (70000, 2048)])
+def test_gemv_f16out_and_resadd(n_rows, k):
+    """fp16 GEMV and the fused residual add: res = f16(f32(res) + f32(f16(y)))."""
+    rng = np.random.default_rng(n_rows + 5 * k)
+    w = q4k_random_np(rng, n_rows * k // 256)
+    xq = orc.quantize_q8_k(rng.normal(0, 1, k).astype(np.float32))
+    ref = orc.gemv(w, xq, n_rows, k)[0].astype(np.float16)
+    y = ops.gemv_q4_k_q8_f16out(dev(w), dev(xq), n_rows, k)
+    np.testing.assert_array_equal(host(y).view(np.uint16), ref.view(np.uint16))
+    res = (rng.normal(0, 4, n_rows)).astype(np.float16)
+    res_d = torch.from_numpy(res.copy()).cuda()
+    y2 = ops.gemv_q4_k_q8_f16out_resadd(dev(w), dev(xq), res_d, n_rows, k)
+    np.testing.assert_array_equal(host(y2).view(np.uint16), ref.view(np.uint16))
+    want = (res.astype(np.float32) + ref.astype(np.float32)).astype(np.float16)
+    np.testing.assert_array_equal(res_d.cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
 @pytest.mark.parametrize("n_tokens", [1, 2, 4, 5, 16])
 def test_gemv_batched(n_tokens):
     rng = np.random.default_rng(100 + n_tokens)
