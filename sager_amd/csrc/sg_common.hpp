@@ -110,12 +110,15 @@ typedef __attribute__((address_space(1))) void* glb_void_p;
 // instruction reads 1 KB of consecutive global memory when the source is
 // contiguous (fully coalesced), and nothing occupies registers while the
 // data is in flight.  src(c) returns the global address of chunk c.
+// With part/nparts, only instructions i = part, part + nparts, ... (several
+// waves sharing one copy).
 template <typename Src>
-__device__ __forceinline__ void dma_chunks(Src src, int n_chunks, uint32_t* dst, int lane) {
+__device__ __forceinline__ void dma_chunks(Src src, int n_chunks, uint32_t* dst, int lane,
+                                           int part = 0, int nparts = 1) {
 #pragma unroll
   for (int i = 0; i < 9; ++i) {
     const int c = lane + 64 * i;
-    if (i * 64 < n_chunks && c < n_chunks)
+    if (i % nparts == part && i * 64 < n_chunks && c < n_chunks)
       __builtin_amdgcn_global_load_lds((glb_void_p)src(c), (lds_void_p)(dst + 256 * i), 16, 0, 0);
   }
 }
@@ -284,6 +287,16 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   v = fmaxf(v, dpp_f<kDppMirror>(v));
   return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)),
                fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+// Maximum of an int over the wave, same value in every lane.
+__device__ __forceinline__ int wave_max_i32(int v) {
+  v = max(v, dpp_i<kDppXor1>(v));
+  v = max(v, dpp_i<kDppXor2>(v));
+  v = max(v, dpp_i<kDppHalfMirror>(v));
+  v = max(v, dpp_i<kDppMirror>(v));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
 // Sum over each aligned group of 8 lanes (every lane of the group gets it).

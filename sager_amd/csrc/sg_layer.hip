@@ -369,13 +369,15 @@ __device__ __forceinline__ void gateup_wave(bool present, int row0, int nrw, int
 }
 
 // Copy gate rows [row0, row0+nrw) and the same up rows into a wave buffer.
+// (part/nparts: this wave's share of the copy instructions, as dma_chunks)
 __device__ __forceinline__ void dma_gateup(const sg_block_q4k* wg, const sg_block_q4k* wu,
-                                           int row0, int nrw, int nbh, uint32_t* buf, int lane) {
+                                           int row0, int nrw, int nbh, uint32_t* buf, int lane,
+                                           int part = 0, int nparts = 1) {
   const char* pg = reinterpret_cast<const char*>(wg + static_cast<long long>(row0) * nbh);
   const char* pu = reinterpret_cast<const char*>(wu + static_cast<long long>(row0) * nbh);
   const int ncg = nrw * nbh * 9;
   dma_chunks([&](int c) { return c < ncg ? pg + 16 * c : pu + 16 * (c - ncg); }, 2 * ncg, buf,
-             lane);
+             lane, part, nparts);
 }
 
 // x values of a wave's first quantization pass (blocks w + nw*u), loaded
@@ -428,6 +430,25 @@ __device__ __forceinline__ void quantize_x(const float* x, int n_blocks, uint32_
 // Teams of tw waves; each thread keeps its logits in lr[] (last pass's
 // token).  Workgroup-wide; the last pass's top[] is readable on return,
 // spec[] only after the caller's next barrier.
+// Logits of the first routing pass into lr[] (what spec_select's pass 0
+// reads): thread tt of team `team` holds experts tt + TT*j of token `team`,
+// 0 outside.  Same team geometry as front_lds.
+template <int EPT>
+__device__ __forceinline__ void logits_preload(const LayerArgs& a, int tid, float* lr) {
+  const int T = a.T, E = a.n_expert;
+  const int nteams = T == 1 ? 1 : (T == 2 ? 2 : 4);
+  const int TT = 64 * (4 / nteams);
+  const int ept = (E + TT - 1) / TT;
+  const int team = tid / TT, tt = tid - team * TT;
+  const bool ok = team < T;
+  const float* lg = a.logits + static_cast<long long>(team) * E;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tt + TT * j;
+    lr[j] = (j < ept && i < E && ok) ? lg[i] : 0.f;
+  }
+}
+
 template <int EPT>
 __device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
                             int tid) {
@@ -447,7 +468,7 @@ __device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L
     for (int j = 0; j < EPT; ++j) {
       const int i = tt + L.TT * j;
       const bool in = j < L.ept && i < E && ok;
-      lr[j] = in ? lg[i] : 0.f;
+      if (t0 > 0) lr[j] = in ? lg[i] : 0.f;  // pass 0: logits_preload
       kr[j] = in ? sel_key(lr[j], i) : 0;
       if (j < L.ept && i < L.npad) keys[i] = kr[j];
       if (j < L.ept && i < L.e32) lv[i] = lr[j];
@@ -742,6 +763,10 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
   const bool publisher = g == a.gmax;
   if (publisher && bx != 0) return;  // one publisher per launch
   const bool shared_grp = a.has_shared && g == 0;
+  // the first routing pass's logits are the head of the routing chain:
+  // issued before anything else
+  float lr[EPT];
+  if (a.logits && !shared_grp) logits_preload<EPT>(a, tid, lr);
   const FrontLds L = front_lds(T, nbh, E, k, !shared_grp);
   const int rpw = 32 / lpr;
   const int row0 = bx * 4 * rpw + wave * rpw;
@@ -792,16 +817,15 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
 
   // stream the gate/up rows of expert e (none when e < 0 or it is absent)
   // for wave w's rows into wave w's buffer
-  auto stream_rows = [&](int e, int w) {
+  auto stream_rows = [&](int e, int w, int part = 0, int nparts = 1) {
     const int r0 = bx * 4 * rpw + w * rpw;
     const int n = min(rpw, a.n_ff - r0);
     if (e < 0 || n <= 0) return;
     const sg_block_q4k* wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
     const sg_block_q4k* wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
-    if (wg && wu) dma_gateup(wg, wu, r0, n, nbh, wbuf[w], lane);
+    if (wg && wu) dma_gateup(wg, wu, r0, n, nbh, wbuf[w], lane, part, nparts);
   };
 
-  float lr[EPT];
   int e_mine = -1;
   int n_groups;
   if (a.logits) {
@@ -831,12 +855,13 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
       bar();
       e_mine = g < gbase + ctrl[1] ? pexp[g] : -1;
       // speculative: the logit-order expert.  One token: waves 0-2 issue
-      // the stream (wave 0 also wave 3's rows) so wave 3 routes unblocked.
+      // the stream (each also a third of wave 3's rows) so wave 3 routes
+      // unblocked.
       if (!t1w) {
         stream_rows(e_mine, wave);
       } else if (wave < 3) {
         stream_rows(e_mine, wave);
-        if (wave == 0) stream_rows(e_mine, 3);
+        stream_rows(e_mine, 3, wave, 3);
       }
     }
     if (t1w) {
@@ -844,7 +869,7 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
         route_wave<4 * EPT>(a, dyn, L, lane);
       } else if (!publisher) {
         quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);  // overlaps the weight stream
-        if (wave == 0) wait_vm();  // wave 3's rows
+        wait_vm();  // this wave's share of wave 3's rows
       }
       bar();
     } else {
@@ -941,8 +966,10 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
 // LDS (h was loaded at kernel start, beside the plan).  The slot outputs of
 // the chunk go to LDS; then the workgroup combines
 // out = residual + sum_kk fma(w_kk, y_kk) in slot order.
+constexpr int kBackHSlots = 5;  // h blocks per wave preloaded at kernel start (T = 1, k = 8: 18)
+
 struct BackLds {
-  int hq, ys, off, wdown, tok, slot, wt, ok, meta, total;
+  int hq, ys, off, wdown, tok, slot, wt, meta, total;
 };
 
 __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, int gmax,
@@ -963,20 +990,18 @@ __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, in
   L.tok = take(emax);
   L.slot = take(emax);
   L.wt = take(T * (k + 1));
-  L.ok = take(T * (k + 1));
   L.meta = take(4);
   L.total = o;
   return L;
 }
 
 // The down rows, Q8_K of h and combine of one chunk of `rows` output rows,
-// with the plan in LDS (off, wdown, tok, slot, wt, ok, meta).  before_h()
-// runs after the first down rows are issued and before h is read;
-// hblock(pass_first, u, e, v) yields the lane's 4 values of h block e.
-template <typename BeforeH, typename HBlock>
-__device__ void back_core(const LayerArgs& a, const BackLds& L, uint32_t* bd,
+// with the plan in LDS (off, wdown, tok, slot, wt, meta).  Wave w
+// quantizes h blocks w + 4j; hpre[j] holds the lane's 4 values of block
+// w + 4j for j < kBackHSlots (loaded at kernel start).
+__device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, uint32_t* bd,
                           uint32_t (*wbuf)[64 * 36], int row0, int nr, float res0,
-                          BeforeH before_h, HBlock hblock) {
+                          const float (&hpre)[kBackHSlots][4]) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, stride = k + 1;
   const int nbf = a.n_ff / kQK;
@@ -989,7 +1014,6 @@ __device__ void back_core(const LayerArgs& a, const BackLds& L, uint32_t* bd,
   const int* tok = reinterpret_cast<const int*>(bd + L.tok);
   const int* slot = reinterpret_cast<const int*>(bd + L.slot);
   const float* wt = reinterpret_cast<const float*>(bd + L.wt);
-  const int* okf = reinterpret_cast<const int*>(bd + L.ok);
   const int* meta = reinterpret_cast<const int*>(bd + L.meta);
   const int nq = T * stride * nbf;
   const int n_out = T * nr;
@@ -1000,26 +1024,54 @@ __device__ void back_core(const LayerArgs& a, const BackLds& L, uint32_t* bd,
   const int rr = (lane / lrow) % rows, blk = lane & (lrow - 1);
 
   for (int gb = 0; gb < G; gb += 4 * gpw) {
-    // down rows of this wave's groups
-    for (int qq = 0; qq < gpw; ++qq) {
-      const int gq = gb + wave * gpw + qq;
-      if (gq >= G) break;
-      const char* wd = reinterpret_cast<const char*>(wdown[gq]);
-      if (wd && nr > 0) {
-        const char* src = wd + static_cast<long long>(row0) * nbf * kQ4Bytes;
-        dma_chunks([&](int c) { return src + 16 * c; }, nr * nbf * 9, buf + qq * gwords, lane);
+    // down rows of this wave's gpw groups as one run of 16-B chunks: chunk
+    // c = group c / cpg, chunk c % cpg of the group's rows; LDS destination
+    // buf + 4c (group qq at buf + qq * gwords).  At most 9 copy
+    // instructions, no loop over groups.
+    {
+      const int cpg = gwords / 4;       // chunks per group slot
+      const int cval = nr * nbf * 9;    // chunks present (nr < rows at the edge)
+      const uint32_t inv = ((1u << 20) + cpg - 1) / cpg;  // c / cpg exact for c < 576
+      const long long roff = static_cast<long long>(row0) * nbf * kQ4Bytes;
+#pragma unroll
+      for (int i = 0; i < 9; ++i) {
+        const int c = lane + 64 * i;
+        if (64 * i >= gpw * cpg) break;
+        const int qq = static_cast<int>((static_cast<uint32_t>(c) * inv) >> 20);
+        const int w = c - qq * cpg;
+        const int gq = gb + wave * gpw + qq;
+        const unsigned long long wd = qq < gpw && gq < G ? wdown[gq] : 0ull;
+        if (wd && w < cval)
+          __builtin_amdgcn_global_load_lds(
+              (glb_void_p)(reinterpret_cast<const char*>(wd) + roff + 16 * w),
+              (lds_void_p)(buf + 256 * i), 16, 0, 0);
       }
     }
     if (gb == 0) {  // Q8_K of every (token, slot) h row while the rows stream in
-      before_h();
-      for (int e0 = wave; e0 < nq; e0 += 16) {
+      // blocks e = wave + 4j: j < kBackHSlots from registers in one
+      // interleaved pass (every block of a one-token layer with k <= 8),
+      // later ones in passes of four loaded here
+      if (wave < nq) {
+        uint32_t* dst[kBackHSlots];
+        int n = 0;
+#pragma unroll
+        for (int j = 0; j < kBackHSlots; ++j) {
+          const int e = wave + 4 * j;
+          dst[j] = hq + (e < nq ? e : wave) * kXStride;
+          n += e < nq;
+        }
+        quantize_n_lds<kBackHSlots>(hpre, dst, n, lane);
+      }
+      for (int e0 = wave + 4 * kBackHSlots; e0 < nq; e0 += 16) {
         float v[4][4];
         uint32_t* dst[4];
         int n = 0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int e = e0 + 4 * u < nq ? e0 + 4 * u : e0;
-          hblock(e0 == wave, u, e, v[u]);
+          const float* hp = a.h + static_cast<long long>(e) * kQK + 4 * lane;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[u][i] = hp[i];
           dst[u] = hq + e * kXStride;
           n += e0 + 4 * u < nq;
         }
@@ -1039,8 +1091,7 @@ __device__ void back_core(const LayerArgs& a, const BackLds& L, uint32_t* bd,
       sm8 = unpack_scales(w36[1], w36[2], w36[3]);
     }
     const int jb = has ? off[gq] : 0, je = has ? off[gq + 1] : 0;
-    int cnt = je - jb;
-    for (int o = 32; o > 0; o >>= 1) cnt = max(cnt, __shfl_xor(cnt, o, 64));
+    const int cnt = wave_max_i32(je - jb);
     for (int ji = 0; ji < cnt; ++ji) {
       const int j = jb + ji;
       const bool ok = j < je;
@@ -1059,23 +1110,24 @@ __device__ void back_core(const LayerArgs& a, const BackLds& L, uint32_t* bd,
     wait_lds();
   }
   bar();
-  const int has_shared = meta[1];
+  // out = residual + sum over slots 0..k of fma(w, y) in slot order.  A slot
+  // whose id was invalid (bounds-killed), whose expert is absent, or the
+  // shared slot without a shared expert has no plan entry, so its y is the
+  // 0 the prologue stored.
   for (int qo = tid; qo < n_out; qo += 256) {
     const int t = qo / nr, r = qo - t * nr;
     const long long o = static_cast<long long>(t) * a.hidden + row0 + r;
     float acc = a.residual ? (qo == tid ? res0 : a.residual[o]) : 0.f;
-    for (int k0 = 0; k0 <= k; k0 += 8) {  // gather 8 slots, then the ordered fma chain
-      float yv[8], wv[8];
+    for (int k0 = 0; k0 <= k; k0 += 16) {  // gather 16 slots, then the ordered fma chain
+      float yv[16], wv[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int kk = k0 + u;
-        const int i = t * stride + (kk <= k ? kk : k);
-        const bool ok = okf[i] < 0 ? has_shared != 0 : okf[i] != 0;
-        yv[u] = ok ? ys[i * rows + r] : 0.f;
+      for (int u = 0; u < 16; ++u) {
+        const int i = t * stride + (k0 + u <= k ? k0 + u : k);
+        yv[u] = ys[i * rows + r];
         wv[u] = wt[i];
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < 16; ++u)
         if (k0 + u <= k) acc = __builtin_fmaf(wv[u], yv[u], acc);
     }
     a.out[o] = acc;
@@ -1103,49 +1155,60 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
   int* tok = reinterpret_cast<int*>(dyn + L.tok);
   int* slot = reinterpret_cast<int*>(dyn + L.slot);
   float* wt = reinterpret_cast<float*>(dyn + L.wt);
-  int* okf = reinterpret_cast<int*>(dyn + L.ok);
   int* meta = reinterpret_cast<int*>(dyn + L.meta);
   float* ys = reinterpret_cast<float*>(dyn + L.ys);
   const int row0 = blockIdx.x * rows;
   const int nr = max(0, min(rows, a.hidden - row0));
 
-  // loads that do not depend on the plan: this wave's first pass of h
-  // blocks (every (token, slot) row, 4 blocks per wave) and the residual
+  // loads that do not depend on the plan: this wave's first kBackHSlots h
+  // blocks (block wave + 4j of the (token, slot) rows) and the residual
   const int nq = T * stride * nbf;
-  float hpre[4][4];
+  float hpre[kBackHSlots][4];
   if (wave < nq) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int e = wave + 4 * u < nq ? wave + 4 * u : wave;
+    for (int j = 0; j < kBackHSlots; ++j) {
+      const int e0 = wave + 4 * j;
+      const int e = e0 < nq ? e0 : wave;
       const float* hp = a.h + static_cast<long long>(e) * kQK + 4 * lane;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) hpre[u][i] = hp[i];
+      for (int i = 0; i < 4; ++i) hpre[j][i] = hp[i];
     }
   }
   const float res0 = residual_pre(a, row0, nr);
 
-  // the plan and routing weights (one round of loads)
-  if (tid < 2) meta[tid] = a.plan.meta[tid];
-  for (int i = tid; i <= a.gmax; i += 256) off[i] = a.plan.off[i];
-  for (int i = tid; i < a.gmax; i += 256) wdown[i] = a.plan.wdown[i];
-  for (int i = tid; i < a.emax; i += 256) {
-    tok[i] = a.plan.tok[i];
-    slot[i] = a.plan.slot[i];
-  }
-  for (int i = tid; i < T * stride; i += 256) {
-    wt[i] = a.weight[i];
-    const int kk = i % stride;
-    const int ee = a.idx[i];
-    okf[i] = kk < k ? (ee >= 0 && ee < a.n_expert) : -1;  // -1: shared slot
+  // the plan and routing weights.  When every array fits one element per
+  // thread, each thread issues all of its loads (clamped indices, no
+  // branches) before it waits once; loads inside separate guarded loops
+  // would each wait for the previous one.
+  const int nw = T * stride;
+  if (a.gmax + 1 <= 256 && a.emax <= 256 && nw <= 256) {
+    const int v_meta = a.plan.meta[min(tid, 1)];
+    const int v_off = a.plan.off[min(tid, a.gmax)];
+    const unsigned long long v_wd = a.plan.wdown[min(tid, a.gmax - 1)];
+    const int v_tok = a.plan.tok[min(tid, a.emax - 1)];
+    const int v_slot = a.plan.slot[min(tid, a.emax - 1)];
+    const float v_wt = a.weight[min(tid, nw - 1)];
+    if (tid < 2) meta[tid] = v_meta;
+    if (tid <= a.gmax) off[tid] = v_off;
+    if (tid < a.gmax) wdown[tid] = v_wd;
+    if (tid < a.emax) {
+      tok[tid] = v_tok;
+      slot[tid] = v_slot;
+    }
+    if (tid < nw) wt[tid] = v_wt;
+  } else {
+    if (tid < 2) meta[tid] = a.plan.meta[tid];
+    for (int i = tid; i <= a.gmax; i += 256) off[i] = a.plan.off[i];
+    for (int i = tid; i < a.gmax; i += 256) wdown[i] = a.plan.wdown[i];
+    for (int i = tid; i < a.emax; i += 256) {
+      tok[i] = a.plan.tok[i];
+      slot[i] = a.plan.slot[i];
+    }
+    for (int i = tid; i < nw; i += 256) wt[i] = a.weight[i];
   }
   for (int i = tid; i < T * stride * rows; i += 256) ys[i] = 0.f;
   bar();
-  back_core(a, L, dyn, wbuf, row0, nr, res0, [] {},
-            [&](bool first, int u, int e, float* v) {
-              const float* hp = a.h + static_cast<long long>(e) * kQK + 4 * lane;
-#pragma unroll
-              for (int i = 0; i < 4; ++i) v[i] = first ? hpre[u][i] : hp[i];
-            });
+  back_core(a, L, dyn, wbuf, row0, nr, res0, hpre);
 }
 
 static void back_geometry(int hidden, int n_ff, int& rows, int& lrow) {
