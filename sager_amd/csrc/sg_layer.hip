@@ -37,7 +37,7 @@ constexpr int kLMaxK = 32;
 constexpr int kLMaxTokens = 16;
 constexpr int kMaxEpt = 16;        // experts per routing thread (1-wave teams, E = 1024)
 
-__host__ __device__ inline int pow2_ceil(int n) {
+__host__ __device__ constexpr inline int pow2_ceil(int n) {
   int l = 1;
   while (l < n) l <<= 1;
   return l;
@@ -101,8 +101,8 @@ struct LayerArgs {
 // Routing runs in teams: one team of 4 waves per token for T = 1, two teams
 // of 2 waves for T = 2, four one-wave teams otherwise (tokens in passes).
 struct FrontLds {
-  int nteams, tw, TT, ept, m, ng, npad, e32, ncp;
-  int tabg, tabu, tabd, keys, lv, ev, cand, top, red, zs, spec, ridx, rw, re, rfirst, poff, pexp,
+  int nteams, tw, TT, ept, m, e32, ncp;
+  int tabg, tabu, tabd, lv, ev, cand, top, red, zs, spec, ridx, rw, re, rfirst, poff, pexp,
       ptok, pslot, ctrl, xs, total;
 };
 
@@ -113,10 +113,8 @@ __host__ __device__ inline FrontLds front_lds(int T, int nbh, int E, int k, bool
   L.TT = 64 * L.tw;
   L.ept = (E + L.TT - 1) / L.TT;
   L.m = k + 1;
-  L.ng = (E + 63) / 64;
-  L.npad = L.ng * 64;
   L.e32 = (E + 31) & ~31;
-  L.ncp = (L.ng * L.m + 3) & ~3;
+  L.ncp = (L.tw * L.m + 3) & ~3;  // a team's candidates: m per wave
   const int gmax = (T * k < E ? T * k : E) + 1;
   int o = 0;
   auto take = [&](int words) {
@@ -130,7 +128,6 @@ __host__ __device__ inline FrontLds front_lds(int T, int nbh, int E, int k, bool
     L.tabg = take(E * 2);
     L.tabu = take(E * 2);
     L.tabd = take(E * 2);
-    L.keys = take(L.nteams * L.npad * 2);
     L.lv = take(L.nteams * L.e32);
     L.ev = take(L.nteams * L.e32);
     L.cand = take(L.nteams * L.ncp * 2);
@@ -152,22 +149,6 @@ __host__ __device__ inline FrontLds front_lds(int T, int nbh, int E, int k, bool
   return L;
 }
 
-// rank of `key` among 64 keys (16-B aligned): how many are larger.
-// All 32 reads are issued before the first compare (LDS latency paid once).
-__device__ __forceinline__ int rank64(const uint64_t* g, uint64_t key) {
-  const u32x4* p = reinterpret_cast<const u32x4*>(g);
-  u32x4 v[32];
-#pragma unroll
-  for (int q = 0; q < 32; ++q) v[q] = p[q];
-  int r = 0;
-#pragma unroll
-  for (int q = 0; q < 32; ++q) {
-    const uint64_t a = (static_cast<uint64_t>(v[q].y) << 32) | v[q].x;
-    const uint64_t b = (static_cast<uint64_t>(v[q].w) << 32) | v[q].z;
-    r += (a > key) + (b > key);
-  }
-  return r;
-}
 // rank among n (multiple of 4) keys, 16-B aligned.
 __device__ __forceinline__ int rank_n(const uint64_t* c, int n, uint64_t key) {
   const u32x4* p = reinterpret_cast<const u32x4*>(c);
@@ -193,30 +174,74 @@ __device__ __forceinline__ int rank_n(const uint64_t* c, int n, uint64_t key) {
   return r;
 }
 
-// Top-m selection of a team over keys[0..npad) (own keys also in kr[]):
-// per 64-key group the m largest, then the m largest of those.  Three
-// barriers; every thread of the workgroup takes part.
+// Top-m selection of a team (tw waves) over the keys kr[] its threads hold
+// (0 = no key; keys are otherwise distinct).  Stage 1, per wave with no
+// LDS traffic: a bitwise radix search over ballot counts finds the wave's
+// m-th largest key - first on the value word, then, only when several keys
+// share the boundary value, on the index word - and the wave's m largest
+// keys go to cand[wave * m ...) in any order (zero-padded).  Stage 2: each
+// candidate's rank among the team's tw*m candidates places it in top[rank]
+// (0 = missing).  Two barriers; every thread of the workgroup takes part.
 template <int EPT>
-__device__ void team_select(const FrontLds& L, int E, const uint64_t* keys, const uint64_t* kr,
-                            uint64_t* cand, uint64_t* top, int tt) {
-  const int m = L.m;
-  for (int i = tt; i < L.ncp; i += L.TT) cand[i] = 0;
-  for (int i = tt; i < m; i += L.TT) top[i] = 0;
-  bar();
+__device__ void team_select(const FrontLds& L, const uint64_t* kr, uint64_t* cand, uint64_t* top,
+                            int tt) {
+  const int m = L.m, lane = tt & 63, wit = tt >> 6;
+  uint32_t hi[EPT], lo[EPT];
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    const int i = tt + L.TT * j;
-    if (j < L.ept && i < E && kr[j] != 0) {
-      const int r = rank64(keys + (i & ~63), kr[j]);
-      if (r < m) cand[(i >> 6) * m + r] = kr[j];
+    hi[j] = static_cast<uint32_t>(kr[j] >> 32);
+    lo[j] = static_cast<uint32_t>(kr[j]);
+  }
+  // th: the largest value word v with at least m keys of value >= v (0 when
+  // the wave has fewer than m keys of nonzero value)
+  uint32_t th = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t c = th | (1u << b);
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) n += __popcll(__ballot(hi[j] >= c));
+    if (n >= m) th = c;
+  }
+  int n_gt = 0, n_eq = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    n_gt += __popcll(__ballot(hi[j] > th));
+    n_eq += __popcll(__ballot(hi[j] == th && kr[j] != 0));
+  }
+  const int need = m - n_gt;  // >= 1
+  // at the boundary value, the `need` largest index words (lowest experts)
+  uint32_t tl = 0;
+  if (n_eq > need) {
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t c = tl | (1u << b);
+      int n = 0;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) n += __popcll(__ballot(hi[j] == th && kr[j] != 0 && lo[j] >= c));
+      if (n >= need) tl = c;
     }
   }
+  uint64_t* wc = cand + wit * m;
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const bool sel = kr[j] != 0 && (hi[j] > th || (hi[j] == th && lo[j] >= tl));
+    const uint64_t bm = __ballot(sel);
+    const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bm >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bm), 0));
+    if (sel) wc[base + below] = kr[j];
+    base += __popcll(bm);
+  }
+  if (lane >= base && lane < m) wc[lane] = 0;
+  const int nc = L.tw * m;
+  if (tt >= nc && tt < L.ncp) cand[tt] = 0;  // rank_n reads whole 16-B pairs
+  if (tt < m) top[tt] = 0;
   bar();
-  for (int c = tt; c < L.ng * m; c += L.TT) {
-    const uint64_t kc = cand[c];
-    if (kc == 0) continue;
-    const int r = rank_n(cand, L.ncp, kc);
-    if (r < m) top[r] = kc;
+  if (tt < nc) {
+    const uint64_t key = cand[tt];
+    if (key != 0) {
+      const int r = rank_n(cand, L.ncp, key);
+      if (r < m) top[r] = key;
+    }
   }
   bar();
 }
@@ -454,7 +479,6 @@ __device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L
                             int tid) {
   const int T = a.T, E = a.n_expert, m = L.m;
   const int wave = tid >> 6, team = wave / L.tw, tt = tid - team * L.TT;
-  uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + L.keys) + team * L.npad;
   float* lv = reinterpret_cast<float*>(dyn + L.lv) + team * L.e32;
   uint64_t* cand = reinterpret_cast<uint64_t*>(dyn + L.cand) + team * L.ncp;
   uint64_t* top = reinterpret_cast<uint64_t*>(dyn + L.top) + team * m;
@@ -470,12 +494,11 @@ __device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L
       const bool in = j < L.ept && i < E && ok;
       if (t0 > 0) lr[j] = in ? lg[i] : 0.f;  // pass 0: logits_preload
       kr[j] = in ? sel_key(lr[j], i) : 0;
-      if (j < L.ept && i < L.npad) keys[i] = kr[j];
       if (j < L.ept && i < L.e32) lv[i] = lr[j];
     }
-    team_select<EPT>(L, E, keys, kr, cand, top, tt);
+    team_select<EPT>(L, kr, cand, top, tt);
     if (ok && tt < m) spec[t * m + tt] = top[tt] ? sel_idx(top[tt]) : -1;
-    if (t0 + L.nteams < T) bar();  // the next pass reuses keys/cand/top
+    if (t0 + L.nteams < T) bar();  // the next pass reuses cand/top
   }
 }
 
@@ -649,7 +672,6 @@ __device__ void exact_route(const LayerArgs& a, uint32_t* dyn, const FrontLds& L
   const int lane = tid & 63, wave = tid >> 6;
   const int tw = L.tw, team = wave / tw, wit = wave - team * tw;
   const int tt = tid - team * L.TT;
-  uint64_t* keys = reinterpret_cast<uint64_t*>(dyn + L.keys) + team * L.npad;
   float* lv = reinterpret_cast<float*>(dyn + L.lv) + team * L.e32;
   float* ev = reinterpret_cast<float*>(dyn + L.ev) + team * L.e32;
   uint64_t* cand = reinterpret_cast<uint64_t*>(dyn + L.cand) + team * L.ncp;
@@ -716,9 +738,8 @@ __device__ void exact_route(const LayerArgs& a, uint32_t* dyn, const FrontLds& L
       for (int j = 0; j < EPT; ++j) {
         const int i = tt + L.TT * j;
         kr[j] = (j < L.ept && i < E && slow_team) ? sel_key(ev[i] / z, i) : 0;
-        if (j < L.ept && i < L.npad) keys[i] = kr[j];
       }
-      team_select<EPT>(L, E, keys, kr, cand, top, tt);
+      team_select<EPT>(L, kr, cand, top, tt);
     }
     if (wit == 0 && ok) {
       int fi;
@@ -999,13 +1020,17 @@ __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, in
 // with the plan in LDS (off, wdown, tok, slot, wt, meta).  Wave w
 // quantizes h blocks w + 4j; hpre[j] holds the lane's 4 values of block
 // w + 4j for j < kBackHSlots (loaded at kernel start).
+// NBF, ROWS: n_ff / 256 and the rows per workgroup when known at compile
+// time (0 = read from a).
+template <int NBF, int ROWS>
 __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, uint32_t* bd,
                           uint32_t (*wbuf)[64 * 36], int row0, int nr, float res0,
                           const float (&hpre)[kBackHSlots][4]) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, stride = k + 1;
-  const int nbf = a.n_ff / kQK;
-  const int rows = a.back_rows, lrow = a.back_lrow;
+  const int nbf = NBF ? NBF : a.n_ff / kQK;
+  const int rows = ROWS ? ROWS : a.back_rows;
+  const int lrow = NBF ? pow2_ceil(NBF) : a.back_lrow;
   const int gpw = 64 / (rows * lrow);  // groups per wave per pass
   uint32_t* hq = bd + L.hq;
   float* ys = reinterpret_cast<float*>(bd + L.ys);
@@ -1142,13 +1167,14 @@ __device__ __forceinline__ float residual_pre(const LayerArgs& a, int row0, int 
   return a.residual[static_cast<long long>(t) * a.hidden + row0 + r];
 }
 
+template <int NBF, int ROWS>
 __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, stride = k + 1;
-  const int nbf = a.n_ff / kQK;
-  const int rows = a.back_rows;
+  const int nbf = NBF ? NBF : a.n_ff / kQK;
+  const int rows = ROWS ? ROWS : a.back_rows;
   const BackLds L = back_lds(T, k, a.n_ff, rows, a.gmax, a.emax);
   int* off = reinterpret_cast<int*>(dyn + L.off);
   unsigned long long* wdown = reinterpret_cast<unsigned long long*>(dyn + L.wdown);
@@ -1208,7 +1234,7 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
   }
   for (int i = tid; i < T * stride * rows; i += 256) ys[i] = 0.f;
   bar();
-  back_core(a, L, dyn, wbuf, row0, nr, res0, hpre);
+  back_core<NBF, ROWS>(a, L, dyn, wbuf, row0, nr, res0, hpre);
 }
 
 static void back_geometry(int hidden, int n_ff, int& rows, int& lrow) {
@@ -1316,8 +1342,13 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     if (int st = check_launch("sg_moe_layer/front")) return st;
   }
   if (stages & 2) {
-    hipLaunchKernelGGL(layer_back_kernel, dim3((hidden + rows - 1) / rows), dim3(256), lds_b, s,
-                       a);
+    // the decode geometry of n_ff = 512 at hidden >= 2048 compiled for its
+    // constants; other shapes read them from the arguments
+    const dim3 gb((hidden + rows - 1) / rows);
+    if (n_ff / kQK == 2 && rows == 8)
+      hipLaunchKernelGGL((layer_back_kernel<2, 8>), gb, dim3(256), lds_b, s, a);
+    else
+      hipLaunchKernelGGL((layer_back_kernel<0, 0>), gb, dim3(256), lds_b, s, a);
     if (int st = check_launch("sg_moe_layer/back")) return st;
   }
   return SG_OK;
