@@ -184,7 +184,7 @@ __device__ __forceinline__ int rank_n(const uint64_t* c, int n, uint64_t key) {
 // (0 = missing).  Two barriers; every thread of the workgroup takes part.
 template <int EPT>
 __device__ void team_select(const FrontLds& L, const uint64_t* kr, uint64_t* cand, uint64_t* top,
-                            int tt) {
+                            int tt, bool wait_before_rank = false) {
   const int m = L.m, lane = tt & 63, wit = tt >> 6;
   uint32_t hi[EPT], lo[EPT];
 #pragma unroll
@@ -235,6 +235,7 @@ __device__ void team_select(const FrontLds& L, const uint64_t* kr, uint64_t* can
   const int nc = L.tw * m;
   if (tt >= nc && tt < L.ncp) cand[tt] = 0;  // rank_n reads whole 16-B pairs
   if (tt < m) top[tt] = 0;
+  if (wait_before_rank) wait_vm();  // the caller's copies are visible after the barrier
   bar();
   if (tt < nc) {
     const uint64_t key = cand[tt];
@@ -476,7 +477,7 @@ __device__ __forceinline__ void logits_preload(const LayerArgs& a, int tid, floa
 
 template <int EPT>
 __device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
-                            int tid) {
+                            int tid, bool wait_copies = false) {
   const int T = a.T, E = a.n_expert, m = L.m;
   const int wave = tid >> 6, team = wave / L.tw, tt = tid - team * L.TT;
   float* lv = reinterpret_cast<float*>(dyn + L.lv) + team * L.e32;
@@ -496,7 +497,7 @@ __device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L
       kr[j] = in ? sel_key(lr[j], i) : 0;
       if (j < L.ept && i < L.e32) lv[i] = lr[j];
     }
-    team_select<EPT>(L, kr, cand, top, tt);
+    team_select<EPT>(L, kr, cand, top, tt, wait_copies && t0 == 0);
     if (ok && tt < m) spec[t * m + tt] = top[tt] ? sel_idx(top[tt]) : -1;
     if (t0 + L.nteams < T) bar();  // the next pass reuses cand/top
   }
@@ -504,9 +505,10 @@ __device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L
 
 // Plan for T == 1 straight from k distinct, valid ids id(0..k-1): group
 // gbase + r = the expert of rank r, its single entry (token 0, slot j).
-// Ends with a barrier.
+// Ends with a barrier unless the caller places one.
 template <typename Id>
-__device__ void plan_t1(uint32_t* dyn, const FrontLds& L, int k, int has_shared, int tid, Id id) {
+__device__ void plan_t1(uint32_t* dyn, const FrontLds& L, int k, int has_shared, int tid, Id id,
+                        bool barrier = true) {
   int* re = reinterpret_cast<int*>(dyn + L.re);
   int* poff = reinterpret_cast<int*>(dyn + L.poff);
   int* pexp = reinterpret_cast<int*>(dyn + L.pexp);
@@ -535,7 +537,7 @@ __device__ void plan_t1(uint32_t* dyn, const FrontLds& L, int k, int has_shared,
     ctrl[0] = k;
     ctrl[1] = k;
   }
-  bar();
+  if (barrier) bar();
 }
 
 // True when ridx[0..n) are distinct valid ids (what routing produces for
@@ -581,7 +583,7 @@ __device__ void route_wave(const LayerArgs& a, uint32_t* dyn, const FrontLds& L,
   const int E = a.n_expert, k = a.k, m = L.m;
   const float* lv = reinterpret_cast<const float*>(dyn + L.lv);
   float* ev = reinterpret_cast<float*>(dyn + L.ev);
-  const int* spec = reinterpret_cast<const int*>(dyn + L.spec);
+  const uint64_t* top = reinterpret_cast<const uint64_t*>(dyn + L.top);
   int* ridx = reinterpret_cast<int*>(dyn + L.ridx);
   float* rw = reinterpret_cast<float*>(dyn + L.rw);
   int* ctrl = reinterpret_cast<int*>(dyn + L.ctrl);
@@ -602,7 +604,7 @@ __device__ void route_wave(const LayerArgs& a, uint32_t* dyn, const FrontLds& L,
   // the wave's LDS writes complete in order before its own reads
   const float z = readlane_f(lane == 0 ? serial_sum(ev, L.e32) : 0.f, 0);
   const bool degen = !(z == z) || z == 0.f;
-  const int ik = lane < m ? spec[lane] : -1;
+  const int ik = lane < m && top[lane] != 0ull ? sel_idx(top[lane]) : -1;  // logit order
   const float pk = (ik >= 0 && !degen) ? ev[ik] / z : -1.f;
   const float lk = ik >= 0 ? lv[ik] : 0.f;
   const float pn = __shfl(pk, lane + 1, 64);
@@ -645,7 +647,7 @@ __device__ void route_wave(const LayerArgs& a, uint32_t* dyn, const FrontLds& L,
   const float wv = wsum > 0.f ? pv / wsum : pv;
   bool changed = false;
   if (lane < k) {
-    changed = fi != ridx[lane];
+    changed = fi != ik;
     ridx[lane] = fi;
     rw[lane] = wv;
   }
@@ -850,7 +852,10 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
   int e_mine = -1;
   int n_groups;
   if (a.logits) {
-    spec_select<EPT>(a, dyn, L, lr, tid);
+    // waves 0-1 wait for the pointer tables inside the selection, so they
+    // are readable when it returns
+    spec_select<EPT>(a, dyn, L, lr, tid, wave < 2);
+    bool streamed = false, routed = false;
     if (T == 1) {
       // top[] of the single token is readable now: with k valid ids the
       // plan is made here, in the same phase as spec[] and ridx[]
@@ -858,8 +863,33 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
       bool valid = true;
       for (int j = 0; j < k; ++j) valid &= top[j] != 0ull;
       if (valid) {
-        if (tid < k) ridx[tid] = sel_idx(top[tid]);
-        plan_t1(dyn, L, k, a.has_shared, tid, [&](int j) { return sel_idx(top[j]); });
+        if (!publisher) {
+          // speculative: the logit-order expert of this group, i.e. the one
+          // of id rank g - gbase among top[] (what plan_t1 assigns), read
+          // straight from top[] so the stream starts before the plan round.
+          // Waves 0-2 issue it (each also a third of wave 3's rows) so
+          // wave 3 routes unblocked.
+          const int want = g - gbase;
+          const int idl = lane < k ? sel_idx(top[lane]) : 0x7FFFFFFF;
+          int r = 0;
+          for (int i = 0; i < k; ++i) r += __builtin_amdgcn_readlane(idl, i) < idl;
+          const uint64_t hit = __ballot(lane < k && r == want);
+          e_mine = hit ? __builtin_amdgcn_readlane(idl, __builtin_ctzll(hit)) : -1;
+          if (wave < 3) {
+            stream_rows(e_mine, wave);
+            stream_rows(e_mine, 3, wave, 3);
+          }
+          streamed = true;
+        }
+        // wave 3 routes exactly now (it reads top[] and lv[], complete since
+        // the selection's last barrier) and writes ridx[] itself; the plan
+        // is published by the barrier after the x quantization below.
+        // wave 2 (the one with the fewest x blocks to quantize) writes the
+        // plan, its lanes in the roles of threads 0..63
+        if (wave == 3) route_wave<4 * EPT>(a, dyn, L, lane);
+        if (wave == 2)
+          plan_t1(dyn, L, k, a.has_shared, lane, [&](int j) { return sel_idx(top[j]); }, false);
+        routed = true;
       } else {
         if (tid < k) ridx[tid] = top[tid] ? sel_idx(top[tid]) : -1;
         bar();
@@ -871,9 +901,7 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
       bar();
       build_plan(dyn, L, T, k, E, a.has_shared, tid);
     }
-    if (!publisher) {
-      if (wave < 2) wait_vm();  // pointer tables
-      bar();
+    if (!publisher && !streamed) {
       e_mine = g < gbase + ctrl[1] ? pexp[g] : -1;
       // speculative: the logit-order expert.  One token: waves 0-2 issue
       // the stream (each also a third of wave 3's rows) so wave 3 routes
@@ -887,7 +915,7 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
     }
     if (t1w) {
       if (wave == 3) {
-        route_wave<4 * EPT>(a, dyn, L, lane);
+        if (!routed) route_wave<4 * EPT>(a, dyn, L, lane);
       } else if (!publisher) {
         quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);  // overlaps the weight stream
         wait_vm();  // this wave's share of wave 3's rows
@@ -976,7 +1004,13 @@ template <int EPT>
 __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
-  front_body<EPT>(a, blockIdx.x, blockIdx.y, wbuf, dyn);
+  // Row y of the grid runs group g.  With a shared expert its row comes
+  // after the routed ones: workgroups are placed on CUs in grid order, so the
+  // routed workgroups (the long routing chain) each get a CU of their own
+  // and the shared expert's (no routing, done early) double up.
+  const int y = blockIdx.y;
+  const int g = !a.has_shared || y >= a.gmax ? y : (y + 1 == a.gmax ? 0 : y + 1);
+  front_body<EPT>(a, blockIdx.x, g, wbuf, dyn);
 }
 
 // ---- back kernel ------------------------------------------------------------------------
