@@ -840,16 +840,19 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
 
   // stream the gate/up rows of expert e (none when e < 0 or it is absent)
   // for wave w's rows into wave w's buffer
+  // (returns whether expert e is present: both its matrices non-null)
   auto stream_rows = [&](int e, int w, int part = 0, int nparts = 1) {
+    if (e < 0) return false;
     const int r0 = bx * 4 * rpw + w * rpw;
     const int n = min(rpw, a.n_ff - r0);
-    if (e < 0 || n <= 0) return;
     const sg_block_q4k* wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
     const sg_block_q4k* wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
-    if (wg && wu) dma_gateup(wg, wu, r0, n, nbh, wbuf[w], lane, part, nparts);
+    if (wg && wu && n > 0) dma_gateup(wg, wu, r0, n, nbh, wbuf[w], lane, part, nparts);
+    return wg && wu;
   };
 
-  int e_mine = -1;
+  int e_mine = -1, slot_mine = -1;
+  bool present_mine = false;
   int n_groups;
   if (a.logits) {
     // waves 0-1 wait for the pointer tables inside the selection, so they
@@ -860,25 +863,25 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
       // top[] of the single token is readable now: with k valid ids the
       // plan is made here, in the same phase as spec[] and ridx[]
       const uint64_t* top = reinterpret_cast<const uint64_t*>(dyn + L.top);
-      bool valid = true;
-      for (int j = 0; j < k; ++j) valid &= top[j] != 0ull;
+      const uint64_t tk = lane < k ? top[lane] : 1ull;  // lane j: key of slot j
+      const bool valid = __ballot(tk == 0ull) == 0ull;
       if (valid) {
         if (!publisher) {
           // speculative: the logit-order expert of this group, i.e. the one
-          // of id rank g - gbase among top[] (what plan_t1 assigns), read
-          // straight from top[] so the stream starts before the plan round.
-          // Waves 0-2 issue it (each also a third of wave 3's rows) so
-          // wave 3 routes unblocked.
+          // of id rank g - gbase among top[] (what plan_t1 assigns), and its
+          // slot, read straight from top[] so the stream starts before the
+          // plan round.  Waves 0-2 issue it (each also a third of wave 3's
+          // rows) so wave 3 routes unblocked.
           const int want = g - gbase;
-          const int idl = lane < k ? sel_idx(top[lane]) : 0x7FFFFFFF;
+          const int idl = lane < k ? sel_idx(tk) : 0x7FFFFFFF;
           int r = 0;
           for (int i = 0; i < k; ++i) r += __builtin_amdgcn_readlane(idl, i) < idl;
           const uint64_t hit = __ballot(lane < k && r == want);
-          e_mine = hit ? __builtin_amdgcn_readlane(idl, __builtin_ctzll(hit)) : -1;
-          if (wave < 3) {
-            stream_rows(e_mine, wave);
-            stream_rows(e_mine, 3, wave, 3);
-          }
+          slot_mine = hit ? __builtin_ctzll(hit) : -1;
+          e_mine = hit ? __builtin_amdgcn_readlane(idl, slot_mine) : -1;
+          if (wave < 3) present_mine = stream_rows(e_mine, wave);
+          if (wave < 3) stream_rows(e_mine, 3, wave, 3);
+          if (wave == 3 && e_mine >= 0) present_mine = tabg[e_mine] != 0ull && tabu[e_mine] != 0ull;
           streamed = true;
         }
         // wave 3 routes exactly now (it reads top[] and lv[], complete since
@@ -924,7 +927,20 @@ __device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[6
     } else {
       exact_route<EPT>(a, dyn, L, lr, tid);
     }
-    if (ctrl[3]) make_plan(dyn, L, T, k, E, a.has_shared, tid);
+    const bool moved = ctrl[3] != 0;  // the exact routing changed an id
+    if (moved) make_plan(dyn, L, T, k, E, a.has_shared, tid);
+    if (streamed && !moved) {
+      // one token, routing as the logits ordered it: this group's expert,
+      // presence and single entry (token 0, slot_mine) are known already
+      if (e_mine < 0) {
+        wait_vm();
+        return;
+      }
+      gateup_wave(present_mine, row0, nrw, nbh, lpr, buf, xs,
+                  [&](int, int& t, int& sl) { t = 0; sl = slot_mine; }, 1, stride, a.n_ff, a.h,
+                  lane);
+      return;
+    }
     n_groups = gbase + ctrl[1];
     if (!publisher) {
       const int e_x = g < n_groups ? pexp[g] : -1;
