@@ -227,7 +227,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["2", "5", "q6", "traffic"], default=None,
                     help="run one leg alone and print its JSON: 2 = the config-2 decode "
-                         "layer (graph-timed, front/back split, parity); 5 = the config-5 prefill "
+                         "layer (graph-timed, front/back split, parity) and the config-3 "
+                         "verify window; 5 = the config-5 prefill "
                          "chunk; q6 = the Q6_K LM head; traffic = eager config-2 front/back "
                          "launches beside a plain 256 MiB copy, for rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE passes")
@@ -333,12 +334,6 @@ def main():
     back_bytes = 9 * MAT_BYTES + 9 * F * 4 + 2 * 9 * H * 4 + H * 4
     layer_bytes = 9 * 3 * MAT_BYTES + H * 4 + E * 4 + H * 4
     del wss
-    if args.only == "2":
-        print(json.dumps({"config2_layer": {
-            "us_per_token": round(us_per_token, 3), "eager_us_per_token": round(eager_us, 3),
-            "front_us": round(front_us, 3), "back_us": round(back_us, 3),
-            "parity": {"bit_exact": bit_exact, "max_rel_err": max_rel}}}), flush=True)
-        return 0
 
     # config 3: verify window of 4 tokens (1 + 3 drafts), logits N(0, 1.5),
     # the same 16 rotated layers; per-token top-8, experts grouped so a shared
@@ -386,6 +381,13 @@ def main():
                "workload": f"{W3} tokens, logits N(0,1.5), {n3} windows over {N_LAYERS} "
                            "rotated layers, graph-replayed"}
     del layers4
+    if args.only == "2":
+        print(json.dumps({"config2_layer": {
+            "us_per_token": round(us_per_token, 3), "eager_us_per_token": round(eager_us, 3),
+            "front_us": round(front_us, 3), "back_us": round(back_us, 3),
+            "parity": {"bit_exact": bit_exact, "max_rel_err": max_rel}},
+            "config3_verify_window": config3}), flush=True)
+        return 0
 
     # config 1: Q4_K GEMV 2048x2048 batch 1, 256 rotated copies (604 MB)
     log("[bench] config-1 GEMV rotation")

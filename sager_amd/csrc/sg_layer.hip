@@ -183,7 +183,7 @@ __device__ __forceinline__ int rank_n(const uint64_t* c, int n, uint64_t key) {
 // candidate's rank among the team's tw*m candidates places it in top[rank]
 // (0 = missing).  Two barriers; every thread of the workgroup takes part.
 template <int EPT>
-__device__ void team_select(const FrontLds& L, const uint64_t* kr, uint64_t* cand, uint64_t* top,
+__device__ __forceinline__ void team_select(const FrontLds& L, const uint64_t* kr, uint64_t* cand, uint64_t* top,
                             int tt, bool wait_before_rank = false) {
   const int m = L.m, lane = tt & 63, wit = tt >> 6;
   uint32_t hi[EPT], lo[EPT];
@@ -252,7 +252,7 @@ __device__ void team_select(const FrontLds& L, const uint64_t* kr, uint64_t* can
 // entries in (expert, token, slot) order.  ctrl[0] = valid routes,
 // ctrl[1] = distinct experts.  Runs on wave 0 when T*k <= 64 (cross-lane
 // reads), else on the whole workgroup; ends with a workgroup barrier.
-__device__ void build_plan(uint32_t* dyn, const FrontLds& L, int T, int k, int E, int has_shared,
+__device__ __forceinline__ void build_plan(uint32_t* dyn, const FrontLds& L, int T, int k, int E, int has_shared,
                            int tid) {
   const int* ridx = reinterpret_cast<const int*>(dyn + L.ridx);
   int* re = reinterpret_cast<int*>(dyn + L.re);
@@ -476,7 +476,7 @@ __device__ __forceinline__ void logits_preload(const LayerArgs& a, int tid, floa
 }
 
 template <int EPT>
-__device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
+__device__ __forceinline__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
                             int tid, bool wait_copies = false) {
   const int T = a.T, E = a.n_expert, m = L.m;
   const int wave = tid >> 6, team = wave / L.tw, tt = tid - team * L.TT;
@@ -507,7 +507,7 @@ __device__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L
 // gbase + r = the expert of rank r, its single entry (token 0, slot j).
 // Ends with a barrier unless the caller places one.
 template <typename Id>
-__device__ void plan_t1(uint32_t* dyn, const FrontLds& L, int k, int has_shared, int tid, Id id,
+__device__ __forceinline__ void plan_t1(uint32_t* dyn, const FrontLds& L, int k, int has_shared, int tid, Id id,
                         bool barrier = true) {
   int* re = reinterpret_cast<int*>(dyn + L.re);
   int* poff = reinterpret_cast<int*>(dyn + L.poff);
@@ -579,7 +579,7 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // (LDS, filled by spec_select), lane l holds experts l + 64j.  Writes ridx,
 // rw and ctrl[3] (1 when an id differs from the logit order).
 template <int EPL>
-__device__ void route_wave(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, int lane) {
+__device__ __forceinline__ void route_wave(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, int lane) {
   const int E = a.n_expert, k = a.k, m = L.m;
   const float* lv = reinterpret_cast<const float*>(dyn + L.lv);
   float* ev = reinterpret_cast<float*>(dyn + L.ev);
@@ -668,7 +668,7 @@ __device__ void route_wave(const LayerArgs& a, uint32_t* dyn, const FrontLds& L,
 // and rw; ctrl[3] = 1 when any id changed.  Workgroup-wide, barriers only
 // (no wait on the weight stream in flight).
 template <int EPT>
-__device__ void exact_route(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
+__device__ __forceinline__ void exact_route(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
                             int tid) {
   const int T = a.T, E = a.n_expert, k = a.k, stride = k + 1, m = L.m;
   const int lane = tid & 63, wave = tid >> 6;
@@ -778,7 +778,7 @@ __device__ void exact_route(const LayerArgs& a, uint32_t* dyn, const FrontLds& L
 // publisher workgroup (blockIdx.y == gmax, x == 0) runs the same routing
 // and writes idx, weight and the plan.
 template <int EPT>
-__device__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[64 * 36],
+__device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[64 * 36],
                            uint32_t* dyn) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, E = a.n_expert, stride = k + 1;
@@ -1024,8 +1024,11 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
   // after the routed ones: workgroups are placed on CUs in grid order, so the
   // routed workgroups (the long routing chain) each get a CU of their own
   // and the shared expert's (no routing, done early) double up.
+  // (one token only: the grid is then about one workgroup per CU; with more
+  // tokens the shared expert's row stays first so it is not the tail)
   const int y = blockIdx.y;
-  const int g = !a.has_shared || y >= a.gmax ? y : (y + 1 == a.gmax ? 0 : y + 1);
+  const int g =
+      a.T != 1 || !a.has_shared || y >= a.gmax ? y : (y + 1 == a.gmax ? 0 : y + 1);
   front_body<EPT>(a, blockIdx.x, g, wbuf, dyn);
 }
 
