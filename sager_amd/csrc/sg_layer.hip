@@ -95,6 +95,7 @@ struct LayerArgs {
   int T, hidden, n_ff, n_expert, k, has_shared, gmax, emax;
   float shared_w;
   int back_rows, back_lrow;  // rows per back workgroup, lanes per row there
+  int back_bufs;             // back waves with a down-row buffer (8, or 4 when LDS is short)
 };
 
 // ---- front kernel LDS layout (dwords) -----------------------------------------------
@@ -1036,11 +1037,13 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
 // One workgroup per chunk of `rows` output rows (hidden/rows >= 256 where the
 // shape allows).  A wave packs `gpw` groups side by side - lane = (group,
 // row, super-block) - and streams their down rows for the chunk into its LDS
-// buffer while all four waves quantize every (token, slot) h row to Q8_K in
+// buffer while all eight waves quantize every (token, slot) h row to Q8_K in
 // LDS (h was loaded at kernel start, beside the plan).  The slot outputs of
 // the chunk go to LDS; then the workgroup combines
 // out = residual + sum_kk fma(w_kk, y_kk) in slot order.
-constexpr int kBackHSlots = 5;  // h blocks per wave preloaded at kernel start (T = 1, k = 8: 18)
+constexpr int kBackWaves = 8;                    // waves per back workgroup
+constexpr int kBackThreads = 64 * kBackWaves;
+constexpr int kBackHSlots = 3;  // h blocks per wave preloaded at kernel start (T = 1, k = 8: 18)
 
 struct BackLds {
   int hq, ys, off, wdown, tok, slot, wt, meta, total;
@@ -1065,14 +1068,14 @@ __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, in
   L.slot = take(emax);
   L.wt = take(T * (k + 1));
   L.meta = take(4);
-  L.total = o;
+  L.total = (o + 3) & ~3;  // the down-row buffers follow, 16-B aligned
   return L;
 }
 
 // The down rows, Q8_K of h and combine of one chunk of `rows` output rows,
 // with the plan in LDS (off, wdown, tok, slot, wt, meta).  Wave w
-// quantizes h blocks w + 4j; hpre[j] holds the lane's 4 values of block
-// w + 4j for j < kBackHSlots (loaded at kernel start).
+// quantizes h blocks w + 8j; hpre[j] holds the lane's 4 values of block
+// w + 8j for j < kBackHSlots (loaded at kernel start).
 // NBF, ROWS: n_ff / 256 and the rows per workgroup when known at compile
 // time (0 = read from a).
 template <int NBF, int ROWS>
@@ -1101,12 +1104,36 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
   const int q = lane / (rows * lrow);  // this lane's group within the wave
   const int rr = (lane / lrow) % rows, blk = lane & (lrow - 1);
 
-  for (int gb = 0; gb < G; gb += 4 * gpw) {
-    // down rows of this wave's gpw groups as one run of 16-B chunks: chunk
-    // c = group c / cpg, chunk c % cpg of the group's rows; LDS destination
-    // buf + 4c (group qq at buf + qq * gwords).  At most 9 copy
-    // instructions, no loop over groups.
-    {
+  const int nbw = a.back_bufs;  // waves that stream and dot down rows
+  // one pass with every buffer packed end to end: the copies are dealt to
+  // all waves rather than issued by the waves that will read them
+  const bool spread = G <= nbw * gpw && gpw * gwords == 64 * 36;
+  for (int gb = 0; gb < G; gb += nbw * gpw) {
+    if (spread) {
+      // every group's down rows as one run of 16-B chunks over all the
+      // buffers (chunk c = group c / cpg, chunk c % cpg of its rows, at
+      // wbuf[0] + 4c), the 1-KB copy instructions dealt round-robin to the
+      // waves; each waits for its own before the barrier below
+      if (gb == 0) {
+        const int cpg = gwords / 4, cval = nr * nbf * 9, total = G * cpg;
+        const uint64_t inv = ((1ull << 24) + cpg - 1) / cpg;  // c / cpg exact for c < 2^24 / cpg
+        const long long roff = static_cast<long long>(row0) * nbf * kQ4Bytes;
+        for (int t = wave; 64 * t < total; t += kBackWaves) {
+          const int c = 64 * t + lane;
+          const int gq = static_cast<int>((static_cast<uint64_t>(c) * inv) >> 24);
+          const int w = c - gq * cpg;
+          const unsigned long long wd = c < total ? wdown[gq] : 0ull;
+          if (wd && w < cval)
+            __builtin_amdgcn_global_load_lds(
+                (glb_void_p)(reinterpret_cast<const char*>(wd) + roff + 16 * w),
+                (lds_void_p)(wbuf[0] + 256 * t), 16, 0, 0);
+        }
+      }
+    } else {
+      // down rows of this wave's gpw groups as one run of 16-B chunks: chunk
+      // c = group c / cpg, chunk c % cpg of the group's rows; LDS destination
+      // buf + 4c (group qq at buf + qq * gwords).  At most 9 copy
+      // instructions, no loop over groups.
       const int cpg = gwords / 4;       // chunks per group slot
       const int cval = nr * nbf * 9;    // chunks present (nr < rows at the edge)
       const uint32_t inv = ((1u << 20) + cpg - 1) / cpg;  // c / cpg exact for c < 576
@@ -1118,7 +1145,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
         const int qq = static_cast<int>((static_cast<uint32_t>(c) * inv) >> 20);
         const int w = c - qq * cpg;
         const int gq = gb + wave * gpw + qq;
-        const unsigned long long wd = qq < gpw && gq < G ? wdown[gq] : 0ull;
+        const unsigned long long wd = qq < gpw && gq < G && wave < nbw ? wdown[gq] : 0ull;
         if (wd && w < cval)
           __builtin_amdgcn_global_load_lds(
               (glb_void_p)(reinterpret_cast<const char*>(wd) + roff + 16 * w),
@@ -1126,7 +1153,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
       }
     }
     if (gb == 0) {  // Q8_K of every (token, slot) h row while the rows stream in
-      // blocks e = wave + 4j: j < kBackHSlots from registers in one
+      // blocks e = wave + 8j: j < kBackHSlots from registers in one
       // interleaved pass (every block of a one-token layer with k <= 8),
       // later ones in passes of four loaded here
       if (wave < nq) {
@@ -1134,32 +1161,33 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
         int n = 0;
 #pragma unroll
         for (int j = 0; j < kBackHSlots; ++j) {
-          const int e = wave + 4 * j;
+          const int e = wave + kBackWaves * j;
           dst[j] = hq + (e < nq ? e : wave) * kXStride;
           n += e < nq;
         }
         quantize_n_lds<kBackHSlots>(hpre, dst, n, lane);
       }
-      for (int e0 = wave + 4 * kBackHSlots; e0 < nq; e0 += 16) {
+      for (int e0 = wave + kBackWaves * kBackHSlots; e0 < nq; e0 += 4 * kBackWaves) {
         float v[4][4];
         uint32_t* dst[4];
         int n = 0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const int e = e0 + 4 * u < nq ? e0 + 4 * u : e0;
+          const int e = e0 + kBackWaves * u < nq ? e0 + kBackWaves * u : e0;
           const float* hp = a.h + static_cast<long long>(e) * kQK + 4 * lane;
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[u][i] = hp[i];
           dst[u] = hq + e * kXStride;
-          n += e0 + 4 * u < nq;
+          n += e0 + kBackWaves * u < nq;
         }
         quantize_n_lds<4>(v, dst, n, lane);
       }
+      if (spread) wait_vm();  // this wave's share of the copies
       bar();
     }
     wait_vm();
     const int gq = gb + wave * gpw + q;
-    const bool has = gq < G;
+    const bool has = gq < G && wave < nbw;
     const bool present = has && wdown[gq] != 0ull;
     const bool live = present && blk < nbf && rr < nr;
     uint32_t w36[36];
@@ -1192,7 +1220,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
   // whose id was invalid (bounds-killed), whose expert is absent, or the
   // shared slot without a shared expert has no plan entry, so its y is the
   // 0 the prologue stored.
-  for (int qo = tid; qo < n_out; qo += 256) {
+  for (int qo = tid; qo < n_out; qo += kBackThreads) {
     const int t = qo / nr, r = qo - t * nr;
     const long long o = static_cast<long long>(t) * a.hidden + row0 + r;
     float acc = a.residual ? (qo == tid ? res0 : a.residual[o]) : 0.f;
@@ -1221,9 +1249,8 @@ __device__ __forceinline__ float residual_pre(const LayerArgs& a, int row0, int 
 }
 
 template <int NBF, int ROWS>
-__global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
-  __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
-  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
+__global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];  // BackLds arrays, then the buffers
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, stride = k + 1;
   const int nbf = NBF ? NBF : a.n_ff / kQK;
@@ -1240,13 +1267,13 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
   const int nr = max(0, min(rows, a.hidden - row0));
 
   // loads that do not depend on the plan: this wave's first kBackHSlots h
-  // blocks (block wave + 4j of the (token, slot) rows) and the residual
+  // blocks (block wave + 8j of the (token, slot) rows) and the residual
   const int nq = T * stride * nbf;
   float hpre[kBackHSlots][4];
   if (wave < nq) {
 #pragma unroll
     for (int j = 0; j < kBackHSlots; ++j) {
-      const int e0 = wave + 4 * j;
+      const int e0 = wave + kBackWaves * j;
       const int e = e0 < nq ? e0 : wave;
       const float* hp = a.h + static_cast<long long>(e) * kQK + 4 * lane;
 #pragma unroll
@@ -1260,7 +1287,7 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
   // branches) before it waits once; loads inside separate guarded loops
   // would each wait for the previous one.
   const int nw = T * stride;
-  if (a.gmax + 1 <= 256 && a.emax <= 256 && nw <= 256) {
+  if (a.gmax + 1 <= kBackThreads && a.emax <= kBackThreads && nw <= kBackThreads) {
     const int v_meta = a.plan.meta[min(tid, 1)];
     const int v_off = a.plan.off[min(tid, a.gmax)];
     const unsigned long long v_wd = a.plan.wdown[min(tid, a.gmax - 1)];
@@ -1277,16 +1304,17 @@ __global__ void __launch_bounds__(256) layer_back_kernel(LayerArgs a) {
     if (tid < nw) wt[tid] = v_wt;
   } else {
     if (tid < 2) meta[tid] = a.plan.meta[tid];
-    for (int i = tid; i <= a.gmax; i += 256) off[i] = a.plan.off[i];
-    for (int i = tid; i < a.gmax; i += 256) wdown[i] = a.plan.wdown[i];
-    for (int i = tid; i < a.emax; i += 256) {
+    for (int i = tid; i <= a.gmax; i += kBackThreads) off[i] = a.plan.off[i];
+    for (int i = tid; i < a.gmax; i += kBackThreads) wdown[i] = a.plan.wdown[i];
+    for (int i = tid; i < a.emax; i += kBackThreads) {
       tok[i] = a.plan.tok[i];
       slot[i] = a.plan.slot[i];
     }
-    for (int i = tid; i < nw; i += 256) wt[i] = a.weight[i];
+    for (int i = tid; i < nw; i += kBackThreads) wt[i] = a.weight[i];
   }
-  for (int i = tid; i < T * stride * rows; i += 256) ys[i] = 0.f;
+  for (int i = tid; i < T * stride * rows; i += kBackThreads) ys[i] = 0.f;
   bar();
+  uint32_t(*wbuf)[64 * 36] = reinterpret_cast<uint32_t(*)[64 * 36]>(dyn + L.total);
   back_core<NBF, ROWS>(a, L, dyn, wbuf, row0, nr, res0, hpre);
 }
 
@@ -1345,7 +1373,10 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
       static_cast<size_t>(front_lds(n_tokens, hidden / kQK, n_expert, k, true).total) * 4;
   const size_t lds_b =
       static_cast<size_t>(back_lds(n_tokens, k, n_ff, rows, ws.gmax, ws.emax).total) * 4;
-  if (lds_f + 4 * 64 * 36 * 4 > 160 * 1024 || lds_b + 4 * 64 * 36 * 4 > 160 * 1024)
+  // the back kernel's down-row buffers: one per wave when they fit, else four
+  const size_t buf_b = 64 * 36 * 4;
+  const int back_bufs = lds_b + kBackWaves * buf_b <= 160 * 1024 ? kBackWaves : 4;
+  if (lds_f + 4 * buf_b > 160 * 1024 || lds_b + back_bufs * buf_b > 160 * 1024)
     return set_error(SG_ERR_UNSUPPORTED, "%s: this shape needs more LDS than a workgroup has",
                      nm);
   unsigned char* base = static_cast<unsigned char*>(workspace);
@@ -1378,6 +1409,7 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   a.shared_w = shared_w;
   a.back_rows = rows;
   a.back_lrow = lrow;
+  a.back_bufs = back_bufs;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rows_wg = 4 * (32 / pow2_ceil(hidden / kQK));
   const FrontLds fl = front_lds(n_tokens, hidden / kQK, n_expert, k, true);
@@ -1399,9 +1431,11 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     // constants; other shapes read them from the arguments
     const dim3 gb((hidden + rows - 1) / rows);
     if (n_ff / kQK == 2 && rows == 8)
-      hipLaunchKernelGGL((layer_back_kernel<2, 8>), gb, dim3(256), lds_b, s, a);
+      hipLaunchKernelGGL((layer_back_kernel<2, 8>), gb, dim3(kBackThreads),
+                         lds_b + back_bufs * buf_b, s, a);
     else
-      hipLaunchKernelGGL((layer_back_kernel<0, 0>), gb, dim3(256), lds_b, s, a);
+      hipLaunchKernelGGL((layer_back_kernel<0, 0>), gb, dim3(kBackThreads),
+                         lds_b + back_bufs * buf_b, s, a);
     if (int st = check_launch("sg_moe_layer/back")) return st;
   }
   return SG_OK;
