@@ -463,23 +463,46 @@ __global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __re
 }
 
 // out[t] = residual[t] + sum_kk fma(w[t][kk], y[pos(t, kk)]) in slot order;
-// pos(t, k) = the shared expert's position off[E] + t when present.
+// pos(t, k) = the shared expert's position off[E] + t when present.  A thread
+// owns four consecutive columns; the positions and weights of eight slots are
+// read first (uniform per workgroup), then their eight 16-B rows are loaded
+// together before the ordered fma chain, so each thread has eight loads in
+// flight instead of one.
 __global__ void __launch_bounds__(256) prefill_combine_kernel(
     float* __restrict__ out, const float* __restrict__ residual, const float* __restrict__ y,
     const float* __restrict__ weight, const int* __restrict__ gslot, const int* __restrict__ off,
     int n_expert, int k, int hidden, int has_shared) {
   const int t = blockIdx.y;
-  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= hidden) return;
   const long long o = static_cast<long long>(t) * hidden + i;
-  float acc = residual ? residual[o] : 0.f;
+  float4 acc = residual ? *reinterpret_cast<const float4*>(residual + o) : make_float4(0.f, 0.f, 0.f, 0.f);
   const int shared_pos = off[n_expert] + t;
-  for (int kk = 0; kk <= k; ++kk) {
-    const int pos = kk < k ? gslot[t * k + kk] : (has_shared ? shared_pos : -1);
-    const float yv = pos >= 0 ? y[static_cast<long long>(pos) * hidden + i] : 0.f;
-    acc = __builtin_fmaf(weight[t * (k + 1) + kk], yv, acc);
+  for (int k0 = 0; k0 <= k; k0 += 8) {
+    int pos[8];
+    float wv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int kk = k0 + u;
+      pos[u] = kk < k ? gslot[t * k + kk] : (kk == k && has_shared ? shared_pos : -1);
+      wv[u] = kk <= k ? weight[t * (k + 1) + kk] : 0.f;
+    }
+    float4 yv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      yv[u] = pos[u] >= 0 ? *reinterpret_cast<const float4*>(y + static_cast<long long>(pos[u]) * hidden + i)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (k0 + u <= k) {
+        acc.x = __builtin_fmaf(wv[u], yv[u].x, acc.x);
+        acc.y = __builtin_fmaf(wv[u], yv[u].y, acc.y);
+        acc.z = __builtin_fmaf(wv[u], yv[u].z, acc.z);
+        acc.w = __builtin_fmaf(wv[u], yv[u].w, acc.w);
+      }
+    }
   }
-  out[o] = acc;
+  *reinterpret_cast<float4*>(out + o) = acc;
 }
 
 // ---- workspace ------------------------------------------------------------------
@@ -650,7 +673,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   hipLaunchKernelGGL(grouped_mfma_kernel<false>, dim3(hidden / kRowsWg, ws.max_tiles),
                      dim3(kThreads), 0, s, gd);
   if (int st = check_launch("sg_moe_prefill/down")) return st;
-  hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 255) / 256, n_tokens), dim3(256), 0, s,
+  hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 1023) / 1024, n_tokens), dim3(256), 0, s,
                      out, residual, y, weight, gslot, off, n_expert, k, hidden, has_shared);
   return check_launch("sg_moe_prefill/combine");
 }
