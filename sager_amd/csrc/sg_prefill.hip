@@ -84,20 +84,25 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
   }
   __syncthreads();
   const int total = n_rows * k;
+  // route i = tid + nth j is (row i / k, slot i % k); when k divides nth the
+  // row advances by nth / k per j and the slot is fixed (no division per route)
+  const bool kdiv = nth % k == 0;
+  const int r0 = tid / k, kk0 = tid - r0 * k, rstep = nth / k;
+  auto row_of = [&](int j, int i) { return kdiv ? r0 + j * rstep : i / k; };
   // every route id this thread handles, loaded up front (independent loads
-  // in flight together; route i = tid + 1024 j)
+  // in flight together)
   int ids[kScanPerThread];
 #pragma unroll
   for (int j = 0; j < kScanPerThread; ++j) {
     const int i = tid + nth * j;
-    const int r = i / k, kk = i - r * k;
+    const int r = row_of(j, i), kk = kdiv ? kk0 : i - r * k;
     ids[j] = i < total ? idx[static_cast<long long>(r) * (k + 1) + kk] : -1;
   }
 #pragma unroll
   for (int j = 0; j < kScanPerThread; ++j) {
     const int i = tid + nth * j;
     if (i >= total) break;
-    const int r = i / k;
+    const int r = row_of(j, i);
     const int e = ids[j];
     if (e < 0 || e >= E) {
       for (int q = 0; q <= k; ++q) weight[static_cast<long long>(r) * (k + 1) + q] = 0.f;
@@ -105,9 +110,37 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
       atomicAdd(&s_bad, 1);
       continue;
     }
-    atomicAdd(&hist[e], 1);
     const uint32_t bit = 1u << (r & 31);
     if (atomicOr(&bm[e * WS + (r >> 5)], bit) & bit) s_dup = 1;
+  }
+  __syncthreads();
+  // the expert histogram: with distinct ids per row, the popcounts of the
+  // expert's bitmap words (thread group of expert e, tpe threads, counts
+  // its share of the words into part[]); with a duplicated id the bitmap
+  // undercounts, so the ids are counted one by one
+  const int tpe = max(1, nth / E);  // threads per expert
+  const int pe = tid / tpe, pq = tid - pe * tpe;
+  const int wpt = (W + tpe - 1) / tpe;
+  const int pw0 = min(W, pq * wpt), pw1 = min(W, pw0 + wpt);
+  if (!s_dup) {
+    int c = 0;
+    if (pe < E)
+      for (int w = pw0; w < pw1; ++w) c += __popc(bm[pe * WS + w]);
+    part[tid] = c;
+    __syncthreads();
+    if (tid < E) {
+      int h = 0;
+      for (int j = 0; j < tpe; ++j) h += part[tid * tpe + j];
+      hist[tid] = h;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kScanPerThread; ++j) {
+      const int i = tid + nth * j;
+      if (i >= total) break;
+      const int e = ids[j];
+      if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+    }
   }
   __syncthreads();
   {  // exclusive prefix sums over the experts (E <= 1024: one per thread)
@@ -141,22 +174,20 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
   __syncthreads();
   if (!s_dup) {
     // per-(expert, word) prefix of route counts, in place of the bitmap's
-    // companion array pre[]: thread group of expert e scans its words
-    const int tpe = max(1, nth / E);  // threads per expert
-    const int e = tid / tpe, q = tid - e * tpe;
-    const int wpt = (W + tpe - 1) / tpe;
-    const int w0 = min(W, q * wpt), w1 = min(W, w0 + wpt);
+    // companion array pre[]: thread group of expert e scans its words (the
+    // per-thread word counts are in part[] from the histogram; the scans
+    // above used part[] as scratch, so they are counted again)
     int c = 0;
-    if (e < E)
-      for (int w = w0; w < w1; ++w) c += __popc(bm[e * WS + w]);
+    if (pe < E)
+      for (int w = pw0; w < pw1; ++w) c += __popc(bm[pe * WS + w]);
     part[tid] = c;
     __syncthreads();
-    if (e < E) {
-      int run = offl[e];
-      for (int j = 0; j < q; ++j) run += part[e * tpe + j];
-      for (int w = w0; w < w1; ++w) {
-        pre[e * WS + w] = run;
-        run += __popc(bm[e * WS + w]);
+    if (pe < E) {
+      int run = offl[pe];
+      for (int j = 0; j < pq; ++j) run += part[pe * tpe + j];
+      for (int w = pw0; w < pw1; ++w) {
+        pre[pe * WS + w] = run;
+        run += __popc(bm[pe * WS + w]);
       }
     }
     __syncthreads();
@@ -166,7 +197,7 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
     for (int j = 0; j < kScanPerThread; ++j) {
       const int i = tid + nth * j;
       if (i >= total) break;
-      const int r = i / k;
+      const int r = row_of(j, i);
       const int ee = ids[j];
       if (ee < 0 || ee >= E) continue;
       const uint32_t word = bm[ee * WS + (r >> 5)];
