@@ -488,6 +488,45 @@ __device__ __forceinline__ void quantize_n_lds(const float (&v)[N][4], uint32_t*
   }
 }
 
+// One Q8_K block per 16-lane DPP row: lane l holds values 16*(l & 15) ..
+// 16*(l & 15) + 15 of its row's block in v[].  Same arithmetic as
+// quantize_n_lds (amax over the block, d = amax / 127, q = q8_code(v / d
+// by the reciprocal), bsums over 32 values), with the block's reductions
+// inside one DPP row: no cross-row steps and no lane reads.  Writes the
+// block to dst (LDS, kXStride layout) when `active`.
+__device__ __forceinline__ void quantize_row16_lds(const float (&v)[16], uint32_t* dst, bool active,
+                                                   int lane) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
+  amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
+  amax = fmaxf(amax, dpp_f<kDppHalfMirror>(amax));
+  amax = fmaxf(amax, dpp_f<kDppMirror>(amax));
+  amax = fmaxf(amax, 1e-30f);
+  const float d = amax / 127.f;
+  const float id = d > 0 ? 1.f / d : 0.f;
+  uint32_t packed[4];
+  int qsum = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    packed[w] = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = q8_code(v[4 * w + i] * id);
+      qsum += q;
+      packed[w] |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * i);
+    }
+  }
+  qsum += dpp_i<kDppXor1>(qsum);  // the 32 values of a bsum: this lane and its neighbour
+  if (active) {
+    const int r = lane & 15;
+    *reinterpret_cast<u32x4*>(dst + 4 * r) = (u32x4){packed[0], packed[1], packed[2], packed[3]};
+    if (r == 0) dst[64] = __builtin_bit_cast(uint32_t, d);
+    if ((r & 1) == 0) dst[65 + (r >> 1)] = __builtin_bit_cast(uint32_t, static_cast<float>(qsum));
+  }
+}
+
 // Stage the Q8_K rows of n tokens (token ids in `tok`, nb blocks per row)
 // into LDS: token j's block b goes to lds + (j*nb + b)*kXStride.
 __device__ __forceinline__ void stage_q8k_rows(const unsigned char* __restrict__ xq,

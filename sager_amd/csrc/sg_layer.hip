@@ -407,49 +407,36 @@ __device__ __forceinline__ void dma_gateup(const sg_block_q4k* wg, const sg_bloc
              lane, part, nparts);
 }
 
-// x values of a wave's first quantization pass (blocks w + nw*u), loaded
-// at kernel start so their latency overlaps the routing.  Waves w < nw of
-// the workgroup take part.
+// x values of a wave's first quantization pass, loaded at kernel start so
+// their latency overlaps the routing: one Q8_K block per 16-lane row, block
+// 4w + (lane >> 4), the lane's 16 values.  Waves w < nw take part.
 __device__ __forceinline__ void x_preload(const float* x, int n_blocks, int w, int nw, int lane,
-                                          float (&pre)[4][4]) {
-  if (w >= n_blocks || w >= nw) return;
+                                          float (&pre)[16]) {
+  if (w >= nw) return;
+  const int b = 4 * w + (lane >> 4);
+  const float* xb = x + static_cast<long long>(b < n_blocks ? b : 0) * kQK + 16 * (lane & 15);
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int b = w + nw * u;
-    const int bb = b < n_blocks ? b : w;
-    const float* xb = x + static_cast<long long>(bb) * kQK + 4 * lane;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pre[u][i] = xb[i];
-  }
+  for (int i = 0; i < 16; ++i) pre[i] = xb[i];
 }
 
-// Q8_K of every token's x into LDS by waves w < nw: wave w takes blocks
-// w, w+nw, ... up to four at a time (interleaved chains); the first pass
-// comes from x_preload.
+// Q8_K of the x rows into LDS (kXStride layout), one block per 16-lane row:
+// pass p of wave w takes block 4 (p nw + w) + (lane >> 4); pass 0's values
+// come from x_preload.
 __device__ __forceinline__ void quantize_x(const float* x, int n_blocks, uint32_t* xs, int w,
-                                           int nw, int lane, const float (&pre)[4][4]) {
+                                           int nw, int lane, const float (&pre)[16]) {
   if (w >= nw) return;
-  for (int b0 = w; b0 < n_blocks; b0 += 4 * nw) {
-    float v[4][4];
-    uint32_t* dst[4];
-    int n = 0;
+  {
+    const int b = 4 * w + (lane >> 4);
+    quantize_row16_lds(pre, xs + (b < n_blocks ? b : 0) * kXStride, b < n_blocks, lane);
+  }
+  for (int b0 = 4 * nw; b0 < n_blocks; b0 += 4 * nw) {
+    const int b = b0 + 4 * w + (lane >> 4);
+    const int bc = b < n_blocks ? b : 0;
+    const float* xb = x + static_cast<long long>(bc) * kQK + 16 * (lane & 15);
+    float v[16];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int b = b0 + nw * u;
-      const int bb = b < n_blocks ? b : b0;
-      const float* xb = x + static_cast<long long>(bb) * kQK + 4 * lane;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[u][i] = b0 == w ? pre[u][i] : xb[i];
-      dst[u] = xs + bb * kXStride;
-      n += b < n_blocks;
-    }
-    if (n <= 2) {  // fewer chains, fewer instructions
-      const float(&v2)[2][4] = *reinterpret_cast<const float(*)[2][4]>(&v[0][0]);
-      uint32_t* const d2[2] = {dst[0], dst[1]};
-      quantize_n_lds<2>(v2, d2, n, lane);
-    } else {
-      quantize_n_lds<4>(v, dst, n, lane);
-    }
+    for (int i = 0; i < 16; ++i) v[i] = xb[i];
+    quantize_row16_lds(v, xs + bc * kXStride, b < n_blocks, lane);
   }
 }
 
@@ -803,7 +790,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   // while waves 0-2 issue the weight stream and quantize x
   const bool t1w = T == 1 && a.logits != nullptr && !shared_grp;
   const int nqw = t1w ? 3 : 4;
-  float xpre[4][4];
+  float xpre[16];
   if (!publisher) x_preload(a.x, nxb, wave, nqw, lane, xpre);
 
   if (shared_grp) {
