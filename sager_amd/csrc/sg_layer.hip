@@ -1183,7 +1183,10 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
       read_block_lds(buf + q * gwords + 36 * (rr * nbf + blk), w36);
       sm8 = unpack_scales(w36[1], w36[2], w36[3]);
     }
-    const int jb = has ? off[gq] : 0, je = has ? off[gq + 1] : 0;
+    // entries of the group, clamped to the plan's capacity (a plan is only
+    // ever read here, never trusted to bound a loop)
+    const int jb = has ? min(max(off[gq], 0), a.emax) : 0;
+    const int je = has ? min(max(off[gq + 1], jb), a.emax) : 0;
     const int cnt = wave_max_i32(je - jb);
     for (int ji = 0; ji < cnt; ++ji) {
       const int j = jb + ji;
