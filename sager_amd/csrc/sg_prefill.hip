@@ -482,15 +482,60 @@ grouped_mfma_kernel(GroupedArgs a) {
 // 16-byte bsums field holds each sub-block sum s split as s = 128*hi + lo,
 // lo = s & 127 in bytes 0-7 and hi = s >> 7 (two's complement) in bytes
 // 8-15.
+// One block per 16-lane row (four per wave, 16 per workgroup): the lane's 16
+// values are four 16-B loads, and the block's max and bsums reduce inside a
+// DPP row.  Same arithmetic as quantize_block_wave.
 __global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __restrict__ in,
                                                                unsigned char* __restrict__ out,
                                                                long long n_blocks) {
-  const long long blk = static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
+  const long long blk =
+      (static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  const long long bc = blk < n_blocks ? blk : n_blocks - 1;  // rows past the end compute, never store
+  const float* src = in + bc * kQK + 16 * (lane & 15);
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    const float4 f = *reinterpret_cast<const float4*>(src + i);
+    v[i] = f.x;
+    v[i + 1] = f.y;
+    v[i + 2] = f.z;
+    v[i + 3] = f.w;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
+  amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
+  amax = fmaxf(amax, dpp_f<kDppHalfMirror>(amax));
+  amax = fmaxf(amax, dpp_f<kDppMirror>(amax));
+  amax = fmaxf(amax, 1e-30f);
+  const float d = amax / 127.f;
+  const float id = d > 0 ? 1.f / d : 0.f;
+  uint32_t packed[4];
+  int qsum = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    packed[w] = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = q8_code(v[4 * w + i] * id);
+      qsum += q;
+      packed[w] |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * i);
+    }
+  }
+  qsum += dpp_i<kDppXor1>(qsum);  // a bsum's 32 values: this lane and its neighbour
   if (blk >= n_blocks) return;
-  const float4 v4 = *reinterpret_cast<const float4*>(in + blk * kQK + 4 * lane);
-  const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-  quantize_block_wave<true>(v, out + blk * kQ8Bytes, lane);
+  unsigned char* ob = out + blk * kQ8Bytes;
+  const int r = lane & 15;
+  uint32_t* qw = reinterpret_cast<uint32_t*>(ob + 4 + 16 * r);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) qw[w] = packed[w];
+  if (r == 0) *reinterpret_cast<float*>(ob) = d;
+  if ((r & 1) == 0) {
+    ob[260 + (r >> 1)] = static_cast<unsigned char>(qsum & 127);
+    ob[268 + (r >> 1)] = static_cast<unsigned char>((qsum >> 7) & 0xFF);
+  }
 }
 
 // out[t] = residual[t] + sum_kk fma(w[t][kk], y[pos(t, kk)]) in slot order;
@@ -568,7 +613,7 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
 static int quantize_split(const float* in, sg_block_q8k* out, int nb_row, int n_rows,
                           hipStream_t s, const char* nm) {
   const long long n_blocks = static_cast<long long>(nb_row) * n_rows;
-  const unsigned grid = static_cast<unsigned>((n_blocks + 3) / 4);
+  const unsigned grid = static_cast<unsigned>((n_blocks + 15) / 16);
   hipLaunchKernelGGL(prefill_quantize_kernel, dim3(grid), dim3(256), 0, s, in,
                      reinterpret_cast<unsigned char*>(out), n_blocks);
   return check_launch(nm);
