@@ -482,6 +482,194 @@ grouped_mfma_kernel(GroupedArgs a) {
 // 16-byte bsums field holds each sub-block sum s split as s = 128*hi + lo,
 // lo = s & 127 in bytes 0-7 and hi = s >> 7 (two's complement) in bytes
 // 8-15.
+// ---- the dispatch scan over many workgroups (prefill path) ----------------
+// The same arrays as dispatch_scan_kernel, in three launches so that the
+// per-route work runs on many CUs:
+// 1. scan_bits_kernel: workgroup w takes the 32 tokens 32w..32w+31 and
+//    writes wbits[w][e], the bitmap of its tokens routed to expert e, plus
+//    wflags[w] = bad routes | (duplicate id in a row) << 16; bad ids get
+//    bounds-kill (weights of the row zeroed, gslot -1).
+// 2. scan_offsets_kernel (one workgroup): the expert histogram as popcounts,
+//    the exclusive scans into off/toff/meta and the tile list, and
+//    woff[w][e] = off[e] + routes of expert e in workgroups before w.  A row
+//    with a duplicated id is rare caller routing: then this workgroup places
+//    every route itself, serially in (token, slot) order, as
+//    dispatch_scan_kernel does.
+// 3. scan_place_kernel: a route of token r to expert e goes to
+//    woff[w][e] + the routes of e from lower tokens of the same workgroup.
+constexpr int kScanTok = 32;  // tokens per workgroup in scan_bits / scan_place
+constexpr int kScanBitsLds = 24 * 1024;  // wbits words scan_offsets_kernel copies to LDS
+
+__global__ void __launch_bounds__(256) scan_bits_kernel(const int* __restrict__ idx,
+                                                        float* __restrict__ weight,
+                                                        int* __restrict__ gslot,
+                                                        uint32_t* __restrict__ wbits,
+                                                        int* __restrict__ wflags, int n_rows,
+                                                        int k, int E) {
+  __shared__ uint32_t bm[1024];
+  __shared__ int s_bad, s_dup;
+  const int w = blockIdx.x, tid = threadIdx.x;
+  for (int e = tid; e < E; e += 256) bm[e] = 0u;
+  if (tid == 0) {
+    s_bad = 0;
+    s_dup = 0;
+  }
+  __syncthreads();
+  const int r0 = w * kScanTok;
+  for (int i = tid; i < kScanTok * k; i += 256) {
+    const int r = r0 + i / k, kk = i % k;
+    if (r >= n_rows) break;
+    const int e = idx[static_cast<long long>(r) * (k + 1) + kk];
+    if (e < 0 || e >= E) {
+      for (int q = 0; q <= k; ++q) weight[static_cast<long long>(r) * (k + 1) + q] = 0.f;
+      gslot[r * k + kk] = -1;
+      atomicAdd(&s_bad, 1);
+      continue;
+    }
+    const uint32_t bit = 1u << (r & 31);
+    if (atomicOr(&bm[e], bit) & bit) s_dup = 1;
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 256) wbits[static_cast<long long>(w) * E + e] = bm[e];
+  if (tid == 0) wflags[w] = s_bad | (s_dup << 16);
+}
+
+__global__ void __launch_bounds__(1024) scan_offsets_kernel(
+    const int* __restrict__ idx, const uint32_t* __restrict__ wbits, const int* __restrict__ wflags,
+    int* __restrict__ woff, int* __restrict__ gslot, int* __restrict__ grows, int* __restrict__ off,
+    int* __restrict__ toff, int* __restrict__ meta, int* __restrict__ tiles, int n_rows, int k,
+    int E, int n_w, int tok_per, int shared_tail) {
+  __shared__ int hist[1024], part[1024];
+  __shared__ int s_bad, s_dup, s_total;
+  extern __shared__ uint32_t wb_lds[];  // a copy of wbits when it fits (kScanBitsLds words)
+  const int tid = threadIdx.x, nth = blockDim.x;
+  if (tid == 0) {
+    s_bad = 0;
+    s_dup = 0;
+  }
+  // the bitmaps into LDS in one round of independent loads (the per-expert
+  // loops below would otherwise wait for each global load in turn)
+  const int nbits = n_w * E;
+  const bool in_lds = nbits <= kScanBitsLds;
+  if (in_lds) {
+#pragma unroll 8
+    for (int i = tid; i < nbits; i += 1024) wb_lds[i] = wbits[i];
+  }
+  const uint32_t* wbs = in_lds ? wb_lds : wbits;
+  __syncthreads();
+  for (int w = tid; w < n_w; w += nth) {
+    const int f = wflags[w];
+    if (f & 0xFFFF) atomicAdd(&s_bad, f & 0xFFFF);
+    if (f >> 16) s_dup = 1;
+  }
+  // thread group of expert e: tpe threads, each over a range of workgroups
+  const int tpe = max(1, nth / E);
+  const int pe = tid / tpe, pq = tid - pe * tpe;
+  const int wpt = (n_w + tpe - 1) / tpe;
+  const int pw0 = min(n_w, pq * wpt), pw1 = min(n_w, pw0 + wpt);
+  int c = 0;
+  if (pe < E)
+    for (int w = pw0; w < pw1; ++w) c += __popc(wbs[static_cast<long long>(w) * E + pe]);
+  part[tid] = c;
+  __syncthreads();
+  if (!s_dup) {
+    if (tid < E) {
+      int h = 0;
+      for (int j = 0; j < tpe; ++j) h += part[tid * tpe + j];
+      hist[tid] = h;
+    }
+  } else if (tid == 0) {  // the bitmaps undercount a duplicated id: count the routes
+    for (int e = 0; e < E; ++e) hist[e] = 0;
+    for (int i = 0; i < n_rows * k; ++i) {
+      const int e = idx[static_cast<long long>(i / k) * (k + 1) + i % k];
+      if (e >= 0 && e < E) ++hist[e];
+    }
+  }
+  __syncthreads();
+  const int my_c = c;  // this thread's popcount share (the scans below reuse part[])
+  int ph = 0;
+  {  // exclusive prefix sums over the experts (E <= 1024: one per thread)
+    const int h = tid < E ? hist[tid] : 0;
+    const int tl = (h + tok_per - 1) / tok_per;
+    int tot_h, tot_t;
+    ph = block_exclusive_scan(h, part, &tot_h);
+    const int pt = block_exclusive_scan(tl, part, &tot_t);
+    if (tid < E) {
+      off[tid] = ph;
+      toff[tid] = pt;
+    }
+    if (tid == 0) {
+      off[E] = tot_h;
+      toff[E] = tot_t;
+      off[E + 1] = tot_h + shared_tail;
+      meta[0] = tot_h;
+      meta[1] = tot_t;
+      meta[2] = s_bad;
+      s_total = tot_h;
+    }
+    if (tid < E)
+      for (int j = 0; j < tl; ++j) tiles[1 + pt + j] = (tid << 16) | j;
+    const int sh_t = (shared_tail + tok_per - 1) / tok_per;
+    for (int j = tid; j < sh_t; j += nth) tiles[1 + tot_t + j] = (E << 16) | j;
+    if (tid == 0) tiles[0] = tot_t + sh_t;
+    if (tid < E) hist[tid] = ph;  // hist now holds off[e]
+  }
+  __syncthreads();
+  if (!s_dup) {
+    // woff[w][e] = off[e] + routes of e in workgroups before w: the thread's
+    // share starts after its group's lower shares
+    part[tid] = my_c;
+    __syncthreads();
+    if (pe < E) {
+      int run = hist[pe];
+      for (int j = 0; j < pq; ++j) run += part[pe * tpe + j];
+      for (int w = pw0; w < pw1; ++w) {
+        woff[static_cast<long long>(w) * E + pe] = run;
+        run += __popc(wbs[static_cast<long long>(w) * E + pe]);
+      }
+    }
+  } else if (tid == 0) {  // duplicated ids in a row: serial placement in (token, slot) order
+    for (int i = 0; i < n_rows * k; ++i) {
+      const int r = i / k, kk = i - r * k;
+      const int e = idx[static_cast<long long>(r) * (k + 1) + kk];
+      if (e < 0 || e >= E) continue;
+      const int pos = hist[e]++;
+      gslot[i] = pos;
+      grows[pos] = r;
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t < shared_tail; t += nth) grows[s_total + t] = t;
+}
+
+__global__ void __launch_bounds__(256) scan_place_kernel(const int* __restrict__ idx,
+                                                         const uint32_t* __restrict__ wbits,
+                                                         const int* __restrict__ wflags,
+                                                         const int* __restrict__ woff,
+                                                         int* __restrict__ gslot,
+                                                         int* __restrict__ grows, int n_rows,
+                                                         int k, int E, int n_w) {
+  __shared__ int s_dup;
+  const int w = blockIdx.x, tid = threadIdx.x;
+  if (tid == 0) s_dup = 0;
+  __syncthreads();
+  for (int j = tid; j < n_w; j += 256)
+    if (wflags[j] >> 16) s_dup = 1;
+  __syncthreads();
+  if (s_dup) return;  // placed serially by scan_offsets_kernel
+  const int r0 = w * kScanTok;
+  for (int i = tid; i < kScanTok * k; i += 256) {
+    const int r = r0 + i / k, kk = i % k;
+    if (r >= n_rows) break;
+    const int e = idx[static_cast<long long>(r) * (k + 1) + kk];
+    if (e < 0 || e >= E) continue;
+    const long long we = static_cast<long long>(w) * E + e;
+    const int pos = woff[we] + __popc(wbits[we] & ((1u << (r & 31)) - 1u));
+    gslot[r * k + kk] = pos;
+    grows[pos] = r;
+  }
+}
+
 // One block per 16-lane row (four per wave, 16 per workgroup): the lane's 16
 // values are four 16-B loads, and the block's max and bsums reduce inside a
 // DPP row.  Same arithmetic as quantize_block_wave.
@@ -583,7 +771,8 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(
 
 // ---- workspace ------------------------------------------------------------------
 struct PrefillWs {
-  size_t xq, gslot, grows, off, toff, meta, tiles, h, hq, y, total;
+  size_t xq, gslot, grows, off, toff, meta, tiles, wbits, woff, wflags, h, hq, y, total;
+  int n_w;        // scan workgroups of kScanTok tokens
   int P;          // positions: T*k routes + T shared
   int max_tiles;  // bound on the work list: every group's last tile may be partial
 };
@@ -602,6 +791,10 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
   w.meta = o;  o = al256(o + 4 * 4);
   w.max_tiles = (T * k + kTokTile - 1) / kTokTile + E + (T + kTokTile - 1) / kTokTile;
   w.tiles = o; o = al256(o + static_cast<size_t>(1 + w.max_tiles) * 4);
+  w.n_w = (T + kScanTok - 1) / kScanTok;
+  w.wbits = o; o = al256(o + static_cast<size_t>(w.n_w) * E * 4);
+  w.woff = o;  o = al256(o + static_cast<size_t>(w.n_w) * E * 4);
+  w.wflags = o; o = al256(o + static_cast<size_t>(w.n_w) * 4);
   w.h = o;     o = al256(o + static_cast<size_t>(w.P) * n_ff * 4);
   w.hq = o;    o = al256(o + static_cast<size_t>(w.P) * (n_ff / kQK) * kQ8Bytes);
   w.y = o;     o = al256(o + static_cast<size_t>(w.P) * hidden * 4);
@@ -708,9 +901,23 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
     if (int st = sg_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w,
                                 stream))
       return st;
-  if (int st = scan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, n_tokens, k, n_expert,
-                           kTokTile, has_shared ? n_tokens : 0, s, nm))
-    return st;
+  {  // the plan over many workgroups (bits, offsets, placement)
+    uint32_t* wbits = reinterpret_cast<uint32_t*>(base + ws.wbits);
+    int* woff = reinterpret_cast<int*>(base + ws.woff);
+    int* wflags = reinterpret_cast<int*>(base + ws.wflags);
+    const int shared_tail = has_shared ? n_tokens : 0;
+    hipLaunchKernelGGL(scan_bits_kernel, dim3(ws.n_w), dim3(256), 0, s, idx, weight, gslot, wbits,
+                       wflags, n_tokens, k, n_expert);
+    if (int st = check_launch("sg_moe_prefill/scan_bits")) return st;
+    const size_t bits_lds = ws.n_w * n_expert <= kScanBitsLds ? static_cast<size_t>(ws.n_w) * n_expert * 4 : 0;
+    hipLaunchKernelGGL(scan_offsets_kernel, dim3(1), dim3(1024), bits_lds, s, idx, wbits, wflags, woff,
+                       gslot, grows, off, toff, meta, tiles, n_tokens, k, n_expert, ws.n_w,
+                       kTokTile, shared_tail);
+    if (int st = check_launch("sg_moe_prefill/scan_offsets")) return st;
+    hipLaunchKernelGGL(scan_place_kernel, dim3(ws.n_w), dim3(256), 0, s, idx, wbits, wflags, woff,
+                       gslot, grows, n_tokens, k, n_expert, ws.n_w);
+    if (int st = check_launch("sg_moe_prefill/scan_place")) return st;
+  }
   const int G = n_expert + has_shared;
   GroupedArgs ga{};
   ga.tab_a = tab_gate;
