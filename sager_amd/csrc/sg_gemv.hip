@@ -64,9 +64,11 @@ struct SegRows {
 struct TableRows {
   const sg_block_q4k* const* ptrs;
   int rows_per, nb, n_ptrs;
+  int shift;  // log2(rows_per) when it is a power of two, else -1
   const unsigned long long* lds = nullptr;
+  __device__ int matrix(int r) const { return shift >= 0 ? r >> shift : r / rows_per; }
   __device__ const char* row(int r) const {
-    const int e = r / rows_per;
+    const int e = matrix(r);
     const unsigned long long base =
         lds ? lds[e] : reinterpret_cast<unsigned long long>(ptrs[e]);
     return reinterpret_cast<const char*>(base) +
@@ -81,7 +83,7 @@ struct TableRows {
   __device__ void attach(const uint32_t* src) {
     if (n_ptrs <= kMaxLdsPtrs) lds = reinterpret_cast<const unsigned long long*>(src);
   }
-  __device__ bool contiguous(int r0, int n) const { return r0 / rows_per == (r0 + n - 1) / rows_per; }
+  __device__ bool contiguous(int r0, int n) const { return matrix(r0) == matrix(r0 + n - 1); }
   // LDS words the staged table occupies (2 per pointer, when it is staged)
   __device__ int table_words() const { return n_ptrs <= kMaxLdsPtrs ? 2 * n_ptrs : 0; }
 };
@@ -367,7 +369,9 @@ int sg_gemv_ptrs_q4_k_q8(const sg_block_q4k* const* ptrs, const sg_block_q8k* x,
     return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_ptrs_q4_k_q8: n_rows=%d k=%d needs %zu B of LDS",
                      n_rows, k, lds);
   hipLaunchKernelGGL((gemv1_kernel<TableRows, F32Out>), dim3(L.grid), dim3(256), lds,
-                     static_cast<hipStream_t>(stream), TableRows{ptrs, rows_per, nb, n_ptrs},
+                     static_cast<hipStream_t>(stream),
+                     TableRows{ptrs, rows_per, nb, n_ptrs,
+                               (rows_per & (rows_per - 1)) == 0 ? __builtin_ctz(rows_per) : -1},
                      reinterpret_cast<const unsigned char*>(x), F32Out{y}, n_rows, nb, lpr,
                      L.gpw);
   return check_launch("sg_gemv_ptrs_q4_k_q8");
