@@ -336,9 +336,6 @@ __device__ __forceinline__ void wave_argmax_dpp(float& bv, int& bi) {
 
 // Quantize one 256-value block with the calling wave; `lane` in 0..63.
 // v[0..3] are the lane's values 4*lane..4*lane+3 of the block.
-// kSplitBsums: the bsums field holds each sub-block sum s as bytes
-// lo = s & 127 (bytes 0-7) and hi = s >> 7 (bytes 8-15), s = 128 hi + lo.
-template <bool kSplitBsums = false>
 __device__ __forceinline__ void quantize_block_wave(const float v[4], unsigned char* ob, int lane) {
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
   amax = fmaxf(wave_max_dpp(amax), 1e-30f);
@@ -354,14 +351,7 @@ __device__ __forceinline__ void quantize_block_wave(const float v[4], unsigned c
   const int s = sum8_dpp(q[0] + q[1] + q[2] + q[3]);
   *reinterpret_cast<uint32_t*>(ob + 4 + 4 * lane) = packed;
   if (lane == 0) *reinterpret_cast<float*>(ob) = d;
-  if ((lane & 7) == 0) {
-    if (kSplitBsums) {
-      ob[260 + (lane >> 3)] = static_cast<unsigned char>(s & 127);
-      ob[268 + (lane >> 3)] = static_cast<unsigned char>((s >> 7) & 0xFF);
-    } else {
-      *reinterpret_cast<int16_t*>(ob + 260 + 2 * (lane >> 3)) = static_cast<int16_t>(s);
-    }
-  }
+  if ((lane & 7) == 0) *reinterpret_cast<int16_t*>(ob + 260 + 2 * (lane >> 3)) = static_cast<int16_t>(s);
 }
 
 
