@@ -441,9 +441,6 @@ __device__ __forceinline__ void quantize_x(const float* x, int n_blocks, uint32_
 }
 
 // Logit-order top-(k+1) of every token: spec[t*m + r] = r-th expert (or -1).
-// Teams of tw waves; each thread keeps its logits in lr[] (last pass's
-// token).  Workgroup-wide; the last pass's top[] is readable on return,
-// spec[] only after the caller's next barrier.
 // Logits of the first routing pass into lr[] (what spec_select's pass 0
 // reads): thread tt of team `team` holds experts tt + TT*j of token `team`,
 // 0 outside.  Same team geometry as front_lds.
@@ -463,6 +460,12 @@ __device__ __forceinline__ void logits_preload(const LayerArgs& a, int tid, floa
   }
 }
 
+// Logit-order top-(k+1) of every token: teams of tw waves, one token per
+// team per pass; each thread keeps its logits in lr[] (pass 0's from
+// logits_preload, then the last pass's token).  Workgroup-wide; the last
+// pass's top[] is readable on return, spec[] only after the caller's next
+// barrier.  wait_copies: the calling wave waits for its outstanding copies
+// before the selection's barrier (so they are visible on return).
 template <int EPT>
 __device__ __forceinline__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
                             int tid, bool wait_copies = false) {
