@@ -77,6 +77,12 @@ static LayerWs layer_ws(int T, int n_ff, int E, int k) {
   return w;
 }
 
+struct FrontLds {
+  int nteams, tw, TT, ept, m, e32, ncp;
+  int tabg, tabu, tabd, lv, ev, cand, top, red, zs, spec, ridx, rw, re, rfirst, poff, pexp,
+      ptok, pslot, ctrl, xs, total;
+};
+
 struct LayerArgs {
   const sg_block_q4k* const* tab_gate;
   const sg_block_q4k* const* tab_up;
@@ -96,16 +102,12 @@ struct LayerArgs {
   float shared_w;
   int back_rows, back_lrow;  // rows per back workgroup, lanes per row there
   int back_bufs;             // back waves with a down-row buffer (8, or 4 when LDS is short)
+  FrontLds front_routed, front_shared;  // front LDS layouts (routing groups, shared group)
 };
 
 // ---- front kernel LDS layout (dwords) -----------------------------------------------
 // Routing runs in teams: one team of 4 waves per token for T = 1, two teams
 // of 2 waves for T = 2, four one-wave teams otherwise (tokens in passes).
-struct FrontLds {
-  int nteams, tw, TT, ept, m, e32, ncp;
-  int tabg, tabu, tabd, lv, ev, cand, top, red, zs, spec, ridx, rw, re, rfirst, poff, pexp,
-      ptok, pslot, ctrl, xs, total;
-};
 
 __host__ __device__ inline FrontLds front_lds(int T, int nbh, int E, int k, bool routed) {
   FrontLds L{};
@@ -768,12 +770,13 @@ __device__ __forceinline__ void exact_route(const LayerArgs& a, uint32_t* dyn, c
 // h for the (token, slot) entries of its group in the exact plan.  The
 // publisher workgroup (blockIdx.y == gmax, x == 0) runs the same routing
 // and writes idx, weight and the plan.
-template <int EPT>
+// NBH: hidden / 256 when compiled for it (0 = read from a).
+template <int EPT, int NBH>
 __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[64 * 36],
                            uint32_t* dyn) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, E = a.n_expert, stride = k + 1;
-  const int nbh = a.hidden / kQK, lpr = pow2_ceil(nbh);
+  const int nbh = NBH ? NBH : a.hidden / kQK, lpr = NBH ? pow2_ceil(NBH) : pow2_ceil(nbh);
   const bool publisher = g == a.gmax;
   if (publisher && bx != 0) return;  // one publisher per launch
   const bool shared_grp = a.has_shared && g == 0;
@@ -781,7 +784,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   // issued before anything else
   float lr[EPT];
   if (a.logits && !shared_grp) logits_preload<EPT>(a, tid, lr);
-  const FrontLds L = front_lds(T, nbh, E, k, !shared_grp);
+  const FrontLds& L = shared_grp ? a.front_shared : a.front_routed;
   const int rpw = 32 / lpr;
   const int row0 = bx * 4 * rpw + wave * rpw;
   const int nrw = max(0, min(rpw, a.n_ff - row0));
@@ -1007,7 +1010,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
               poff[g + 1] - j0, stride, a.n_ff, a.h, lane);
 }
 
-template <int EPT>
+template <int EPT, int NBH>
 __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
@@ -1020,7 +1023,7 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
   const int y = blockIdx.y;
   const int g =
       a.T != 1 || !a.has_shared || y >= a.gmax ? y : (y + 1 == a.gmax ? 0 : y + 1);
-  front_body<EPT>(a, blockIdx.x, g, wbuf, dyn);
+  front_body<EPT, NBH>(a, blockIdx.x, g, wbuf, dyn);
 }
 
 // ---- back kernel ------------------------------------------------------------------------
@@ -1406,17 +1409,21 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rows_wg = 4 * (32 / pow2_ceil(hidden / kQK));
   const FrontLds fl = front_lds(n_tokens, hidden / kQK, n_expert, k, true);
+  a.front_routed = fl;
+  a.front_shared = front_lds(n_tokens, hidden / kQK, n_expert, k, false);
   if (stages & 1) {
     // y < gmax: compute workgroups of group y; y == gmax: the publisher
     const dim3 grid((n_ff + rows_wg - 1) / rows_wg, ws.gmax + 1);
-    if (fl.ept <= 1)
-      hipLaunchKernelGGL(layer_front_kernel<1>, grid, dim3(256), lds_f, s, a);
+    if (fl.ept <= 1 && hidden / kQK == 8)  // the decode shape, compiled for hidden 2048
+      hipLaunchKernelGGL((layer_front_kernel<1, 8>), grid, dim3(256), lds_f, s, a);
+    else if (fl.ept <= 1)
+      hipLaunchKernelGGL((layer_front_kernel<1, 0>), grid, dim3(256), lds_f, s, a);
     else if (fl.ept <= 2)
-      hipLaunchKernelGGL(layer_front_kernel<2>, grid, dim3(256), lds_f, s, a);
+      hipLaunchKernelGGL((layer_front_kernel<2, 0>), grid, dim3(256), lds_f, s, a);
     else if (fl.ept <= 4)
-      hipLaunchKernelGGL(layer_front_kernel<4>, grid, dim3(256), lds_f, s, a);
+      hipLaunchKernelGGL((layer_front_kernel<4, 0>), grid, dim3(256), lds_f, s, a);
     else
-      hipLaunchKernelGGL(layer_front_kernel<kMaxEpt>, grid, dim3(256), lds_f, s, a);
+      hipLaunchKernelGGL((layer_front_kernel<kMaxEpt, 0>), grid, dim3(256), lds_f, s, a);
     if (int st = check_launch("sg_moe_layer/front")) return st;
   }
   if (stages & 2) {
