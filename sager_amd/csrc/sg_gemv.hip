@@ -111,8 +111,10 @@ __device__ __forceinline__ void dma_rows(const Rows& rows, int r0, int n, int nb
   }
 }
 
-// y[r] = W[r] . x, one token.  Wave W takes the contiguous row groups
-// [W*gpw, (W+1)*gpw) (a group = 64/lpr rows, one 9 KB buffer): it issues the
+// y[r] = W[r] . x, one token.  Wave W of the NW takes the row groups W,
+// W + NW, W + 2 NW, ... (a group = 64/lpr rows, one 9 KB buffer), so that the
+// chip reads one window of the matrix at a time (contiguous ranges per wave
+// measured 2-4 % slower); it issues the
 // next group's copy as soon as the current one has been read into
 // registers, so one group is always in flight while it computes.  The row
 // results stay in LDS until the wave's last group and are then written
@@ -159,8 +161,8 @@ __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned ch
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int rpw = 64 / lpr;
   const int n_groups = (n_rows + rpw - 1) / rpw;
-  const int g_begin = (blockIdx.x * kWaves + wv) * gpw;
-  const int g_end = min(n_groups, g_begin + gpw);
+  const int NW = gridDim.x * kWaves;
+  const int g_begin = blockIdx.x * kWaves + wv, g_end = n_groups;
   auto rows_of = [&](int gg) { return min(rpw, n_rows - gg * rpw); };
   // the first group's weights first: their HBM latency overlaps the staging
   if (g_begin < g_end) dma_rows(rows, g_begin * rpw, rows_of(g_begin), nb, wbuf[wv], lane);
@@ -178,21 +180,24 @@ __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned ch
   float xd = 0.f, bsf[8];
   load_x_regs(xs_dyn + (active ? blk : 0) * kXStride, xr, xd, bsf);
 
-  for (int g = g_begin; g < g_end; ++g) {
+  for (int g = g_begin, li = 0; g < g_end; g += NW, ++li) {
     const int n = rows_of(g);
     wait_vm();  // group g has landed
     uint32_t w36[36];
     const bool live = active && rr < n;
     if (live) read_block_lds(wbuf[wv] + (rr * nb + blk) * 36, w36);
     wait_lds();
-    if (g + 1 < g_end) dma_rows(rows, (g + 1) * rpw, rows_of(g + 1), nb, wbuf[wv], lane);
+    if (g + NW < g_end) dma_rows(rows, (g + NW) * rpw, rows_of(g + NW), nb, wbuf[wv], lane);
     const float s = live ? q4k_block_dot(w36, xr, xd, bsf) : 0.f;
     const float acc = row_sum_last(s, blk, nb);
-    if (blk == nb - 1 && rr < n) res[(g - g_begin) * rpw + rr] = acc;
+    if (blk == nb - 1 && rr < n) res[li * rpw + rr] = acc;
   }
   wait_lds();  // this wave's result writes (read back by its own lanes)
-  const int w_rows = max(0, min(n_rows, g_end * rpw) - g_begin * rpw);
-  for (int i = lane; i < w_rows; i += 64) out.store(g_begin * rpw + i, res[i]);
+  // result li * rpw + row of the wave belongs to group g_begin + li * NW
+  for (int i = lane; i < gpw * rpw; i += 64) {
+    const int r = (g_begin + (i / rpw) * NW) * rpw + i % rpw;
+    if (r < n_rows) out.store(r, res[i]);
+  }
 }
 
 // y[t*n_rows + r] = W[r] . x[t] for t < n_tokens; weights read once.

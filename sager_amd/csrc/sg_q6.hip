@@ -62,9 +62,11 @@ __global__ void __launch_bounds__(256) gemv_q6_kernel(const unsigned char* __res
               wv * gpw * R;
   const uint32_t row_bytes = static_cast<uint32_t>(nb) * kQ6Bytes;
   const int n_groups = (n_rows + R - 1) / R;
-  // wave W takes the contiguous groups [W * gpw, (W + 1) * gpw)
-  const int g_begin = (blockIdx.x * kQ6Waves + wv) * gpw;
-  const int g_end = min(n_groups, g_begin + gpw);
+  // wave W of the NW takes groups W, W + NW, W + 2 NW, ...: at any moment the
+  // chip reads one window of the matrix (a contiguous range per wave, its
+  // waves far apart in HBM, measured 7 % slower on the 418 MB head)
+  const int NW = gridDim.x * kQ6Waves;
+  const int g_begin = blockIdx.x * kQ6Waves + wv, g_end = n_groups;
   const u32x4 rw = buffer_desc(w6, static_cast<uint32_t>(n_rows) * row_bytes);
   const uint32_t last_blk = static_cast<uint32_t>(n_rows) * nb - 1;
 
@@ -89,7 +91,7 @@ __global__ void __launch_bounds__(256) gemv_q6_kernel(const unsigned char* __res
   auto instrs = [&](int gg) { return (min(R, n_rows - gg * R) * nb * kQ6SlotChunks + 63) / 64; };
   int g = g_begin;
   for (int j = 0; j < kQ6Depth - 1; ++j)
-    if (g + j < g_end) issue(g + j, ring + j * buf_words);
+    if (g + j * NW < g_end) issue(g + j * NW, ring + j * buf_words);
 
   // stage x: qs words, d, and the 16 sums of 16 codes per block
   for (int i = threadIdx.x; i < nb * 65; i += blockDim.x) {
@@ -116,17 +118,17 @@ __global__ void __launch_bounds__(256) gemv_q6_kernel(const unsigned char* __res
   const uint32_t nib = (qq & 2) ? 4 : 0, hsh = 2 * qq;
   const int xw = (qn * 128 + qq * 32 + is * 16) / 4;  // first qs word of the sub-group
 
-  for (int cur = 0; g < g_end; ++g, cur = cur + 1 == kQ6Depth ? 0 : cur + 1) {
+  for (int cur = 0, li = 0; g < g_end; g += NW, ++li, cur = cur + 1 == kQ6Depth ? 0 : cur + 1) {
     // group g has landed: only the copies of the next kQ6Depth - 2 groups may
     // still be in flight
     int younger = 0;
 #pragma unroll
     for (int j = 1; j < kQ6Depth - 1; ++j)
-      if (g + j < g_end) younger += instrs(g + j);
+      if (g + j * NW < g_end) younger += instrs(g + j * NW);
     wait_vm_n(younger);
     // refill the slot of group g - 1 (read in the previous iteration) with
     // g + depth - 1 before computing on g
-    const int g2 = g + kQ6Depth - 1;
+    const int g2 = g + (kQ6Depth - 1) * NW;
     if (g2 < g_end) {
       wait_lds();  // every read of the ring so far has returned
       issue(g2, ring + (cur == 0 ? kQ6Depth - 1 : cur - 1) * buf_words);
@@ -174,12 +176,15 @@ __global__ void __launch_bounds__(256) gemv_q6_kernel(const unsigned char* __res
       acc += dpp_f<0x104>(acc);
       acc += dpp_f<0x102>(acc);
       acc += dpp_f<0x101>(acc);
-      if (l == 0 && row < nr) ys[r0 - g_begin * R + row] = acc;
+      if (l == 0 && row < nr) ys[li * R + row] = acc;
     }
   }
   wait_lds();  // this wave's result writes (read back by its own lanes)
-  const int w_rows = max(0, min(n_rows, g_end * R) - g_begin * R);
-  for (int i = lane; i < w_rows; i += 64) y[g_begin * R + i] = ys[i];
+  // result li * R + row of the wave belongs to group g_begin + li * NW
+  for (int i = lane; i < gpw * R; i += 64) {
+    const int r = (g_begin + (i / R) * NW) * R + i % R;
+    if (r < n_rows) y[r] = ys[i];
+  }
 }
 
 }  // namespace sg
