@@ -94,6 +94,11 @@ int sg_gemv_q4_k_q8(const sg_block_q4k* w, const sg_block_q8k* x, float* y,
 int sg_gemv_q4_k_q8_batched(const sg_block_q4k* w, const sg_block_q8k* x,
                             float* y, int n_rows, int k, int n_tokens,
                             void* stream);
+/* The same with fp16 y.  Replaces cuda::gemv_q4_k_q8_f16out_batched
+ * (cuda_ops.hpp:67-70). */
+int sg_gemv_q4_k_q8_f16out_batched(const sg_block_q4k* w, const sg_block_q8k* x,
+                                   uint16_t* y, int n_rows, int k, int n_tokens,
+                                   void* stream);
 
 /* ---- dense-projection GEMVs (fp16 outputs) ---------------------------
  * The same Q4_K x Q8_K row dot (bit-identical to sg_gemv_q4_k_q8), rounded
@@ -137,6 +142,12 @@ int sg_gemv_q6_k_q8(const void* w6, const sg_block_q8k* x, float* y, int n_rows,
 int sg_gemv_ptrs_q4_k_q8(const sg_block_q4k* const* ptrs,
                          const sg_block_q8k* x, float* y, int n_ptrs,
                          int rows_per, int k, void* stream);
+/* The same with fp16 y (the fp32 row result rounded to nearest even), the
+ * argument meaning of cuda::gemv_ptrs_q4_k_q8_f16out (cuda_ops.hpp:60-63,
+ * q4_k.cu:184-213). */
+int sg_gemv_ptrs_q4_k_q8_f16out(const sg_block_q4k* const* ptrs,
+                                const sg_block_q8k* x, uint16_t* y, int n_ptrs,
+                                int rows_per, int k, void* stream);
 
 /* Test hook: the int32 sub-block dot sums the GEMVs use,
  * dots[(r*(k/256) + b)*8 + s] = sum_l nibble * xq for sub-block s of block b.
@@ -171,6 +182,42 @@ int sg_moe_combine(float* out, const float* residual, const float* expert_y,
                    const float* weight, int n_used, int hidden, int n_rows,
                    void* stream);
 
+/* ---- fp16-buffer launchers (the session loop's own buffers) ------------
+ * fp16 values are IEEE binary16 bits; every conversion to fp16 rounds to
+ * nearest even (__float2half), conversions to fp32 are exact. */
+
+/* out[i] = f16(g/(1+exp(-g))*u) over rows*n_ff values, g, u fp16.
+ * Replaces cuda::silu_mul_f16 (cuda_ops.hpp:305-306, norm_rotary.cu:133-141). */
+int sg_silu_mul_f16(uint16_t* out, const uint16_t* g, const uint16_t* u, int rows, int n_ff,
+                    void* stream);
+
+/* out[r][i] = f16(f32(out[r][i]) + sum_{kk=0..n_used} fma(weight[r][kk],
+ * f32(expert_y[r][kk][i]), .)) in kk order; out holds the residual on entry.
+ * weight rows have stride n_used+1, expert_y is fp16 [n_rows][n_used+1][hidden].
+ * Replaces cuda::moe_combine_batched_f16 (cuda_ops.hpp:379-381,
+ * moe.cu:265-280). */
+int sg_moe_combine_batched_f16(uint16_t* out, const uint16_t* expert_y, const float* weight,
+                               int n_used, int hidden, int n_rows, void* stream);
+
+/* out[i] *= sigmoid(g[0]) on fp16 out[n] (the shared expert's scalar gate,
+ * fp32 logit g).  Replaces cuda::sigmoid_gate_scalar_f16 (cuda_ops.hpp:315-316,
+ * norm_rotary.cu:177-184). */
+int sg_sigmoid_gate_scalar_f16(uint16_t* out, const float* g, int n, void* stream);
+/* out[r*hidden + i] *= sigmoid(g[r]).  Replaces
+ * cuda::sigmoid_gate_scalar_batched_f16 (cuda_ops.hpp:384-386, moe.cu:282-292). */
+int sg_sigmoid_gate_scalar_batched_f16(uint16_t* out, const float* g, int n_rows, int hidden,
+                                       void* stream);
+
+/* y[t*n_rows + r] = sum_i w[r][i] * f32(x[t][i]) for W fp32 [n_rows][k] and
+ * x fp16 [n_tokens][k]: the router logits and the shared-expert gate logit.
+ * Per row, lane l of 32 accumulates i = l, l+32, ... with fma, then a
+ * shfl_down tree (16, 8, 4, 2, 1): the reference kernel's order
+ * (q4_k.cu:133-149, 285-303; the mtok variant keeps the same order,
+ * q4_k.cu:1434-1438).  Replaces cuda::gemv_f32_out_f16x (n_tokens = 1) and
+ * gemv_f32_out_f16x_batched / _mtok. */
+int sg_gemv_f32_out_f16x(const float* w, const uint16_t* x, float* y, int n_rows, int k,
+                         int n_tokens, void* stream);
+
 /* ---- fused MoE layer (decode step / verify window) --------------------
  * One MoE layer for n_tokens (1..16) tokens, in the stage order of the
  * reference's device path Session::moe_dispatch_device
@@ -184,6 +231,14 @@ int sg_moe_combine(float* out, const float* residual, const float* expert_y,
  *                     layer's slice of the [3][layer][E] pointer table
  *                     (session.cpp:2787-2796).
  *   sh_gate/up/down:  shared expert (n_ff x hidden etc.), or all NULL.
+ *   sh_gate_w: fp32 [hidden] scalar gate row of the shared expert (qwen3.5
+ *             files, LayerWeights::shared_gate_w, weights.hpp:54), or NULL.
+ *             When set, the shared expert's output of token t is scaled by
+ *             sigmoid(sh_gate_w . x[t]) before the combine, as
+ *             gemv_f32_out_f16x_batched + sigmoid_gate_scalar_batched_f16
+ *             do (session.cpp:2904-2909, layer.cpp:128-134).  The dot is
+ *             taken in the reference kernel's fp32 lane order (q4_k.cu:
+ *             133-149, 285-303); ignored without a shared expert.
  *   x:        fp32 [n_tokens][hidden] layer input.
  *   logits:   fp32 [n_tokens][n_expert]; if NULL, idx/weight are INPUTS
  *             (routing decided by the caller, e.g. sampled routing).
@@ -192,6 +247,9 @@ int sg_moe_combine(float* out, const float* residual, const float* expert_y,
  *   idx, weight: [n_tokens][k+1] (slot k of weight = shared_w).
  *   workspace: device buffer of at least sg_moe_layer_workspace_bytes()
  *             (scratch: the plan and h between the two launches).
+ * The reference applies the gate to the shared output before the combine,
+ * so slot k adds fma(shared_w, y_shared * sigmoid(g), acc); weight[t][k]
+ * stays shared_w.
  * Routes with an id outside [0, n_expert) zero that token's whole weight row
  * (shared slot included), as moe_dispatch_scan does (moe.cu:385-396); a null
  * table entry is an absent expert and contributes zero (q4_k.cu:697-710).
@@ -203,7 +261,7 @@ int sg_moe_layer(const sg_block_q4k* const* tab_gate,
                  const sg_block_q4k* const* tab_up,
                  const sg_block_q4k* const* tab_down,
                  const sg_block_q4k* sh_gate, const sg_block_q4k* sh_up,
-                 const sg_block_q4k* sh_down, const float* x,
+                 const sg_block_q4k* sh_down, const float* sh_gate_w, const float* x,
                  const float* logits, const float* residual, float* out,
                  int* idx, float* weight, void* workspace,
                  size_t workspace_bytes, int n_tokens, int hidden, int n_ff,
@@ -221,9 +279,10 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate,
                         const sg_block_q4k* const* tab_up,
                         const sg_block_q4k* const* tab_down,
                         const sg_block_q4k* sh_gate, const sg_block_q4k* sh_up,
-                        const sg_block_q4k* sh_down, const float* x,
-                        const float* logits, const float* residual, float* out,
-                        int* idx, float* weight, void* workspace,
+                        const sg_block_q4k* sh_down, const float* sh_gate_w,
+                        const float* x, const float* logits,
+                        const float* residual, float* out, int* idx,
+                        float* weight, void* workspace,
                         size_t workspace_bytes, int n_tokens, int hidden,
                         int n_ff, int n_expert, int k, float shared_w,
                         int stages, void* stream);
@@ -246,8 +305,30 @@ int sg_moe_dispatch_scan(const int* idx, float* weight, int* gslot, int* grows,
                          int* off, int* toff, int* meta, int n_rows, int k,
                          int n_expert, int tok_per, void* stream);
 
-/* A whole MoE layer for a prefill chunk of n_tokens tokens (up to the scan
- * limit above), same arguments and semantics as sg_moe_layer: Q8_K(x),
+/* The same plan built by three launches over many workgroups (32 tokens
+ * each: bitmaps, then one workgroup of offsets, then placement), with no
+ * limit on n_rows beyond int indexing; the order inside an expert is the
+ * same (token, then slot), so every array equals sg_moe_dispatch_scan's.
+ * It is the plan sg_moe_prefill builds.  Extra outputs:
+ *   shared_tail: the shared expert's rows (0 = none, else n_rows) appended
+ *                after the routed ones: off[E+1] = off[E] + shared_tail and
+ *                grows[off[E] + t] = t;
+ *   tiles:       NULL, or the grouped kernels' work list: tiles[0] = count,
+ *                then (expert << 16 | tile) for each tok_per-row tile of each
+ *                group (the shared expert as expert E); it needs
+ *                2 + (n_rows*k + tok_per-1)/tok_per + n_expert +
+ *                (shared_tail + tok_per-1)/tok_per entries.
+ * workspace: at least sg_moe_dispatch_plan_workspace_bytes(n_rows,
+ * n_expert) bytes of scratch.  n_expert <= 1024, k <= 32.  Replaces
+ * cuda::moe_dispatch_scan (cuda_ops.hpp:219-222) for large prefill chunks. */
+size_t sg_moe_dispatch_plan_workspace_bytes(int n_rows, int n_expert);
+int sg_moe_dispatch_plan(const int* idx, float* weight, int* gslot, int* grows, int* off,
+                         int* toff, int* meta, int* tiles, void* workspace,
+                         size_t workspace_bytes, int n_rows, int k, int n_expert, int tok_per,
+                         int shared_tail, void* stream);
+
+/* A whole MoE layer for a prefill chunk of n_tokens tokens (n_expert <=
+ * 1024, k <= 32; no further limit on n_tokens), same arguments and semantics as sg_moe_layer: Q8_K(x),
  * router top-k (logits != NULL) or caller routing, the device plan, gate/up
  * + SiLU and down as grouped int8-MFMA contractions over every routed expert
  * (the shared expert as one more group), combine in slot order.  Replaces
@@ -263,7 +344,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate,
                    const sg_block_q4k* const* tab_up,
                    const sg_block_q4k* const* tab_down,
                    const sg_block_q4k* sh_gate, const sg_block_q4k* sh_up,
-                   const sg_block_q4k* sh_down, const float* x,
+                   const sg_block_q4k* sh_down, const float* sh_gate_w, const float* x,
                    const float* logits, const float* residual, float* out,
                    int* idx, float* weight, void* workspace,
                    size_t workspace_bytes, int n_tokens, int hidden, int n_ff,

@@ -34,6 +34,8 @@ def lib():
                                               ctypes.c_float]
         L.orc_dequant.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
         L.orc_dequant_q6k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.orc_sigmoid.restype = ctypes.c_float
+        L.orc_sigmoid.argtypes = [ctypes.c_float]
         _lib = L
     return _lib
 
@@ -143,6 +145,21 @@ def moe_combine(expert_y, weight, residual=None):
     return out
 
 
+def gemv_f32_lanes(w, x):
+    """y [T, n_rows] = W fp32 [n_rows, k] . x fp32 [T, k] in the reference
+    fp32 GEMV's lane order (q4_k.cu:133-149)."""
+    w = _c(w, np.float32)
+    x = _c(np.atleast_2d(x), np.float32)
+    n_rows, k = w.shape
+    y = np.zeros((x.shape[0], n_rows), np.float32)
+    lib().orc_gemv_f32_lanes(P(w), P(x), P(y), n_rows, k, x.shape[0])
+    return y
+
+
+def sigmoid(g):
+    return np.float32(lib().orc_sigmoid(ctypes.c_float(float(g))))
+
+
 def _ptr_table(mats):
     arr = (ctypes.c_void_p * len(mats))()
     for i, m in enumerate(mats):
@@ -151,9 +168,11 @@ def _ptr_table(mats):
 
 
 def moe_layer(gate, up, down, shared, x, logits=None, idx=None, weight=None, residual=None,
-              hidden=2048, n_ff=512, k=8, shared_w=1.0, n_threads=1, prefill=False):
+              hidden=2048, n_ff=512, k=8, shared_w=1.0, n_threads=1, prefill=False,
+              shared_gate_w=None):
     """gate/up/down: lists of per-expert uint8 arrays (None = absent);
-    shared: (g, u, d) or None.  Returns out [T, hidden], idx, weight.
+    shared: (g, u, d) or None; shared_gate_w: fp32 [hidden] gate row of the
+    shared expert or None.  Returns out [T, hidden], idx, weight.
     prefill=True: every GEMV in the integer-first epilogue order of the
     MFMA prefill path (orc_moe_prefill)."""
     x = _c(np.atleast_2d(x), np.float32)
@@ -170,6 +189,8 @@ def moe_layer(gate, up, down, shared, x, logits=None, idx=None, weight=None, res
         sg, su, sd = (m.ctypes.data for m in shared)
     out = np.zeros((T, hidden), np.float32)
     res = _c(residual, np.float32) if residual is not None else None
+    sgw = _c(shared_gate_w, np.float32) if shared_gate_w is not None else None
+    psgw = P(sgw) if sgw is not None else None
     if prefill:
         if logits is not None:
             logits = _c(np.atleast_2d(logits), np.float32)
@@ -178,7 +199,7 @@ def moe_layer(gate, up, down, shared, x, logits=None, idx=None, weight=None, res
         else:
             idx, weight = _c(idx, np.int32), _c(weight, np.float32).copy()
         lib().orc_moe_prefill(tg, tu, td, ctypes.c_void_p(sg), ctypes.c_void_p(su),
-                              ctypes.c_void_p(sd), P(x),
+                              ctypes.c_void_p(sd), psgw, P(x),
                               P(logits) if logits is not None else None,
                               P(res) if res is not None else None, P(out), P(idx), P(weight), T,
                               hidden, n_ff, n_expert, k, ctypes.c_float(shared_w), n_threads)
@@ -189,13 +210,13 @@ def moe_layer(gate, up, down, shared, x, logits=None, idx=None, weight=None, res
         idx = np.full((T, k + 1), -1, np.int32)
         weight = np.zeros((T, k + 1), np.float32)
         lib().orc_moe_layer(tg, tu, td, ctypes.c_void_p(sg), ctypes.c_void_p(su),
-                            ctypes.c_void_p(sd), P(x), P(logits),
+                            ctypes.c_void_p(sd), psgw, P(x), P(logits),
                             P(res) if res is not None else None, P(out), P(idx), P(weight), T,
                             hidden, n_ff, n_expert, k, ctypes.c_float(shared_w), n_threads)
     else:
         idx, weight = _c(idx, np.int32), _c(weight, np.float32).copy()
         lib().orc_moe_layer_routed(tg, tu, td, ctypes.c_void_p(sg), ctypes.c_void_p(su),
-                                   ctypes.c_void_p(sd), P(x), P(idx), P(weight),
+                                   ctypes.c_void_p(sd), psgw, P(x), P(idx), P(weight),
                                    P(res) if res is not None else None, P(out), T, hidden,
                                    n_ff, n_expert, k, n_threads)
         # the oracle zeroes weights of bounds-killed rows on its own copy

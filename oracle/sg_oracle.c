@@ -455,6 +455,35 @@ void orc_moe_combine(float* out, const float* residual, const float* expert_y,
   }
 }
 
+/* ---- fp32 weight x activation GEMV: router logits and the shared gate ----
+ * gemv_f32_out_kernel / gemv_f32_out_batched_kernel (q4_k.cu:133-149,
+ * 285-303): per row, lane l of a 32-lane warp accumulates elements
+ * l, l+32, ... (nvcc contracts `acc += w * x` into one FMA), then
+ * `acc += __shfl_down_sync(acc, off)` for off = 16, 8, 4, 2, 1; lane 0's
+ * value is the row.  A lane whose partner l+off is past 31 keeps its own
+ * value, so lane 0's result depends only on lanes 0..31 as written below. */
+static float rowdot_lanes32(const float* w, const float* x, int k) {
+  float acc[32];
+  for (int l = 0; l < 32; ++l) {
+    float a = 0.f;
+    for (int i = l; i < k; i += 32) a = fmaf(w[i], x[i], a);
+    acc[l] = a;
+  }
+  for (int off = 16; off > 0; off >>= 1)
+    for (int l = 0; l + off < 32; ++l) acc[l] = acc[l] + acc[l + off];
+  return acc[0];
+}
+
+void orc_gemv_f32_lanes(const float* w, const float* x, float* y, int n_rows, int k,
+                        int n_tokens) {
+  for (int t = 0; t < n_tokens; ++t)
+    for (int r = 0; r < n_rows; ++r)
+      y[(int64_t)t * n_rows + r] = rowdot_lanes32(w + (int64_t)r * k, x + (int64_t)t * k, k);
+}
+
+/* 1 / (1 + exp(-g)) (moe.cu:289, norm_rotary.cu:182) */
+float orc_sigmoid(float g) { return 1.f / (1.f + orc_expf(-g)); }
+
 /* ---- worker pool (pool.cpp semantics: one job per expert FFN) ----------- */
 
 typedef struct {
@@ -527,7 +556,8 @@ static void pool_run(ffn_job* jobs, int n_jobs, int n_threads) {
 
 static void moe_layer_routed(const void* const* tab_gate, const void* const* tab_up,
                              const void* const* tab_down, const void* sh_gate,
-                             const void* sh_up, const void* sh_down, const float* x,
+                             const void* sh_up, const void* sh_down, const float* sh_gate_w,
+                             const float* x,
                              const int* idx, const float* weight, const float* residual,
                              float* out, int n_tokens, int hidden, int n_ff, int n_expert,
                              int k, int n_threads, int int_first) {
@@ -566,6 +596,14 @@ static void moe_layer_routed(const void* const* tab_gate, const void* const* tab
     }
   }
   pool_run(jobs, nj, n_threads);
+  /* qwen3.5 shared-expert gate (session.cpp:2904-2909): the shared output
+   * of token t is scaled by sigmoid(sh_gate_w . x[t]) before the combine */
+  if (sh_gate_w && sh_gate && sh_up && sh_down)
+    for (int t = 0; t < n_tokens; ++t) {
+      const float s = orc_sigmoid(rowdot_lanes32(sh_gate_w, x + (int64_t)t * hidden, hidden));
+      float* yk = ys + ((size_t)t * slots + k) * hidden;
+      for (int i = 0; i < hidden; ++i) yk[i] = yk[i] * s;
+    }
   orc_moe_combine(out, residual, ys, w, k, hidden, n_tokens);
   free(w);
   free(jobs);
@@ -575,12 +613,13 @@ static void moe_layer_routed(const void* const* tab_gate, const void* const* tab
 
 void orc_moe_layer_routed(const void* const* tab_gate, const void* const* tab_up,
                           const void* const* tab_down, const void* sh_gate, const void* sh_up,
-                          const void* sh_down, const float* x, const int* idx,
+                          const void* sh_down, const float* sh_gate_w, const float* x,
+                          const int* idx,
                           const float* weight, const float* residual, float* out,
                           int n_tokens, int hidden, int n_ff, int n_expert, int k,
                           int n_threads) {
-  moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, x, idx, weight,
-                   residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads, 0);
+  moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w, x, idx,
+                   weight, residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads, 0);
 }
 
 /* The prefill layer: the same routing, experts and combine as
@@ -588,23 +627,23 @@ void orc_moe_layer_routed(const void* const* tab_gate, const void* const* tab_up
  * orc_gemv_q4k_q8_int (what the MFMA prefill kernels compute). */
 void orc_moe_prefill(const void* const* tab_gate, const void* const* tab_up,
                      const void* const* tab_down, const void* sh_gate, const void* sh_up,
-                     const void* sh_down, const float* x, const float* logits,
-                     const float* residual, float* out, int* idx, float* weight, int n_tokens,
-                     int hidden, int n_ff, int n_expert, int k, float shared_w,
-                     int n_threads) {
+                     const void* sh_down, const float* sh_gate_w, const float* x,
+                     const float* logits, const float* residual, float* out, int* idx,
+                     float* weight, int n_tokens, int hidden, int n_ff, int n_expert, int k,
+                     float shared_w, int n_threads) {
   if (logits) orc_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w);
-  moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, x, idx, weight,
-                   residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads, 1);
+  moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w, x, idx,
+                   weight, residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads, 1);
 }
 
 void orc_moe_layer(const void* const* tab_gate, const void* const* tab_up,
                    const void* const* tab_down, const void* sh_gate,
-                   const void* sh_up, const void* sh_down, const float* x,
-                   const float* logits, const float* residual, float* out,
+                   const void* sh_up, const void* sh_down, const float* sh_gate_w,
+                   const float* x, const float* logits, const float* residual, float* out,
                    int* idx, float* weight, int n_tokens, int hidden, int n_ff,
                    int n_expert, int k, float shared_w, int n_threads) {
   orc_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w);
-  orc_moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, x,
+  orc_moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w, x,
                        idx, weight, residual, out, n_tokens, hidden, n_ff,
                        n_expert, k, n_threads);
 }

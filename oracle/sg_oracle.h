@@ -15,6 +15,8 @@
  *   - router softmax/top-k/renorm      src/kernels/cuda/moe.cu:25-85
  *   - the fp32 combine                 src/kernels/cuda/moe.cu:265-280
  *   - the MoE layer stage order        src/core/session.cpp:2482-3030
+ *   - fp32 x GEMV (router, shared gate) src/kernels/cuda/q4_k.cu:133-149
+ *   - the shared-expert sigmoid gate   src/core/session.cpp:2904-2909
  *
  * Every function is pinned by a test (golden vectors from the reference's own
  * CPU sources, closed forms, brute force, or order-free invariants); see the
@@ -89,17 +91,28 @@ void orc_router_topk(const float* logits, int* idx, float* weight, int n_expert,
 void orc_moe_combine(float* out, const float* residual, const float* expert_y,
                      const float* weight, int n_used, int hidden, int n_rows);
 
+/* y[t][r] = W[r] . x[t], W fp32 [n_rows][k], x fp32 [n_tokens][k], in the
+ * reference kernel's order (q4_k.cu:133-149): 32 lane-strided fma chains,
+ * then the shfl_down tree 16, 8, 4, 2, 1. */
+void orc_gemv_f32_lanes(const float* w, const float* x, float* y, int n_rows, int k,
+                        int n_tokens);
+/* 1 / (1 + exp(-g)) with orc_expf. */
+float orc_sigmoid(float g);
+
 /* One MoE layer for n_tokens tokens, device-path stage order
  * (session.cpp:2482-3030): quantize x, route, each routed expert and the
  * shared expert through orc_expert_ffn semantics, combine with slot k =
  * shared (weight shared_w). tab_* are [n_expert] pointers; sh_* may be NULL
  * (no shared expert: slot k contributes 0). residual may be NULL (= 0).
  * idx/weight outputs: [n_tokens][k+1]. n_threads > 1 runs the expert jobs
- * on a worker pool (same results). */
+ * on a worker pool (same results).  sh_gate_w (fp32 [hidden] or NULL):
+ * the shared output of token t is multiplied by
+ * orc_sigmoid(orc_gemv_f32_lanes(sh_gate_w, x[t])) before the combine
+ * (session.cpp:2904-2909); ignored without a shared expert. */
 void orc_moe_layer(const void* const* tab_gate, const void* const* tab_up,
                    const void* const* tab_down, const void* sh_gate,
-                   const void* sh_up, const void* sh_down, const float* x,
-                   const float* logits, const float* residual, float* out,
+                   const void* sh_up, const void* sh_down, const float* sh_gate_w,
+                   const float* x, const float* logits, const float* residual, float* out,
                    int* idx, float* weight, int n_tokens, int hidden, int n_ff,
                    int n_expert, int k, float shared_w, int n_threads);
 
@@ -108,17 +121,17 @@ void orc_moe_layer(const void* const* tab_gate, const void* const* tab_up,
  * (idx/weight then inputs). */
 void orc_moe_prefill(const void* const* tab_gate, const void* const* tab_up,
                      const void* const* tab_down, const void* sh_gate, const void* sh_up,
-                     const void* sh_down, const float* x, const float* logits,
-                     const float* residual, float* out, int* idx, float* weight, int n_tokens,
-                     int hidden, int n_ff, int n_expert, int k, float shared_w,
-                     int n_threads);
+                     const void* sh_down, const float* sh_gate_w, const float* x,
+                     const float* logits, const float* residual, float* out, int* idx,
+                     float* weight, int n_tokens, int hidden, int n_ff, int n_expert, int k,
+                     float shared_w, int n_threads);
 
 /* Same as orc_moe_layer but with routing given (idx/weight [n_tokens][k+1]
  * already filled, e.g. sampled routing); no softmax. */
 void orc_moe_layer_routed(const void* const* tab_gate,
                           const void* const* tab_up,
                           const void* const* tab_down, const void* sh_gate,
-                          const void* sh_up, const void* sh_down,
+                          const void* sh_up, const void* sh_down, const float* sh_gate_w,
                           const float* x, const int* idx, const float* weight,
                           const float* residual, float* out, int n_tokens,
                           int hidden, int n_ff, int n_expert, int k,

@@ -41,14 +41,24 @@ SIGNATURES = {
     "sg_router_topk": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _F, _VP]),
     "sg_silu_mul": (_I, [_VP, _VP, _VP, _I, _VP]),
     "sg_moe_combine": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _VP]),
+    "sg_silu_mul_f16": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
+    "sg_moe_combine_batched_f16": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
+    "sg_sigmoid_gate_scalar_f16": (_I, [_VP, _VP, _I, _VP]),
+    "sg_sigmoid_gate_scalar_batched_f16": (_I, [_VP, _VP, _I, _I, _VP]),
+    "sg_gemv_f32_out_f16x": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
+    "sg_gemv_ptrs_q4_k_q8_f16out": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
+    "sg_gemv_q4_k_q8_f16out_batched": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
     "sg_moe_layer_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
-    "sg_moe_layer": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+    "sg_moe_layer": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                           _VP, _SZ, _I, _I, _I, _I, _I, _F, _VP]),
     "sg_moe_layer_stages": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
-                                 _VP, _SZ, _I, _I, _I, _I, _I, _F, _I, _VP]),
+                                 _VP, _VP, _SZ, _I, _I, _I, _I, _I, _F, _I, _VP]),
     "sg_moe_dispatch_scan": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
+    "sg_moe_dispatch_plan_workspace_bytes": (_SZ, [_I, _I]),
+    "sg_moe_dispatch_plan": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I,
+                                  _I, _I, _VP]),
     "sg_moe_prefill_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
-    "sg_moe_prefill": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+    "sg_moe_prefill": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                             _VP, _SZ, _I, _I, _I, _I, _I, _F, _VP]),
     "sg_gguf_expert_dims": (_I, [ctypes.c_char_p, _VP, _VP, _VP, _VP, _VP]),
     "sg_expert_pool_load_gguf": (_I, [ctypes.c_char_p, _VP]),

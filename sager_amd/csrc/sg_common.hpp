@@ -246,6 +246,44 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.f + expf_sg(-g)) * u;
 }
 
+// fp16 bits <-> fp32; the conversion to fp16 rounds the fp32 value to
+// nearest even (__float2half of the reference's sth(), moe.cu:12-14).
+__device__ __forceinline__ float f16v(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+__device__ __forceinline__ uint16_t f16b(float v) {
+  // v is materialized as an fp32 value first: otherwise the compiler fuses
+  // the producing multiply or fma with the conversion into one mixed-
+  // precision fma (v_fma_mix*_f16), which rounds once instead of twice and
+  // adds +0 to a -0 product.
+  asm("" : "+v"(v));
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+// sigmoid(g) = 1 / (1 + exp(-g)), the shared-expert gate
+// (moe.cu:289, norm_rotary.cu:182).
+__host__ __device__ __forceinline__ float sigmoid_sg(float g) {
+  return 1.f / (1.f + expf_sg(-g));
+}
+
+// fp32 weight row . activation row in the order of the reference's fp32
+// GEMV (gemv_f32_out_kernel, q4_k.cu:133-149; the shared-expert gate and
+// router logits): lane l of 32 accumulates elements l, l+32, l+64, ... as
+// acc = fma(w, x, acc) (nvcc contracts `acc += w * x`), then a shfl_down
+// tree over offsets 16, 8, 4, 2, 1.  Run by 32 lanes together (l = lane
+// & 31, all 32 active); the row value is in lane l = 0.  xv(i) gives x[i]
+// as fp32.
+template <typename XV>
+__device__ __forceinline__ float rowdot_f32_lanes32(const float* __restrict__ w, XV xv, int k,
+                                                    int l) {
+  float acc = 0.f;
+#pragma unroll 8
+  for (int i = l; i < k; i += 32) acc = __builtin_fmaf(w[i], xv(i), acc);
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) acc += __shfl_down(acc, off, 32);
+  return acc;
+}
+
 // ---- Q8_K code of one scaled value ----------------------------------------
 // round-half-even, then the x86 float->int conversion the reference runs on
 // (NaN and out-of-range -> INT_MIN), then the +-127 clamp.

@@ -128,27 +128,25 @@ struct F32Out {
   float* y;
   __device__ void store(int r, float v) const { y[r] = v; }
 };
-__device__ __forceinline__ uint16_t f16_bits(float v) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
-}
-__device__ __forceinline__ float f16_value(uint16_t b) {
-  return static_cast<float>(__builtin_bit_cast(_Float16, b));
-}
+struct F16Out {
+  uint16_t* y;
+  __device__ void store(int r, float v) const { y[r] = f16b(v); }
+};
 struct F16SegOut {
   uint16_t* y[3];
   int end[3];
   __device__ void store(int r, float v) const {
     const int m = r < end[0] ? 0 : (r < end[1] ? 1 : 2);
-    y[m][r - (m ? end[m - 1] : 0)] = f16_bits(v);
+    y[m][r - (m ? end[m - 1] : 0)] = f16b(v);
   }
 };
 struct F16ResAddOut {
   uint16_t* y;
   uint16_t* res;
   __device__ void store(int r, float v) const {
-    const uint16_t h = f16_bits(v);
+    const uint16_t h = f16b(v);
     y[r] = h;
-    res[r] = f16_bits(f16_value(res[r]) + f16_value(h));
+    res[r] = f16b(f16v(res[r]) + f16v(h));
   }
 };
 
@@ -200,10 +198,12 @@ __global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned ch
   }
 }
 
-// y[t*n_rows + r] = W[r] . x[t] for t < n_tokens; weights read once.
+// y[t*n_rows + r] = W[r] . x[t] for t < n_tokens; weights read once.  The
+// row result goes out through Out (fp32, or rounded to fp16).
+template <typename Out>
 __global__ void __launch_bounds__(256) gemv_batched_kernel(const sg_block_q4k* __restrict__ w,
                                                            const unsigned char* __restrict__ xq,
-                                                           float* __restrict__ y, int n_rows,
+                                                           Out y, int n_rows,
                                                            int nb, int lpr, int n_tokens) {
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[kWaves][kBufWords];
   extern __shared__ __attribute__((aligned(16))) uint32_t xs_dyn[];  // T * nb * kXStride
@@ -243,7 +243,7 @@ __global__ void __launch_bounds__(256) gemv_batched_kernel(const sg_block_q4k* _
         s = block_sum(w36[0], sm8, ip, xd, bsf);
       }
       const float acc = row_sum_last(s, blk, nb);
-      if (blk == nb - 1 && rr < n) y[static_cast<long long>(t) * n_rows + r0 + rr] = acc;
+      if (blk == nb - 1 && rr < n) y.store(t * n_rows + r0 + rr, acc);
     }
   }
 }
@@ -333,6 +333,51 @@ static int launch_gemv1(Rows rows, const sg_block_q8k* x, Out out, int n_rows, i
   return check_launch(nm);
 }
 
+// the pointer-table GEMV over an output policy
+template <typename Out>
+static int launch_ptrs(const sg_block_q4k* const* ptrs, const sg_block_q8k* x, Out y, int n_ptrs,
+                       int rows_per, int k, hipStream_t s, const char* nm) {
+  if (!ptrs || !x) return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  if (n_ptrs <= 0 || rows_per <= 0 || static_cast<long long>(n_ptrs) * rows_per > 0x7fffffffLL)
+    return set_error(SG_ERR_GEOMETRY, "%s: n_ptrs=%d rows_per=%d", nm, n_ptrs, rows_per);
+  const int n_rows = n_ptrs * rows_per;
+  if (int st = check_gemv_geometry(nm, n_rows, k)) return st;
+  const int nb = k / kQK, lpr = lanes_per_row(nb);
+  const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
+  const Gemv1Launch L = gemv1_launch(n_groups, 64 / lpr);
+  const size_t lds = static_cast<size_t>(nb) * kXStride * 4 +
+                     (n_ptrs <= kMaxLdsPtrs ? static_cast<size_t>(n_ptrs) * 8 : 0) + L.res_bytes;
+  if (lds > 96 * 1024)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows=%d k=%d needs %zu B of LDS", nm, n_rows, k,
+                     lds);
+  hipLaunchKernelGGL((gemv1_kernel<TableRows, Out>), dim3(L.grid), dim3(256), lds, s,
+                     TableRows{ptrs, rows_per, nb, n_ptrs,
+                               (rows_per & (rows_per - 1)) == 0 ? __builtin_ctz(rows_per) : -1},
+                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr, L.gpw);
+  return check_launch(nm);
+}
+
+// the batched GEMV over an output policy (fp32 or fp16 rows)
+template <typename Out>
+static int launch_batched(const sg_block_q4k* w, const sg_block_q8k* x, Out y, int n_rows, int k,
+                          int n_tokens, hipStream_t s, const char* nm) {
+  if (!w || !x) return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  if (int st = check_gemv_geometry(nm, n_rows, k)) return st;
+  if (n_tokens <= 0 || n_tokens > kMaxTokens)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: n_tokens=%d not in [1,%d]", nm, n_tokens,
+                     kMaxTokens);
+  if (static_cast<long long>(n_rows) * n_tokens > 0x7fffffffLL)
+    return set_error(SG_ERR_GEOMETRY, "%s: n_rows*n_tokens too large", nm);
+  const int nb = k / kQK, lpr = lanes_per_row(nb);
+  const size_t lds = static_cast<size_t>(nb) * n_tokens * kXStride * 4;
+  if (lds > 96 * 1024)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: k*n_tokens too large for LDS", nm);
+  const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
+  hipLaunchKernelGGL((gemv_batched_kernel<Out>), dim3(gemv_grid(n_groups)), dim3(256), lds, s, w,
+                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr, n_tokens);
+  return check_launch(nm);
+}
+
 }  // namespace sg
 
 using namespace sg;
@@ -358,47 +403,30 @@ int sg_gemv_q4_k_q8(const sg_block_q4k* w, const sg_block_q8k* x, float* y, int 
 
 int sg_gemv_ptrs_q4_k_q8(const sg_block_q4k* const* ptrs, const sg_block_q8k* x, float* y,
                          int n_ptrs, int rows_per, int k, void* stream) {
-  if (!ptrs || !x || !y)
-    return set_error(SG_ERR_INVALID_ARGUMENT, "sg_gemv_ptrs_q4_k_q8: null pointer");
-  if (n_ptrs <= 0 || rows_per <= 0 || static_cast<long long>(n_ptrs) * rows_per > 0x7fffffffLL)
-    return set_error(SG_ERR_GEOMETRY, "sg_gemv_ptrs_q4_k_q8: n_ptrs=%d rows_per=%d", n_ptrs,
-                     rows_per);
-  const int n_rows = n_ptrs * rows_per;
-  if (int st = check_gemv_geometry("sg_gemv_ptrs_q4_k_q8", n_rows, k)) return st;
-  const int nb = k / kQK, lpr = lanes_per_row(nb);
-  const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
-  const Gemv1Launch L = gemv1_launch(n_groups, 64 / lpr);
-  const size_t lds = static_cast<size_t>(nb) * kXStride * 4 +
-                     (n_ptrs <= kMaxLdsPtrs ? static_cast<size_t>(n_ptrs) * 8 : 0) + L.res_bytes;
-  if (lds > 96 * 1024)
-    return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_ptrs_q4_k_q8: n_rows=%d k=%d needs %zu B of LDS",
-                     n_rows, k, lds);
-  hipLaunchKernelGGL((gemv1_kernel<TableRows, F32Out>), dim3(L.grid), dim3(256), lds,
-                     static_cast<hipStream_t>(stream),
-                     TableRows{ptrs, rows_per, nb, n_ptrs,
-                               (rows_per & (rows_per - 1)) == 0 ? __builtin_ctz(rows_per) : -1},
-                     reinterpret_cast<const unsigned char*>(x), F32Out{y}, n_rows, nb, lpr,
-                     L.gpw);
-  return check_launch("sg_gemv_ptrs_q4_k_q8");
+  if (!y) return set_error(SG_ERR_INVALID_ARGUMENT, "sg_gemv_ptrs_q4_k_q8: null pointer");
+  return launch_ptrs(ptrs, x, F32Out{y}, n_ptrs, rows_per, k, static_cast<hipStream_t>(stream),
+                     "sg_gemv_ptrs_q4_k_q8");
+}
+
+int sg_gemv_ptrs_q4_k_q8_f16out(const sg_block_q4k* const* ptrs, const sg_block_q8k* x,
+                                uint16_t* y, int n_ptrs, int rows_per, int k, void* stream) {
+  if (!y) return set_error(SG_ERR_INVALID_ARGUMENT, "sg_gemv_ptrs_q4_k_q8_f16out: null pointer");
+  return launch_ptrs(ptrs, x, F16Out{y}, n_ptrs, rows_per, k, static_cast<hipStream_t>(stream),
+                     "sg_gemv_ptrs_q4_k_q8_f16out");
 }
 
 int sg_gemv_q4_k_q8_batched(const sg_block_q4k* w, const sg_block_q8k* x, float* y, int n_rows,
                             int k, int n_tokens, void* stream) {
-  if (!w || !x || !y)
-    return set_error(SG_ERR_INVALID_ARGUMENT, "sg_gemv_q4_k_q8_batched: null pointer");
-  if (int st = check_gemv_geometry("sg_gemv_q4_k_q8_batched", n_rows, k)) return st;
-  if (n_tokens <= 0 || n_tokens > kMaxTokens)
-    return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_q4_k_q8_batched: n_tokens=%d not in [1,%d]",
-                     n_tokens, kMaxTokens);
-  const int nb = k / kQK, lpr = lanes_per_row(nb);
-  const size_t lds = static_cast<size_t>(nb) * n_tokens * kXStride * 4;
-  if (lds > 96 * 1024)
-    return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_q4_k_q8_batched: k*n_tokens too large for LDS");
-  const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
-  hipLaunchKernelGGL(gemv_batched_kernel, dim3(gemv_grid(n_groups)), dim3(256), lds,
-                     static_cast<hipStream_t>(stream), w,
-                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr, n_tokens);
-  return check_launch("sg_gemv_q4_k_q8_batched");
+  if (!y) return set_error(SG_ERR_INVALID_ARGUMENT, "sg_gemv_q4_k_q8_batched: null pointer");
+  return launch_batched(w, x, F32Out{y}, n_rows, k, n_tokens, static_cast<hipStream_t>(stream),
+                        "sg_gemv_q4_k_q8_batched");
+}
+
+int sg_gemv_q4_k_q8_f16out_batched(const sg_block_q4k* w, const sg_block_q8k* x, uint16_t* y,
+                                   int n_rows, int k, int n_tokens, void* stream) {
+  if (!y) return set_error(SG_ERR_INVALID_ARGUMENT, "sg_gemv_q4_k_q8_f16out_batched: null pointer");
+  return launch_batched(w, x, F16Out{y}, n_rows, k, n_tokens, static_cast<hipStream_t>(stream),
+                        "sg_gemv_q4_k_q8_f16out_batched");
 }
 
 int sg_q4k_subblock_dots(const sg_block_q4k* w, const sg_block_q8k* x, int32_t* dots, int n_rows,

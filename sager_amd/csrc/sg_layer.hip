@@ -55,7 +55,7 @@ struct LayerPlan {
 };
 
 struct LayerWs {
-  size_t meta, off, expert, tok, slot, wdown, h, total;
+  size_t meta, off, expert, tok, slot, wdown, sgate, h, total;
   int gmax, emax;
 };
 
@@ -72,6 +72,7 @@ static LayerWs layer_ws(int T, int n_ff, int E, int k) {
   w.tok = o;    o = align256(o + w.emax * sizeof(int));
   w.slot = o;   o = align256(o + w.emax * sizeof(int));
   w.wdown = o;  o = align256(o + w.gmax * sizeof(unsigned long long));
+  w.sgate = o;  o = align256(o + static_cast<size_t>(T) * sizeof(float));
   w.h = o;      o = align256(o + static_cast<size_t>(T) * (k + 1) * n_ff * sizeof(float));
   w.total = o;
   return w;
@@ -90,6 +91,7 @@ struct LayerArgs {
   const sg_block_q4k* sh_gate;
   const sg_block_q4k* sh_up;
   const sg_block_q4k* sh_down;
+  const float* sh_gate_w;  // fp32 [hidden] shared-expert gate row, or null
   const float* x;
   const float* logits;
   const float* residual;
@@ -98,6 +100,7 @@ struct LayerArgs {
   float* weight;
   LayerPlan plan;
   float* h;
+  float* sgate;  // [T] sigmoid(sh_gate_w . x[t]) when sh_gate_w is set
   int T, hidden, n_ff, n_expert, k, has_shared, gmax, emax;
   float shared_w;
   int back_rows, back_lrow;  // rows per back workgroup, lanes per row there
@@ -806,6 +809,17 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
     // entries: tokens 0..T-1 in slot k, no plan needed
     gateup_wave(true, row0, nrw, nbh, lpr, buf, xs,
                 [&](int j, int& t, int& sl) { t = j; sl = k; }, T, stride, a.n_ff, a.h, lane);
+    if (a.sh_gate_w && bx == 0) {
+      // the shared expert's scalar gate of every token (session.cpp:2904-2909):
+      // one token per 32-lane half-wave, the result read by the back kernel
+      const int l = lane & 31, half = tid >> 5;
+      for (int t0 = 0; t0 < T; t0 += 8) {
+        const int t = min(t0 + half, T - 1);
+        const float* xt = a.x + static_cast<long long>(t) * a.hidden;
+        const float gl = rowdot_f32_lanes32(a.sh_gate_w, [&](int i) { return xt[i]; }, a.hidden, l);
+        if (l == 0 && t0 + half < T) a.sgate[t] = sigmoid_sg(gl);
+      }
+    }
     return;
   }
 
@@ -1039,7 +1053,7 @@ constexpr int kBackThreads = 64 * kBackWaves;
 constexpr int kBackHSlots = 3;  // h blocks per wave preloaded at kernel start (T = 1, k = 8: 18)
 
 struct BackLds {
-  int hq, ys, off, wdown, tok, slot, wt, meta, total;
+  int hq, ys, off, wdown, tok, slot, wt, sg, meta, total;
 };
 
 __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, int gmax,
@@ -1060,6 +1074,7 @@ __host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, in
   L.tok = take(emax);
   L.slot = take(emax);
   L.wt = take(T * (k + 1));
+  L.sg = take(T);
   L.meta = take(4);
   L.total = (o + 3) & ~3;  // the down-row buffers follow, 16-B aligned
   return L;
@@ -1088,6 +1103,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
   const int* tok = reinterpret_cast<const int*>(bd + L.tok);
   const int* slot = reinterpret_cast<const int*>(bd + L.slot);
   const float* wt = reinterpret_cast<const float*>(bd + L.wt);
+  const float* sgl = reinterpret_cast<const float*>(bd + L.sg);
   const int* meta = reinterpret_cast<const int*>(bd + L.meta);
   const int nq = T * stride * nbf;
   const int n_out = T * nr;
@@ -1220,6 +1236,10 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
     const int t = qo / nr, r = qo - t * nr;
     const long long o = static_cast<long long>(t) * a.hidden + row0 + r;
     float acc = a.residual ? (qo == tid ? res0 : a.residual[o]) : 0.f;
+    // the shared slot's output scaled by its gate first (1.0 without a
+    // gate, which leaves it unchanged), as sigmoid_gate_scalar_batched_f16
+    // does before the combine (session.cpp:2904-2909)
+    const float gs = sgl[t];
     for (int k0 = 0; k0 <= k; k0 += 16) {  // gather 16 slots, then the ordered fma chain
       float yv[16], wv[16];
 #pragma unroll
@@ -1227,6 +1247,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
         const int i = t * stride + (k0 + u <= k ? k0 + u : k);
         yv[u] = ys[i * rows + r];
         wv[u] = wt[i];
+        if (k0 + u == k) yv[u] *= gs;
       }
 #pragma unroll
       for (int u = 0; u < 16; ++u)
@@ -1257,6 +1278,7 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs a) {
   int* tok = reinterpret_cast<int*>(dyn + L.tok);
   int* slot = reinterpret_cast<int*>(dyn + L.slot);
   float* wt = reinterpret_cast<float*>(dyn + L.wt);
+  float* sgl = reinterpret_cast<float*>(dyn + L.sg);
   int* meta = reinterpret_cast<int*>(dyn + L.meta);
   float* ys = reinterpret_cast<float*>(dyn + L.ys);
   const int row0 = blockIdx.x * rows;
@@ -1290,6 +1312,7 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs a) {
     const int v_tok = a.plan.tok[min(tid, a.emax - 1)];
     const int v_slot = a.plan.slot[min(tid, a.emax - 1)];
     const float v_wt = a.weight[min(tid, nw - 1)];
+    const float v_sg = a.sgate ? a.sgate[min(tid, T - 1)] : 1.f;
     if (tid < 2) meta[tid] = v_meta;
     if (tid <= a.gmax) off[tid] = v_off;
     if (tid < a.gmax) wdown[tid] = v_wd;
@@ -1298,6 +1321,7 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs a) {
       slot[tid] = v_slot;
     }
     if (tid < nw) wt[tid] = v_wt;
+    if (tid < T) sgl[tid] = v_sg;
   } else {
     if (tid < 2) meta[tid] = a.plan.meta[tid];
     for (int i = tid; i <= a.gmax; i += kBackThreads) off[i] = a.plan.off[i];
@@ -1307,6 +1331,7 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs a) {
       slot[i] = a.plan.slot[i];
     }
     for (int i = tid; i < nw; i += kBackThreads) wt[i] = a.weight[i];
+    for (int i = tid; i < T; i += kBackThreads) sgl[i] = a.sgate ? a.sgate[i] : 1.f;
   }
   for (int i = tid; i < T * stride * rows; i += kBackThreads) ys[i] = 0.f;
   bar();
@@ -1334,10 +1359,11 @@ size_t sg_moe_layer_workspace_bytes(int n_tokens, int hidden, int n_ff, int n_ex
 
 int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
                         const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
-                        const sg_block_q4k* sh_up, const sg_block_q4k* sh_down, const float* x,
-                        const float* logits, const float* residual, float* out, int* idx,
-                        float* weight, void* workspace, size_t workspace_bytes, int n_tokens,
-                        int hidden, int n_ff, int n_expert, int k, float shared_w, int stages,
+                        const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
+                        const float* sh_gate_w, const float* x, const float* logits,
+                        const float* residual, float* out, int* idx, float* weight,
+                        void* workspace, size_t workspace_bytes, int n_tokens, int hidden,
+                        int n_ff, int n_expert, int k, float shared_w, int stages,
                         void* stream) {
   const char* nm = "sg_moe_layer";
   if (stages <= 0 || stages > 3)
@@ -1383,6 +1409,8 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   a.sh_gate = sh_gate;
   a.sh_up = sh_up;
   a.sh_down = sh_down;
+  // the gate scales the shared expert only: without one it has nothing to scale
+  a.sh_gate_w = n_sh == 3 ? sh_gate_w : nullptr;
   a.x = x;
   a.logits = logits;
   a.residual = residual;
@@ -1394,6 +1422,7 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
                      reinterpret_cast<int*>(base + ws.tok), reinterpret_cast<int*>(base + ws.slot),
                      reinterpret_cast<unsigned long long*>(base + ws.wdown)};
   a.h = reinterpret_cast<float*>(base + ws.h);
+  a.sgate = a.sh_gate_w ? reinterpret_cast<float*>(base + ws.sgate) : nullptr;
   a.T = n_tokens;
   a.hidden = hidden;
   a.n_ff = n_ff;
@@ -1443,13 +1472,14 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
 
 int sg_moe_layer(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
                  const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
-                 const sg_block_q4k* sh_up, const sg_block_q4k* sh_down, const float* x,
-                 const float* logits, const float* residual, float* out, int* idx,
-                 float* weight, void* workspace, size_t workspace_bytes, int n_tokens, int hidden,
-                 int n_ff, int n_expert, int k, float shared_w, void* stream) {
-  return sg_moe_layer_stages(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, x, logits,
-                             residual, out, idx, weight, workspace, workspace_bytes, n_tokens,
-                             hidden, n_ff, n_expert, k, shared_w, 3, stream);
+                 const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
+                 const float* sh_gate_w, const float* x, const float* logits,
+                 const float* residual, float* out, int* idx, float* weight, void* workspace,
+                 size_t workspace_bytes, int n_tokens, int hidden, int n_ff, int n_expert, int k,
+                 float shared_w, void* stream) {
+  return sg_moe_layer_stages(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w, x,
+                             logits, residual, out, idx, weight, workspace, workspace_bytes,
+                             n_tokens, hidden, n_ff, n_expert, k, shared_w, 3, stream);
 }
 
 }  // extern "C"

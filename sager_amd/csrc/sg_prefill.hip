@@ -607,11 +607,13 @@ __global__ void __launch_bounds__(1024) scan_offsets_kernel(
       meta[2] = s_bad;
       s_total = tot_h;
     }
-    if (tid < E)
-      for (int j = 0; j < tl; ++j) tiles[1 + pt + j] = (tid << 16) | j;
-    const int sh_t = (shared_tail + tok_per - 1) / tok_per;
-    for (int j = tid; j < sh_t; j += nth) tiles[1 + tot_t + j] = (E << 16) | j;
-    if (tid == 0) tiles[0] = tot_t + sh_t;
+    if (tiles) {
+      if (tid < E)
+        for (int j = 0; j < tl; ++j) tiles[1 + pt + j] = (tid << 16) | j;
+      const int sh_t = (shared_tail + tok_per - 1) / tok_per;
+      for (int j = tid; j < sh_t; j += nth) tiles[1 + tot_t + j] = (E << 16) | j;
+      if (tid == 0) tiles[0] = tot_t + sh_t;
+    }
     if (tid < E) hist[tid] = ph;  // hist now holds off[e]
   }
   __syncthreads();
@@ -735,13 +737,17 @@ __global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __re
 __global__ void __launch_bounds__(256) prefill_combine_kernel(
     float* __restrict__ out, const float* __restrict__ residual, const float* __restrict__ y,
     const float* __restrict__ weight, const int* __restrict__ gslot, const int* __restrict__ off,
-    int n_expert, int k, int hidden, int has_shared) {
+    const float* __restrict__ sgate, int n_expert, int k, int hidden, int has_shared) {
   const int t = blockIdx.y;
   const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= hidden) return;
   const long long o = static_cast<long long>(t) * hidden + i;
   float4 acc = residual ? *reinterpret_cast<const float4*>(residual + o) : make_float4(0.f, 0.f, 0.f, 0.f);
   const int shared_pos = off[n_expert] + t;
+  // the shared slot's output scaled by its gate first (1.0 without a gate
+  // leaves it unchanged), as sigmoid_gate_scalar_batched_f16 does before
+  // the combine (session.cpp:2904-2909)
+  const float gs = sgate ? sgate[t] : 1.f;
   for (int k0 = 0; k0 <= k; k0 += 8) {
     int pos[8];
     float wv[8];
@@ -757,6 +763,14 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(
       yv[u] = pos[u] >= 0 ? *reinterpret_cast<const float4*>(y + static_cast<long long>(pos[u]) * hidden + i)
                           : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (k0 + u == k) {
+        yv[u].x *= gs;
+        yv[u].y *= gs;
+        yv[u].z *= gs;
+        yv[u].w *= gs;
+      }
+#pragma unroll
     for (int u = 0; u < 8; ++u) {
       if (k0 + u <= k) {
         acc.x = __builtin_fmaf(wv[u], yv[u].x, acc.x);
@@ -769,15 +783,46 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(
   *reinterpret_cast<float4*>(out + o) = acc;
 }
 
+// sgate[t] = sigmoid(w . x[t]): the shared expert's scalar gate
+// (session.cpp:2904-2909, gemv_f32_out_f16x_batched then
+// sigmoid_gate_scalar_batched_f16), one token per 32-lane half-wave in the
+// reference's fp32 lane order.
+__global__ void __launch_bounds__(256) shared_gate_kernel(const float* __restrict__ w,
+                                                          const float* __restrict__ x,
+                                                          float* __restrict__ sgate, int n_tokens,
+                                                          int hidden) {
+  const int l = threadIdx.x & 31;
+  const int t0 = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int t = t0 < n_tokens ? t0 : n_tokens - 1;  // whole halves stay active for the shuffles
+  const float* xt = x + static_cast<long long>(t) * hidden;
+  const float g = rowdot_f32_lanes32(w, [&](int i) { return xt[i]; }, hidden, l);
+  if (l == 0 && t0 < n_tokens) sgate[t0] = sigmoid_sg(g);
+}
+
 // ---- workspace ------------------------------------------------------------------
+static size_t al256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+// scratch of the three-launch plan: wbits and woff [n_w][E], wflags [n_w]
+struct PlanWs {
+  size_t wbits, woff, wflags, total;
+  int n_w;
+};
+static PlanWs plan_ws(int n_rows, int E) {
+  PlanWs p{};
+  p.n_w = (n_rows + kScanTok - 1) / kScanTok;
+  size_t o = 0;
+  p.wbits = o;  o = al256(o + static_cast<size_t>(p.n_w) * E * 4);
+  p.woff = o;   o = al256(o + static_cast<size_t>(p.n_w) * E * 4);
+  p.wflags = o; o = al256(o + static_cast<size_t>(p.n_w) * 4);
+  p.total = o;
+  return p;
+}
+
 struct PrefillWs {
-  size_t xq, gslot, grows, off, toff, meta, tiles, wbits, woff, wflags, h, hq, y, total;
-  int n_w;        // scan workgroups of kScanTok tokens
+  size_t xq, gslot, grows, off, toff, meta, tiles, plan, sgate, h, hq, y, total;
   int P;          // positions: T*k routes + T shared
   int max_tiles;  // bound on the work list: every group's last tile may be partial
 };
-
-static size_t al256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
   PrefillWs w{};
@@ -791,10 +836,8 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
   w.meta = o;  o = al256(o + 4 * 4);
   w.max_tiles = (T * k + kTokTile - 1) / kTokTile + E + (T + kTokTile - 1) / kTokTile;
   w.tiles = o; o = al256(o + static_cast<size_t>(1 + w.max_tiles) * 4);
-  w.n_w = (T + kScanTok - 1) / kScanTok;
-  w.wbits = o; o = al256(o + static_cast<size_t>(w.n_w) * E * 4);
-  w.woff = o;  o = al256(o + static_cast<size_t>(w.n_w) * E * 4);
-  w.wflags = o; o = al256(o + static_cast<size_t>(w.n_w) * 4);
+  w.plan = o;  o = al256(o + plan_ws(T, E).total);
+  w.sgate = o; o = al256(o + static_cast<size_t>(T) * 4);
   w.h = o;     o = al256(o + static_cast<size_t>(w.P) * n_ff * 4);
   w.hq = o;    o = al256(o + static_cast<size_t>(w.P) * (n_ff / kQK) * kQ8Bytes);
   w.y = o;     o = al256(o + static_cast<size_t>(w.P) * hidden * 4);
@@ -830,6 +873,39 @@ static int scan_launch(const int* idx, float* weight, int* gslot, int* grows, in
   return check_launch(nm);
 }
 
+// the plan over many workgroups (bits, offsets, placement) on scratch `ws`
+static int plan_launch(const int* idx, float* weight, int* gslot, int* grows, int* off,
+                       int* toff, int* meta, int* tiles, unsigned char* ws, int n_rows, int k,
+                       int E, int tok_per, int shared_tail, hipStream_t s, const char* nm) {
+  const PlanWs p = plan_ws(n_rows, E);
+  uint32_t* wbits = reinterpret_cast<uint32_t*>(ws + p.wbits);
+  int* woff = reinterpret_cast<int*>(ws + p.woff);
+  int* wflags = reinterpret_cast<int*>(ws + p.wflags);
+  hipLaunchKernelGGL(scan_bits_kernel, dim3(p.n_w), dim3(256), 0, s, idx, weight, gslot, wbits,
+                     wflags, n_rows, k, E);
+  if (int st = check_launch(nm)) return st;
+  const size_t bits_lds =
+      p.n_w * E <= kScanBitsLds ? static_cast<size_t>(p.n_w) * E * 4 : 0;
+  hipLaunchKernelGGL(scan_offsets_kernel, dim3(1), dim3(1024), bits_lds, s, idx, wbits, wflags,
+                     woff, gslot, grows, off, toff, meta, tiles, n_rows, k, E, p.n_w, tok_per,
+                     shared_tail);
+  if (int st = check_launch(nm)) return st;
+  hipLaunchKernelGGL(scan_place_kernel, dim3(p.n_w), dim3(256), 0, s, idx, wbits, wflags, woff,
+                     gslot, grows, n_rows, k, E, p.n_w);
+  return check_launch(nm);
+}
+
+// limits of the three-launch plan: E <= 1024 (one LDS bitmap word per
+// expert), int route and tile indices
+static int plan_check(int n_rows, int k, int E, int tok_per, const char* nm) {
+  if (n_rows <= 0 || k <= 0 || k > 32 || E <= 0 || E > 1024 || tok_per <= 0)
+    return set_error(SG_ERR_GEOMETRY, "%s: n_rows=%d k=%d (<=32) n_expert=%d (<=1024) tok_per=%d",
+                     nm, n_rows, k, E, tok_per);
+  if (static_cast<long long>(n_rows) * (k + 1) > 0x7fffffffLL)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows=%d x k=%d routes too many", nm, n_rows, k);
+  return SG_OK;
+}
+
 }  // namespace sg
 
 using namespace sg;
@@ -853,6 +929,29 @@ int sg_moe_dispatch_scan(const int* idx, float* weight, int* gslot, int* grows, 
                      static_cast<hipStream_t>(stream), nm);
 }
 
+size_t sg_moe_dispatch_plan_workspace_bytes(int n_rows, int n_expert) {
+  if (n_rows <= 0 || n_expert <= 0) return 0;
+  return plan_ws(n_rows, n_expert).total;
+}
+
+int sg_moe_dispatch_plan(const int* idx, float* weight, int* gslot, int* grows, int* off,
+                         int* toff, int* meta, int* tiles, void* workspace,
+                         size_t workspace_bytes, int n_rows, int k, int n_expert, int tok_per,
+                         int shared_tail, void* stream) {
+  const char* nm = "sg_moe_dispatch_plan";
+  if (!idx || !weight || !gslot || !grows || !off || !toff || !meta || !workspace)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  if (int st = plan_check(n_rows, k, n_expert, tok_per, nm)) return st;
+  if (shared_tail < 0 || shared_tail > n_rows)
+    return set_error(SG_ERR_GEOMETRY, "%s: shared_tail=%d not in [0, n_rows]", nm, shared_tail);
+  if (workspace_bytes < plan_ws(n_rows, n_expert).total)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: workspace %zu < %zu bytes", nm,
+                     workspace_bytes, plan_ws(n_rows, n_expert).total);
+  return plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles,
+                     static_cast<unsigned char*>(workspace), n_rows, k, n_expert, tok_per,
+                     shared_tail, static_cast<hipStream_t>(stream), nm);
+}
+
 size_t sg_moe_prefill_workspace_bytes(int n_tokens, int hidden, int n_ff, int n_expert, int k) {
   if (n_tokens <= 0 || hidden <= 0 || n_ff <= 0 || n_expert <= 0 || k <= 0) return 0;
   return prefill_ws(n_tokens, hidden, n_ff, n_expert, k).total;
@@ -860,10 +959,11 @@ size_t sg_moe_prefill_workspace_bytes(int n_tokens, int hidden, int n_ff, int n_
 
 int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
                    const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
-                   const sg_block_q4k* sh_up, const sg_block_q4k* sh_down, const float* x,
-                   const float* logits, const float* residual, float* out, int* idx,
-                   float* weight, void* workspace, size_t workspace_bytes, int n_tokens,
-                   int hidden, int n_ff, int n_expert, int k, float shared_w, void* stream) {
+                   const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
+                   const float* sh_gate_w, const float* x, const float* logits,
+                   const float* residual, float* out, int* idx, float* weight, void* workspace,
+                   size_t workspace_bytes, int n_tokens, int hidden, int n_ff, int n_expert, int k,
+                   float shared_w, void* stream) {
   const char* nm = "sg_moe_prefill";
   if (!tab_gate || !tab_up || !tab_down || !x || !out || !idx || !weight || !workspace)
     return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
@@ -879,9 +979,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   if (workspace_bytes < ws.total)
     return set_error(SG_ERR_INVALID_ARGUMENT, "%s: workspace %zu < %zu bytes", nm,
                      workspace_bytes, ws.total);
-  if (scan_lds_words(n_tokens, n_expert) > kScanLdsWords || n_tokens * k > 1024 * kScanPerThread)
-    return set_error(SG_ERR_UNSUPPORTED, "%s: n_tokens=%d x n_expert=%d too large", nm, n_tokens,
-                     n_expert);
+  if (int st = plan_check(n_tokens, k, n_expert, kTokTile, nm)) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   unsigned char* base = static_cast<unsigned char*>(workspace);
   auto* xq = reinterpret_cast<sg_block_q8k*>(base + ws.xq);
@@ -895,29 +993,23 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   auto* hq = reinterpret_cast<sg_block_q8k*>(base + ws.hq);
   float* y = reinterpret_cast<float*>(base + ws.y);
   const int has_shared = n_sh == 3;
+  // the gate scales the shared expert only: without one it has nothing to scale
+  float* sgate = has_shared && sh_gate_w ? reinterpret_cast<float*>(base + ws.sgate) : nullptr;
 
   if (int st = quantize_split(x, xq, hidden / kQK, n_tokens, s, nm)) return st;
+  if (sgate) {
+    hipLaunchKernelGGL(shared_gate_kernel, dim3((n_tokens + 7) / 8), dim3(256), 0, s, sh_gate_w, x,
+                       sgate, n_tokens, hidden);
+    if (int st = check_launch("sg_moe_prefill/shared_gate")) return st;
+  }
   if (logits)
     if (int st = sg_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w,
                                 stream))
       return st;
-  {  // the plan over many workgroups (bits, offsets, placement)
-    uint32_t* wbits = reinterpret_cast<uint32_t*>(base + ws.wbits);
-    int* woff = reinterpret_cast<int*>(base + ws.woff);
-    int* wflags = reinterpret_cast<int*>(base + ws.wflags);
-    const int shared_tail = has_shared ? n_tokens : 0;
-    hipLaunchKernelGGL(scan_bits_kernel, dim3(ws.n_w), dim3(256), 0, s, idx, weight, gslot, wbits,
-                       wflags, n_tokens, k, n_expert);
-    if (int st = check_launch("sg_moe_prefill/scan_bits")) return st;
-    const size_t bits_lds = ws.n_w * n_expert <= kScanBitsLds ? static_cast<size_t>(ws.n_w) * n_expert * 4 : 0;
-    hipLaunchKernelGGL(scan_offsets_kernel, dim3(1), dim3(1024), bits_lds, s, idx, wbits, wflags, woff,
-                       gslot, grows, off, toff, meta, tiles, n_tokens, k, n_expert, ws.n_w,
-                       kTokTile, shared_tail);
-    if (int st = check_launch("sg_moe_prefill/scan_offsets")) return st;
-    hipLaunchKernelGGL(scan_place_kernel, dim3(ws.n_w), dim3(256), 0, s, idx, wbits, wflags, woff,
-                       gslot, grows, n_tokens, k, n_expert, ws.n_w);
-    if (int st = check_launch("sg_moe_prefill/scan_place")) return st;
-  }
+  if (int st = plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, base + ws.plan,
+                           n_tokens, k, n_expert, kTokTile, has_shared ? n_tokens : 0, s,
+                           "sg_moe_prefill/plan"))
+    return st;
   const int G = n_expert + has_shared;
   GroupedArgs ga{};
   ga.tab_a = tab_gate;
@@ -957,7 +1049,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
                      dim3(kThreads), 0, s, gd);
   if (int st = check_launch("sg_moe_prefill/down")) return st;
   hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 1023) / 1024, n_tokens), dim3(256), 0, s,
-                     out, residual, y, weight, gslot, off, n_expert, k, hidden, has_shared);
+                     out, residual, y, weight, gslot, off, sgate, n_expert, k, hidden, has_shared);
   return check_launch("sg_moe_prefill/combine");
 }
 

@@ -143,6 +143,39 @@ def gemv_ptrs_q4_k_q8(ptrs, x_q8, n_ptrs, rows_per, k, y=None):
     return y
 
 
+def gemv_ptrs_q4_k_q8_f16out(ptrs, x_q8, n_ptrs, rows_per, k, y=None):
+    """cuda::gemv_ptrs_q4_k_q8_f16out (cuda_ops.hpp:60-63): fp16 y."""
+    if y is None:
+        y = torch.empty(n_ptrs * rows_per, dtype=torch.float16, device=x_q8.device)
+    _check(load().sg_gemv_ptrs_q4_k_q8_f16out(_ptr(ptrs), _ptr(x_q8), _ptr(y), n_ptrs, rows_per,
+                                              k, _stream()))
+    return y
+
+
+def gemv_q4_k_q8_f16out_batched(w, x_q8, n_rows, k, n_tokens, y=None):
+    """cuda::gemv_q4_k_q8_f16out_batched (cuda_ops.hpp:67-70): fp16 y[n_tokens, n_rows]."""
+    if y is None:
+        y = torch.empty((n_tokens, n_rows), dtype=torch.float16, device=w.device)
+    _check(load().sg_gemv_q4_k_q8_f16out_batched(_ptr(w), _ptr(x_q8), _ptr(y), n_rows, k,
+                                                 n_tokens, _stream()))
+    return y
+
+
+def gemv_f32_out_f16x(w, x, y=None):
+    """cuda::gemv_f32_out_f16x / _batched (q4_k.cu:1713-1718, 1987-1991):
+    W fp32 [n_rows, k] . x fp16 [n_tokens, k] -> y fp32 [n_tokens, n_rows]
+    (router logits, the shared expert's gate logit)."""
+    n_rows, k = w.shape
+    x2 = x.reshape(-1, k)
+    if x2.dtype != torch.float16 or w.dtype != torch.float32:
+        raise SagerError("w must be fp32 and x fp16")
+    if y is None:
+        y = torch.empty((x2.shape[0], n_rows), dtype=torch.float32, device=w.device)
+    _check(load().sg_gemv_f32_out_f16x(_ptr(w), _ptr(x2), _ptr(y), n_rows, k, x2.shape[0],
+                                       _stream()))
+    return y
+
+
 def subblock_dots(w, x_q8, n_rows, k):
     """int32 sub-block dot sums [n_rows, k/256, 8] (test hook)."""
     d = torch.empty((n_rows, k // QK, 8), dtype=torch.int32, device=w.device)
@@ -187,16 +220,56 @@ def moe_combine_batched(expert_y, weight, residual=None, out=None):
     return out
 
 
+def silu_mul_f16(g, u, out=None):
+    """cuda::silu_mul_f16 (cuda_ops.hpp:305-306) on fp16 [rows, n_ff] buffers."""
+    if g.dtype != torch.float16 or u.dtype != torch.float16:
+        raise SagerError("g and u must be fp16")
+    if out is None:
+        out = torch.empty_like(g)
+    n_ff = g.shape[-1]
+    _check(load().sg_silu_mul_f16(_ptr(out), _ptr(g), _ptr(u), g.numel() // n_ff, n_ff,
+                                  _stream()))
+    return out
+
+
+def moe_combine_batched_f16(out, expert_y, weight):
+    """cuda::moe_combine_batched_f16 (cuda_ops.hpp:379-381): out fp16
+    [n_rows, hidden] holds the residual and receives the sum in place;
+    expert_y fp16 [n_rows, n_used+1, hidden], weight fp32 [n_rows, n_used+1]."""
+    n_rows, slots, hidden = expert_y.shape
+    _check(load().sg_moe_combine_batched_f16(_ptr(out), _ptr(expert_y), _ptr(weight), slots - 1,
+                                             hidden, n_rows, _stream()))
+    return out
+
+
+def sigmoid_gate_scalar_batched_f16(out, g):
+    """cuda::sigmoid_gate_scalar_batched_f16 (cuda_ops.hpp:384-386):
+    out fp16 [n_rows, hidden] *= sigmoid(g[row]) in place."""
+    out2 = out.reshape(g.numel(), -1)
+    _check(load().sg_sigmoid_gate_scalar_batched_f16(_ptr(out2), _ptr(g), out2.shape[0],
+                                                     out2.shape[1], _stream()))
+    return out
+
+
+def sigmoid_gate_scalar_f16(out, g):
+    """cuda::sigmoid_gate_scalar_f16 (cuda_ops.hpp:315-316): out fp16 [n] *= sigmoid(g[0])."""
+    _check(load().sg_sigmoid_gate_scalar_f16(_ptr(out), _ptr(g), out.numel(), _stream()))
+    return out
+
+
 class MoeLayer:
     """One MoE layer's device-side pointer tables and workspace; ``forward``
     is the device-path dispatch of Session::moe_dispatch_device
     (session.cpp:2482-3030) as one call.  ``stages``: 3 = front and back (the
-    whole layer), 1 / 2 = one of the two launches."""
+    whole layer), 1 / 2 = one of the two launches.  ``shared_gate_w``: the
+    shared expert's fp32 [hidden] gate row (LayerWeights::shared_gate_w), or
+    None."""
 
     def __init__(self, tab_gate, tab_up, tab_down, shared=None, hidden=2048, n_ff=512,
-                 n_expert=256, k=8, max_tokens=1, shared_w=1.0):
+                 n_expert=256, k=8, max_tokens=1, shared_w=1.0, shared_gate_w=None):
         self.tab_gate, self.tab_up, self.tab_down = tab_gate, tab_up, tab_down
         self.shared = shared
+        self.shared_gate_w = shared_gate_w
         self.hidden, self.n_ff, self.n_expert, self.k = hidden, n_ff, n_expert, k
         self.shared_w = float(shared_w)
         self.max_tokens = max_tokens
@@ -219,9 +292,9 @@ class MoeLayer:
         ws = self.workspace if workspace is None else workspace
         _check(load().sg_moe_layer_stages(
             _ptr(self.tab_gate), _ptr(self.tab_up), _ptr(self.tab_down), _ptr(sg), _ptr(su),
-            _ptr(sd), _ptr(x), _ptr(logits), _ptr(residual), _ptr(out), _ptr(idx), _ptr(weight),
-            _ptr(ws), ws.numel(), T, self.hidden, self.n_ff, self.n_expert, self.k,
-            self.shared_w, stages, _stream()))
+            _ptr(sd), _ptr(self.shared_gate_w), _ptr(x), _ptr(logits), _ptr(residual), _ptr(out),
+            _ptr(idx), _ptr(weight), _ptr(ws), ws.numel(), T, self.hidden, self.n_ff,
+            self.n_expert, self.k, self.shared_w, stages, _stream()))
         return out, idx, weight
 
 
@@ -241,14 +314,38 @@ def moe_dispatch_scan(idx, weight, n_expert, k, tok_per=64):
     return dict(gslot=gslot, grows=grows, off=off, toff=toff, meta=meta)
 
 
+def moe_dispatch_plan(idx, weight, n_expert, k, tok_per=64, shared_tail=0, tiles=True):
+    """The multi-workgroup plan (sg_moe_dispatch_plan): the arrays of
+    moe_dispatch_scan plus the grouped kernels' tile list; `weight` is
+    bounds-killed in place."""
+    n_rows = idx.shape[0]
+    dev = idx.device
+    gslot = torch.empty(n_rows * k, dtype=torch.int32, device=dev)
+    grows = torch.empty(n_rows * k + shared_tail, dtype=torch.int32, device=dev)
+    off = torch.empty(n_expert + 2, dtype=torch.int32, device=dev)
+    toff = torch.empty(n_expert + 2, dtype=torch.int32, device=dev)
+    meta = torch.zeros(4, dtype=torch.int32, device=dev)
+    n_tiles = (2 + (n_rows * k + tok_per - 1) // tok_per + n_expert
+               + (shared_tail + tok_per - 1) // tok_per)
+    tl = torch.empty(n_tiles, dtype=torch.int32, device=dev) if tiles else None
+    nbytes = load().sg_moe_dispatch_plan_workspace_bytes(n_rows, n_expert)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    _check(load().sg_moe_dispatch_plan(_ptr(idx), _ptr(weight), _ptr(gslot), _ptr(grows),
+                                       _ptr(off), _ptr(toff), _ptr(meta), _ptr(tl), _ptr(ws),
+                                       nbytes, n_rows, k, n_expert, tok_per, shared_tail,
+                                       _stream()))
+    return dict(gslot=gslot, grows=grows, off=off, toff=toff, meta=meta, tiles=tl)
+
+
 class MoePrefill(MoeLayer):
     """The same layer for a prefill chunk of up to max_tokens tokens: the
     device plan and int8-MFMA grouped contractions (sg_moe_prefill)."""
 
     def __init__(self, tab_gate, tab_up, tab_down, shared=None, hidden=2048, n_ff=512,
-                 n_expert=256, k=8, max_tokens=2048, shared_w=1.0):
+                 n_expert=256, k=8, max_tokens=2048, shared_w=1.0, shared_gate_w=None):
         self.tab_gate, self.tab_up, self.tab_down = tab_gate, tab_up, tab_down
         self.shared = shared
+        self.shared_gate_w = shared_gate_w
         self.hidden, self.n_ff, self.n_expert, self.k = hidden, n_ff, n_expert, k
         self.shared_w = float(shared_w)
         self.max_tokens = max_tokens
@@ -271,9 +368,9 @@ class MoePrefill(MoeLayer):
         ws = self.workspace if workspace is None else workspace
         _check(load().sg_moe_prefill(
             _ptr(self.tab_gate), _ptr(self.tab_up), _ptr(self.tab_down), _ptr(sg), _ptr(su),
-            _ptr(sd), _ptr(x), _ptr(logits), _ptr(residual), _ptr(out), _ptr(idx), _ptr(weight),
-            _ptr(ws), ws.numel(), T, self.hidden, self.n_ff, self.n_expert, self.k,
-            self.shared_w, _stream()))
+            _ptr(sd), _ptr(self.shared_gate_w), _ptr(x), _ptr(logits), _ptr(residual), _ptr(out),
+            _ptr(idx), _ptr(weight), _ptr(ws), ws.numel(), T, self.hidden, self.n_ff,
+            self.n_expert, self.k, self.shared_w, _stream()))
         return out, idx, weight
 
 

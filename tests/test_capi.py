@@ -48,10 +48,17 @@ def test_validation_without_launch(lib):
     assert lib.sg_router_topk(bad, bad, bad, 256, 8, 8, 1, 1.0, None) == 4   # stride < k+1
     ws = lib.sg_moe_layer_workspace_bytes(1, 2048, 512, 256, 8)
     assert ws > 0
-    args = [bad] * 3 + [None] * 3 + [bad, bad, None, bad, bad, bad, bad]
+    args = [bad] * 3 + [None] * 3 + [None] + [bad, bad, None, bad, bad, bad, bad]
     assert lib.sg_moe_layer(*args, ws - 1, 1, 2048, 512, 256, 8, 1.0, None) == 1
     assert lib.sg_moe_layer(*args, ws, 17, 2048, 512, 256, 8, 1.0, None) == 8
     assert lib.sg_moe_layer(*args, ws, 1, 2048, 512, 256, 33, 1.0, None) == 4
     sh = [bad, None, None]
-    args2 = [bad] * 3 + sh + [bad, bad, None, bad, bad, bad, bad]
+    args2 = [bad] * 3 + sh + [None] + [bad, bad, None, bad, bad, bad, bad]
     assert lib.sg_moe_layer(*args2, ws, 1, 2048, 512, 256, 8, 1.0, None) == 1
+    # fp16-buffer launchers and the fp32 x fp16 GEMV reject bad geometry
+    assert lib.sg_silu_mul_f16(bad, bad, bad, 0, 512, None) == 4
+    assert lib.sg_moe_combine_batched_f16(bad, bad, bad, 8, 2048, 70000, None) == 4
+    assert lib.sg_sigmoid_gate_scalar_batched_f16(None, bad, 1, 2048, None) == 1
+    assert lib.sg_gemv_f32_out_f16x(bad, bad, bad, 256, 0, 1, None) == 4
+    assert lib.sg_gemv_ptrs_q4_k_q8_f16out(bad, bad, bad, 0, 512, 2048, None) == 4
+    assert lib.sg_gemv_q4_k_q8_f16out_batched(bad, bad, bad, 8, 2048, 17, None) == 8

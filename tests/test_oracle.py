@@ -466,3 +466,95 @@ def test_q6k_gemv_vs_fp64(n_rows, k):
     ref = wf @ (xd * xv)
     y = orc.gemv_q6k(w6, xq, n_rows, k).astype(np.float64)
     assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+# ---- fp32 GEMV in the reference lane order, sigmoid, the shared gate -------
+
+def test_gemv_f32_lanes_order_pinned():
+    """Values chosen so that the lane-strided sequential fma chain and the
+    shfl_down tree (q4_k.cu:133-149) give exactly 1.0 while other orders do
+    not: lane 0 sums 2^24, 1, 1, -2^24 in index order (the 1s are absorbed:
+    0), lanes 1 and 17 cancel at the first tree step (off 16) before lane
+    9's 1 is added at the second (off 8)."""
+    k = 128
+    w = np.ones((1, k), np.float32)
+    x = np.zeros(k, np.float32)
+    x[0], x[32], x[64], x[96] = 2.0**24, 1.0, 1.0, -2.0**24
+    x[1], x[17], x[9] = 2.0**25, -2.0**25, 1.0
+    assert orc.gemv_f32_lanes(w, x)[0, 0] == np.float32(1.0)
+    # a plain index-order float32 sum loses both 1s and lane 9's
+    acc = np.float32(0)
+    for v in x:
+        acc = np.float32(acc + v)
+    assert acc != np.float32(1.0)
+
+
+def test_gemv_f32_lanes_vs_fp64():
+    rng = np.random.default_rng(31)
+    for n_rows, k, T in ((7, 2048, 3), (256, 2048, 1), (5, 96, 2), (3, 40, 1)):
+        w = rng.normal(0, 0.05, (n_rows, k)).astype(np.float32)
+        x = rng.normal(0, 1, (T, k)).astype(np.float32)
+        y = orc.gemv_f32_lanes(w, x)
+        ref = x.astype(np.float64) @ w.astype(np.float64).T
+        bound = 1e-6 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T) + 1e-30
+        assert (np.abs(y - ref) <= bound).all()
+        # exact on integers small enough that every partial sum is exact
+        wi = rng.integers(-8, 9, (n_rows, k)).astype(np.float32)
+        xi = rng.integers(-8, 9, (T, k)).astype(np.float32)
+        np.testing.assert_array_equal(orc.gemv_f32_lanes(wi, xi),
+                                      (xi.astype(np.int64) @ wi.astype(np.int64).T))
+
+
+def test_sigmoid_closed_form():
+    assert orc.sigmoid(0.0) == np.float32(0.5)
+    assert orc.sigmoid(200.0) == np.float32(1.0)
+    assert orc.sigmoid(-200.0) == np.float32(0.0)
+    rng = np.random.default_rng(5)
+    for g in rng.normal(0, 4, 2000).astype(np.float32):
+        ref = 1.0 / (1.0 + math.exp(-float(g)))
+        got = float(orc.sigmoid(g))
+        # exp correctly rounded, then two float32 roundings (add, divide)
+        assert abs(got - ref) <= 3 * np.spacing(np.float32(ref)), (g, got, ref)
+
+
+@pytest.mark.parametrize("prefill", [False, True])
+def test_moe_layer_shared_gate_is_scaled_shared_slot(prefill):
+    """The gated layer = the ungated experts, with the shared slot's output
+    multiplied by sigmoid(gate_w . x[t]) before the combine."""
+    rng = np.random.default_rng(44)
+    H, F, E, K, T = 512, 256, 8, 3, 3
+    g, u, d = _experts(rng, E + 1, H, F)
+    sh = (g[E], u[E], d[E])
+    x = rng.normal(0, 1, (T, H)).astype(np.float32)
+    lg = rng.normal(0, 1, (T, E)).astype(np.float32)
+    gw = rng.normal(0, 0.05, H).astype(np.float32)
+    res = rng.normal(0, 1, (T, H)).astype(np.float32)
+    out, idx, w = orc.moe_layer(g[:E], u[:E], d[:E], sh, x, logits=lg, residual=res, hidden=H,
+                                n_ff=F, k=K, shared_gate_w=gw, prefill=prefill, shared_w=0.5)
+    out0, idx0, _ = orc.moe_layer(g[:E], u[:E], d[:E], sh, x, logits=lg, residual=res, hidden=H,
+                                  n_ff=F, k=K, prefill=prefill, shared_w=0.5)
+    np.testing.assert_array_equal(idx, idx0)
+    assert not np.array_equal(out, out0)
+    gl = orc.gemv_f32_lanes(gw[None], x)[:, 0]
+    xq = orc.quantize_q8_k(x)
+    for t in range(T):
+        ys = []
+        for m in list(idx[t, :K]) + [None]:
+            wg, wu, wd = sh if m is None else (g[m], u[m], d[m])
+            if prefill:
+                gg = orc.gemv_int(wg, xq[t], F, H)[0]
+                uu = orc.gemv_int(wu, xq[t], F, H)[0]
+                hh = orc.quantize_q8_k(orc.silu_mul(gg, uu))
+                ys.append(orc.gemv_int(wd, hh, H, F)[0])
+            else:
+                ys.append(orc.expert_ffn(wg, wu, wd, x[t], H, F))
+        s = orc.sigmoid(gl[t])
+        ys[-1] = (ys[-1] * s).astype(np.float32)
+        ref = orc.moe_combine(np.stack(ys)[None], w[t:t + 1], res[t:t + 1])
+        np.testing.assert_array_equal(out[t], ref[0])
+    # without a shared expert the gate has nothing to scale
+    o1, _, _ = orc.moe_layer(g[:E], u[:E], d[:E], None, x, logits=lg, hidden=H, n_ff=F, k=K,
+                             shared_gate_w=gw, prefill=prefill)
+    o2, _, _ = orc.moe_layer(g[:E], u[:E], d[:E], None, x, logits=lg, hidden=H, n_ff=F, k=K,
+                             prefill=prefill)
+    np.testing.assert_array_equal(o1, o2)
