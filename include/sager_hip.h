@@ -267,6 +267,25 @@ int sg_moe_layer(const sg_block_q4k* const* tab_gate,
                  size_t workspace_bytes, int n_tokens, int hidden, int n_ff,
                  int n_expert, int k, float shared_w, void* stream);
 
+/* sg_moe_layer without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * library keeps one 1 MiB scratch array per GPU (a file-scope device array,
+ * held until the process ends) and uses it as the workspace; shapes whose
+ * sg_moe_layer_workspace_bytes() exceeds 1 MiB are rejected with
+ * SG_ERR_UNSUPPORTED (at hidden 2048, n_ff 512, top-8 + shared: up to 16
+ * tokens).  Allocates nothing.  Every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU (two streams, two threads) race:
+ * order them on one stream. */
+int sg_moe_layer_noalloc(const sg_block_q4k* const* tab_gate,
+                         const sg_block_q4k* const* tab_up,
+                         const sg_block_q4k* const* tab_down,
+                         const sg_block_q4k* sh_gate, const sg_block_q4k* sh_up,
+                         const sg_block_q4k* sh_down, const float* sh_gate_w,
+                         const float* x, const float* logits, const float* residual,
+                         float* out, int* idx, float* weight, int n_tokens, int hidden,
+                         int n_ff, int n_expert, int k, float shared_w, void* stream);
+
 /* The two launches of sg_moe_layer, selectable: bit 0 = front (top-k,
  * Q8_K of x, the expert-major plan, gate/up GEMV + SiLU), bit 1 = back
  * (Q8_K of h, down GEMV, combine).  The back stage reads what the front left

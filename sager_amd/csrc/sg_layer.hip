@@ -27,6 +27,8 @@
 // (session.cpp:2482-3030); router moe.cu:25-85 / 165-234; dispatch plan
 // moe.cu:366-444 (made deterministic); combine moe.cu:265-280; expert chain
 // q4_avx2.cpp:175-196.
+#include <mutex>
+
 #include "sg_common.hpp"
 #include "sg_router.hpp"
 
@@ -1346,6 +1348,38 @@ static void back_geometry(int hidden, int n_ff, int& rows, int& lrow) {
   rows = r;
 }
 
+// ---- the allocation-free layer: scratch in a file-scope device array ------------
+// One 1 MiB array per GPU, held until the process ends; sg_moe_layer_noalloc
+// uses it as the layer workspace.  Its device address is looked up once per
+// device (hipGetSymbolAddress with that device current) and kept per device:
+// in host code `scratch` names a host-side stand-in, never the device memory.
+constexpr size_t kScratchBytes = size_t(1) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// the current device's address of `scratch`
+static int scratch_address(void** out, const char* nm) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(SG_ERR_HIP, "%s: hipGetDevice: %s", nm, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: device %d beyond %d", nm, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(SG_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", nm,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SG_OK;
+}
+
 }  // namespace sg
 
 using namespace sg;
@@ -1480,6 +1514,29 @@ int sg_moe_layer(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const*
   return sg_moe_layer_stages(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w, x,
                              logits, residual, out, idx, weight, workspace, workspace_bytes,
                              n_tokens, hidden, n_ff, n_expert, k, shared_w, 3, stream);
+}
+
+int sg_moe_layer_noalloc(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
+                         const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
+                         const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
+                         const float* sh_gate_w, const float* x, const float* logits,
+                         const float* residual, float* out, int* idx, float* weight,
+                         int n_tokens, int hidden, int n_ff, int n_expert, int k,
+                         float shared_w, void* stream) {
+  const char* nm = "sg_moe_layer_noalloc";
+  const size_t need = sg_moe_layer_workspace_bytes(n_tokens, hidden, n_ff, n_expert, k);
+  if (need > kScratchBytes)
+    return set_error(SG_ERR_UNSUPPORTED,
+                     "%s: this shape needs %zu B of workspace, more than the %zu B scratch "
+                     "(use sg_moe_layer with a caller workspace)",
+                     nm, need, kScratchBytes);
+  void* ws = nullptr;
+  if (int st = scratch_address(&ws, nm)) return st;
+  // nothing in the workspace has to start at zero: the front launch writes
+  // the plan, h and the gates that the back launch then reads
+  return sg_moe_layer_stages(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w, x,
+                             logits, residual, out, idx, weight, ws, kScratchBytes, n_tokens,
+                             hidden, n_ff, n_expert, k, shared_w, 3, stream);
 }
 
 }  // extern "C"
