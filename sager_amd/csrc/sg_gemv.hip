@@ -150,17 +150,18 @@ struct F16ResAddOut {
   }
 };
 
-template <typename Rows, typename Out>
-__global__ void __launch_bounds__(256) gemv1_kernel(Rows rows, const unsigned char* __restrict__ xq,
-                                                    Out out, int n_rows, int nb, int lpr,
-                                                    int gpw) {
-  __shared__ __attribute__((aligned(16))) uint32_t wbuf[kWaves][kBufWords];
+template <typename Rows, typename Out, int NWV>
+__global__ void __launch_bounds__(64 * NWV) gemv1_kernel(Rows rows,
+                                                         const unsigned char* __restrict__ xq,
+                                                         Out out, int n_rows, int nb, int lpr,
+                                                         int gpw) {
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[NWV][kBufWords];
   extern __shared__ __attribute__((aligned(16))) uint32_t xs_dyn[];  // nb * kXStride, table, results
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int rpw = 64 / lpr;
   const int n_groups = (n_rows + rpw - 1) / rpw;
-  const int NW = gridDim.x * kWaves;
-  const int g_begin = blockIdx.x * kWaves + wv, g_end = n_groups;
+  const int NW = gridDim.x * NWV;
+  const int g_begin = blockIdx.x * NWV + wv, g_end = n_groups;
   auto rows_of = [&](int gg) { return min(rpw, n_rows - gg * rpw); };
   // the first group's weights first: their HBM latency overlaps the staging
   if (g_begin < g_end) dma_rows(rows, g_begin * rpw, rows_of(g_begin), nb, wbuf[wv], lane);
@@ -290,20 +291,41 @@ static unsigned gemv_grid(long long n_groups) {
   return static_cast<unsigned>(wgs < cap ? (wgs > 0 ? wgs : 1) : cap);
 }
 
-// gemv1_kernel's launch: grid, contiguous groups per wave and the LDS its
-// per-wave results take
+// gemv1_kernel's launch: waves per workgroup, grid, groups per wave and the
+// LDS its per-wave results take.  A matrix of fewer row groups than four per
+// CU (config 1's 2048 x 2048 is 256 groups) runs one wave per workgroup, one
+// group each, so its waves spread over every CU instead of a quarter of them.
 struct Gemv1Launch {
+  int nwv;
   unsigned grid;
   int gpw;
   size_t res_bytes;
 };
 static Gemv1Launch gemv1_launch(long long n_groups, int rpw) {
   Gemv1Launch l{};
-  l.grid = gemv_grid(n_groups);
-  const long long waves = static_cast<long long>(l.grid) * kWaves;
+  if (n_groups < 256LL * kWaves) {
+    l.nwv = 1;
+    l.grid = static_cast<unsigned>(n_groups > 0 ? n_groups : 1);
+  } else {
+    l.nwv = kWaves;
+    l.grid = gemv_grid(n_groups);
+  }
+  const long long waves = static_cast<long long>(l.grid) * l.nwv;
   l.gpw = static_cast<int>((n_groups + waves - 1) / waves);
-  l.res_bytes = static_cast<size_t>(kWaves) * l.gpw * rpw * 4;
+  l.res_bytes = static_cast<size_t>(l.nwv) * l.gpw * rpw * 4;
   return l;
+}
+
+template <typename Rows, typename Out>
+static void gemv1_go(const Gemv1Launch& L, size_t lds, hipStream_t s, Rows rows,
+                     const sg_block_q8k* x, Out out, int n_rows, int nb, int lpr) {
+  const unsigned char* xb = reinterpret_cast<const unsigned char*>(x);
+  if (L.nwv == 1)
+    hipLaunchKernelGGL((gemv1_kernel<Rows, Out, 1>), dim3(L.grid), dim3(64), lds, s, rows, xb, out,
+                       n_rows, nb, lpr, L.gpw);
+  else
+    hipLaunchKernelGGL((gemv1_kernel<Rows, Out, kWaves>), dim3(L.grid), dim3(64 * kWaves), lds, s,
+                       rows, xb, out, n_rows, nb, lpr, L.gpw);
 }
 
 static int check_gemv_geometry(const char* name, int n_rows, int k) {
@@ -328,8 +350,7 @@ static int launch_gemv1(Rows rows, const sg_block_q8k* x, Out out, int n_rows, i
   if (lds > 96 * 1024)
     return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows=%d k=%d needs %zu B of LDS", nm, n_rows, k,
                      lds);
-  hipLaunchKernelGGL((gemv1_kernel<Rows, Out>), dim3(L.grid), dim3(256), lds, s, rows,
-                     reinterpret_cast<const unsigned char*>(x), out, n_rows, nb, lpr, L.gpw);
+  gemv1_go(L, lds, s, rows, x, out, n_rows, nb, lpr);
   return check_launch(nm);
 }
 
@@ -350,10 +371,10 @@ static int launch_ptrs(const sg_block_q4k* const* ptrs, const sg_block_q8k* x, O
   if (lds > 96 * 1024)
     return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows=%d k=%d needs %zu B of LDS", nm, n_rows, k,
                      lds);
-  hipLaunchKernelGGL((gemv1_kernel<TableRows, Out>), dim3(L.grid), dim3(256), lds, s,
-                     TableRows{ptrs, rows_per, nb, n_ptrs,
-                               (rows_per & (rows_per - 1)) == 0 ? __builtin_ctz(rows_per) : -1},
-                     reinterpret_cast<const unsigned char*>(x), y, n_rows, nb, lpr, L.gpw);
+  gemv1_go(L, lds, s,
+           TableRows{ptrs, rows_per, nb, n_ptrs,
+                     (rows_per & (rows_per - 1)) == 0 ? __builtin_ctz(rows_per) : -1},
+           x, y, n_rows, nb, lpr);
   return check_launch(nm);
 }
 
@@ -386,19 +407,10 @@ extern "C" {
 
 int sg_gemv_q4_k_q8(const sg_block_q4k* w, const sg_block_q8k* x, float* y, int n_rows, int k,
                     void* stream) {
-  if (!w || !x || !y) return set_error(SG_ERR_INVALID_ARGUMENT, "sg_gemv_q4_k_q8: null pointer");
-  if (int st = check_gemv_geometry("sg_gemv_q4_k_q8", n_rows, k)) return st;
-  const int nb = k / kQK, lpr = lanes_per_row(nb);
-  const long long n_groups = (n_rows + (64 / lpr) - 1) / (64 / lpr);
-  const Gemv1Launch L = gemv1_launch(n_groups, 64 / lpr);
-  const size_t lds = static_cast<size_t>(nb) * kXStride * 4 + L.res_bytes;
-  if (lds > 96 * 1024)
-    return set_error(SG_ERR_UNSUPPORTED, "sg_gemv_q4_k_q8: n_rows=%d k=%d needs %zu B of LDS",
-                     n_rows, k, lds);
-  hipLaunchKernelGGL((gemv1_kernel<PlainRows, F32Out>), dim3(L.grid), dim3(256), lds,
-                     static_cast<hipStream_t>(stream), PlainRows{w, nb},
-                     reinterpret_cast<const unsigned char*>(x), F32Out{y}, n_rows, nb, lpr, L.gpw);
-  return check_launch("sg_gemv_q4_k_q8");
+  const char* nm = "sg_gemv_q4_k_q8";
+  if (!w || !x || !y) return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  return launch_gemv1(PlainRows{w, k / kQK}, x, F32Out{y}, n_rows, k,
+                      static_cast<hipStream_t>(stream), nm);
 }
 
 int sg_gemv_ptrs_q4_k_q8(const sg_block_q4k* const* ptrs, const sg_block_q8k* x, float* y,

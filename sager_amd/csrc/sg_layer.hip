@@ -34,6 +34,32 @@
 
 namespace sg {
 
+// ---- latency timeline (built only with -DSG_TIMELINE; no code otherwise) ----
+// mark(kernel, slot) stores the 100 MHz real-time counter for the calling
+// wave into tl_stamps: front waves at ((wg * 4 + wave) * 16 + slot), back
+// waves from kTlBack on.  sg_debug_timeline() copies and clears it.
+#ifdef SG_TIMELINE
+constexpr int kTlBack = 1 << 15;
+static __device__ unsigned long long tl_stamps[2 * kTlBack];
+__device__ __forceinline__ void tl_mark(int base, int waves, int slot) {
+  const int wg = blockIdx.y * gridDim.x + blockIdx.x;
+  const int i = base + (wg * waves + (threadIdx.x >> 6)) * 16 + slot;
+  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+  if ((threadIdx.x & 63) == 0 && i < base + kTlBack) tl_stamps[i] = t;
+  if (slot == 0 && (threadIdx.x & 63) == 0 && i + 15 < base + kTlBack) {
+    // slot 15: the XCC (bits 0-3 of HW_REG_XCC_ID) and the CU (HW_ID)
+    const unsigned xcc = __builtin_amdgcn_s_getreg((15 << 11) | 20);
+    const unsigned hwid = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+    tl_stamps[i + 15] = (static_cast<unsigned long long>(hwid) << 32) | xcc | (1ull << 62);
+  }
+}
+#define SG_MARK_FRONT(slot) tl_mark(0, 4, slot)
+#define SG_MARK_BACK(slot) tl_mark(kTlBack, 8, slot)
+#else
+#define SG_MARK_FRONT(slot) ((void)0)
+#define SG_MARK_BACK(slot) ((void)0)
+#endif
+
 constexpr int kLMaxExperts = 1024;
 constexpr int kLMaxK = 32;
 constexpr int kLMaxTokens = 16;
@@ -572,6 +598,38 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return v;
 }
 
+// Whether the exact routing of one token (route_wave) is sure to select the
+// logit-order ids top[0..k) in that order, decided by one wave from the
+// k+1 leading logits alone, without the normalizer: every logit finite
+// (so z = sum e lies in [1, E], nothing degenerates), and along the logit
+// order each e_j = exp(l_j - max) either equals its successor's logit
+// (tie: index order on both sides) or exceeds the successor's e by more
+// than 2^-20 relative with the successor >= 2^-100 (the boundary pair k-1,
+// k always strictly).  Then p_j = e_j / z > p_{j+1} for any z in [1, E]:
+// the quotients are normal and more than two floats apart, so route_wave's
+// check (p strictly decreasing or equal logits) passes.  A false result
+// only means "run route_wave".  Wave-uniform.
+__device__ __forceinline__ bool route_is_logit_order(const LayerArgs& a, const uint32_t* dyn,
+                                                     const FrontLds& L, int lane) {
+  const int E = a.n_expert, k = a.k, m = L.m;
+  const float* lv = reinterpret_cast<const float*>(dyn + L.lv);
+  const uint64_t* top = reinterpret_cast<const uint64_t*>(dyn + L.top);
+  bool fin = true;
+  for (int i = lane; i < E; i += 64) fin &= __builtin_isfinite(lv[i]);
+  const int ik = lane < m && top[lane] != 0ull ? sel_idx(top[lane]) : -1;
+  const float lk = ik >= 0 ? lv[ik] : 0.f;
+  const float mx = readlane_f(lk, 0);
+  const float ek = expf_sg(lk - mx);
+  const float en = __shfl(ek, lane + 1, 64);
+  const float ln = __shfl(lk, lane + 1, 64);
+  const int in = __shfl(ik, lane + 1, 64);
+  const bool gap = ek > en * 1.0000019073486328f && en >= 7.8886090522101181e-31f;  // 2^-19, 2^-100
+  bool ok = true;
+  if (lane + 1 < k) ok = ik >= 0 && in >= 0 && (lk == ln || gap);
+  else if (lane + 1 == k && E > k) ok = ik >= 0 && in >= 0 && gap;
+  return __ballot(!(ok && fin)) == 0ull;
+}
+
 // Exact routing of ONE token by one wave, no workgroup barrier (moe.cu:25-85):
 // same arithmetic and checks as exact_route below.  Logits come from lv[]
 // (LDS, filled by spec_select), lane l holds experts l + 64j.  Writes ridx,
@@ -656,6 +714,104 @@ __device__ __forceinline__ void route_wave(const LayerArgs& a, uint32_t* dyn, co
   }
 }
 
+// Exact routing of ONE token by the whole workgroup straight from the
+// logits (moe.cu:25-85), for the publisher: max, one exp per expert per
+// thread, the normalizer summed serially in index order, then the top k of
+// the probability keys (value desc, index asc: the reference's k rounds of
+// first-strict-max) by team_select; a degenerate row (NaN, empty
+// normalizer) takes kk % E with weight -1.  Weights renormalized by their
+// k-order sum.  Writes ridx[0..k), rw[0..k] and the one-token plan; ends
+// with a barrier.
+template <int EPT>
+__device__ __forceinline__ void route_direct_t1(const LayerArgs& a, uint32_t* dyn, const FrontLds& L,
+                                                const float* lr, int tid) {
+  const int E = a.n_expert, k = a.k;
+  const int lane = tid & 63, wave = tid >> 6;
+  float* ev = reinterpret_cast<float*>(dyn + L.ev);
+  uint64_t* cand = reinterpret_cast<uint64_t*>(dyn + L.cand);
+  uint64_t* top = reinterpret_cast<uint64_t*>(dyn + L.top);
+  float* red = reinterpret_cast<float*>(dyn + L.red);
+  float* zs = reinterpret_cast<float*>(dyn + L.zs);
+  int* ridx = reinterpret_cast<int*>(dyn + L.ridx);
+  float* rw = reinterpret_cast<float*>(dyn + L.rw);
+  float mx = -1e30f;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j)
+    if (j < L.ept && tid + L.TT * j < E) mx = fmaxf(mx, lr[j]);
+  mx = team_max(mx, red, wave, L.tw, lane);
+  SG_MARK_FRONT(9);
+  float e[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tid + L.TT * j;
+    e[j] = (j < L.ept && i < E) ? expf_sg(lr[j] - mx) : 0.f;
+    if (j < L.ept && i < L.e32) ev[i] = e[j];
+  }
+  bar();
+  SG_MARK_FRONT(10);
+  if (tid == 0) zs[0] = serial_sum(ev, L.e32);
+  bar();
+  SG_MARK_FRONT(11);
+  const float z = zs[0];
+  const bool degen = !(z == z) || z == 0.f;
+  if (!degen) {
+    uint64_t kr[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int i = tid + L.TT * j;
+      kr[j] = (j < L.ept && i < E) ? sel_key(e[j] / z, i) : 0ull;
+    }
+    team_select<EPT>(L, kr, cand, top, tid);
+  }
+  SG_MARK_FRONT(12);
+  if (wave == 0) {
+    int fi = 0;
+    float pv = -1.f;
+    if (lane < k) {
+      fi = degen ? lane % E : (top[lane] ? sel_idx(top[lane]) : 0);
+      if (!degen) pv = ev[fi] / z;
+    }
+    float wsum = 0.f;
+    for (int kk = 0; kk < k; ++kk) wsum += readlane_f(pv, kk);
+    const float wv = wsum > 0.f ? pv / wsum : pv;
+    if (lane < k) {
+      ridx[lane] = fi;
+      rw[lane] = wv;
+    }
+    if (lane == 0) rw[k] = a.shared_w;
+    // the plan straight from the ids in registers (distinct and valid: k
+    // of E distinct keys, or kk % E with k <= E), as plan_t1 builds it
+    int* re = reinterpret_cast<int*>(dyn + L.re);
+    int* poff = reinterpret_cast<int*>(dyn + L.poff);
+    int* pexp = reinterpret_cast<int*>(dyn + L.pexp);
+    int* ptok = reinterpret_cast<int*>(dyn + L.ptok);
+    int* pslot = reinterpret_cast<int*>(dyn + L.pslot);
+    int* ctrl = reinterpret_cast<int*>(dyn + L.ctrl);
+    const int gbase = a.has_shared, ebase = a.has_shared ? 1 : 0;
+    int r = 0;
+    for (int j = 0; j < k; ++j) r += __builtin_amdgcn_readlane(fi, j) < fi;
+    if (lane < k) {
+      re[lane] = fi;
+      poff[gbase + r] = ebase + r;
+      pexp[gbase + r] = fi;
+      ptok[ebase + r] = 0;
+      pslot[ebase + r] = lane;
+    }
+    if (lane == 0) {
+      if (a.has_shared) {
+        poff[0] = 0;
+        pexp[0] = -1;
+        ptok[0] = 0;
+        pslot[0] = k;
+      }
+      poff[gbase + k] = ebase + k;
+      ctrl[0] = k;
+      ctrl[1] = k;
+    }
+  }
+  bar();
+}
+
 // Exact routing of every token (moe.cu:25-85): max, exp, the normalizer
 // summed serially in index order, p = e / z.  p is a monotone function of
 // the logit, so the logit order (spec[]) is the probability order unless two
@@ -701,14 +857,17 @@ __device__ __forceinline__ void exact_route(const LayerArgs& a, uint32_t* dyn, c
     for (int j = 0; j < EPT; ++j)
       if (j < L.ept && tt + L.TT * j < E && ok) mx = fmaxf(mx, lr[j]);
     mx = team_max(mx, red, wit, tw, lane);
+    SG_MARK_FRONT(9);
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
       const int i = tt + L.TT * j;
       if (j < L.ept && i < L.e32) ev[i] = (ok && i < E) ? expf_sg(lr[j] - mx) : 0.f;
     }
     bar();
+    SG_MARK_FRONT(10);
     if (tt == 0) zs[team] = serial_sum(ev, L.e32);
     bar();
+    SG_MARK_FRONT(11);
     const float z = zs[team];
     const bool degen = !(z == z) || z == 0.f;
     bool fast = false;
@@ -784,6 +943,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   const int nbh = NBH ? NBH : a.hidden / kQK, lpr = NBH ? pow2_ceil(NBH) : pow2_ceil(nbh);
   const bool publisher = g == a.gmax;
   if (publisher && bx != 0) return;  // one publisher per launch
+  SG_MARK_FRONT(0);
   const bool shared_grp = a.has_shared && g == 0;
   // the first routing pass's logits are the head of the routing chain:
   // issued before anything else
@@ -806,11 +966,13 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
 
   if (shared_grp) {
     if (nrw > 0) dma_gateup(a.sh_gate, a.sh_up, row0, nrw, nbh, buf, lane);
+    SG_MARK_FRONT(3);
     quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);
     bar();
     // entries: tokens 0..T-1 in slot k, no plan needed
     gateup_wave(true, row0, nrw, nbh, lpr, buf, xs,
                 [&](int j, int& t, int& sl) { t = j; sl = k; }, T, stride, a.n_ff, a.h, lane);
+    SG_MARK_FRONT(6);
     if (a.sh_gate_w && bx == 0) {
       // the shared expert's scalar gate of every token (session.cpp:2904-2909):
       // one token per 32-lane half-wave, the result read by the back kernel
@@ -837,8 +999,19 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   const int* ptok = reinterpret_cast<const int*>(dyn + L.ptok);
   const int* pslot = reinterpret_cast<const int*>(dyn + L.pslot);
 
-  // expert pointer tables into LDS (gate and up; down for the publisher)
-  if (wave < 2 || (wave == 2 && publisher)) {
+  // expert pointer tables into LDS (gate and up; down for the publisher).
+  // The publisher's down table goes through registers when E <= 256: it is
+  // written to LDS only when publishing, long after it landed, so no LDS
+  // access of wave 2 waits for it meanwhile.
+  const bool tabd_regs = publisher && E <= 256;
+  unsigned long long tdv[4];
+  if (tabd_regs && wave == 2) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      tdv[j] = lane + 64 * j < E ? reinterpret_cast<unsigned long long>(a.tab_down[lane + 64 * j])
+                                 : 0ull;
+  }
+  if (wave < 2 || (wave == 2 && publisher && !tabd_regs)) {
     const sg_block_q4k* const* tab = wave == 0 ? a.tab_gate : (wave == 1 ? a.tab_up : a.tab_down);
     uint32_t* dst = dyn + (wave == 0 ? L.tabg : (wave == 1 ? L.tabu : L.tabd));
     const char* src = reinterpret_cast<const char*>(tab);
@@ -864,10 +1037,21 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   int e_mine = -1, slot_mine = -1;
   bool present_mine = false;
   int n_groups;
-  if (a.logits) {
+  if (a.logits && publisher && T == 1) {
+    // the publisher routes exactly from the logits with every wave; it has
+    // no stream to start and needs the weights, not the logit order
+#ifdef SG_TL_TWICE
+    route_direct_t1<EPT>(a, dyn, L, lr, tid);  // and the plan
+    SG_MARK_FRONT(13);
+#endif
+    route_direct_t1<EPT>(a, dyn, L, lr, tid);  // and the plan
+    SG_MARK_FRONT(7);
+    n_groups = gbase + ctrl[1];
+  } else if (a.logits) {
     // waves 0-1 wait for the pointer tables inside the selection, so they
     // are readable when it returns
     spec_select<EPT>(a, dyn, L, lr, tid, wave < 2);
+    SG_MARK_FRONT(2);
     bool streamed = false, routed = false;
     if (T == 1) {
       // top[] of the single token is readable now: with k valid ids the
@@ -893,15 +1077,27 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
           if (wave < 3) stream_rows(e_mine, 3, wave, 3);
           if (wave == 3 && e_mine >= 0) present_mine = tabg[e_mine] != 0ull && tabu[e_mine] != 0ull;
           streamed = true;
+          SG_MARK_FRONT(3);
         }
         // wave 3 routes exactly now (it reads top[] and lv[], complete since
         // the selection's last barrier) and writes ridx[] itself; the plan
         // is published by the barrier after the x quantization below.
         // wave 2 (the one with the fewest x blocks to quantize) writes the
         // plan, its lanes in the roles of threads 0..63
-        if (wave == 3) route_wave<4 * EPT>(a, dyn, L, lane);
-        if (wave == 2)
+        // (a compute workgroup skips it when the logit order is provably
+        // the exact one: only the publisher needs the weights; the
+        // publisher routes with all four waves below)
+        if (wave == 3 && !publisher) {
+          if (route_is_logit_order(a, dyn, L, lane)) {
+            if (lane == 0) ctrl[3] = 0;
+          } else {
+            route_wave<4 * EPT>(a, dyn, L, lane);
+          }
+        }
+        if (wave == 2) {
           plan_t1(dyn, L, k, a.has_shared, lane, [&](int j) { return sel_idx(top[j]); }, false);
+          if (publisher && lane < k) ridx[lane] = sel_idx(top[lane]);  // what exact_route compares
+        }
         routed = true;
       } else {
         if (tid < k) ridx[tid] = top[tid] ? sel_idx(top[tid]) : -1;
@@ -926,19 +1122,27 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
         stream_rows(e_mine, 3, wave, 3);
       }
     }
-    if (t1w) {
+    if (t1w && publisher) {
+      // no weight stream to overlap: the whole workgroup routes exactly (one
+      // exp per thread instead of four per lane of one wave)
+      exact_route<EPT>(a, dyn, L, lr, tid);
+      SG_MARK_FRONT(7);
+    } else if (t1w) {
       if (wave == 3) {
         if (!routed) route_wave<4 * EPT>(a, dyn, L, lane);
-      } else if (!publisher) {
+      } else {
         quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);  // overlaps the weight stream
         wait_vm();  // this wave's share of wave 3's rows
       }
+      SG_MARK_FRONT(4);
       bar();
+      SG_MARK_FRONT(5);
     } else {
       exact_route<EPT>(a, dyn, L, lr, tid);
     }
     const bool moved = ctrl[3] != 0;  // the exact routing changed an id
     if (moved) make_plan(dyn, L, T, k, E, a.has_shared, tid);
+    SG_MARK_FRONT(8);
     if (streamed && !moved) {
       // one token, routing as the logits ordered it: this group's expert,
       // presence and single entry (token 0, slot_mine) are known already
@@ -949,6 +1153,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
       gateup_wave(present_mine, row0, nrw, nbh, lpr, buf, xs,
                   [&](int, int& t, int& sl) { t = 0; sl = slot_mine; }, 1, stride, a.n_ff, a.h,
                   lane);
+      SG_MARK_FRONT(6);
       return;
     }
     n_groups = gbase + ctrl[1];
@@ -977,8 +1182,15 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
 
   if (publisher) {
     // publish idx, weight, plan and down pointers
+    if (tabd_regs && wave == 2) {
+      unsigned long long* td = reinterpret_cast<unsigned long long*>(dyn + L.tabd);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (lane + 64 * j < E) td[lane + 64 * j] = tdv[j];
+    }
     wait_vm();  // pointer tables
     bar();
+    SG_MARK_FRONT(5);
     const int* re = reinterpret_cast<const int*>(dyn + L.re);
     const int nv = ctrl[0];
     for (int t = tid; t < T; t += 256) {
@@ -1008,6 +1220,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
       a.plan.meta[1] = a.has_shared;
       a.plan.meta[2] = nv;
     }
+    SG_MARK_FRONT(6);
     return;
   }
   if (g >= n_groups) {
@@ -1163,6 +1376,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
               (lds_void_p)(buf + 256 * i), 16, 0, 0);
       }
     }
+    SG_MARK_BACK(2);
     if (gb == 0) {  // Q8_K of every (token, slot) h row while the rows stream in
       // blocks e = wave + 8j: j < kBackHSlots from registers in one
       // interleaved pass (every block of a one-token layer with k <= 8),
@@ -1193,10 +1407,12 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
         }
         quantize_n_lds<4>(v, dst, n, lane);
       }
+      SG_MARK_BACK(3);
       if (spread) wait_vm();  // this wave's share of the copies
       bar();
     }
     wait_vm();
+    SG_MARK_BACK(4);
     const int gq = gb + wave * gpw + q;
     const bool has = gq < G && wave < nbw;
     const bool present = has && wdown[gq] != 0ull;
@@ -1229,6 +1445,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
     }
     wait_lds();
   }
+  SG_MARK_BACK(5);
   bar();
   // out = residual + sum over slots 0..k of fma(w, y) in slot order.  A slot
   // whose id was invalid (bounds-killed), whose expert is absent, or the
@@ -1257,6 +1474,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
     }
     a.out[o] = acc;
   }
+  SG_MARK_BACK(6);
 }
 
 // residual of the first combine pass (qo = tid), loaded early
@@ -1285,6 +1503,7 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs a) {
   float* ys = reinterpret_cast<float*>(dyn + L.ys);
   const int row0 = blockIdx.x * rows;
   const int nr = max(0, min(rows, a.hidden - row0));
+  SG_MARK_BACK(0);
 
   // loads that do not depend on the plan: this wave's first kBackHSlots h
   // blocks (block wave + 8j of the (token, slot) rows) and the residual
@@ -1337,6 +1556,7 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs a) {
   }
   for (int i = tid; i < T * stride * rows; i += kBackThreads) ys[i] = 0.f;
   bar();
+  SG_MARK_BACK(1);
   uint32_t(*wbuf)[64 * 36] = reinterpret_cast<uint32_t(*)[64 * 36]>(dyn + L.total);
   back_core<NBF, ROWS>(a, L, dyn, wbuf, row0, nr, res0, hpre);
 }
@@ -1538,5 +1758,16 @@ int sg_moe_layer_noalloc(const sg_block_q4k* const* tab_gate, const sg_block_q4k
                              logits, residual, out, idx, weight, ws, kScratchBytes, n_tokens,
                              hidden, n_ff, n_expert, k, shared_w, 3, stream);
 }
+
+#ifdef SG_TIMELINE
+// copy the timeline stamps (2 * 32768 words) to host memory and clear them
+int sg_debug_timeline(unsigned long long* host) {
+  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(tl_stamps), sizeof(tl_stamps)) != hipSuccess)
+    return SG_ERR_HIP;
+  static unsigned long long zeros[2 * kTlBack];
+  return hipMemcpyToSymbol(HIP_SYMBOL(tl_stamps), zeros, sizeof(zeros)) == hipSuccess ? SG_OK
+                                                                                      : SG_ERR_HIP;
+}
+#endif
 
 }  // extern "C"

@@ -13,7 +13,8 @@
 namespace sg {
 
 __device__ __forceinline__ uint64_t sel_key(float v, int i) {
-  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  // -0 keys as +0: the two compare equal, so the lower index goes first
+  const uint32_t b = v == 0.f ? 0u : __builtin_bit_cast(uint32_t, v);
   const uint32_t o = (v != v) ? 0u : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
   return (static_cast<uint64_t>(o) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
 }

@@ -393,6 +393,43 @@ def test_moe_layer_routing_edge_cases(T):
     np.testing.assert_array_equal(host(out).view(np.uint32), ref.view(np.uint32))
 
 
+def _t1_edge_rows(E, K):
+    rng = np.random.default_rng(4711)
+    rows = []
+    base = rng.normal(0, 1, E).astype(np.float32)
+    o = np.argsort(-base, kind="stable")
+    r = base.copy(); r[o[3]] = r[o[2]]; rows.append(r)              # interior tie
+    r = base.copy(); r[o[K]] = r[o[K - 1]]; rows.append(r)          # tie across the boundary
+    r = np.zeros(E, np.float32) - 3.0
+    r[[2, 5, 11]] = [0.0, -0.0, 0.0]; r[[1, 30]] = [-0.0, 0.0]      # signed zeros at the top
+    rows.append(r)
+    r = base.copy(); r[[0, 6]] = -np.inf; rows.append(r)            # -inf: not all finite
+    r = base.copy(); r[9] = np.nan; rows.append(r)                  # degenerate
+    r = base.copy(); r[o[1]] = np.nextafter(r[o[0]], np.float32(-9.0)); rows.append(r)  # 1 ulp apart
+    r = base.copy(); r[o[K]] = r[o[K - 1]] - np.float32(2e-6); rows.append(r)   # near the margin
+    r = (base * 40.0).astype(np.float32); rows.append(r)           # tiny tail probabilities
+    return rows
+
+
+def test_moe_layer_t1_routing_edge_cases():
+    """One token: rows where the logit-order shortcut of the compute
+    workgroups must hold or must hand over to the exact routing - ties inside
+    and across the top-k boundary, signed zeros, -inf, NaN, logits one ulp
+    apart, a gap near the shortcut's margin, very small probabilities."""
+    H, F, E, K = 512, 256, 64, 8
+    rng = np.random.default_rng(61)
+    g, u, d = _expert_pool(rng, E + 1, H, F)
+    shared = (g.pop(), u.pop(), d.pop())
+    layer = _layer(g, u, d, shared, H, F, K, 1)
+    x = rng.normal(0, 1, (1, H)).astype(np.float32)
+    for lg in _t1_edge_rows(E, K):
+        out, idx, w = layer.forward(dev(x), dev(lg[None]))
+        ref, ri, rw = orc.moe_layer(g, u, d, shared, x, logits=lg[None], hidden=H, n_ff=F, k=K)
+        np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K])
+        np.testing.assert_array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+        np.testing.assert_array_equal(host(out).view(np.uint32), ref.view(np.uint32))
+
+
 def _collision_logits(E, K, seed):
     """Search (on the oracle) for a logit row where two distinct logits, one
     float ulp apart, give the same probability, so the probability order
