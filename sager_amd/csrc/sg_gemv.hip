@@ -292,9 +292,9 @@ static unsigned gemv_grid(long long n_groups) {
 }
 
 // gemv1_kernel's launch: waves per workgroup, grid, groups per wave and the
-// LDS its per-wave results take.  A matrix of fewer row groups than four per
-// CU (config 1's 2048 x 2048 is 256 groups) runs one wave per workgroup, one
-// group each, so its waves spread over every CU instead of a quarter of them.
+// LDS its per-wave results take.  (One wave per workgroup over more CUs was
+// measured slower on the 2048 x 2048 matrix: each workgroup stages x again,
+// with a quarter of the threads.)
 struct Gemv1Launch {
   int nwv;
   unsigned grid;
@@ -303,13 +303,8 @@ struct Gemv1Launch {
 };
 static Gemv1Launch gemv1_launch(long long n_groups, int rpw) {
   Gemv1Launch l{};
-  if (n_groups < 256LL * kWaves) {
-    l.nwv = 1;
-    l.grid = static_cast<unsigned>(n_groups > 0 ? n_groups : 1);
-  } else {
-    l.nwv = kWaves;
-    l.grid = gemv_grid(n_groups);
-  }
+  l.nwv = kWaves;
+  l.grid = gemv_grid(n_groups);
   const long long waves = static_cast<long long>(l.grid) * l.nwv;
   l.gpw = static_cast<int>((n_groups + waves - 1) / waves);
   l.res_bytes = static_cast<size_t>(l.nwv) * l.gpw * rpw * 4;
