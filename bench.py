@@ -61,6 +61,32 @@ def make_layers(torch, ops, pool, max_tokens=1):
     return layers
 
 
+def capture(torch, fn):
+    """Capture fn() into a HIP graph on a side stream; returns (graph, stream)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            fn()
+    torch.cuda.synchronize()
+    return g, s
+
+
+def replay_ms(torch, g, s):
+    """One replay of graph g, bracketed by synchronization, timed with events on
+    its stream; ms."""
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
+
+
 def time_graph(torch, fn, reps):
     """Capture fn() once into a HIP graph, replay `reps` times; return ms per
     replay measured with events on the replay stream."""
@@ -109,17 +135,40 @@ def cpu_baseline(pool_l0, xs, lgs, budget_s=8.0):
             outs.append(out[0])
         i += 1
     med = statistics.median(times[2:] if len(times) > 4 else times)
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    model = cpu_model()
     return {"value": round(med * 1e6, 1), "unit": "us/token", "cores": nthreads, "kind": "port",
             "sample": f"{len(times)} MoE-layer decode steps of config 2 (layer 0, seeded x/logits), "
                       f"median; nproc={os.cpu_count()}, cpu={model}"}, outs
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_gemv_baseline(orc, mats, xq, budget_s=3.0):
+    """Config 1 on the host: the AVX2 oracle GEMV (restating
+    gemv_q4_k_q8_avx2, q4_avx2.cpp:124-145, single-threaded per call as the
+    reference's is) over distinct 2048 x 2048 matrices, median time."""
+    times = []
+    t_end = time.time() + budget_s
+    i = 0
+    while (time.time() < t_end or len(times) < 20) and len(times) < 2000:
+        t0 = time.perf_counter()
+        orc.gemv(mats[i % len(mats)], xq, 2048, 2048)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    med = statistics.median(times)
+    b = 2048 * 8 * 144 + 8 * 276 + 2048 * 4
+    return {"value": round(b / med / 1e9, 2), "unit": "GB/s", "us": round(med * 1e6, 1),
+            "cores": 1, "kind": "port",
+            "sample": f"{len(times)} GEMVs over {len(mats)} distinct matrices, median; "
+                      f"nproc={os.cpu_count()}, cpu={cpu_model()}"}
 
 
 def run_config5(torch, np, ops, gen, orc, q4k_random_dev, reps=10):
@@ -194,11 +243,13 @@ def run_q6_head(torch, np, ops, gen, orc, head_rows, xq):
     return out
 
 
-def traffic_run(torch, np, layers, n_steps=32):
+def traffic_run(torch, np, ops, gen, layers, n_steps=32):
     """Dispatches for the HBM-traffic passes: a plain 256 MiB device copy
     (the scale reference: it reads and writes exactly 256 MiB), then n_steps
     config-2 decode steps on rotated layers as separate front and back
-    launches."""
+    launches, 32 config-1 GEMVs on distinct 2048 x 2048 matrices, and one
+    config-5 prefill chunk (2048 tokens)."""
+    from sager_amd.synth import q4k_random_dev
     src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(4):
@@ -214,8 +265,149 @@ def traffic_run(torch, np, layers, n_steps=32):
             layers[i % N_LAYERS].forward(xs[i:i + 1], lgs[i:i + 1], out=out[i:i + 1],
                                          idx=idx[i:i + 1], weight=wgt[i:i + 1], stages=st)
     torch.cuda.synchronize()
+    gw = q4k_random_dev(32 * 2048 * 8, gen).view(32, 2048 * 8, 144)
+    xq = ops.quantize_q8_k(torch.randn((1, 2048), device="cuda", generator=gen))
+    ys = torch.empty((32, 2048), dtype=torch.float32, device="cuda")
+    for j in range(32):
+        ops.gemv_q4_k_q8(gw[j], xq, 2048, 2048, y=ys[j])
+    torch.cuda.synchronize()
+    del gw
+    T5 = 2048
+    pool5 = torch.empty((3, E, F * H // 256, 144), dtype=torch.uint8, device="cuda")
+    q4k_random_dev(3 * E * F * H // 256, gen, out=pool5.view(-1, 144))
+    tabs5 = [torch.tensor([pool5[m, e].data_ptr() for e in range(E)], dtype=torch.int64,
+                          device="cuda") for m in range(3)]
+    pre = ops.MoePrefill(*tabs5, None, hidden=H, n_ff=F, n_expert=E, k=K, max_tokens=T5)
+    rng5 = np.random.default_rng(5)
+    x5 = torch.from_numpy(rng5.normal(0, 1, (T5, H)).astype(np.float32)).cuda()
+    l5 = torch.from_numpy(rng5.uniform(0, 1, (T5, E)).astype(np.float32)).cuda()
+    pre.forward(x5, l5)
+    torch.cuda.synchronize()
     print(json.dumps({"traffic_run": {"copy_bytes": 2 * src.numel() * 4, "steps": n_steps}}),
           flush=True)
+    return 0
+
+
+def source_hash():
+    """sha256 of the kernel sources (sager_amd/csrc), to tie a committed
+    counter summary to the build it describes."""
+    import hashlib
+    h = hashlib.sha256()
+    d = os.path.join(ROOT, "sager_amd", "csrc")
+    for f in sorted(os.listdir(d)):
+        h.update(f.encode())
+        with open(os.path.join(d, f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+# algorithmic HBM bytes per dispatch of the kernels the traffic run launches
+T5_ROUTES = 2048 * K
+TRAFFIC_KERNELS = {
+    # substring of the kernel name -> (label, algorithmic bytes)
+    "layer_front_kernel": ("decode front (config 2)", 9 * 2 * MAT_BYTES + H * 4 + E * 4 + 9 * F * 4),
+    "layer_back_kernel": ("decode back (config 2)",
+                          9 * MAT_BYTES + 9 * F * 4 + 2 * 9 * H * 4 + H * 4),
+    "gemv1_kernel<sg::PlainRows, sg::F32Out": ("GEMV 2048x2048 (config 1)",
+                                               2048 * 8 * 144 + 8 * 276 + 2048 * 4),
+    "grouped_mfma_kernel<true>": ("prefill gate/up + SiLU (config 5)",
+                                  E * 2 * MAT_BYTES + 2048 * 8 * 276 + T5_ROUTES * F * 4),
+    "grouped_mfma_kernel<false>": ("prefill down (config 5)",
+                                   E * MAT_BYTES + T5_ROUTES * 2 * 276 + T5_ROUTES * H * 4),
+    "prefill_combine_kernel": ("prefill combine (config 5)",
+                               T5_ROUTES * H * 4 + 2048 * H * 4),
+}
+
+
+def traffic_summary(fetch_csv, write_csv):
+    """Turn the two counter passes over `bench.py --only traffic` (FETCH_SIZE,
+    then WRITE_SIZE, KiB per dispatch) into profiles/traffic_kernels.{json,md}:
+    each counter scaled by what it reads for the plain 256 MiB copy."""
+    import csv
+    def load(path, counter):
+        rows = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            rows.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return rows
+    fe, wr = load(fetch_csv, "FETCH_SIZE"), load(write_csv, "WRITE_SIZE")
+    copy_kib = (64 << 20) * 4 / 1024
+    def copy_med(rows):
+        v = [x for n, xs in rows.items() if "copyBuffer" in n for x in xs if x > copy_kib / 4]
+        return statistics.median(v[-4:])
+    f_scale, w_scale = copy_kib / copy_med(fe), copy_kib / copy_med(wr)
+    out = {"workload": "bench.py --only traffic: 32 config-2 decode steps (front and back "
+                       "launches) on 16 rotated layers, 32 config-1 GEMVs on distinct "
+                       "matrices, one config-5 prefill chunk",
+           "source_hash": source_hash(),
+           "copy_reference": {"bytes_each_way": (64 << 20) * 4,
+                              "fetch_kib_median": copy_med(fe), "write_kib_median": copy_med(wr),
+                              "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)},
+           "kernels": {}}
+    for key, (label, alg) in TRAFFIC_KERNELS.items():
+        fv = [x for n, xs in fe.items() if key in n for x in xs]
+        wv = [x for n, xs in wr.items() if key in n for x in xs]
+        if not fv or not wv:
+            continue
+        fk, wk = statistics.median(fv), statistics.median(wv)
+        hbm = int(round(fk * 1024 * f_scale + wk * 1024 * w_scale))
+        out["kernels"][key] = {"label": label, "dispatches": len(fv), "fetch_kib": fk,
+                               "write_kib": wk, "hbm_bytes": hbm, "algorithmic_bytes": alg,
+                               "ratio": round(hbm / alg, 3)}
+    base = os.path.join(ROOT, "profiles", "traffic_kernels")
+    with open(base + ".json", "w") as fh:
+        json.dump(out, fh, indent=1)
+    with open(base + ".md", "w") as fh:
+        fh.write("# HBM traffic per dispatch (FETCH_SIZE + WRITE_SIZE)\n\n")
+        fh.write("Two rocprofv3 counter passes over the same committed command, run from /tmp "
+                 "on one MI355X, then this summary:\n\n```\n"
+                 "rocprofv3 --pmc FETCH_SIZE --output-format csv -d <fetch> -o run -- "
+                 "python3 <repo>/bench.py --only traffic\n"
+                 "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <write> -o run -- "
+                 "python3 <repo>/bench.py --only traffic\n"
+                 "python3 <repo>/bench.py --traffic-summary <fetch>/run_counter_collection.csv "
+                 "<write>/run_counter_collection.csv\n```\n\n")
+        fh.write(f"Kernel sources hash `{out['source_hash']}` (bench.py reports `traffic` only "
+                 "while it matches). Scale factors from the plain 256 MiB copy "
+                 f"(reads and writes 262,144 KiB): FETCH_SIZE x {f_scale:.4f}, "
+                 f"WRITE_SIZE x {w_scale:.4f}.\n\n")
+        fh.write("| kernel | dispatches | FETCH KiB | WRITE KiB | HBM bytes | algorithmic bytes "
+                 "| ratio |\n|---|---|---|---|---|---|---|\n")
+        for key, v in out["kernels"].items():
+            fh.write(f"| {v['label']} (`{key}`) | {v['dispatches']} | {v['fetch_kib']:.1f} | "
+                     f"{v['write_kib']:.1f} | {v['hbm_bytes']:,} | {v['algorithmic_bytes']:,} | "
+                     f"{v['ratio']} |\n")
+    print(json.dumps(out))
+    return 0
+
+
+def kernel_summary(trace_csv, out_md, title, command):
+    """Per-kernel duration statistics of a rocprofv3 --kernel-trace CSV,
+    grouped by (kernel, grid size) so that launches of one template at
+    different shapes (the 2048-row GEMV and the LM head) stay apart; written
+    as a markdown table with the command that produced the trace."""
+    import csv
+    groups = {}
+    for r in csv.DictReader(open(trace_csv)):
+        name = r["Kernel_Name"]
+        if "sg::" not in name:
+            continue
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        key = (name.split("(")[0].replace("void ", ""), grid // max(wg, 1))
+        groups.setdefault(key, []).append(dur)
+    with open(out_md, "w") as fh:
+        fh.write(f"# {title}\n\n```\n{command}\n```\n\n")
+        fh.write("Kernel-only durations (End - Start of each dispatch in the kernel trace), "
+                 "grouped by kernel and grid.\n\n")
+        fh.write("| kernel | workgroups | dispatches | median us | mean us | min us | max us |\n")
+        fh.write("|---|---|---|---|---|---|---|\n")
+        for (name, nwg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            fh.write(f"| `{name}` | {nwg} | {len(d)} | {statistics.median(d):.2f} | "
+                     f"{statistics.fmean(d):.2f} | {min(d):.2f} | {max(d):.2f} |\n")
+    print(open(out_md).read())
     return 0
 
 
@@ -225,6 +417,12 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-summary", nargs=4, metavar=("TRACE_CSV", "OUT_MD", "TITLE", "CMD"),
+                    help="write a per-kernel duration table from a rocprofv3 kernel trace "
+                         "(no GPU needed)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic_kernels.{json,md} from the two counter passes "
+                         "over --only traffic (no GPU needed)")
     ap.add_argument("--only", choices=["2", "5", "q6", "traffic"], default=None,
                     help="run one leg alone and print its JSON: 2 = the config-2 decode "
                          "layer (graph-timed, front/back split, parity) and the config-3 "
@@ -233,6 +431,10 @@ def main():
                          "launches beside a plain 256 MiB copy, for rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE passes")
     args = ap.parse_args()
+    if args.traffic_summary:
+        return traffic_summary(*args.traffic_summary)
+    if args.kernel_summary:
+        return kernel_summary(*args.kernel_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(the path shards by expert across GPUs; see the design notes)", file=sys.stderr)
@@ -263,9 +465,13 @@ def main():
     pool = build_pool(torch, N_LAYERS, gen)
     layers = make_layers(torch, ops, pool)
     if args.only == "traffic":
-        return traffic_run(torch, np, layers)
+        return traffic_run(torch, np, ops, gen, layers)
 
-    n_in = args.steps + args.warmup
+    # the timed region is replayed R times, each replay a graph of K steps over
+    # its own inputs (so consecutive replays read different experts); the
+    # value is the median replay
+    R = 5
+    n_in = args.warmup + args.steps * R
     rng = np.random.default_rng(2)
     xs = rng.normal(0, 1, (n_in, H)).astype(np.float32)
     lgs = rng.normal(0, 1, (n_in, E)).astype(np.float32)
@@ -280,27 +486,32 @@ def main():
                                      idx=idx[i:i + 1], weight=wgt[i:i + 1], stages=stages,
                                      workspace=ws)
 
-    # warmup (eager), then eager timing of the same K steps
+    # warmup (eager), then eager timing of the first replay's K steps
     log("[bench] warmup + eager pass")
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.warmup, n_in):
+    for i in range(args.warmup, args.warmup + args.steps):
         step(i)
     torch.cuda.synchronize()
     eager_us = (time.perf_counter() - t0) / args.steps * 1e6
 
-    # timed: the K steps replayed from one HIP graph
+    # timed: R replays, each of a HIP graph of K steps on distinct inputs
     log("[bench] graph-timed pass")
-    ms_graph, _ = time_graph(torch, lambda: [step(i) for i in range(args.warmup, n_in)], 1)
+    graphs = [capture(torch, lambda r=r: [step(i) for i in range(args.warmup + r * args.steps,
+                                                                  args.warmup + (r + 1) * args.steps)])
+              for r in range(R)]
+    replay_times = [replay_ms(torch, g, st) for g, st in graphs]
+    ms_graph = statistics.median(replay_times)
+    del graphs
     torch.cuda.synchronize()
     us_per_token = ms_graph * 1e3 / args.steps
 
     # parity spot check of the timed outputs (layer 0 steps) against the oracle
     from oracle import oracle as orc
     l0 = pool[0].cpu().numpy()
-    chk = [i for i in range(args.warmup, n_in) if i % N_LAYERS == 0][:2]
+    chk = [i for i in range(args.warmup, n_in) if i % N_LAYERS == 0][:3]
     out_h = out.cpu().numpy()
     bit_exact = True
     max_rel = 0.0
@@ -315,17 +526,28 @@ def main():
 
     # per-kernel timing over 128 distinct (layer, step) workspaces: the front
     # kernel (routing + gate/up + SiLU) and the back kernel (down + combine)
+    # (128 launches on their own inputs, whatever --steps is: about 128 x 9
+    # distinct experts over the 16 layers, 1.4 GB of gate/up rows per replay)
     log("[bench] per-kernel timing")
     S = 128
+    rng_k = np.random.default_rng(12)
+    xk = torch.from_numpy(rng_k.normal(0, 1, (S, H)).astype(np.float32)).cuda()
+    lk = torch.from_numpy(rng_k.normal(0, 1, (S, E)).astype(np.float32)).cuda()
+    ok_ = torch.empty((S, H), dtype=torch.float32, device="cuda")
+    ik_ = torch.empty((S, K + 1), dtype=torch.int32, device="cuda")
+    wk_ = torch.empty((S, K + 1), dtype=torch.float32, device="cuda")
     wss = [torch.zeros_like(layers[0].workspace) for _ in range(S)]
+
+    def kstep(j, stages):
+        layers[j % N_LAYERS].forward(xk[j:j + 1], lk[j:j + 1], out=ok_[j:j + 1], idx=ik_[j:j + 1],
+                                     weight=wk_[j:j + 1], stages=stages, workspace=wss[j])
+
     for j in range(S):
-        step(j % n_in, stages=3, ws=wss[j])
+        kstep(j, 3)
     torch.cuda.synchronize()
     reps = 10
-    ms_fr, _ = time_graph(torch, lambda: [step(j % n_in, stages=1, ws=wss[j]) for j in range(S)],
-                          reps)
-    ms_bk, _ = time_graph(torch, lambda: [step(j % n_in, stages=2, ws=wss[j]) for j in range(S)],
-                          reps)
+    ms_fr, _ = time_graph(torch, lambda: [kstep(j, 1) for j in range(S)], reps)
+    ms_bk, _ = time_graph(torch, lambda: [kstep(j, 2) for j in range(S)], reps)
     front_us = ms_fr * 1e3 / S
     back_us = ms_bk * 1e3 / S
     # algorithmic bytes: 9 experts' gate+up rows, x, logits, h written
@@ -407,6 +629,11 @@ def main():
     ms_ptr, _ = time_graph(torch, lambda: ops.gemv_ptrs_q4_k_q8(ptrs, xq, n_rot, 2048, 2048,
                                                                 y=ys.view(-1)), 20)
     ptr_bytes = n_rot * 2048 * 8 * 144 + 8 * 276 + n_rot * 2048 * 4
+    cpu1 = None
+    if not args.no_cpu:
+        log("[bench] config-1 CPU baseline")
+        cpu1 = cpu_gemv_baseline(orc, [gemv_w[j].cpu().numpy() for j in range(64)],
+                                 xq.cpu().numpy())
     del gemv_w
     torch.cuda.empty_cache()
     # LM-head shape (config 4 tail): 248320 x 2048, 286 MB
@@ -466,23 +693,49 @@ def main():
     acts_h = acts.cpu().numpy()
     exact4 = True
     rel4 = 0.0
+    host4 = []
     for L in range(NL4):
         gl, ul, dl = [None] * E, [None] * E, [None] * E
         for e in routes[L]:
             gl[e], ul[e], dl[e] = (pool4[L, m, e].cpu().numpy() for m in range(3))
+        host4.append((gl, ul, dl))
         ref, _, _ = orc.moe_layer(gl, ul, dl, None, x4_h[L], idx=idx4[L].cpu().numpy(),
                                   weight=w4[L].cpu().numpy(), hidden=H, n_ff=F, k=K)
         exact4 &= bool((acts_h[L] == ref).all())
         floor = 1e-3 * np.abs(ref).max()
         rel4 = max(rel4, float((np.abs(acts_h[L] - ref) / np.maximum(np.abs(ref), floor)).max()))
     # and of the LM head on the last layer's quantized output
-    yref4 = orc.gemv(head.cpu().numpy(), xq4.cpu().numpy(), head_rows, 2048)[0]
+    head_h = head.cpu().numpy()
+    yref4 = orc.gemv(head_h, xq4.cpu().numpy(), head_rows, 2048)[0]
     y4_h = y4.cpu().numpy()
     head_floor = 1e-3 * np.abs(yref4).max()
     head_parity = {"bit_exact": bool((y4_h == yref4).all()),
                    "max_rel_err": float((np.abs(y4_h - yref4) /
                                          np.maximum(np.abs(yref4), head_floor)).max())}
+    cpu4 = None
+    if not args.no_cpu:
+        # the same token on the host: 40 layers of 8 expert jobs on
+        # hardware_concurrency/2 workers (pool.cpp:39-40), then Q8_K and the
+        # head GEMV single-threaded as gemv_q4_k_q8_avx2 runs
+        log("[bench] config-4 CPU baseline")
+        nth = max(1, (os.cpu_count() or 2) // 2)
+        i4h, w4h = idx4.cpu().numpy(), w4.cpu().numpy()
+        t4 = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            for L in range(NL4):
+                o4, _, _ = orc.moe_layer(*host4[L], None, x4_h[L], idx=i4h[L], weight=w4h[L],
+                                         hidden=H, n_ff=F, k=K, n_threads=nth)
+            orc.gemv(head_h, orc.quantize_q8_k(o4), head_rows, 2048)
+            t4.append(time.perf_counter() - t0)
+        cpu4 = {"value": round(statistics.median(t4) * 1e6, 1), "unit": "us/token",
+                "cores": nth, "kind": "port",
+                "sample": f"{len(t4)} tokens through the 40 layers + LM head, median; experts on "
+                          f"{nth} threads, head single-threaded; nproc={os.cpu_count()}, "
+                          f"cpu={cpu_model()}"}
+    del host4, head_h
     config4 = {"us_per_token": round(ms4 * 1e3, 2),
+               "cpu_baseline": cpu4,
                "gbs": round(stack_bytes / (ms4 * 1e-3) / 1e9, 1),
                "frac": round(stack_bytes / (ms4 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                "algorithmic_bytes": stack_bytes,
@@ -506,12 +759,17 @@ def main():
     # HBM bytes per front launch from the two rocprofv3 counter passes over
     # `bench.py --only traffic` (FETCH_SIZE, WRITE_SIZE, scaled by a 256 MiB
     # copy), committed under profiles/
-    traffic = None
+    traffic, traffic_note = None, "no committed counter summary"
     try:
-        with open(os.path.join(ROOT, "profiles", "moe_layer_config2_traffic.json")) as fh:
-            traffic = json.load(fh)["layer_front_kernel"]["hbm_bytes"]
+        with open(os.path.join(ROOT, "profiles", "traffic_kernels.json")) as fh:
+            tk = json.load(fh)
+        if tk.get("source_hash") == source_hash():
+            traffic = tk["kernels"]["layer_front_kernel"]["hbm_bytes"]
+            traffic_note = "profiles/traffic_kernels.json (same kernel sources)"
+        else:
+            traffic_note = "profiles/traffic_kernels.json describes other kernel sources"
     except (OSError, KeyError, ValueError):
-        traffic = None
+        pass
     res = {
         "metric": "MoE layer decode us/token at top-8/256 (Q4_K experts, batch 1)",
         "value": round(us_per_token, 3),
@@ -527,10 +785,14 @@ def main():
         "data": "synthetic (seeded Q4_K experts, N(0,1) x and logits)",
         "config": {"workload": "config 2: MoE layer decode, hidden 2048, 256 experts "
                                "(gate/up 512x2048, down 2048x512) + shared, top-8, batch 1",
-                   "layers_rotated": N_LAYERS, "timing": "HIP graph of K steps"},
+                   "layers_rotated": N_LAYERS,
+                   "timing": f"median of {R} replays, each a HIP graph of K steps on its own "
+                             "inputs",
+                   "replay_us_per_token": [round(t * 1e3 / args.steps, 3) for t in replay_times]},
         "roofline": {"kernel": "layer_front_kernel (routing + 9 experts x gate/up + SiLU)",
                      "bound": "hbm", "achieved": round(fr_gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(fr_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_note,
                      "algorithmic_bytes": front_bytes, "avg_us": round(front_us, 3)},
         "cpu_baseline": cpu,
         "parity": {"checked_steps": len(chk), "max_rel_err": max_rel, "bit_exact": bit_exact},
@@ -547,7 +809,8 @@ def main():
                                                      / PEAK_HBM_GBS, 4),
                          "gbs": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1),
                          "frac": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-                         "rotation": f"{n_rot} distinct 2048x2048 matrices, graph-replayed"},
+                         "rotation": f"{n_rot} distinct 2048x2048 matrices, graph-replayed",
+                         "cpu_baseline": cpu1},
         "lm_head_q6k_gemv": q6_head,
         "lm_head_gemv": {"shape": "248320x2048", "us": round(ms_head * 1e3, 2),
                          "gbs": round(head_bytes / (ms_head * 1e-3) / 1e9, 1),
