@@ -80,10 +80,12 @@ struct LayerPlan {
   int* tok;     // [emax] entry token
   int* slot;    // [emax] entry slot
   unsigned long long* wdown;  // [gmax] down matrix of the group, 0 = absent expert
+  unsigned long long* wgate;  // [gmax] gate matrix of the group, 0 = absent expert
+  unsigned long long* wup;    // [gmax] up matrix of the group, 0 = absent expert
 };
 
 struct LayerWs {
-  size_t meta, off, expert, tok, slot, wdown, sgate, h, total;
+  size_t meta, off, expert, tok, slot, wdown, wgate, wup, sgate, h, total;
   int gmax, emax;
 };
 
@@ -100,6 +102,8 @@ static LayerWs layer_ws(int T, int n_ff, int E, int k) {
   w.tok = o;    o = align256(o + w.emax * sizeof(int));
   w.slot = o;   o = align256(o + w.emax * sizeof(int));
   w.wdown = o;  o = align256(o + w.gmax * sizeof(unsigned long long));
+  w.wgate = o;  o = align256(o + w.gmax * sizeof(unsigned long long));
+  w.wup = o;    o = align256(o + w.gmax * sizeof(unsigned long long));
   w.sgate = o;  o = align256(o + static_cast<size_t>(T) * sizeof(float));
   w.h = o;      o = align256(o + static_cast<size_t>(T) * (k + 1) * n_ff * sizeof(float));
   w.total = o;
@@ -133,6 +137,7 @@ struct LayerArgs {
   float shared_w;
   int back_rows, back_lrow;  // rows per back workgroup, lanes per row there
   int back_bufs;             // back waves with a down-row buffer (8, or 4 when LDS is short)
+  int publish_only;          // front launch of the publisher alone (the routing launch)
   FrontLds front_routed, front_shared;  // front LDS layouts (routing groups, shared group)
 };
 
@@ -935,6 +940,19 @@ __device__ __forceinline__ void exact_route(const LayerArgs& a, uint32_t* dyn, c
 // publisher workgroup (blockIdx.y == gmax, x == 0) runs the same routing
 // and writes idx, weight and the plan.
 // NBH: hidden / 256 when compiled for it (0 = read from a).
+// The shared expert's scalar gate of every token (session.cpp:2904-2909),
+// sgate[t] = sigmoid(sh_gate_w . x[t]) in the reference's fp32 lane order:
+// one token per 32-lane half-wave of the workgroup; read by the back kernel.
+__device__ __forceinline__ void shared_gate_tokens(const LayerArgs& a, int tid) {
+  const int l = tid & 31, half = tid >> 5;
+  for (int t0 = 0; t0 < a.T; t0 += 8) {
+    const int t = min(t0 + half, a.T - 1);
+    const float* xt = a.x + static_cast<long long>(t) * a.hidden;
+    const float gl = rowdot_f32_lanes32(a.sh_gate_w, [&](int i) { return xt[i]; }, a.hidden, l);
+    if (l == 0 && t0 + half < a.T) a.sgate[t] = sigmoid_sg(gl);
+  }
+}
+
 template <int EPT, int NBH>
 __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[64 * 36],
                            uint32_t* dyn) {
@@ -973,17 +991,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
     gateup_wave(true, row0, nrw, nbh, lpr, buf, xs,
                 [&](int j, int& t, int& sl) { t = j; sl = k; }, T, stride, a.n_ff, a.h, lane);
     SG_MARK_FRONT(6);
-    if (a.sh_gate_w && bx == 0) {
-      // the shared expert's scalar gate of every token (session.cpp:2904-2909):
-      // one token per 32-lane half-wave, the result read by the back kernel
-      const int l = lane & 31, half = tid >> 5;
-      for (int t0 = 0; t0 < T; t0 += 8) {
-        const int t = min(t0 + half, T - 1);
-        const float* xt = a.x + static_cast<long long>(t) * a.hidden;
-        const float gl = rowdot_f32_lanes32(a.sh_gate_w, [&](int i) { return xt[i]; }, a.hidden, l);
-        if (l == 0 && t0 + half < T) a.sgate[t] = sigmoid_sg(gl);
-      }
-    }
+    if (a.sh_gate_w && bx == 0) shared_gate_tokens(a, tid);
     return;
   }
 
@@ -1210,6 +1218,8 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
       const unsigned long long dp =
           e >= 0 ? tabd[e] : reinterpret_cast<unsigned long long>(a.sh_down);
       a.plan.wdown[i] = (gp && up) ? dp : 0ull;
+      a.plan.wgate[i] = (gp && up) ? gp : 0ull;
+      a.plan.wup[i] = (gp && up) ? up : 0ull;
     }
     for (int i = tid; i < (a.has_shared ? T : 0) + nv; i += 256) {
       a.plan.tok[i] = ptok[i];
@@ -1250,9 +1260,52 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
   // (one token only: the grid is then about one workgroup per CU; with more
   // tokens the shared expert's row stays first so it is not the tail)
   const int y = blockIdx.y;
-  const int g =
-      a.T != 1 || !a.has_shared || y >= a.gmax ? y : (y + 1 == a.gmax ? 0 : y + 1);
+  const int g = a.publish_only
+                    ? a.gmax
+                    : (a.T != 1 || !a.has_shared || y >= a.gmax ? y : (y + 1 == a.gmax ? 0 : y + 1));
   front_body<EPT, NBH>(a, blockIdx.x, g, wbuf, dyn);
+}
+
+// Gate/up + SiLU of one (row chunk, group) from the plan the routing launch
+// left in the workspace: several tokens (a verify window), where routing in
+// every compute workgroup would cost more than a launch.  Grid (row chunks
+// of 16, gmax); groups beyond the plan's count exit.
+template <int NBH>
+__global__ void __launch_bounds__(256) layer_gateup_kernel(LayerArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
+  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];  // xs, then entry tok / slot
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = a.T, k = a.k, stride = k + 1, g = blockIdx.y, bx = blockIdx.x;
+  const int nbh = NBH ? NBH : a.hidden / kQK, lpr = NBH ? pow2_ceil(NBH) : pow2_ceil(nbh);
+  const int rpw = 32 / lpr;
+  const int row0 = bx * 4 * rpw + wave * rpw;
+  const int nrw = max(0, min(rpw, a.n_ff - row0));
+  const int nxb = T * nbh;
+  float xpre[16];
+  x_preload(a.x, nxb, wave, 4, lane, xpre);
+  const int n_groups = a.plan.meta[0];
+  if (g >= n_groups) return;
+  const unsigned long long wg = a.plan.wgate[g], wu = a.plan.wup[g];
+  const bool present = wg != 0ull && wu != 0ull;
+  if (present && nrw > 0)
+    dma_gateup(reinterpret_cast<const sg_block_q4k*>(wg), reinterpret_cast<const sg_block_q4k*>(wu),
+               row0, nrw, nbh, wbuf[wave], lane);
+  // entries of the group (clamped to the plan's capacity)
+  const int j0 = min(max(a.plan.off[g], 0), a.emax);
+  const int n = min(max(a.plan.off[g + 1], j0), a.emax) - j0;
+  uint32_t* xs = dyn;
+  int* etok = reinterpret_cast<int*>(dyn + ((T * nbh * kXStride + 3) & ~3));
+  int* eslot = etok + a.emax;
+  for (int i = tid; i < n; i += 256) {
+    etok[i] = a.plan.tok[j0 + i];
+    eslot[i] = a.plan.slot[j0 + i];
+  }
+  quantize_x(a.x, nxb, xs, wave, 4, lane, xpre);
+  bar();
+  gateup_wave(present, row0, nrw, nbh, lpr, wbuf[wave], xs,
+              [&](int j, int& t, int& sl) { t = etok[j]; sl = eslot[j]; }, n, stride, a.n_ff, a.h,
+              lane);
+  if (g == 0 && a.has_shared && a.sh_gate_w && bx == 0) shared_gate_tokens(a, tid);
 }
 
 // ---- back kernel ------------------------------------------------------------------------
@@ -1674,7 +1727,9 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   a.plan = LayerPlan{reinterpret_cast<int*>(base + ws.meta), reinterpret_cast<int*>(base + ws.off),
                      reinterpret_cast<int*>(base + ws.expert),
                      reinterpret_cast<int*>(base + ws.tok), reinterpret_cast<int*>(base + ws.slot),
-                     reinterpret_cast<unsigned long long*>(base + ws.wdown)};
+                     reinterpret_cast<unsigned long long*>(base + ws.wdown),
+                     reinterpret_cast<unsigned long long*>(base + ws.wgate),
+                     reinterpret_cast<unsigned long long*>(base + ws.wup)};
   a.h = reinterpret_cast<float*>(base + ws.h);
   a.sgate = a.sh_gate_w ? reinterpret_cast<float*>(base + ws.sgate) : nullptr;
   a.T = n_tokens;
@@ -1694,9 +1749,19 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   const FrontLds fl = front_lds(n_tokens, hidden / kQK, n_expert, k, true);
   a.front_routed = fl;
   a.front_shared = front_lds(n_tokens, hidden / kQK, n_expert, k, false);
+  // several tokens: routing launch (the publisher alone), then the gate/up
+  // launch reading its plan; one token: one fused launch whose compute
+  // workgroups route speculatively beside their weight stream
+  const size_t lds_g =
+      (static_cast<size_t>((n_tokens * (hidden / kQK) * kXStride + 3) & ~3) + 2 * ws.emax) * 4;
+  a.publish_only = n_tokens > 1;
+  if (a.publish_only && lds_g + 4 * buf_b > 160 * 1024)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: this shape needs more LDS than a workgroup has",
+                     nm);
   if (stages & 1) {
     // y < gmax: compute workgroups of group y; y == gmax: the publisher
-    const dim3 grid((n_ff + rows_wg - 1) / rows_wg, ws.gmax + 1);
+    const dim3 grid = a.publish_only ? dim3(1, 1)
+                                     : dim3((n_ff + rows_wg - 1) / rows_wg, ws.gmax + 1);
     if (fl.ept <= 1 && hidden / kQK == 8)  // the decode shape, compiled for hidden 2048
       hipLaunchKernelGGL((layer_front_kernel<1, 8>), grid, dim3(256), lds_f, s, a);
     else if (fl.ept <= 1)
@@ -1708,6 +1773,14 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     else
       hipLaunchKernelGGL((layer_front_kernel<kMaxEpt, 0>), grid, dim3(256), lds_f, s, a);
     if (int st = check_launch("sg_moe_layer/front")) return st;
+    if (a.publish_only) {
+      const dim3 gg((n_ff + rows_wg - 1) / rows_wg, ws.gmax);
+      if (hidden / kQK == 8)
+        hipLaunchKernelGGL((layer_gateup_kernel<8>), gg, dim3(256), lds_g, s, a);
+      else
+        hipLaunchKernelGGL((layer_gateup_kernel<0>), gg, dim3(256), lds_g, s, a);
+      if (int st = check_launch("sg_moe_layer/gateup")) return st;
+    }
   }
   if (stages & 2) {
     // the decode geometry of n_ff = 512 at hidden >= 2048 compiled for its
