@@ -220,7 +220,12 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
 }
 
 // ---- grouped int8-MFMA contraction ------------------------------------------------
+// Positions of one group per tile, in blocks of 16.  A 128-position tile
+// reads each expert's weights once at the config-5 shape (64 +- 8 routes per
+// expert) but needs 114 KB of LDS, one workgroup per CU, and measured 10 %
+// slower than 64-position tiles at two workgroups per CU.
 constexpr int kTokTile = 64;
+constexpr int kTokBlocks = kTokTile / 16;
 constexpr int kRowsWg = 128;                 // weight rows per workgroup
 constexpr int kWRowWords = 36;               // one 144-B block
 constexpr int kWBufWords = kRowsWg * kWRowWords;   // 18 KB
@@ -230,6 +235,8 @@ constexpr int kWBufWords = kRowsWg * kWRowWords;   // 18 KB
 constexpr int kXRow = 76;
 constexpr int kXBufWords = kTokTile * kXRow;        // 19 KB
 constexpr int kThreads = 512;                 // eight waves
+// LDS: two weight and two token buffers, then the tile's token rows
+constexpr size_t kGroupedLds = (2 * kWBufWords + 2 * kXBufWords + kTokTile) * 4;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -249,21 +256,29 @@ struct GroupedArgs {
   int n_rows;               // rows of each weight matrix
   int n_out;                // output row stride (= n_rows)
   int n_expert, n_groups;
+  int n_slices;             // column slices per tile (workgroups sharing one tile)
 };
 
-
-
+// One workgroup = one column slice of one tile (up to 128 positions of one
+// group).  The 1-D grid is laid out so that every slice of a tile runs on
+// one XCD and is dispatched together: workgroup L runs on XCD L % 8, and
+// XCD x's j-th workgroup takes tile x + 8 (j / S), slice j % S.  The tile's
+// token rows are then fetched from HBM once and served to its other slices
+// from that XCD's L2.
 template <bool kGateUp>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
 grouped_mfma_kernel(GroupedArgs a) {
-  __shared__ __attribute__((aligned(16))) uint32_t wbuf[2][kWBufWords];
-  __shared__ __attribute__((aligned(16))) uint32_t xbuf[2][kXBufWords];
-  __shared__ int trow[kTokTile];
+  extern __shared__ __attribute__((aligned(16))) uint32_t gl_lds[];
+  uint32_t* wbuf0 = gl_lds;
+  uint32_t* xbuf0 = gl_lds + 2 * kWBufWords;
+  int* trow = reinterpret_cast<int*>(gl_lds + 2 * kWBufWords + 2 * kXBufWords);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   static_assert(kThreads == 512, "eight waves, one 16-row block each");
-  // one tile (up to kTokTile positions of one group) per workgroup row
-  if (static_cast<int>(blockIdx.y) >= a.tiles[0]) return;
-  const int item = a.tiles[1 + blockIdx.y];
+  const int S = a.n_slices;
+  const int L = blockIdx.x, xcd = L & 7, jx = L >> 3;
+  const int tile = xcd + 8 * (jx / S), slice = jx - (jx / S) * S;
+  if (tile >= a.tiles[0]) return;
+  const int item = a.tiles[1 + tile];
   const int g = item >> 16;
   const int p0 = a.off[g] + kTokTile * (item & 0xFFFF);
   const int p1 = min(a.off[g + 1], p0 + kTokTile);
@@ -276,7 +291,7 @@ grouped_mfma_kernel(GroupedArgs a) {
   // down: output columns [c0, c0 + 128) from weight rows c0 ..; gate/up:
   // h columns [c0, c0 + 64) from gate rows c0 .. (waves 0-3) and the same
   // up rows (waves 4-7)
-  const int c0 = blockIdx.x * (kGateUp ? kRowsWg / 2 : kRowsWg);
+  const int c0 = slice * (kGateUp ? kRowsWg / 2 : kRowsWg);
   const int lr = lane & 15, lq = lane >> 4;     // MFMA: row/column in the tile, K quarter
 
   if (!ma || !mb || !mc) {  // absent expert: its outputs are zero
@@ -286,7 +301,7 @@ grouped_mfma_kernel(GroupedArgs a) {
     return;
   }
 
-  // the 128 weight rows of super-block b into wbuf[s] (gate/up: 64 gate
+  // the 128 weight rows of super-block b into buffer s (gate/up: 64 gate
   // rows, then the same 64 up rows).  Wave w copies chunks [144w, 144w+144)
   // (16 B each, chunk c = part c%9 of row c/9), rows of one matrix; the
   // per-lane offsets are fixed for the kernel, the block's offset b*144 goes
@@ -306,30 +321,31 @@ grouped_mfma_kernel(GroupedArgs a) {
 #pragma unroll
     for (int i = 0; i < 3; ++i)
       if (64 * i + lane < kWChunks)
-        dma16(wbuf[s] + 4 * (wave * kWChunks + 64 * i), wofs[i], rw4, b * kQ4Bytes);
+        dma16(wbuf0 + s * kWBufWords + 4 * (wave * kWChunks + 64 * i), wofs[i], rw4,
+              b * kQ4Bytes);
   };
-  // the tile's token rows of super-block b into xbuf[s], 76 words per token
-  // in 16-B chunks: chunks 0-15 the 64 qs words, 16 the split bsums (eight
-  // lo bytes, eight hi bytes), 17 d and three pad words, 18 padding (a copy
-  // of chunk 17).  LDS chunk c = 19t + j is filled from
-  // the matching 16 B of token t's block (buffer_load_dwordx4 ... lds:
-  // lane-consecutive chunks land LDS-consecutive); offsets are set per
-  // token tile, b*276 is the scalar offset.
-  constexpr int kXChunks = kTokTile * kXRow / 4;    // 1216 = 19 instructions
-  static_assert(kXChunks % 64 == 0, "whole instructions");
-  constexpr int kXInstr = (kXChunks / 64 + 7) / 8;  // per wave: 3
+  // the tile's token rows of super-block b into token buffer s, 76 words per
+  // token in 16-B chunks: chunks 0-15 the 64 qs words, 16 the split bsums
+  // (eight lo bytes, eight hi bytes), 17 d and three pad words, 18 padding
+  // (a copy of chunk 17).  LDS chunk c = 19t + j is filled from the matching
+  // 16 B of token t's block (buffer_load_dwordx4 ... lds: lane-consecutive
+  // chunks land LDS-consecutive); offsets are set per tile, b*276 is the
+  // scalar offset.  Only the 16-token blocks that hold tokens are copied.
+  const int t0 = p0, nt = p1 - p0;
+  const int ntb = (nt + 15) >> 4;  // token blocks holding tokens (wave-uniform)
+  const int xchunks = ntb * 16 * 19;
+  constexpr int kXInstr = (kTokTile * 19 / 64 + 7) / 8;  // per wave: 3
   const u32x4 rx4 = buffer_desc(a.xq, 0x7FFFFFFFu);
   uint32_t xofs[kXInstr];
   auto stage_x = [&](int b, int s) {
 #pragma unroll
     for (int i = 0; i < kXInstr; ++i) {
       const int q = wave + 8 * i;  // the instruction's 64-chunk slice
-      if (64 * q < kXChunks)
-        dma16(xbuf[s] + 256 * q, xofs[i], rx4, b * kQ8Bytes);
+      if (64 * q < xchunks)
+        dma16(xbuf0 + s * kXBufWords + 256 * q, xofs[i], rx4, b * kQ8Bytes);
     }
   };
 
-  const int t0 = p0, nt = p1 - p0;
   if (tid < kTokTile) {  // block index of each token row (rows past nt repeat the first)
     const int t = tid < nt ? tid : 0;
     trow[tid] = (kGateUp ? a.grows[t0 + t] : t0 + t) * nb;
@@ -337,20 +353,19 @@ grouped_mfma_kernel(GroupedArgs a) {
   bar();
 #pragma unroll
   for (int i = 0; i < kXInstr; ++i) {
-    const int c = min(64 * (wave + 8 * i) + lane, kXChunks - 1);
+    const int c = min(64 * (wave + 8 * i) + lane, kTokTile * 19 - 1);
     const int t = c / 19, j = c - t * 19;
     const int gw = j < 16 ? 1 + 4 * j : (j == 16 ? 65 : 0);  // qs, bsums, then d
     xofs[i] = static_cast<uint32_t>(trow[t]) * kQ8Bytes + 4 * gw;
   }
-  // the wave's MFMA tiles: token blocks ti = 0..3 (16 tokens each) of weight
+  // the wave's MFMA tiles: token blocks ti < ntb (16 tokens each) of weight
   // row block `wave`; the lane's four output tokens of block ti are the MFMA
   // result rows 16ti + 4lq + i, its weight row is 16 wave + lr.  The
-  // weight-side work (nibble unpack, scales) is shared by the four blocks.
-  constexpr int NT = 4;
-  const int ntb = (nt + 15) >> 4;  // token blocks holding tokens (wave-uniform)
-  float acc[NT][4];
+  // weight-side work (nibble unpack, scales) is done once per super-block
+  // and shared by every token block.
+  float acc[kTokBlocks][4];
 #pragma unroll
-  for (int ti = 0; ti < NT; ++ti)
+  for (int ti = 0; ti < kTokBlocks; ++ti)
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[ti][i] = 0.f;
   typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -368,8 +383,8 @@ grouped_mfma_kernel(GroupedArgs a) {
       stage_w(b + 1, s ^ 1);
       stage_x(b + 1, s ^ 1);
     }
-    const uint32_t* W = wbuf[s] + (16 * wave + lr) * kWRowWords;
-    const uint32_t* X = xbuf[s];
+    const uint32_t* W = wbuf0 + s * kWBufWords + (16 * wave + lr) * kWRowWords;
+    const uint32_t* X = xbuf0 + s * kXBufWords;
     // I = sum_s sc_s * ip_s with the 6-bit scale split as sc = 8*sh + sl
     // (sh, sl in [0, 7]) and folded into the weight operand: nibble * sl
     // and nibble * sh are at most 105, so each byte of the packed product
@@ -388,7 +403,7 @@ grouped_mfma_kernel(GroupedArgs a) {
     const uint32_t sch[2] = {(sm.sc_lo >> 3) & 0x07070707u, (sm.sc_hi >> 3) & 0x07070707u};
     const uint32_t nsh = 4 * (lq >> 1);                          // nibble of this lane
     const uint32_t sel_l = 0x0C000C00u + 0x00010001u * (lq >> 1);  // its sub-block's byte
-    v4i cl[NT], ch[NT];
+    v4i bl[4], bh[4];
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       const uint4 q = *reinterpret_cast<const uint4*>(W + 4 + 8 * gq + 4 * (lq & 1));
@@ -398,17 +413,8 @@ grouped_mfma_kernel(GroupedArgs a) {
       const uint32_t sh = __builtin_amdgcn_perm(0u, sch[gq >> 1], sel);
       const uint32_t n0 = (q.x >> nsh) & 0x0F0F0F0Fu, n1 = (q.y >> nsh) & 0x0F0F0F0Fu;
       const uint32_t n2 = (q.z >> nsh) & 0x0F0F0F0Fu, n3 = (q.w >> nsh) & 0x0F0F0F0Fu;
-      const v4i bl = {pmul(n0, sl), pmul(n1, sl), pmul(n2, sl), pmul(n3, sl)};
-      const v4i bh = {pmul(n0, sh), pmul(n1, sh), pmul(n2, sh), pmul(n3, sh)};
-#pragma unroll
-      for (int ti = 0; ti < NT; ++ti) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(X + (16 * ti + lr) * kXRow + 16 * gq + 4 * lq);
-        const v4i av = {static_cast<int>(xv.x), static_cast<int>(xv.y), static_cast<int>(xv.z),
-                        static_cast<int>(xv.w)};
-        const v4i z = {0, 0, 0, 0};
-        cl[ti] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bl, gq ? cl[ti] : z, 0, 0, 0);
-        ch[ti] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bh, gq ? ch[ti] : z, 0, 0, 0);
-      }
+      bl[gq] = v4i{pmul(n0, sl), pmul(n1, sl), pmul(n2, sl), pmul(n3, sl)};
+      bh[gq] = v4i{pmul(n0, sh), pmul(n1, sh), pmul(n2, sh), pmul(n3, sh)};
     }
     // M = sum_s mn_s * bsum_s by MFMA: A = a token row's eight bsums split
     // exactly as 128*hi + lo (hi in [-32, 31], lo in [0, 127], both int8,
@@ -421,15 +427,25 @@ grouped_mfma_kernel(GroupedArgs a) {
     const float d = half_bits_to_float(dd & 0xFFFFu);
     const float dmin = half_bits_to_float(dd >> 16);
 #pragma unroll
-    for (int ti = 0; ti < NT; ++ti) {
+    for (int ti = 0; ti < kTokBlocks; ++ti) {
       if (ti >= ntb) continue;  // wave-uniform: a token block past the tile's end
-      const long* bs = reinterpret_cast<const long*>(X + (16 * ti + lr) * kXRow + 64);
+      const uint32_t* Xt = X + (16 * ti + lr) * kXRow;
       const v4i z = {0, 0, 0, 0};
+      v4i cl = z, ch = z;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(Xt + 16 * gq + 4 * lq);
+        const v4i av = {static_cast<int>(xv.x), static_cast<int>(xv.y), static_cast<int>(xv.z),
+                        static_cast<int>(xv.w)};
+        cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bl[gq], cl, 0, 0, 0);
+        ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bh[gq], ch, 0, 0, 0);
+      }
+      const long* bs = reinterpret_cast<const long*>(Xt + 64);
       const v4i mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(bs[1], bmn, z, 0, 0, 0);
       const v4i ml = __builtin_amdgcn_mfma_i32_16x16x32_i8(bs[0], bmn, z, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int I = ch[ti][i] * 8 + cl[ti][i];
+        const int I = ch[i] * 8 + cl[i];
         const int M = mh[i] * 128 + ml[i];
         const float xd = __builtin_bit_cast(float, X[(16 * ti + 4 * lq + i) * kXRow + 68]);
         const float t =
@@ -440,25 +456,28 @@ grouped_mfma_kernel(GroupedArgs a) {
   }
   // outputs of the lane's tokens
   if (kGateUp) {  // h = silu(gate) * up; wave w (gate) and w + 4 (up) hold the same h
-    // positions and each takes half of them: token blocks 0-1 in the gate
-    // wave, 2-3 in the up wave, swapping the other half through LDS
-    bar();  // every wave is done with xbuf
-    float* pair = reinterpret_cast<float*>(xbuf);  // [8 waves][2 blocks * 4][64 lanes]
+    // positions and each takes half of them: the first half of the token
+    // blocks in the gate wave, the second in the up wave, swapping the other
+    // half through LDS
+    bar();  // every wave is done with the token buffers
+    float* pair = reinterpret_cast<float*>(xbuf0);  // [8 waves][kTokBlocks / 2 * 4][64 lanes]
     const bool up_wave = wave >= 4;
 #pragma unroll
-    for (int tj = 0; tj < 2; ++tj)
+    for (int tj = 0; tj < kTokBlocks / 2; ++tj)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        pair[(wave * 8 + 4 * tj + i) * 64 + lane] = acc[up_wave ? tj : 2 + tj][i];
+        pair[(wave * 2 * kTokBlocks + 4 * tj + i) * 64 + lane] =
+            acc[up_wave ? tj : kTokBlocks / 2 + tj][i];
     bar();
     const int partner = wave ^ 4;
 #pragma unroll
-    for (int tj = 0; tj < 2; ++tj) {
-      const int ti = up_wave ? 2 + tj : tj;
+    for (int tj = 0; tj < kTokBlocks / 2; ++tj) {
+      const int ti = up_wave ? kTokBlocks / 2 + tj : tj;
+      if (ti >= ntb) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tt = 16 * ti + 4 * lq + i;
-        const float other = pair[(partner * 8 + 4 * tj + i) * 64 + lane];
+        const float other = pair[(partner * 2 * kTokBlocks + 4 * tj + i) * 64 + lane];
         const float gv = up_wave ? other : acc[ti][i], uv = up_wave ? acc[ti][i] : other;
         if (tt < nt)
           a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * (wave & 3) + lr] =
@@ -467,7 +486,8 @@ grouped_mfma_kernel(GroupedArgs a) {
     }
   } else {
 #pragma unroll
-    for (int ti = 0; ti < NT; ++ti) {
+    for (int ti = 0; ti < kTokBlocks; ++ti) {
+      if (ti >= ntb) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tt = 16 * ti + 4 * lq + i;
@@ -1028,8 +1048,11 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   ga.n_out = n_ff;
   ga.n_expert = n_expert;
   ga.n_groups = G;
-  hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(n_ff / (kRowsWg / 2), ws.max_tiles),
-                     dim3(kThreads), 0, s, ga);
+  // 1-D grids: a multiple of 8 tiles (one per XCD) times the slices
+  const int tiles8 = (ws.max_tiles + 7) / 8 * 8;
+  ga.n_slices = n_ff / (kRowsWg / 2);
+  hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(tiles8 * ga.n_slices), dim3(kThreads),
+                     kGroupedLds, s, ga);
   if (int st = check_launch("sg_moe_prefill/gate_up")) return st;
   if (int st = quantize_split(h, hq, n_ff / kQK, ws.P, s, nm)) return st;
   GroupedArgs gd = ga;
@@ -1045,8 +1068,9 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   gd.nb = n_ff / kQK;
   gd.n_rows = hidden;
   gd.n_out = hidden;
-  hipLaunchKernelGGL(grouped_mfma_kernel<false>, dim3(hidden / kRowsWg, ws.max_tiles),
-                     dim3(kThreads), 0, s, gd);
+  gd.n_slices = hidden / kRowsWg;
+  hipLaunchKernelGGL(grouped_mfma_kernel<false>, dim3(tiles8 * gd.n_slices), dim3(kThreads),
+                     kGroupedLds, s, gd);
   if (int st = check_launch("sg_moe_prefill/down")) return st;
   hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 1023) / 1024, n_tokens), dim3(256), 0, s,
                      out, residual, y, weight, gslot, off, sgate, n_expert, k, hidden, has_shared);
