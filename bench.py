@@ -411,6 +411,53 @@ def kernel_summary(trace_csv, out_md, title, command):
     return 0
 
 
+def mfma_summary(counter_csv, out_md, command):
+    """int8-MFMA utilisation of the prefill's grouped kernels from one
+    rocprofv3 --pmc pass over `bench.py --only 5` (SQ_INSTS_VALU_MFMA_MOPS_I8
+    in units of 512 int8 ops, SQ_INSTS_MFMA, SQ_INSTS_VALU): the achieved
+    rate of the MFMAs issued and of the algorithmic work, each over the
+    dispatch duration."""
+    import csv
+    disp = {}
+    for r in csv.DictReader(open(counter_csv)):
+        if "grouped_mfma_kernel" not in r["Kernel_Name"]:
+            continue
+        d = disp.setdefault(r["Dispatch_Id"], {"name": r["Kernel_Name"].split("(")[0],
+                                               "ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+        d[r["Counter_Name"]] = float(r["Counter_Value"])
+    rows = {}
+    for d in disp.values():
+        rows.setdefault(d["name"], []).append(d)
+    alg = {"grouped_mfma_kernel<true>": T5_ROUTES * 2 * F * H * 2,
+           "grouped_mfma_kernel<false>": T5_ROUTES * H * F * 2}
+    with open(out_md, "w") as fh:
+        fh.write("# int8 MFMA work of the prefill grouped contractions (config 5)\n\n")
+        fh.write(f"```\n{command}\n```\n\n")
+        fh.write("Per-dispatch medians of one counter pass. Hardware int8 ops = "
+                 "SQ_INSTS_VALU_MFMA_MOPS_I8 x 512: every MFMA issued, including the two "
+                 "scale chains (sc = 8 sh + sl), the min MFMAs and the padding rows of partial "
+                 "16-token blocks. Algorithmic ops = 2 x routes x rows x K of the contraction. "
+                 "Rates use the duration of the counted dispatch; peak "
+                 f"{PEAK_INT8_TOPS:.0f} dense int8 TOPS.\n\n")
+        fh.write("| kernel | dispatches | us | MFMA instr | VALU instr | VALU/MFMA | hw int8 ops (G) "
+                 "| hw TOPS | hw frac | algorithmic ops (G) | algorithmic TOPS | algorithmic frac |\n"
+                 "|---|---|---|---|---|---|---|---|---|---|---|---|\n")
+        for name, ds in rows.items():
+            med = lambda k: statistics.median(x[k] for x in ds)
+            us = med("ns") / 1e3
+            ops = med("SQ_INSTS_VALU_MFMA_MOPS_I8") * 512
+            key = name.replace("void ", "").replace("sg::", "")
+            aops = alg.get(key, 0)
+            tops, atops = ops / (us * 1e-6) / 1e12, aops / (us * 1e-6) / 1e12
+            fh.write(f"| `{name.replace('void ', '')}` | {len(ds)} | {us:.1f} | "
+                     f"{med('SQ_INSTS_MFMA'):.3g} | {med('SQ_INSTS_VALU'):.3g} | "
+                     f"{med('SQ_INSTS_VALU') / max(med('SQ_INSTS_MFMA'), 1):.1f} | {ops / 1e9:.1f} | "
+                     f"{tops:.0f} | {tops / PEAK_INT8_TOPS:.3f} | {aops / 1e9:.1f} | {atops:.0f} | "
+                     f"{atops / PEAK_INT8_TOPS:.3f} |\n")
+    print(open(out_md).read())
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -420,6 +467,9 @@ def main():
     ap.add_argument("--kernel-summary", nargs=4, metavar=("TRACE_CSV", "OUT_MD", "TITLE", "CMD"),
                     help="write a per-kernel duration table from a rocprofv3 kernel trace "
                          "(no GPU needed)")
+    ap.add_argument("--mfma-summary", nargs=3, metavar=("COUNTER_CSV", "OUT_MD", "CMD"),
+                    help="write the prefill's int8-MFMA utilisation table from one counter pass "
+                         "over --only 5 (no GPU needed)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write profiles/traffic_kernels.{json,md} from the two counter passes "
                          "over --only traffic (no GPU needed)")
@@ -435,6 +485,8 @@ def main():
         return traffic_summary(*args.traffic_summary)
     if args.kernel_summary:
         return kernel_summary(*args.kernel_summary)
+    if args.mfma_summary:
+        return mfma_summary(*args.mfma_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(the path shards by expert across GPUs; see the design notes)", file=sys.stderr)
