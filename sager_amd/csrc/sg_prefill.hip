@@ -219,12 +219,29 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
   for (int t = tid; t < shared_tail; t += nth) grows[s_total + t] = t;
 }
 
+// ---- latency timeline (built only with -DSG_TIMELINE; no code otherwise) ----
+// Wave 0 of each grouped workgroup stores the 100 MHz real-time counter at
+// its marks: slot 0 start, 1 first copies issued, 2 + b after block b's
+// data landed (b < 8), 10 + b after block b's compute, 14 end ... folded
+// into 16 words per workgroup at pf_stamps[L * 16 + slot].
+#ifdef SG_TIMELINE
+constexpr int kPfMax = 1 << 16;
+static __device__ unsigned long long pf_stamps[kPfMax * 16];
+__device__ __forceinline__ void pf_mark(int base, int slot) {
+  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0 && blockIdx.x < kPfMax / 2) pf_stamps[(base + blockIdx.x) * 16 + slot] = t;
+}
+#define SG_PF_MARK(slot) pf_mark(kGateUp ? 0 : kPfMax / 2, slot)
+#else
+#define SG_PF_MARK(slot) ((void)0)
+#endif
+
 // ---- grouped int8-MFMA contraction ------------------------------------------------
-// Positions of one group per tile, in blocks of 16.  A 128-position tile
-// reads each expert's weights once at the config-5 shape (64 +- 8 routes per
-// expert) but needs 114 KB of LDS, one workgroup per CU, and measured 10 %
-// slower than 64-position tiles at two workgroups per CU.
-constexpr int kTokTile = 64;
+// Positions of one group per tile, in blocks of 16: 96 holds every expert's
+// routes at the config-5 shape (64 +- 8 per expert) in one tile, so each
+// expert's weights are unpacked once per column slice, and two workgroups
+// still fit a CU's LDS.
+constexpr int kTokTile = 96;
 constexpr int kTokBlocks = kTokTile / 16;
 constexpr int kRowsWg = 128;                 // weight rows per workgroup
 constexpr int kWRowWords = 36;               // one 144-B block
@@ -233,10 +250,13 @@ constexpr int kWBufWords = kRowsWg * kWRowWords;   // 18 KB
 // stride is 12 banks mod 32, so eight lanes reading 16 B of eight
 // consecutive rows (one ds_read_b128 pass) touch every bank once.
 constexpr int kXRow = 76;
-constexpr int kXBufWords = kTokTile * kXRow;        // 19 KB
+// a whole number of 64-lane copy instructions (1 KB each): the last one may
+// run past the tile's rows, into this padding
+constexpr int kXBufWords = (kTokTile * kXRow + 255) / 256 * 256;  // 29 KB
 constexpr int kThreads = 512;                 // eight waves
-// LDS: two weight and two token buffers, then the tile's token rows
-constexpr size_t kGroupedLds = (2 * kWBufWords + 2 * kXBufWords + kTokTile) * 4;
+// LDS: one weight buffer (each wave refills its own rows once it has read
+// them), two token buffers, then the tile's token rows: 77 KB
+constexpr size_t kGroupedLds = (kWBufWords + 2 * kXBufWords + kTokTile) * 4;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -250,7 +270,8 @@ struct GroupedArgs {
   const unsigned char* xq;  // Q8_K rows: x [T][nb] (gate/up) or h [P][nb] (down)
   const int* off;           // [G+1] position range of each group
   const int* grows;         // [P] token of each position (gate/up only)
-  const int* tiles;         // work list: [0] = count, then group << 16 | tile index
+  const int4* trec;         // work list: {group, first, end position} per tile, group -1 past it
+  int n_rec;                // records in trec
   float* out;               // [P][n_out]: h (gate/up pass) or y (down)
   int nb;                   // super-blocks per weight row
   int n_rows;               // rows of each weight matrix
@@ -270,19 +291,18 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
 grouped_mfma_kernel(GroupedArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t gl_lds[];
   uint32_t* wbuf0 = gl_lds;
-  uint32_t* xbuf0 = gl_lds + 2 * kWBufWords;
-  int* trow = reinterpret_cast<int*>(gl_lds + 2 * kWBufWords + 2 * kXBufWords);
+  uint32_t* xbuf0 = gl_lds + kWBufWords;
+  int* trow = reinterpret_cast<int*>(gl_lds + kWBufWords + 2 * kXBufWords);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   static_assert(kThreads == 512, "eight waves, one 16-row block each");
+  SG_PF_MARK(0);
   const int S = a.n_slices;
   const int L = blockIdx.x, xcd = L & 7, jx = L >> 3;
   const int tile = xcd + 8 * (jx / S), slice = jx - (jx / S) * S;
-  if (tile >= a.tiles[0]) return;
-  const int item = a.tiles[1 + tile];
-  const int g = item >> 16;
-  const int p0 = a.off[g] + kTokTile * (item & 0xFFFF);
-  const int p1 = min(a.off[g + 1], p0 + kTokTile);
-  if (g >= a.n_groups || p0 >= p1) return;
+  if (tile >= a.n_rec) return;
+  const int4 rec = a.trec[tile];
+  const int g = rec.x, p0 = rec.y, p1 = rec.z;
+  if (g < 0 || g >= a.n_groups || p0 >= p1) return;
   const bool shared = g >= a.n_expert;
   const sg_block_q4k* ma = shared ? a.sh_a : a.tab_a[g];
   const sg_block_q4k* mb = kGateUp ? (shared ? a.sh_b : a.tab_b[g]) : ma;
@@ -317,12 +337,11 @@ grouped_mfma_kernel(GroupedArgs a) {
     const int rr = kGateUp ? (row & 63) : row;
     wofs[i] = static_cast<uint32_t>((c0 + rr) * nb) * kQ4Bytes + 16 * part;
   }
-  auto stage_w = [&](int b, int s) {
+  auto stage_w = [&](int b) {  // into the wave's own rows of the weight buffer
 #pragma unroll
     for (int i = 0; i < 3; ++i)
       if (64 * i + lane < kWChunks)
-        dma16(wbuf0 + s * kWBufWords + 4 * (wave * kWChunks + 64 * i), wofs[i], rw4,
-              b * kQ4Bytes);
+        dma16(wbuf0 + 4 * (wave * kWChunks + 64 * i), wofs[i], rw4, b * kQ4Bytes);
   };
   // the tile's token rows of super-block b into token buffer s, 76 words per
   // token in 16-B chunks: chunks 0-15 the 64 qs words, 16 the split bsums
@@ -373,17 +392,28 @@ grouped_mfma_kernel(GroupedArgs a) {
     return __builtin_bit_cast(int, __builtin_bit_cast(u16x2, q) * __builtin_bit_cast(u16x2, s2));
   };
 
-  stage_w(0, 0);
+  stage_w(0);
   stage_x(0, 0);
+  SG_PF_MARK(1);
   for (int b = 0; b < nb; ++b) {
     const int s = b & 1;
     wait_vm();  // this wave's copies of block b have landed
     bar();      // ... and every wave's
+    if (b < 8) SG_PF_MARK(2 + b);
+    // the lane's weight words of block b into registers: the header and,
+    // per K group, 16 qs bytes; then the wave refills its rows with block
+    // b + 1 while it computes (the rows are the wave's own: no barrier)
+    const uint32_t* Wl = wbuf0 + (16 * wave + lr) * kWRowWords;
+    const uint4 whdr = *reinterpret_cast<const uint4*>(Wl);
+    uint4 wq[4];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq)
+      wq[gq] = *reinterpret_cast<const uint4*>(Wl + 4 + 8 * gq + 4 * (lq & 1));
+    wait_lds();
     if (b + 1 < nb) {  // the next block streams in while this one computes
-      stage_w(b + 1, s ^ 1);
+      stage_w(b + 1);
       stage_x(b + 1, s ^ 1);
     }
-    const uint32_t* W = wbuf0 + s * kWBufWords + (16 * wave + lr) * kWRowWords;
     const uint32_t* X = xbuf0 + s * kXBufWords;
     // I = sum_s sc_s * ip_s with the 6-bit scale split as sc = 8*sh + sl
     // (sh, sl in [0, 7]) and folded into the weight operand: nibble * sl
@@ -398,7 +428,7 @@ grouped_mfma_kernel(GroupedArgs a) {
     // ones: k = 64gq + 16lq + j, i.e. sub-block 2gq + (lq >> 1), the low
     // (lq < 2) or high nibbles of qs bytes 32gq + 16(lq & 1) + j - one
     // ds_read_b128 on each side.
-    const ScaleMins sm = unpack_scales(W[1], W[2], W[3]);
+    const ScaleMins sm = unpack_scales(whdr.y, whdr.z, whdr.w);
     const uint32_t scl[2] = {sm.sc_lo & 0x07070707u, sm.sc_hi & 0x07070707u};
     const uint32_t sch[2] = {(sm.sc_lo >> 3) & 0x07070707u, (sm.sc_hi >> 3) & 0x07070707u};
     const uint32_t nsh = 4 * (lq >> 1);                          // nibble of this lane
@@ -406,7 +436,7 @@ grouped_mfma_kernel(GroupedArgs a) {
     v4i bl[4], bh[4];
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
-      const uint4 q = *reinterpret_cast<const uint4*>(W + 4 + 8 * gq + 4 * (lq & 1));
+      const uint4 q = wq[gq];
       // sl and sh of sub-block 2gq + (lq >> 1), spread to both 16-bit halves
       const uint32_t sel = sel_l + 0x00010001u * ((2 * gq) & 3);
       const uint32_t sl = __builtin_amdgcn_perm(0u, scl[gq >> 1], sel);
@@ -421,7 +451,7 @@ grouped_mfma_kernel(GroupedArgs a) {
     // written so by the quantizer), B = the row's eight 6-bit mins in the
     // first K quarter (lanes 0-15) and zeros elsewhere, so the other lanes'
     // A bytes do not count.  M = 128 * C(hi) + C(lo).
-    const uint32_t dd = W[0];
+    const uint32_t dd = whdr.x;
     const long bmn =
         lq == 0 ? static_cast<long>(sm.mn_lo) | (static_cast<long>(sm.mn_hi) << 32) : 0l;
     const float d = half_bits_to_float(dd & 0xFFFFu);
@@ -454,6 +484,7 @@ grouped_mfma_kernel(GroupedArgs a) {
       }
     }
   }
+  SG_PF_MARK(10);
   // outputs of the lane's tokens
   if (kGateUp) {  // h = silu(gate) * up; wave w (gate) and w + 4 (up) hold the same h
     // positions and each takes half of them: the first half of the token
@@ -495,6 +526,15 @@ grouped_mfma_kernel(GroupedArgs a) {
           a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * wave + lr] = acc[ti][i];
       }
     }
+  }
+  SG_PF_MARK(11);
+  if (threadIdx.x == 0) {  // the tile's size, for the timeline reader
+    SG_PF_MARK(12);
+#ifdef SG_TIMELINE
+    if (blockIdx.x < kPfMax / 2)
+      pf_stamps[((kGateUp ? 0 : kPfMax / 2) + blockIdx.x) * 16 + 13] =
+          (static_cast<unsigned long long>(nt) << 32) | g;
+#endif
   }
 }
 
@@ -557,8 +597,9 @@ __global__ void __launch_bounds__(256) scan_bits_kernel(const int* __restrict__ 
 __global__ void __launch_bounds__(1024) scan_offsets_kernel(
     const int* __restrict__ idx, const uint32_t* __restrict__ wbits, const int* __restrict__ wflags,
     int* __restrict__ woff, int* __restrict__ gslot, int* __restrict__ grows, int* __restrict__ off,
-    int* __restrict__ toff, int* __restrict__ meta, int* __restrict__ tiles, int n_rows, int k,
-    int E, int n_w, int tok_per, int shared_tail) {
+    int* __restrict__ toff, int* __restrict__ meta, int* __restrict__ tiles,
+    int4* __restrict__ trec, int n_rec, int n_rows, int k, int E, int n_w, int tok_per,
+    int shared_tail) {
   __shared__ int hist[1024], part[1024];
   __shared__ int s_bad, s_dup, s_total;
   extern __shared__ uint32_t wb_lds[];  // a copy of wbits when it fits (kScanBitsLds words)
@@ -633,6 +674,15 @@ __global__ void __launch_bounds__(1024) scan_offsets_kernel(
       const int sh_t = (shared_tail + tok_per - 1) / tok_per;
       for (int j = tid; j < sh_t; j += nth) tiles[1 + tot_t + j] = (E << 16) | j;
       if (tid == 0) tiles[0] = tot_t + sh_t;
+    }
+    if (trec) {  // the same work list as records {group, first, end position}, -1 beyond it
+      if (tid < E)
+        for (int j = 0; j < tl; ++j)
+          trec[pt + j] = int4{tid, ph + tok_per * j, min(ph + h, ph + tok_per * (j + 1)), 0};
+      const int sh_t = (shared_tail + tok_per - 1) / tok_per;
+      for (int j = tid; j < sh_t; j += nth)
+        trec[tot_t + j] = int4{E, tot_h + tok_per * j, min(tot_h + shared_tail, tot_h + tok_per * (j + 1)), 0};
+      for (int t = tot_t + sh_t + tid; t < n_rec; t += nth) trec[t] = int4{-1, 0, 0, 0};
     }
     if (tid < E) hist[tid] = ph;  // hist now holds off[e]
   }
@@ -839,7 +889,7 @@ static PlanWs plan_ws(int n_rows, int E) {
 }
 
 struct PrefillWs {
-  size_t xq, gslot, grows, off, toff, meta, tiles, plan, sgate, h, hq, y, total;
+  size_t xq, gslot, grows, off, toff, meta, tiles, trec, plan, sgate, h, hq, y, total;
   int P;          // positions: T*k routes + T shared
   int max_tiles;  // bound on the work list: every group's last tile may be partial
 };
@@ -856,6 +906,7 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
   w.meta = o;  o = al256(o + 4 * 4);
   w.max_tiles = (T * k + kTokTile - 1) / kTokTile + E + (T + kTokTile - 1) / kTokTile;
   w.tiles = o; o = al256(o + static_cast<size_t>(1 + w.max_tiles) * 4);
+  w.trec = o;  o = al256(o + static_cast<size_t>(w.max_tiles) * 16);
   w.plan = o;  o = al256(o + plan_ws(T, E).total);
   w.sgate = o; o = al256(o + static_cast<size_t>(T) * 4);
   w.h = o;     o = al256(o + static_cast<size_t>(w.P) * n_ff * 4);
@@ -895,8 +946,9 @@ static int scan_launch(const int* idx, float* weight, int* gslot, int* grows, in
 
 // the plan over many workgroups (bits, offsets, placement) on scratch `ws`
 static int plan_launch(const int* idx, float* weight, int* gslot, int* grows, int* off,
-                       int* toff, int* meta, int* tiles, unsigned char* ws, int n_rows, int k,
-                       int E, int tok_per, int shared_tail, hipStream_t s, const char* nm) {
+                       int* toff, int* meta, int* tiles, int4* trec, int n_rec, unsigned char* ws,
+                       int n_rows, int k, int E, int tok_per, int shared_tail, hipStream_t s,
+                       const char* nm) {
   const PlanWs p = plan_ws(n_rows, E);
   uint32_t* wbits = reinterpret_cast<uint32_t*>(ws + p.wbits);
   int* woff = reinterpret_cast<int*>(ws + p.woff);
@@ -907,8 +959,8 @@ static int plan_launch(const int* idx, float* weight, int* gslot, int* grows, in
   const size_t bits_lds =
       p.n_w * E <= kScanBitsLds ? static_cast<size_t>(p.n_w) * E * 4 : 0;
   hipLaunchKernelGGL(scan_offsets_kernel, dim3(1), dim3(1024), bits_lds, s, idx, wbits, wflags,
-                     woff, gslot, grows, off, toff, meta, tiles, n_rows, k, E, p.n_w, tok_per,
-                     shared_tail);
+                     woff, gslot, grows, off, toff, meta, tiles, trec, n_rec, n_rows, k, E, p.n_w,
+                     tok_per, shared_tail);
   if (int st = check_launch(nm)) return st;
   hipLaunchKernelGGL(scan_place_kernel, dim3(p.n_w), dim3(256), 0, s, idx, wbits, wflags, woff,
                      gslot, grows, n_rows, k, E, p.n_w);
@@ -967,7 +1019,7 @@ int sg_moe_dispatch_plan(const int* idx, float* weight, int* gslot, int* grows, 
   if (workspace_bytes < plan_ws(n_rows, n_expert).total)
     return set_error(SG_ERR_INVALID_ARGUMENT, "%s: workspace %zu < %zu bytes", nm,
                      workspace_bytes, plan_ws(n_rows, n_expert).total);
-  return plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles,
+  return plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, nullptr, 0,
                      static_cast<unsigned char*>(workspace), n_rows, k, n_expert, tok_per,
                      shared_tail, static_cast<hipStream_t>(stream), nm);
 }
@@ -1009,6 +1061,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   int* toff = reinterpret_cast<int*>(base + ws.toff);
   int* meta = reinterpret_cast<int*>(base + ws.meta);
   int* tiles = reinterpret_cast<int*>(base + ws.tiles);
+  int4* trec = reinterpret_cast<int4*>(base + ws.trec);
   float* h = reinterpret_cast<float*>(base + ws.h);
   auto* hq = reinterpret_cast<sg_block_q8k*>(base + ws.hq);
   float* y = reinterpret_cast<float*>(base + ws.y);
@@ -1026,7 +1079,8 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
     if (int st = sg_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w,
                                 stream))
       return st;
-  if (int st = plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, base + ws.plan,
+  if (int st = plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, trec, ws.max_tiles,
+                           base + ws.plan,
                            n_tokens, k, n_expert, kTokTile, has_shared ? n_tokens : 0, s,
                            "sg_moe_prefill/plan"))
     return st;
@@ -1041,7 +1095,8 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   ga.xq = reinterpret_cast<const unsigned char*>(xq);
   ga.off = off;
   ga.grows = grows;
-  ga.tiles = tiles;
+  ga.trec = trec;
+  ga.n_rec = ws.max_tiles;
   ga.out = h;
   ga.nb = hidden / kQK;
   ga.n_rows = n_ff;
@@ -1076,5 +1131,16 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
                      out, residual, y, weight, gslot, off, sgate, n_expert, k, hidden, has_shared);
   return check_launch("sg_moe_prefill/combine");
 }
+
+#ifdef SG_TIMELINE
+int sg_debug_prefill_timeline(unsigned long long* host, int n_wg) {
+  if (n_wg > kPfMax) n_wg = kPfMax;
+  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(pf_stamps), size_t(n_wg) * 16 * 8) != hipSuccess)
+    return SG_ERR_HIP;
+  static unsigned long long zeros[kPfMax * 16];
+  return hipMemcpyToSymbol(HIP_SYMBOL(pf_stamps), zeros, sizeof(zeros)) == hipSuccess ? SG_OK
+                                                                                    : SG_ERR_HIP;
+}
+#endif
 
 }  // extern "C"
