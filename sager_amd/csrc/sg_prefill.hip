@@ -59,6 +59,14 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total)
   return before + x - v;
 }
 
+// One tile of the grouped kernels' work list: a group (expert, or E for the
+// shared expert; -1 past the list), its positions [p0, p1), and the group's
+// three matrices (absent: 0 when any of them is null).
+struct TileRec {
+  int g, p0, p1, pad;
+  unsigned long long wg, wu, wd, pad2;
+};
+
 __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
     const int* __restrict__ idx, float* __restrict__ weight, int* __restrict__ gslot,
     int* __restrict__ grows, int* __restrict__ off, int* __restrict__ toff,
@@ -261,22 +269,16 @@ constexpr size_t kGroupedLds = (kWBufWords + 2 * kXBufWords + kTokTile) * 4;
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct GroupedArgs {
-  const sg_block_q4k* const* tab_a;  // gate (gate/up pass) or down
-  const sg_block_q4k* const* tab_b;  // up (gate/up pass)
-  const sg_block_q4k* const* tab_c;  // the third matrix: an expert is absent if any is null
-  const sg_block_q4k* sh_a;          // shared expert (group E)
-  const sg_block_q4k* sh_b;
-  const sg_block_q4k* sh_c;
   const unsigned char* xq;  // Q8_K rows: x [T][nb] (gate/up) or h [P][nb] (down)
   const int* off;           // [G+1] position range of each group
   const int* grows;         // [P] token of each position (gate/up only)
-  const int4* trec;         // work list: {group, first, end position} per tile, group -1 past it
+  const TileRec* trec;      // work list: one record per tile, group -1 past it
   int n_rec;                // records in trec
   float* out;               // [P][n_out]: h (gate/up pass) or y (down)
   int nb;                   // super-blocks per weight row
   int n_rows;               // rows of each weight matrix
   int n_out;                // output row stride (= n_rows)
-  int n_expert, n_groups;
+  int n_groups;
   int n_slices;             // column slices per tile (workgroups sharing one tile)
 };
 
@@ -300,13 +302,12 @@ grouped_mfma_kernel(GroupedArgs a) {
   const int L = blockIdx.x, xcd = L & 7, jx = L >> 3;
   const int tile = xcd + 8 * (jx / S), slice = jx - (jx / S) * S;
   if (tile >= a.n_rec) return;
-  const int4 rec = a.trec[tile];
-  const int g = rec.x, p0 = rec.y, p1 = rec.z;
+  const TileRec rec = a.trec[tile];
+  const int g = rec.g, p0 = rec.p0, p1 = rec.p1;
   if (g < 0 || g >= a.n_groups || p0 >= p1) return;
-  const bool shared = g >= a.n_expert;
-  const sg_block_q4k* ma = shared ? a.sh_a : a.tab_a[g];
-  const sg_block_q4k* mb = kGateUp ? (shared ? a.sh_b : a.tab_b[g]) : ma;
-  const sg_block_q4k* mc = shared ? a.sh_c : a.tab_c[g];
+  // gate/up pass: gate rows (a) and up rows (b); down pass: down rows
+  const sg_block_q4k* ma = reinterpret_cast<const sg_block_q4k*>(kGateUp ? rec.wg : rec.wd);
+  const sg_block_q4k* mb = reinterpret_cast<const sg_block_q4k*>(kGateUp ? rec.wu : rec.wd);
   const int nb = a.nb;
   // down: output columns [c0, c0 + 128) from weight rows c0 ..; gate/up:
   // h columns [c0, c0 + 64) from gate rows c0 .. (waves 0-3) and the same
@@ -314,7 +315,7 @@ grouped_mfma_kernel(GroupedArgs a) {
   const int c0 = slice * (kGateUp ? kRowsWg / 2 : kRowsWg);
   const int lr = lane & 15, lq = lane >> 4;     // MFMA: row/column in the tile, K quarter
 
-  if (!ma || !mb || !mc) {  // absent expert: its outputs are zero
+  if (!ma) {  // absent expert (a null gate, up or down matrix): its outputs are zero
     for (long long p = p0; p < p1; ++p)
       for (int r = tid; r < (kGateUp ? kRowsWg / 2 : kRowsWg); r += kThreads)
         a.out[p * a.n_out + c0 + r] = 0.f;
@@ -343,6 +344,7 @@ grouped_mfma_kernel(GroupedArgs a) {
       if (64 * i + lane < kWChunks)
         dma16(wbuf0 + 4 * (wave * kWChunks + 64 * i), wofs[i], rw4, b * kQ4Bytes);
   };
+  stage_w(0);  // the first weight block needs only the record: issued before the token rows
   // the tile's token rows of super-block b into token buffer s, 76 words per
   // token in 16-B chunks: chunks 0-15 the 64 qs words, 16 the split bsums
   // (eight lo bytes, eight hi bytes), 17 d and three pad words, 18 padding
@@ -392,7 +394,6 @@ grouped_mfma_kernel(GroupedArgs a) {
     return __builtin_bit_cast(int, __builtin_bit_cast(u16x2, q) * __builtin_bit_cast(u16x2, s2));
   };
 
-  stage_w(0);
   stage_x(0, 0);
   SG_PF_MARK(1);
   for (int b = 0; b < nb; ++b) {
@@ -598,8 +599,10 @@ __global__ void __launch_bounds__(1024) scan_offsets_kernel(
     const int* __restrict__ idx, const uint32_t* __restrict__ wbits, const int* __restrict__ wflags,
     int* __restrict__ woff, int* __restrict__ gslot, int* __restrict__ grows, int* __restrict__ off,
     int* __restrict__ toff, int* __restrict__ meta, int* __restrict__ tiles,
-    int4* __restrict__ trec, int n_rec, int n_rows, int k, int E, int n_w, int tok_per,
-    int shared_tail) {
+    TileRec* __restrict__ trec, int n_rec, const sg_block_q4k* const* tab_g,
+    const sg_block_q4k* const* tab_u, const sg_block_q4k* const* tab_d, const sg_block_q4k* sh_g,
+    const sg_block_q4k* sh_u, const sg_block_q4k* sh_d, int n_rows, int k, int E, int n_w,
+    int tok_per, int shared_tail) {
   __shared__ int hist[1024], part[1024];
   __shared__ int s_bad, s_dup, s_total;
   extern __shared__ uint32_t wb_lds[];  // a copy of wbits when it fits (kScanBitsLds words)
@@ -675,14 +678,28 @@ __global__ void __launch_bounds__(1024) scan_offsets_kernel(
       for (int j = tid; j < sh_t; j += nth) tiles[1 + tot_t + j] = (E << 16) | j;
       if (tid == 0) tiles[0] = tot_t + sh_t;
     }
-    if (trec) {  // the same work list as records {group, first, end position}, -1 beyond it
-      if (tid < E)
+    if (trec) {  // the same work list as records with the matrices, group -1 beyond it
+      auto put = [&](int t, int g, int p0, int p1, const sg_block_q4k* mg, const sg_block_q4k* mu,
+                     const sg_block_q4k* md) {
+        const bool present = mg && mu && md;
+        trec[t] = TileRec{g, p0, p1, 0,
+                          present ? reinterpret_cast<unsigned long long>(mg) : 0ull,
+                          present ? reinterpret_cast<unsigned long long>(mu) : 0ull,
+                          present ? reinterpret_cast<unsigned long long>(md) : 0ull, 0ull};
+      };
+      if (tid < E && tl > 0) {
+        const sg_block_q4k* mg = tab_g[tid];
+        const sg_block_q4k* mu = tab_u[tid];
+        const sg_block_q4k* md = tab_d[tid];
         for (int j = 0; j < tl; ++j)
-          trec[pt + j] = int4{tid, ph + tok_per * j, min(ph + h, ph + tok_per * (j + 1)), 0};
+          put(pt + j, tid, ph + tok_per * j, min(ph + h, ph + tok_per * (j + 1)), mg, mu, md);
+      }
       const int sh_t = (shared_tail + tok_per - 1) / tok_per;
       for (int j = tid; j < sh_t; j += nth)
-        trec[tot_t + j] = int4{E, tot_h + tok_per * j, min(tot_h + shared_tail, tot_h + tok_per * (j + 1)), 0};
-      for (int t = tot_t + sh_t + tid; t < n_rec; t += nth) trec[t] = int4{-1, 0, 0, 0};
+        put(tot_t + j, E, tot_h + tok_per * j, min(tot_h + shared_tail, tot_h + tok_per * (j + 1)),
+            sh_g, sh_u, sh_d);
+      for (int t = tot_t + sh_t + tid; t < n_rec; t += nth)
+        trec[t] = TileRec{-1, 0, 0, 0, 0ull, 0ull, 0ull, 0ull};
     }
     if (tid < E) hist[tid] = ph;  // hist now holds off[e]
   }
@@ -906,7 +923,7 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
   w.meta = o;  o = al256(o + 4 * 4);
   w.max_tiles = (T * k + kTokTile - 1) / kTokTile + E + (T + kTokTile - 1) / kTokTile;
   w.tiles = o; o = al256(o + static_cast<size_t>(1 + w.max_tiles) * 4);
-  w.trec = o;  o = al256(o + static_cast<size_t>(w.max_tiles) * 16);
+  w.trec = o;  o = al256(o + static_cast<size_t>(w.max_tiles) * sizeof(TileRec));
   w.plan = o;  o = al256(o + plan_ws(T, E).total);
   w.sgate = o; o = al256(o + static_cast<size_t>(T) * 4);
   w.h = o;     o = al256(o + static_cast<size_t>(w.P) * n_ff * 4);
@@ -945,10 +962,17 @@ static int scan_launch(const int* idx, float* weight, int* gslot, int* grows, in
 }
 
 // the plan over many workgroups (bits, offsets, placement) on scratch `ws`
+struct PlanTables {  // the matrices the tile records carry (all null: no records)
+  const sg_block_q4k* const* g;
+  const sg_block_q4k* const* u;
+  const sg_block_q4k* const* d;
+  const sg_block_q4k *sg, *su, *sd;
+};
+
 static int plan_launch(const int* idx, float* weight, int* gslot, int* grows, int* off,
-                       int* toff, int* meta, int* tiles, int4* trec, int n_rec, unsigned char* ws,
-                       int n_rows, int k, int E, int tok_per, int shared_tail, hipStream_t s,
-                       const char* nm) {
+                       int* toff, int* meta, int* tiles, TileRec* trec, int n_rec,
+                       const PlanTables& pt, unsigned char* ws, int n_rows, int k, int E,
+                       int tok_per, int shared_tail, hipStream_t s, const char* nm) {
   const PlanWs p = plan_ws(n_rows, E);
   uint32_t* wbits = reinterpret_cast<uint32_t*>(ws + p.wbits);
   int* woff = reinterpret_cast<int*>(ws + p.woff);
@@ -959,8 +983,8 @@ static int plan_launch(const int* idx, float* weight, int* gslot, int* grows, in
   const size_t bits_lds =
       p.n_w * E <= kScanBitsLds ? static_cast<size_t>(p.n_w) * E * 4 : 0;
   hipLaunchKernelGGL(scan_offsets_kernel, dim3(1), dim3(1024), bits_lds, s, idx, wbits, wflags,
-                     woff, gslot, grows, off, toff, meta, tiles, trec, n_rec, n_rows, k, E, p.n_w,
-                     tok_per, shared_tail);
+                     woff, gslot, grows, off, toff, meta, tiles, trec, n_rec, pt.g, pt.u, pt.d,
+                     pt.sg, pt.su, pt.sd, n_rows, k, E, p.n_w, tok_per, shared_tail);
   if (int st = check_launch(nm)) return st;
   hipLaunchKernelGGL(scan_place_kernel, dim3(p.n_w), dim3(256), 0, s, idx, wbits, wflags, woff,
                      gslot, grows, n_rows, k, E, p.n_w);
@@ -1019,7 +1043,7 @@ int sg_moe_dispatch_plan(const int* idx, float* weight, int* gslot, int* grows, 
   if (workspace_bytes < plan_ws(n_rows, n_expert).total)
     return set_error(SG_ERR_INVALID_ARGUMENT, "%s: workspace %zu < %zu bytes", nm,
                      workspace_bytes, plan_ws(n_rows, n_expert).total);
-  return plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, nullptr, 0,
+  return plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, nullptr, 0, PlanTables{},
                      static_cast<unsigned char*>(workspace), n_rows, k, n_expert, tok_per,
                      shared_tail, static_cast<hipStream_t>(stream), nm);
 }
@@ -1061,7 +1085,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   int* toff = reinterpret_cast<int*>(base + ws.toff);
   int* meta = reinterpret_cast<int*>(base + ws.meta);
   int* tiles = reinterpret_cast<int*>(base + ws.tiles);
-  int4* trec = reinterpret_cast<int4*>(base + ws.trec);
+  TileRec* trec = reinterpret_cast<TileRec*>(base + ws.trec);
   float* h = reinterpret_cast<float*>(base + ws.h);
   auto* hq = reinterpret_cast<sg_block_q8k*>(base + ws.hq);
   float* y = reinterpret_cast<float*>(base + ws.y);
@@ -1080,18 +1104,13 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
                                 stream))
       return st;
   if (int st = plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, trec, ws.max_tiles,
+                           PlanTables{tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down},
                            base + ws.plan,
                            n_tokens, k, n_expert, kTokTile, has_shared ? n_tokens : 0, s,
                            "sg_moe_prefill/plan"))
     return st;
   const int G = n_expert + has_shared;
   GroupedArgs ga{};
-  ga.tab_a = tab_gate;
-  ga.tab_b = tab_up;
-  ga.tab_c = tab_down;
-  ga.sh_a = sh_gate;
-  ga.sh_b = sh_up;
-  ga.sh_c = sh_down;
   ga.xq = reinterpret_cast<const unsigned char*>(xq);
   ga.off = off;
   ga.grows = grows;
@@ -1101,7 +1120,6 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   ga.nb = hidden / kQK;
   ga.n_rows = n_ff;
   ga.n_out = n_ff;
-  ga.n_expert = n_expert;
   ga.n_groups = G;
   // 1-D grids: a multiple of 8 tiles (one per XCD) times the slices
   const int tiles8 = (ws.max_tiles + 7) / 8 * 8;
@@ -1111,12 +1129,6 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   if (int st = check_launch("sg_moe_prefill/gate_up")) return st;
   if (int st = quantize_split(h, hq, n_ff / kQK, ws.P, s, nm)) return st;
   GroupedArgs gd = ga;
-  gd.tab_a = tab_down;
-  gd.tab_b = tab_down;
-  gd.tab_c = tab_gate;  // an expert without gate/up contributes zero
-  gd.sh_a = sh_down;
-  gd.sh_b = sh_down;
-  gd.sh_c = sh_gate;
   gd.xq = reinterpret_cast<const unsigned char*>(hq);
   gd.grows = nullptr;
   gd.out = y;
