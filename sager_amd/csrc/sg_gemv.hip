@@ -12,6 +12,9 @@
 // acc += sum order, q4_avx2.cpp:130-143) with DPP lane shifts.  The next group's copy is issued
 // as soon as the block is in registers, so it overlaps the arithmetic.
 //
+// Small matrices (up to 262144 super-blocks) take gemv_lat_kernel instead:
+// four lanes per super-block, loads straight into registers, one pass.
+//
 // Reference kernels replaced: gemv_q4_k_q8 / gemv_mtok_ro_f32_kernel
 // (q4_k.cu:57-91, 1360-1422, 1534-1562), gemv_q4_k_q8_batched and the mtok
 // variants (q4_k.cu:218-282, 359-498), gemv_ptrs_q4_k_q8_f16out
@@ -19,6 +22,20 @@
 #include "sg_common.hpp"
 
 namespace sg {
+
+// ---- latency timeline (built only with -DSG_TIMELINE; no code otherwise) ----
+#ifdef SG_TIMELINE
+constexpr int kGvMax = 4096;
+static __device__ unsigned long long gv_stamps[kGvMax * 16];
+__device__ __forceinline__ void gv_mark(int slot) {
+  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+  const int i = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if ((threadIdx.x & 63) == 0 && i < kGvMax) gv_stamps[i * 16 + slot] = t;
+}
+#define SG_GV_MARK(slot) gv_mark(slot)
+#else
+#define SG_GV_MARK(slot) ((void)0)
+#endif
 
 constexpr int kMaxNb = 64;       // k <= 16384
 constexpr int kMaxTokens = 16;   // batched GEMV token tile
@@ -163,13 +180,16 @@ __global__ void __launch_bounds__(64 * NWV) gemv1_kernel(Rows rows,
   const int NW = gridDim.x * NWV;
   const int g_begin = blockIdx.x * NWV + wv, g_end = n_groups;
   auto rows_of = [&](int gg) { return min(rpw, n_rows - gg * rpw); };
+  SG_GV_MARK(0);
   // the first group's weights first: their HBM latency overlaps the staging
   if (g_begin < g_end) dma_rows(rows, g_begin * rpw, rows_of(g_begin), nb, wbuf[wv], lane);
+  SG_GV_MARK(1);
   stage_q8k(xq, nb, xs_dyn, threadIdx.x, blockDim.x);
   uint32_t* tab = xs_dyn + nb * kXStride;  // row table, when the rows have one
   rows.stage(tab, threadIdx.x, blockDim.x);
   float* res = reinterpret_cast<float*>(tab + rows.table_words()) + wv * gpw * rpw;
   bar();
+  SG_GV_MARK(2);
   rows.attach(tab);
 
   const int blk = lane & (lpr - 1);
@@ -182,6 +202,7 @@ __global__ void __launch_bounds__(64 * NWV) gemv1_kernel(Rows rows,
   for (int g = g_begin, li = 0; g < g_end; g += NW, ++li) {
     const int n = rows_of(g);
     wait_vm();  // group g has landed
+    if (li == 0) SG_GV_MARK(3);
     uint32_t w36[36];
     const bool live = active && rr < n;
     if (live) read_block_lds(wbuf[wv] + (rr * nb + blk) * 36, w36);
@@ -191,12 +212,108 @@ __global__ void __launch_bounds__(64 * NWV) gemv1_kernel(Rows rows,
     const float acc = row_sum_last(s, blk, nb);
     if (blk == nb - 1 && rr < n) res[li * rpw + rr] = acc;
   }
+  SG_GV_MARK(4);
   wait_lds();  // this wave's result writes (read back by its own lanes)
   // result li * rpw + row of the wave belongs to group g_begin + li * NW
   for (int i = lane; i < gpw * rpw; i += 64) {
     const int r = (g_begin + (i / rpw) * NW) * rpw + i % rpw;
     if (r < n_rows) out.store(r, res[i]);
   }
+  SG_GV_MARK(5);
+}
+
+// y[r] = W[r] . x for a small matrix (latency-bound: a few MB, read in one
+// pass by the whole chip).  Four lanes share a super-block, each taking one
+// sub-block pair (8 qs words of weights, 16 qs words of activations), so a
+// 2048 x 2048 matrix spreads over 1024 one-wave workgroups instead of 256
+// waves.  Every lane loads its weight and activation words straight into
+// registers at entry: no LDS, no barrier, one memory latency before the
+// arithmetic.  The super-block epilogue keeps the reference's order
+// (sum = fma(xd, t_s, sum) for s = 0..7, q4_avx2.cpp:30-39,134-141): the
+// running sum moves from the lane of pair p to that of pair p+1 with a DPP
+// row shift, and the row's block sums are then added in block order by
+// row_sum_last after one lane permute.  nb <= 16 (k <= 4096).
+constexpr int kLatMaxNb = 16;
+#ifndef SG_LAT_WAVES
+#define SG_LAT_WAVES 4
+#endif
+constexpr int kLatWaves = SG_LAT_WAVES;  // waves per workgroup
+constexpr int kDppRowShr1 = 0x111;
+typedef uint32_t u32x4u __attribute__((ext_vector_type(4), aligned(4)));
+
+template <typename Rows, typename Out>
+__global__ void __launch_bounds__(64 * kLatWaves) gemv_lat_kernel(
+    Rows rows, const unsigned char* __restrict__ xq, Out out, int n_rows, int nb, int lpr) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * kLatWaves + (threadIdx.x >> 6);
+  const int part = lane & 3, blk = (lane >> 2) & (lpr - 1), rr = lane / (4 * lpr);
+  const int rpw = 16 / lpr;
+  const int r = wave * rpw + rr;
+  const bool live = blk < nb && r < n_rows;
+  SG_GV_MARK(0);
+  // every lane loads (clamped to a valid block) and dead lanes zero their
+  // words afterwards: no branch, so all arguments are fetched in one round
+  const u32x4* wp = reinterpret_cast<const u32x4*>(rows.row(min(r, n_rows - 1)) +
+                                                   min(blk, nb - 1) * kQ4Bytes);
+  u32x4 h = wp[0], qa = wp[1 + 2 * part], qb = wp[2 + 2 * part];
+  const unsigned char* xb = xq + min(blk, nb - 1) * kQ8Bytes;
+  const u32x4u* xp = reinterpret_cast<const u32x4u*>(xb + 4 + 64 * part);
+  uint32_t xw[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4u v = xp[i];
+    xw[4 * i] = v.x;
+    xw[4 * i + 1] = v.y;
+    xw[4 * i + 2] = v.z;
+    xw[4 * i + 3] = v.w;
+  }
+  float xd = *reinterpret_cast<const float*>(xb);
+  uint32_t bs = *reinterpret_cast<const uint32_t*>(xb + 260 + 4 * part);
+  if (!live) {
+    h = u32x4{0u, 0u, 0u, 0u};
+    qa = h;
+    qb = h;
+    bs = 0;
+    xd = 0.f;
+  }
+  SG_GV_MARK(1);
+  const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+  int32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    lo = __builtin_amdgcn_sdot4(static_cast<int>(q[j] & 0x0F0F0F0Fu), static_cast<int>(xw[j]), lo,
+                                false);
+    hi = __builtin_amdgcn_sdot4(static_cast<int>((q[j] >> 4) & 0x0F0F0F0Fu),
+                                static_cast<int>(xw[8 + j]), hi, false);
+  }
+  const ScaleMins sm8 = unpack_scales(h.y, h.z, h.w);
+  const float d = half_bits_to_float(h.x & 0xFFFFu);
+  const float dmin = half_bits_to_float(h.x >> 16);
+  const uint32_t scw = part < 2 ? sm8.sc_lo : sm8.sc_hi;
+  const uint32_t mnw = part < 2 ? sm8.mn_lo : sm8.mn_hi;
+  const int i0 = (2 * part) & 3;
+  const float b0 = static_cast<float>(static_cast<int16_t>(bs & 0xFFFFu));
+  const float b1 = static_cast<float>(static_cast<int16_t>(bs >> 16));
+  const float t0 = __builtin_fmaf(d * byte_f(scw, i0), static_cast<float>(lo),
+                                  -((dmin * byte_f(mnw, i0)) * b0));
+  const float t1 = __builtin_fmaf(d * byte_f(scw, i0 + 1), static_cast<float>(hi),
+                                  -((dmin * byte_f(mnw, i0 + 1)) * b1));
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float prev = j == 0 ? 0.f : dpp_f<kDppRowShr1>(acc);
+    if (part == j) acc = __builtin_fmaf(xd, t1, __builtin_fmaf(xd, t0, prev));
+  }
+  // block sums (lane 4b+3 of each row) to lanes row*lpr + b
+  const int c = lane & 15;
+  const int src = (c / lpr) * 4 * lpr + 4 * (c & (lpr - 1)) + 3;
+  const float sb = __builtin_bit_cast(
+      float, __builtin_amdgcn_ds_bpermute(src << 2, __builtin_bit_cast(int, acc)));
+  const int cb = c & (lpr - 1);
+  const float row = row_sum_last(sb, cb, nb);
+  const int ro = wave * rpw + c / lpr;
+  if (lane < 16 && cb == nb - 1 && ro < n_rows) out.store(ro, row);
+  SG_GV_MARK(2);
 }
 
 // y[t*n_rows + r] = W[r] . x[t] for t < n_tokens; weights read once.  The
@@ -311,9 +428,31 @@ static Gemv1Launch gemv1_launch(long long n_groups, int rpw) {
   return l;
 }
 
+// Matrices of at most this many super-blocks (and nb <= 16) take
+// gemv_lat_kernel.  Measured with cold matrices (graph replays over rotated
+// copies), it is faster up to 32768 x 2048 (2048 x 2048: 3.35 against
+// 4.84 us); from 65536 x 2048 on, the streaming kernel is (248320 x 2048:
+// 52 against 57 us).
+#ifndef SG_LAT_MAX_BLOCKS
+#define SG_LAT_MAX_BLOCKS 262144
+#endif
+static bool use_lat(int n_rows, int nb) {
+  return nb <= kLatMaxNb && static_cast<long long>(n_rows) * nb <= SG_LAT_MAX_BLOCKS;
+}
+template <typename Rows, typename Out>
+static void gemv_lat_go(hipStream_t s, Rows rows, const sg_block_q8k* x, Out out, int n_rows,
+                        int nb) {
+  const int lpr = lanes_per_row(nb), rpw = 16 / lpr;
+  const int waves = (n_rows + rpw - 1) / rpw;
+  hipLaunchKernelGGL((gemv_lat_kernel<Rows, Out>), dim3((waves + kLatWaves - 1) / kLatWaves),
+                     dim3(64 * kLatWaves), 0, s,
+                     rows, reinterpret_cast<const unsigned char*>(x), out, n_rows, nb, lpr);
+}
+
 template <typename Rows, typename Out>
 static void gemv1_go(const Gemv1Launch& L, size_t lds, hipStream_t s, Rows rows,
                      const sg_block_q8k* x, Out out, int n_rows, int nb, int lpr) {
+  if (use_lat(n_rows, nb)) return gemv_lat_go(s, rows, x, out, n_rows, nb);
   const unsigned char* xb = reinterpret_cast<const unsigned char*>(x);
   if (L.nwv == 1)
     hipLaunchKernelGGL((gemv1_kernel<Rows, Out, 1>), dim3(L.grid), dim3(64), lds, s, rows, xb, out,
@@ -488,5 +627,15 @@ int sg_gemv_q4_k_q8_f16out_resadd(const sg_block_q4k* w, const sg_block_q8k* x, 
   return launch_gemv1(PlainRows{w, k / kQK}, x, F16ResAddOut{y, res_inout}, n_rows, k,
                       static_cast<hipStream_t>(stream), nm);
 }
+
+#ifdef SG_TIMELINE
+int sg_debug_gemv_timeline(unsigned long long* host) {
+  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(gv_stamps), sizeof(gv_stamps)) != hipSuccess)
+    return SG_ERR_HIP;
+  static unsigned long long zeros[kGvMax * 16];
+  return hipMemcpyToSymbol(HIP_SYMBOL(gv_stamps), zeros, sizeof(zeros)) == hipSuccess ? SG_OK
+                                                                                    : SG_ERR_HIP;
+}
+#endif
 
 }  // extern "C"

@@ -93,7 +93,8 @@ def test_gemv_golden(gold, case):
 
 
 @pytest.mark.parametrize("n_rows,k", [(2048, 2048), (512, 2048), (2048, 512), (1001, 768),
-                                      (3, 256), (70, 16384), (4096, 4096)])
+                                      (3, 256), (70, 16384), (4096, 4096), (777, 2304),
+                                      (32768, 2048), (32769, 2048)])
 def test_gemv_shapes(n_rows, k):
     rng = np.random.default_rng(7 * n_rows + k)
     w, xq = _case(rng, n_rows, k)
