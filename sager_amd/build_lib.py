@@ -23,6 +23,10 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the first 16 dwords of scalar (non-struct) kernel arguments arrive in
+    # SGPRs at wave start, so a kernel's first loads do not wait for a
+    # kernel-argument fetch (2048 x 2048 GEMV, cold: 3.25 -> 2.86 us)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall", "-Wno-unused-function",
 ]
 

@@ -19,6 +19,8 @@
 // (q4_k.cu:57-91, 1360-1422, 1534-1562), gemv_q4_k_q8_batched and the mtok
 // variants (q4_k.cu:218-282, 359-498), gemv_ptrs_q4_k_q8_f16out
 // (q4_k.cu:184-213).
+#include <type_traits>
+
 #include "sg_common.hpp"
 
 namespace sg {
@@ -242,12 +244,13 @@ constexpr int kDppRowShr1 = 0x111;
 typedef uint32_t u32x4u __attribute__((ext_vector_type(4), aligned(4)));
 
 template <typename Rows, typename Out>
-__global__ void __launch_bounds__(64 * kLatWaves) gemv_lat_kernel(
-    Rows rows, const unsigned char* __restrict__ xq, Out out, int n_rows, int nb, int lpr) {
+__device__ __forceinline__ void gemv_lat_body(const Rows& rows, const unsigned char* __restrict__ xq,
+                                              const Out& out, int n_rows, int nb, int lg) {
+  const int lpr = 1 << lg;
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * kLatWaves + (threadIdx.x >> 6);
-  const int part = lane & 3, blk = (lane >> 2) & (lpr - 1), rr = lane / (4 * lpr);
-  const int rpw = 16 / lpr;
+  const int part = lane & 3, blk = (lane >> 2) & (lpr - 1), rr = lane >> (2 + lg);
+  const int rpw = 16 >> lg;
   const int r = wave * rpw + rr;
   const bool live = blk < nb && r < n_rows;
   SG_GV_MARK(0);
@@ -306,14 +309,26 @@ __global__ void __launch_bounds__(64 * kLatWaves) gemv_lat_kernel(
   }
   // block sums (lane 4b+3 of each row) to lanes row*lpr + b
   const int c = lane & 15;
-  const int src = (c / lpr) * 4 * lpr + 4 * (c & (lpr - 1)) + 3;
+  const int src = ((c >> lg) << (2 + lg)) + 4 * (c & (lpr - 1)) + 3;
   const float sb = __builtin_bit_cast(
       float, __builtin_amdgcn_ds_bpermute(src << 2, __builtin_bit_cast(int, acc)));
   const int cb = c & (lpr - 1);
   const float row = row_sum_last(sb, cb, nb);
-  const int ro = wave * rpw + c / lpr;
+  const int ro = wave * rpw + (c >> lg);
   if (lane < 16 && cb == nb - 1 && ro < n_rows) out.store(ro, row);
   SG_GV_MARK(2);
+}
+template <typename Rows, typename Out>
+__global__ void __launch_bounds__(64 * kLatWaves) gemv_lat_kernel(
+    Rows rows, const unsigned char* __restrict__ xq, Out out, int n_rows, int nb, int lg) {
+  gemv_lat_body(rows, xq, out, n_rows, nb, lg);
+}
+// The plain fp32 GEMV with scalar arguments only, which the code object can
+// preload into SGPRs (no kernel-argument load before the first address).
+__global__ void __launch_bounds__(64 * kLatWaves) gemv_lat_plain_kernel(
+    const sg_block_q4k* __restrict__ w, const unsigned char* __restrict__ xq, float* y, int n_rows,
+    int nb, int lg) {
+  gemv_lat_body(PlainRows{w, nb}, xq, F32Out{y}, n_rows, nb, lg);
 }
 
 // y[t*n_rows + r] = W[r] . x[t] for t < n_tokens; weights read once.  The
@@ -444,9 +459,14 @@ static void gemv_lat_go(hipStream_t s, Rows rows, const sg_block_q8k* x, Out out
                         int nb) {
   const int lpr = lanes_per_row(nb), rpw = 16 / lpr;
   const int waves = (n_rows + rpw - 1) / rpw;
-  hipLaunchKernelGGL((gemv_lat_kernel<Rows, Out>), dim3((waves + kLatWaves - 1) / kLatWaves),
-                     dim3(64 * kLatWaves), 0, s,
-                     rows, reinterpret_cast<const unsigned char*>(x), out, n_rows, nb, lpr);
+  const dim3 grid((waves + kLatWaves - 1) / kLatWaves), block(64 * kLatWaves);
+  const unsigned char* xb = reinterpret_cast<const unsigned char*>(x);
+  const int lg = __builtin_ctz(lpr);
+  if constexpr (std::is_same_v<Rows, PlainRows> && std::is_same_v<Out, F32Out>)
+    hipLaunchKernelGGL(gemv_lat_plain_kernel, grid, block, 0, s, rows.w, xb, out.y, n_rows, nb, lg);
+  else
+    hipLaunchKernelGGL((gemv_lat_kernel<Rows, Out>), grid, block, 0, s, rows, xb, out, n_rows, nb,
+                       lg);
 }
 
 template <typename Rows, typename Out>
