@@ -591,18 +591,6 @@ __device__ __forceinline__ void make_plan(uint32_t* dyn, const FrontLds& L, int 
     build_plan(dyn, L, T, k, E, has_shared, tid);
 }
 
-// Maximum of a 64-bit key over the wave (butterfly), same value in every lane.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), o, 64);
-    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), o, 64);
-    const uint64_t w = (static_cast<uint64_t>(hi) << 32) | lo;
-    v = w > v ? w : v;
-  }
-  return v;
-}
-
 // Whether the exact routing of one token (route_wave) is sure to select the
 // logit-order ids top[0..k) in that order, decided by one wave from the
 // k+1 leading logits alone, without the normalizer: every logit finite

@@ -21,6 +21,48 @@ __device__ __forceinline__ uint64_t sel_key(float v, int i) {
 __device__ __forceinline__ int sel_idx(uint64_t key) {
   return static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(key));
 }
+// The value of a key made from a non-NaN float (-0 comes back as +0).
+__device__ __forceinline__ float sel_val(uint64_t key) {
+  const uint32_t o = static_cast<uint32_t>(key >> 32);
+  return __builtin_bit_cast(float, (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+
+// Largest 32-bit value over the wave, the same in every lane (DPP within
+// each 16-lane row, then the four row maxima).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, static_cast<uint32_t>(dpp_i<kDppXor1>(static_cast<int>(v))));
+  v = max(v, static_cast<uint32_t>(dpp_i<kDppXor2>(static_cast<int>(v))));
+  v = max(v, static_cast<uint32_t>(dpp_i<kDppHalfMirror>(static_cast<int>(v))));
+  v = max(v, static_cast<uint32_t>(dpp_i<kDppMirror>(static_cast<int>(v))));
+  const uint32_t a = __builtin_amdgcn_readlane(static_cast<int>(v), 0);
+  const uint32_t b = __builtin_amdgcn_readlane(static_cast<int>(v), 16);
+  const uint32_t c = __builtin_amdgcn_readlane(static_cast<int>(v), 32);
+  const uint32_t d = __builtin_amdgcn_readlane(static_cast<int>(v), 48);
+  return max(max(a, b), max(c, d));
+}
+
+// Largest 64-bit key over the wave, the same in every lane: DPP exchanges
+// within each 16-lane row, then the four row maxima.  No branches.
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const int lo = dpp_i<CTRL>(static_cast<int>(static_cast<uint32_t>(v)));
+  const int hi = dpp_i<CTRL>(static_cast<int>(static_cast<uint32_t>(v >> 32)));
+  return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), l);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), l);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = max_u64(v, dpp_u64<kDppXor1>(v));
+  v = max_u64(v, dpp_u64<kDppXor2>(v));
+  v = max_u64(v, dpp_u64<kDppHalfMirror>(v));
+  v = max_u64(v, dpp_u64<kDppMirror>(v));
+  return max_u64(max_u64(readlane_u64(v, 0), readlane_u64(v, 16)),
+                 max_u64(readlane_u64(v, 32), readlane_u64(v, 48)));
+}
 
 // Top-m keys (m <= 33) of keys[0..n) for a team of nthr threads (thread tt).
 // Two levels: the top m of every 64-key group (rank by direct comparison
