@@ -168,7 +168,7 @@ __host__ __device__ inline FrontLds front_lds(int T, int nbh, int E, int k, bool
     L.tabu = take(E * 2);
     L.tabd = take(E * 2);
     L.lv = take(L.nteams * L.e32);
-    L.ev = take(L.nteams * L.e32);
+    L.ev = take(4 * L.e32);  // a team's (one token) or a wave's (routing launch) exps
     L.cand = take(L.nteams * L.ncp * 2);
     L.top = take(L.nteams * L.m * 2);
     L.red = take(L.nteams * 4);
@@ -305,27 +305,50 @@ __device__ __forceinline__ void build_plan(uint32_t* dyn, const FrontLds& L, int
   const int gbase = has_shared, ebase = has_shared ? T : 0;
   if (R <= 64) {
     if (tid < 64) {
+      // every lane reads all R ids (and first flags) back from LDS with
+      // broadcast 16-B reads: the wave's own writes, visible to its later
+      // reads without a barrier (cross-lane register reads in a loop would
+      // wait on each other in turn)
       const int lane = tid;
       int e = lane < R ? ridx[lane] : -1;
-      if (e >= E) e = -1;
-      bool first = e >= 0;
-      for (int j = 0; j < R; ++j) {
-        const int ej = __builtin_amdgcn_readlane(e, j);
-        first &= !(j < lane && ej == e);
-      }
-      const int fi = first;
-      int rank = 0, grp = 0;
-      for (int j = 0; j < R; ++j) {
-        const int ej = __builtin_amdgcn_readlane(e, j);
-        const int fj = __builtin_amdgcn_readlane(fi, j);
-        if (ej >= 0) {
-          rank += ej < e || (ej == e && j < lane);
-          grp += fj && ej < e;
+      if (e < 0 || e >= E) e = -1;
+      if (lane < R) re[lane] = e;
+      // The flags are sign bits of integer differences (ids lie in
+      // [-1, 1024)), so the loops are plain integer arithmetic: comparisons
+      // would each make a lane mask, and 4 R of them exhaust the scalar
+      // registers.
+      // (a bit-field extract, which the compiler keeps as arithmetic)
+      auto lt = [](int x, int y) {
+        return static_cast<int>(__builtin_amdgcn_ubfe(static_cast<unsigned>(x - y), 31, 1));
+      };
+      auto eq = [](int x, int y) {
+        return static_cast<int>(__builtin_amdgcn_ubfe(static_cast<unsigned>((x ^ y) - 1), 31, 1));
+      };
+      int dup = 0, rank = 0;
+      for (int j0 = 0; j0 < R; j0 += 4) {
+        const int4 v = *reinterpret_cast<const int4*>(re + j0);
+        const int ev4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int j = j0 + u, ej = ev4[u];
+          const int ok = lt(j, R) & (1 - lt(ej, 0));
+          const int before = lt(j, lane), same = eq(ej, e);
+          rank += ok & (lt(ej, e) | (same & before));
+          dup |= ok & before & same;
         }
+      }
+      const bool first = e >= 0 && !dup;
+      if (lane < R) rfirst[lane] = first;
+      int grp = 0;
+      for (int j0 = 0; j0 < R; j0 += 4) {
+        const int4 v = *reinterpret_cast<const int4*>(re + j0);
+        const int4 f = *reinterpret_cast<const int4*>(rfirst + j0);
+        const int ev4[4] = {v.x, v.y, v.z, v.w}, fv4[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) grp += lt(j0 + u, R) & fv4[u] & lt(ev4[u], e);
       }
       const int nv = __popcll(__ballot(e >= 0));
       const int nf = __popcll(__ballot(first));
-      if (lane < R) re[lane] = e;
       if (e >= 0) {
         ptok[ebase + rank] = lane / k;
         pslot[ebase + rank] = lane % k;
@@ -1033,7 +1056,21 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   int e_mine = -1, slot_mine = -1;
   bool present_mine = false;
   int n_groups;
-  if (a.logits && publisher && T == 1) {
+  if (a.logits && publisher && T > 1) {
+    // the routing launch of several tokens: one wave per token, each the
+    // standalone router's exact routing (router_wave), then the plan
+    // experts per lane: E <= 64 kPl (the launch picks EPT with E <= 128 EPT)
+    constexpr int kPl = 2 * EPT < 16 ? 2 * EPT : 16;
+    float* evw = reinterpret_cast<float*>(dyn + L.ev) + wave * L.e32;
+    for (int t = wave; t < T; t += 4)
+      router_wave<kPl>(a.logits + static_cast<long long>(t) * E, E, k, a.shared_w, ridx + t * k,
+                       rw + t * stride, evw, lane);
+    SG_MARK_FRONT(9);
+    bar();
+    build_plan(dyn, L, T, k, E, a.has_shared, tid);
+    SG_MARK_FRONT(10);
+    n_groups = gbase + ctrl[1];
+  } else if (a.logits && publisher && T == 1) {
     // the publisher routes exactly from the logits with every wave; it has
     // no stream to start and needs the weights, not the logit order
 #ifdef SG_TL_TWICE

@@ -126,4 +126,95 @@ __device__ __forceinline__ float serial_sum(const float* x, int n32) {
   return z;
 }
 
+// ---- router: one wave per token row ----------------------------------------
+// Softmax with the max and the normalizer sum taken in index order, k rounds
+// of (value desc, index asc) argmax over non-NaN probabilities, degenerate
+// rounds pick kk % n_expert, weights renormalized by their k-order sum,
+// slot k = shared_w.  oi/ow may point to LDS or global memory; lane 0
+// writes them.  All 64 lanes must be active.  PL = experts per lane
+// (n_expert <= 64 PL).
+template <int PL>
+__device__ __forceinline__ void router_wave(const float* __restrict__ lg, int n_expert, int k, float shared_w,
+                            int* oi, float* ow, float* ev, int lane) {
+  constexpr int kPerLane = PL;
+  float p[kPerLane];
+  float mx = -1e30f;
+#pragma unroll
+  for (int j = 0; j < kPerLane; ++j) {
+    const int i = lane + 64 * j;
+    const float v = lg[i < n_expert ? i : n_expert - 1];  // no branch: one wait for all
+    p[j] = i < n_expert ? v : 0.f;
+    if (i < n_expert) mx = fmaxf(mx, p[j]);
+  }
+  mx = wave_max_dpp(mx);
+  const int e32 = (n_expert + 31) & ~31;
+#pragma unroll
+  for (int j = 0; j < kPerLane; ++j) {
+    const int i = lane + 64 * j;
+    if (i < n_expert) p[j] = expf_sg(p[j] - mx);
+    if (i < e32) ev[i] = i < n_expert ? p[j] : 0.f;  // +0 padding leaves the sum unchanged
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // normalizer z = (((0 + e_0) + e_1) + ...) in index order, by one lane
+  float z = lane == 0 ? serial_sum(ev, e32) : 0.f;
+  z = readlane_f(z, 0);
+#pragma unroll
+  for (int j = 0; j < kPerLane; ++j)
+    if (lane + 64 * j < n_expert) p[j] = p[j] / z;
+
+  // k rounds of first-strict-max over the non-NaN probabilities, without
+  // branches: each value is held as its order-preserving 32-bit image (0 =
+  // not selectable: NaN, past n_expert or already taken; every other
+  // probability maps above 0x7FFFFFFF).  A round takes the wave maximum of
+  // the images, then among the experts holding it the lowest index (the
+  // lowest j, then the lowest lane, since index = lane + 64 j).  Lane kk
+  // keeps round kk's pick.
+  uint32_t hv[kPerLane];
+#pragma unroll
+  for (int j = 0; j < kPerLane; ++j) {
+    const int i = lane + 64 * j;
+    hv[j] = (i < n_expert && p[j] == p[j]) ? static_cast<uint32_t>(sel_key(p[j], i) >> 32) : 0u;
+  }
+  float wsum = 0.f;
+  int my_i = 0;
+  float my_w = 0.f;
+  for (int kk = 0; kk < k; ++kk) {
+    uint32_t h = hv[0];
+#pragma unroll
+    for (int j = 1; j < kPerLane; ++j) h = max(h, hv[j]);
+    h = wave_max_u32(h);
+    int bi = kk % n_expert;  // nothing selectable: the degenerate pick
+    float bv = -1.f;
+    if (h != 0u) {
+      int jb = kPerLane;
+      uint64_t mb = 0;
+#pragma unroll
+      for (int j = kPerLane - 1; j >= 0; --j) {
+        const uint64_t m = __ballot(hv[j] == h);
+        if (m) {
+          jb = j;
+          mb = m;
+        }
+      }
+      bi = 64 * jb + __builtin_ctzll(mb);
+      bv = sel_val(static_cast<uint64_t>(h) << 32);
+    }
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j)
+      if (lane + 64 * j == bi) hv[j] = 0u;
+    if (lane == kk) {
+      my_i = bi;
+      my_w = bv;
+    }
+    wsum += bv;
+  }
+  if (lane < k) {
+    oi[lane] = my_i;
+    ow[lane] = wsum > 0.f ? my_w / wsum : my_w;
+  }
+  if (lane == 0) ow[k] = shared_w;
+}
+
 }  // namespace sg
