@@ -1059,12 +1059,17 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   if (a.logits && publisher && T > 1) {
     // the routing launch of several tokens: one wave per token, each the
     // standalone router's exact routing (router_wave), then the plan
-    // experts per lane: E <= 64 kPl (the launch picks EPT with E <= 128 EPT)
-    constexpr int kPl = 2 * EPT < 16 ? 2 * EPT : 16;
+    // experts per lane: E <= 64 PL (the launch picks EPT with E <= 64 EPT
+    // for three or more tokens, E <= 128 EPT for two)
+    constexpr int kPl1 = EPT < 16 ? EPT : 16, kPl2 = 2 * EPT < 16 ? 2 * EPT : 16;
     float* evw = reinterpret_cast<float*>(dyn + L.ev) + wave * L.e32;
-    for (int t = wave; t < T; t += 4)
-      router_wave<kPl>(a.logits + static_cast<long long>(t) * E, E, k, a.shared_w, ridx + t * k,
-                       rw + t * stride, evw, lane);
+    for (int t = wave; t < T; t += 4) {
+      const float* lg = a.logits + static_cast<long long>(t) * E;
+      if (T == 2)
+        router_wave<kPl2>(lg, E, k, a.shared_w, ridx + t * k, rw + t * stride, evw, lane);
+      else
+        router_wave<kPl1>(lg, E, k, a.shared_w, ridx + t * k, rw + t * stride, evw, lane);
+    }
     SG_MARK_FRONT(9);
     bar();
     build_plan(dyn, L, T, k, E, a.has_shared, tid);
