@@ -308,7 +308,7 @@ TRAFFIC_KERNELS = {
     "layer_front_kernel": ("decode front (config 2)", 9 * 2 * MAT_BYTES + H * 4 + E * 4 + 9 * F * 4),
     "layer_back_kernel": ("decode back (config 2)",
                           9 * MAT_BYTES + 9 * F * 4 + 2 * 9 * H * 4 + H * 4),
-    "gemv1_kernel<sg::PlainRows, sg::F32Out": ("GEMV 2048x2048 (config 1)",
+    "gemv_lat_plain_kernel": ("GEMV 2048x2048 (config 1)",
                                                2048 * 8 * 144 + 8 * 276 + 2048 * 4),
     "grouped_mfma_kernel<true>": ("prefill gate/up + SiLU (config 5)",
                                   E * 2 * MAT_BYTES + 2048 * 8 * 276 + T5_ROUTES * F * 4),
