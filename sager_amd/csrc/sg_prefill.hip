@@ -262,6 +262,10 @@ constexpr int kXRow = 76;
 // run past the tile's rows, into this padding
 constexpr int kXBufWords = (kTokTile * kXRow + 255) / 256 * 256;  // 29 KB
 constexpr int kThreads = 512;                 // eight waves
+#ifndef SG_DOWN_SPW
+#define SG_DOWN_SPW 8
+#endif
+constexpr int kDownSlicesPerWg = SG_DOWN_SPW;  // down pass, nb <= 2
 // LDS: one weight buffer (each wave refills its own rows once it has read
 // them), two token buffers, then the tile's token rows: 77 KB
 constexpr size_t kGroupedLds = (kWBufWords + 2 * kXBufWords + kTokTile) * 4;
@@ -279,7 +283,9 @@ struct GroupedArgs {
   int n_rows;               // rows of each weight matrix
   int n_out;                // output row stride (= n_rows)
   int n_groups;
-  int n_slices;             // column slices per tile (workgroups sharing one tile)
+  int n_slices;             // column slices per tile
+  int spw;                  // slices per workgroup (down pass with nb <= 2: the token
+                            // rows stay in LDS across them), a divisor of n_slices
 };
 
 // One workgroup = one column slice of one tile (up to 128 positions of one
@@ -298,9 +304,10 @@ grouped_mfma_kernel(GroupedArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   static_assert(kThreads == 512, "eight waves, one 16-row block each");
   SG_PF_MARK(0);
-  const int S = a.n_slices;
+  // the workgroup's slices: sgrp * spw .. sgrp * spw + spw - 1, in turn
+  const int spw = kGateUp ? 1 : a.spw, S = a.n_slices / spw;
   const int L = blockIdx.x, xcd = L & 7, jx = L >> 3;
-  const int tile = xcd + 8 * (jx / S), slice = jx - (jx / S) * S;
+  const int tile = xcd + 8 * (jx / S), sgrp = jx - (jx / S) * S;
   if (tile >= a.n_rec) return;
   const TileRec rec = a.trec[tile];
   const int g = rec.g, p0 = rec.p0, p1 = rec.p1;
@@ -312,13 +319,13 @@ grouped_mfma_kernel(GroupedArgs a) {
   // down: output columns [c0, c0 + 128) from weight rows c0 ..; gate/up:
   // h columns [c0, c0 + 64) from gate rows c0 .. (waves 0-3) and the same
   // up rows (waves 4-7)
-  const int c0 = slice * (kGateUp ? kRowsWg / 2 : kRowsWg);
+  constexpr int kCols = kGateUp ? kRowsWg / 2 : kRowsWg;  // output columns per slice
+  int c0 = sgrp * spw * kCols;
   const int lr = lane & 15, lq = lane >> 4;     // MFMA: row/column in the tile, K quarter
 
   if (!ma) {  // absent expert (a null gate, up or down matrix): its outputs are zero
     for (long long p = p0; p < p1; ++p)
-      for (int r = tid; r < (kGateUp ? kRowsWg / 2 : kRowsWg); r += kThreads)
-        a.out[p * a.n_out + c0 + r] = 0.f;
+      for (int r = tid; r < spw * kCols; r += kThreads) a.out[p * a.n_out + c0 + r] = 0.f;
     return;
   }
 
@@ -331,13 +338,16 @@ grouped_mfma_kernel(GroupedArgs a) {
   const sg_block_q4k* mw = uniform_ptr((kGateUp && wave >= 4) ? mb : ma);
   const u32x4 rw4 = buffer_desc(mw, a.n_rows * nb * kQ4Bytes);
   uint32_t wofs[3];
+  auto set_wofs = [&](int cs) {  // the per-lane chunk offsets of slice columns cs ..
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const int cc = min(wave * kWChunks + lane + 64 * i, kRowsWg * 9 - 1);
-    const int row = cc / 9, part = cc - row * 9;
-    const int rr = kGateUp ? (row & 63) : row;
-    wofs[i] = static_cast<uint32_t>((c0 + rr) * nb) * kQ4Bytes + 16 * part;
-  }
+    for (int i = 0; i < 3; ++i) {
+      const int cc = min(wave * kWChunks + lane + 64 * i, kRowsWg * 9 - 1);
+      const int row = cc / 9, part = cc - row * 9;
+      const int rr = kGateUp ? (row & 63) : row;
+      wofs[i] = static_cast<uint32_t>((cs + rr) * nb) * kQ4Bytes + 16 * part;
+    }
+  };
+  set_wofs(c0);
   auto stage_w = [&](int b) {  // into the wave's own rows of the weight buffer
 #pragma unroll
     for (int i = 0; i < 3; ++i)
@@ -385,10 +395,6 @@ grouped_mfma_kernel(GroupedArgs a) {
   // weight-side work (nibble unpack, scales) is done once per super-block
   // and shared by every token block.
   float acc[kTokBlocks][4];
-#pragma unroll
-  for (int ti = 0; ti < kTokBlocks; ++ti)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[ti][i] = 0.f;
   typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
   auto pmul = [](uint32_t q, uint32_t s2) -> int {  // 4 bytes x s2 (the same 16 bits twice)
     return __builtin_bit_cast(int, __builtin_bit_cast(u16x2, q) * __builtin_bit_cast(u16x2, s2));
@@ -396,6 +402,11 @@ grouped_mfma_kernel(GroupedArgs a) {
 
   stage_x(0, 0);
   SG_PF_MARK(1);
+  for (int q = 0; q < spw; ++q, c0 += kCols) {
+#pragma unroll
+  for (int ti = 0; ti < kTokBlocks; ++ti)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[ti][i] = 0.f;
   for (int b = 0; b < nb; ++b) {
     const int s = b & 1;
     wait_vm();  // this wave's copies of block b have landed
@@ -413,7 +424,10 @@ grouped_mfma_kernel(GroupedArgs a) {
     wait_lds();
     if (b + 1 < nb) {  // the next block streams in while this one computes
       stage_w(b + 1);
-      stage_x(b + 1, s ^ 1);
+      if (q == 0) stage_x(b + 1, s ^ 1);  // later slices reuse the resident rows
+    } else if (q + 1 < spw) {  // the next slice's first block
+      set_wofs(c0 + kCols);
+      stage_w(0);
     }
     const uint32_t* X = xbuf0 + s * kXBufWords;
     // I = sum_s sc_s * ip_s with the 6-bit scale split as sc = 8*sh + sl
@@ -528,6 +542,7 @@ grouped_mfma_kernel(GroupedArgs a) {
       }
     }
   }
+  }  // slices
   SG_PF_MARK(11);
   if (threadIdx.x == 0) {  // the tile's size, for the timeline reader
     SG_PF_MARK(12);
@@ -1124,6 +1139,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   // 1-D grids: a multiple of 8 tiles (one per XCD) times the slices
   const int tiles8 = (ws.max_tiles + 7) / 8 * 8;
   ga.n_slices = n_ff / (kRowsWg / 2);
+  ga.spw = 1;
   hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(tiles8 * ga.n_slices), dim3(kThreads),
                      kGroupedLds, s, ga);
   if (int st = check_launch("sg_moe_prefill/gate_up")) return st;
@@ -1136,7 +1152,13 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   gd.n_rows = hidden;
   gd.n_out = hidden;
   gd.n_slices = hidden / kRowsWg;
-  hipLaunchKernelGGL(grouped_mfma_kernel<false>, dim3(tiles8 * gd.n_slices), dim3(kThreads),
+  // with at most two super-blocks per row the tile's token rows fit both
+  // token buffers, so one workgroup runs several column slices on them
+  gd.spw = 1;
+  if (gd.nb <= 2)
+    while (gd.spw < kDownSlicesPerWg && gd.n_slices % (2 * gd.spw) == 0) gd.spw *= 2;
+  hipLaunchKernelGGL(grouped_mfma_kernel<false>, dim3(tiles8 * (gd.n_slices / gd.spw)),
+                     dim3(kThreads),
                      kGroupedLds, s, gd);
   if (int st = check_launch("sg_moe_prefill/down")) return st;
   hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 1023) / 1024, n_tokens), dim3(256), 0, s,
