@@ -284,8 +284,8 @@ struct GroupedArgs {
   int n_out;                // output row stride (= n_rows)
   int n_groups;
   int n_slices;             // column slices per tile
-  int spw;                  // slices per workgroup (down pass with nb <= 2: the token
-                            // rows stay in LDS across them), a divisor of n_slices
+  int spw;                  // slices per workgroup (the kMulti down pass, nb <= 2: the
+                            // token rows stay in LDS across them), a divisor of n_slices
 };
 
 // One workgroup = one column slice of one tile (up to 128 positions of one
@@ -294,7 +294,7 @@ struct GroupedArgs {
 // XCD x's j-th workgroup takes tile x + 8 (j / S), slice j % S.  The tile's
 // token rows are then fetched from HBM once and served to its other slices
 // from that XCD's L2.
-template <bool kGateUp>
+template <bool kGateUp, bool kMulti = false>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
 grouped_mfma_kernel(GroupedArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t gl_lds[];
@@ -305,7 +305,7 @@ grouped_mfma_kernel(GroupedArgs a) {
   static_assert(kThreads == 512, "eight waves, one 16-row block each");
   SG_PF_MARK(0);
   // the workgroup's slices: sgrp * spw .. sgrp * spw + spw - 1, in turn
-  const int spw = kGateUp ? 1 : a.spw, S = a.n_slices / spw;
+  const int spw = kMulti ? a.spw : 1, S = a.n_slices / spw;
   const int L = blockIdx.x, xcd = L & 7, jx = L >> 3;
   const int tile = xcd + 8 * (jx / S), sgrp = jx - (jx / S) * S;
   if (tile >= a.n_rec) return;
@@ -401,7 +401,9 @@ grouped_mfma_kernel(GroupedArgs a) {
   };
 
   stage_x(0, 0);
+  if (kMulti && nb > 1) stage_x(1, 1);  // the whole tile's rows, kept for every slice
   SG_PF_MARK(1);
+#pragma unroll 1
   for (int q = 0; q < spw; ++q, c0 += kCols) {
 #pragma unroll
   for (int ti = 0; ti < kTokBlocks; ++ti)
@@ -424,8 +426,8 @@ grouped_mfma_kernel(GroupedArgs a) {
     wait_lds();
     if (b + 1 < nb) {  // the next block streams in while this one computes
       stage_w(b + 1);
-      if (q == 0) stage_x(b + 1, s ^ 1);  // later slices reuse the resident rows
-    } else if (q + 1 < spw) {  // the next slice's first block
+      if (!kMulti) stage_x(b + 1, s ^ 1);
+    } else if (kMulti && q + 1 < spw) {  // the next slice's first block
       set_wofs(c0 + kCols);
       stage_w(0);
     }
@@ -531,14 +533,18 @@ grouped_mfma_kernel(GroupedArgs a) {
       }
     }
   } else {
+    // the lane's first output row, opaque to the compiler: otherwise it
+    // hoists the 24 store addresses out of the slice loop and spills
+    int tl0 = t0 + 4 * lq;
+    asm volatile("" : "+v"(tl0));
+    float* ob = a.out + c0 + 16 * wave + lr;
 #pragma unroll
     for (int ti = 0; ti < kTokBlocks; ++ti) {
       if (ti >= ntb) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tt = 16 * ti + 4 * lq + i;
-        if (tt < nt)
-          a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * wave + lr] = acc[ti][i];
+        if (tt < nt) ob[static_cast<long long>(tl0 + 16 * ti + i) * a.n_out] = acc[ti][i];
       }
     }
   }
@@ -1157,9 +1163,12 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   gd.spw = 1;
   if (gd.nb <= 2)
     while (gd.spw < kDownSlicesPerWg && gd.n_slices % (2 * gd.spw) == 0) gd.spw *= 2;
-  hipLaunchKernelGGL(grouped_mfma_kernel<false>, dim3(tiles8 * (gd.n_slices / gd.spw)),
-                     dim3(kThreads),
-                     kGroupedLds, s, gd);
+  if (gd.spw > 1)
+    hipLaunchKernelGGL((grouped_mfma_kernel<false, true>), dim3(tiles8 * (gd.n_slices / gd.spw)),
+                       dim3(kThreads), kGroupedLds, s, gd);
+  else
+    hipLaunchKernelGGL((grouped_mfma_kernel<false, false>), dim3(tiles8 * gd.n_slices),
+                       dim3(kThreads), kGroupedLds, s, gd);
   if (int st = check_launch("sg_moe_prefill/down")) return st;
   hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 1023) / 1024, n_tokens), dim3(256), 0, s,
                      out, residual, y, weight, gslot, off, sgate, n_expert, k, hidden, has_shared);
