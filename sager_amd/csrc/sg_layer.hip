@@ -506,8 +506,8 @@ __device__ __forceinline__ void quantize_x(const float* x, int n_blocks, uint32_
 // reads): thread tt of team `team` holds experts tt + TT*j of token `team`,
 // 0 outside.  Same team geometry as front_lds.
 template <int EPT>
-__device__ __forceinline__ void logits_preload(const LayerArgs& a, int tid, float* lr) {
-  const int T = a.T, E = a.n_expert;
+__device__ __forceinline__ void logits_preload(const LayerArgs& a, int T, int tid, float* lr) {
+  const int E = a.n_expert;
   const int nteams = T == 1 ? 1 : (T == 2 ? 2 : 4);
   const int TT = 64 * (4 / nteams);
   const int ept = (E + TT - 1) / TT;
@@ -528,9 +528,9 @@ __device__ __forceinline__ void logits_preload(const LayerArgs& a, int tid, floa
 // barrier.  wait_copies: the calling wave waits for its outstanding copies
 // before the selection's barrier (so they are visible on return).
 template <int EPT>
-__device__ __forceinline__ void spec_select(const LayerArgs& a, uint32_t* dyn, const FrontLds& L, float* lr,
-                            int tid, bool wait_copies = false) {
-  const int T = a.T, E = a.n_expert, m = L.m;
+__device__ __forceinline__ void spec_select(const LayerArgs& a, int T, uint32_t* dyn, const FrontLds& L,
+                            float* lr, int tid, bool wait_copies = false) {
+  const int E = a.n_expert, m = L.m;
   const int wave = tid >> 6, team = wave / L.tw, tt = tid - team * L.TT;
   float* lv = reinterpret_cast<float*>(dyn + L.lv) + team * L.e32;
   uint64_t* cand = reinterpret_cast<uint64_t*>(dyn + L.cand) + team * L.ncp;
@@ -964,11 +964,13 @@ __device__ __forceinline__ void shared_gate_tokens(const LayerArgs& a, int tid) 
   }
 }
 
-template <int EPT, int NBH>
+// kOne: the one-token decode instance (T = 1 at compile time, so the
+// several-token paths are not compiled into it)
+template <int EPT, int NBH, bool kOne>
 __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, uint32_t (*wbuf)[64 * 36],
                            uint32_t* dyn) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int T = a.T, k = a.k, E = a.n_expert, stride = k + 1;
+  const int T = kOne ? 1 : a.T, k = a.k, E = a.n_expert, stride = k + 1;
   const int nbh = NBH ? NBH : a.hidden / kQK, lpr = NBH ? pow2_ceil(NBH) : pow2_ceil(nbh);
   const bool publisher = g == a.gmax;
   if (publisher && bx != 0) return;  // one publisher per launch
@@ -977,7 +979,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   // the first routing pass's logits are the head of the routing chain:
   // issued before anything else
   float lr[EPT];
-  if (a.logits && !shared_grp) logits_preload<EPT>(a, tid, lr);
+  if (a.logits && !shared_grp) logits_preload<EPT>(a, T, tid, lr);
   const FrontLds& L = shared_grp ? a.front_shared : a.front_routed;
   const int rpw = 32 / lpr;
   const int row0 = bx * 4 * rpw + wave * rpw;
@@ -1088,7 +1090,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   } else if (a.logits) {
     // waves 0-1 wait for the pointer tables inside the selection, so they
     // are readable when it returns
-    spec_select<EPT>(a, dyn, L, lr, tid, wave < 2);
+    spec_select<EPT>(a, T, dyn, L, lr, tid, wave < 2);
     SG_MARK_FRONT(2);
     bool streamed = false, routed = false;
     if (T == 1) {
@@ -1279,7 +1281,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
               poff[g + 1] - j0, stride, a.n_ff, a.h, lane);
 }
 
-template <int EPT, int NBH>
+template <int EPT, int NBH, bool kOne = false>
 __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
@@ -1290,10 +1292,12 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
   // (one token only: the grid is then about one workgroup per CU; with more
   // tokens the shared expert's row stays first so it is not the tail)
   const int y = blockIdx.y;
-  const int g = a.publish_only
+  const int g = !kOne && a.publish_only
                     ? a.gmax
-                    : (a.T != 1 || !a.has_shared || y >= a.gmax ? y : (y + 1 == a.gmax ? 0 : y + 1));
-  front_body<EPT, NBH>(a, blockIdx.x, g, wbuf, dyn);
+                    : ((!kOne && a.T != 1) || !a.has_shared || y >= a.gmax
+                           ? y
+                           : (y + 1 == a.gmax ? 0 : y + 1));
+  front_body<EPT, NBH, kOne>(a, blockIdx.x, g, wbuf, dyn);
 }
 
 // Gate/up + SiLU of one (row chunk, group) from the plan the routing launch
@@ -1792,7 +1796,9 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     // y < gmax: compute workgroups of group y; y == gmax: the publisher
     const dim3 grid = a.publish_only ? dim3(1, 1)
                                      : dim3((n_ff + rows_wg - 1) / rows_wg, ws.gmax + 1);
-    if (fl.ept <= 1 && hidden / kQK == 8)  // the decode shape, compiled for hidden 2048
+    if (fl.ept <= 1 && hidden / kQK == 8 && n_tokens == 1)  // one-token decode, hidden 2048
+      hipLaunchKernelGGL((layer_front_kernel<1, 8, true>), grid, dim3(256), lds_f, s, a);
+    else if (fl.ept <= 1 && hidden / kQK == 8)  // the decode shape, compiled for hidden 2048
       hipLaunchKernelGGL((layer_front_kernel<1, 8>), grid, dim3(256), lds_f, s, a);
     else if (fl.ept <= 1)
       hipLaunchKernelGGL((layer_front_kernel<1, 0>), grid, dim3(256), lds_f, s, a);
