@@ -145,7 +145,7 @@ struct LayerArgs {
 // Routing runs in teams: one team of 4 waves per token for T = 1, two teams
 // of 2 waves for T = 2, four one-wave teams otherwise (tokens in passes).
 
-__host__ __device__ inline FrontLds front_lds(int T, int nbh, int E, int k, bool routed) {
+__host__ __device__ constexpr FrontLds front_lds(int T, int nbh, int E, int k, bool routed) {
   FrontLds L{};
   L.nteams = T == 1 ? 1 : (T == 2 ? 2 : 4);
   L.tw = 4 / L.nteams;
@@ -1281,8 +1281,24 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
               poff[g + 1] - j0, stride, a.n_ff, a.h, lane);
 }
 
-template <int EPT, int NBH, bool kOne = false>
-__global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs a) {
+// The decode model shape (one token, hidden 2048, n_ff 512, 256 experts,
+// top-8): its instance sees these and the LDS layout as constants.
+constexpr int kShapeHidden = 2048, kShapeFf = 512, kShapeE = 256, kShapeK = 8;
+
+template <int EPT, int NBH, bool kOne = false, bool kShape = false>
+__global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs args) {
+  LayerArgs a = args;
+  if constexpr (kShape) {
+    a.T = 1;
+    a.hidden = kShapeHidden;
+    a.n_ff = kShapeFf;
+    a.n_expert = kShapeE;
+    a.k = kShapeK;
+    a.gmax = kShapeK + 1;
+    a.emax = kShapeK + 1;
+    a.front_routed = front_lds(1, kShapeHidden / kQK, kShapeE, kShapeK, true);
+    a.front_shared = front_lds(1, kShapeHidden / kQK, kShapeE, kShapeK, false);
+  }
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
   // Row y of the grid runs group g.  With a shared expert its row comes
@@ -1796,7 +1812,10 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     // y < gmax: compute workgroups of group y; y == gmax: the publisher
     const dim3 grid = a.publish_only ? dim3(1, 1)
                                      : dim3((n_ff + rows_wg - 1) / rows_wg, ws.gmax + 1);
-    if (fl.ept <= 1 && hidden / kQK == 8 && n_tokens == 1)  // one-token decode, hidden 2048
+    if (n_tokens == 1 && hidden == kShapeHidden && n_ff == kShapeFf && n_expert == kShapeE &&
+        k == kShapeK)  // the decode model shape
+      hipLaunchKernelGGL((layer_front_kernel<1, 8, true, true>), grid, dim3(256), lds_f, s, a);
+    else if (fl.ept <= 1 && hidden / kQK == 8 && n_tokens == 1)  // one-token decode, hidden 2048
       hipLaunchKernelGGL((layer_front_kernel<1, 8, true>), grid, dim3(256), lds_f, s, a);
     else if (fl.ept <= 1 && hidden / kQK == 8)  // the decode shape, compiled for hidden 2048
       hipLaunchKernelGGL((layer_front_kernel<1, 8>), grid, dim3(256), lds_f, s, a);
