@@ -1374,8 +1374,8 @@ struct BackLds {
   int hq, ys, off, wdown, tok, slot, wt, sg, meta, total;
 };
 
-__host__ __device__ inline BackLds back_lds(int T, int k, int n_ff, int rows, int gmax,
-                                            int emax) {
+__host__ __device__ constexpr BackLds back_lds(int T, int k, int n_ff, int rows, int gmax,
+                                               int emax) {
   BackLds L{};
   const int nbf = n_ff / kQK;
   int o = 0;
@@ -1588,8 +1588,23 @@ __device__ __forceinline__ float residual_pre(const LayerArgs& a, int row0, int 
   return a.residual[static_cast<long long>(t) * a.hidden + row0 + r];
 }
 
-template <int NBF, int ROWS>
-__global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs a) {
+template <int NBF, int ROWS, bool kShape = false>
+__global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args) {
+  // kShape (the decode model shape, as in the front kernel): the shape and
+  // the LDS layout are constants
+  LayerArgs a = args;
+  if constexpr (kShape) {
+    a.T = 1;
+    a.hidden = kShapeHidden;
+    a.n_ff = kShapeFf;
+    a.n_expert = kShapeE;
+    a.k = kShapeK;
+    a.gmax = kShapeK + 1;
+    a.emax = kShapeK + 1;
+    a.back_rows = 8;
+    a.back_lrow = 2;
+    a.back_bufs = kBackWaves;
+  }
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];  // BackLds arrays, then the buffers
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, stride = k + 1;
@@ -1841,7 +1856,11 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     // the decode geometry of n_ff = 512 at hidden >= 2048 compiled for its
     // constants; other shapes read them from the arguments
     const dim3 gb((hidden + rows - 1) / rows);
-    if (n_ff / kQK == 2 && rows == 8)
+    if (n_tokens == 1 && hidden == kShapeHidden && n_ff == kShapeFf && n_expert == kShapeE &&
+        k == kShapeK && rows == 8 && back_bufs == kBackWaves)  // the decode model shape
+      hipLaunchKernelGGL((layer_back_kernel<2, 8, true>), gb, dim3(kBackThreads),
+                         lds_b + back_bufs * buf_b, s, a);
+    else if (n_ff / kQK == 2 && rows == 8)
       hipLaunchKernelGGL((layer_back_kernel<2, 8>), gb, dim3(kBackThreads),
                          lds_b + back_bufs * buf_b, s, a);
     else
