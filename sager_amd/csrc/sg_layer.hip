@@ -1286,11 +1286,13 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
 constexpr int kShapeHidden = 2048, kShapeFf = 512, kShapeE = 256, kShapeK = 8;
 constexpr int kShapeWindow = 4;  // the verify window's tokens (one plus three drafts)
 
-// The model shape with kT tokens, as the launcher derives it (kT = 0: none).
-template <int kT>
+// The model shape with kT tokens, with or without a shared expert, as the
+// launcher derives it (kT = 0: none).
+template <int kT, bool kSh>
 __device__ __forceinline__ void apply_shape(LayerArgs& a) {
   if constexpr (kT > 0) {
     a.T = kT;
+    a.has_shared = kSh;
     a.hidden = kShapeHidden;
     a.n_ff = kShapeFf;
     a.n_expert = kShapeE;
@@ -1305,10 +1307,10 @@ __host__ inline bool is_shape(int T, int hidden, int n_ff, int E, int k, int kT)
   return T == kT && hidden == kShapeHidden && n_ff == kShapeFf && E == kShapeE && k == kShapeK;
 }
 
-template <int EPT, int NBH, bool kOne = false, int kShapeT = 0>
+template <int EPT, int NBH, bool kOne = false, int kShapeT = 0, bool kSh = false>
 __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs args) {
   LayerArgs a = args;
-  apply_shape<kShapeT>(a);
+  apply_shape<kShapeT, kSh>(a);
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
   // Row y of the grid runs group g.  With a shared expert its row comes
@@ -1330,10 +1332,10 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs args) {
 // left in the workspace: several tokens (a verify window), where routing in
 // every compute workgroup would cost more than a launch.  Grid (row chunks
 // of 16, gmax); groups beyond the plan's count exit.
-template <int NBH, int kShapeT = 0>
+template <int NBH, int kShapeT = 0, bool kSh = false>
 __global__ void __launch_bounds__(256) layer_gateup_kernel(LayerArgs args) {
   LayerArgs a = args;
-  apply_shape<kShapeT>(a);
+  apply_shape<kShapeT, kSh>(a);
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];  // xs, then entry tok / slot
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1600,12 +1602,12 @@ __device__ __forceinline__ float residual_pre(const LayerArgs& a, int row0, int 
   return a.residual[static_cast<long long>(t) * a.hidden + row0 + r];
 }
 
-template <int NBF, int ROWS, int kShapeT = 0>
+template <int NBF, int ROWS, int kShapeT = 0, bool kSh = false>
 __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args) {
   // kShapeT > 0 (the model shape with kShapeT tokens, as in the front
   // kernel): the shape and the LDS layout are constants
   LayerArgs a = args;
-  apply_shape<kShapeT>(a);
+  apply_shape<kShapeT, kSh>(a);
   if constexpr (kShapeT > 0) {
     a.back_rows = 8;
     a.back_lrow = 2;
@@ -1833,11 +1835,13 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     // y < gmax: compute workgroups of group y; y == gmax: the publisher
     const dim3 grid = a.publish_only ? dim3(1, 1)
                                      : dim3((n_ff + rows_wg - 1) / rows_wg, ws.gmax + 1);
-    if (is_shape(n_tokens, hidden, n_ff, n_expert, k, 1))  // the decode model shape
-      hipLaunchKernelGGL((layer_front_kernel<1, 8, true, 1>), grid, dim3(256), lds_f, s, a);
-    else if (is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow))  // its verify window
-      hipLaunchKernelGGL((layer_front_kernel<4, 8, false, kShapeWindow>), grid, dim3(256), lds_f,
-                         s, a);
+    if (is_shape(n_tokens, hidden, n_ff, n_expert, k, 1) && a.has_shared)  // the model shape
+      hipLaunchKernelGGL((layer_front_kernel<1, 8, true, 1, true>), grid, dim3(256), lds_f, s, a);
+    else if (is_shape(n_tokens, hidden, n_ff, n_expert, k, 1))
+      hipLaunchKernelGGL((layer_front_kernel<1, 8, true, 1, false>), grid, dim3(256), lds_f, s, a);
+    else if (is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) && a.has_shared)
+      hipLaunchKernelGGL((layer_front_kernel<4, 8, false, kShapeWindow, true>), grid, dim3(256),
+                         lds_f, s, a);  // its verify window
     else if (fl.ept <= 1 && hidden / kQK == 8 && n_tokens == 1)  // one-token decode, hidden 2048
       hipLaunchKernelGGL((layer_front_kernel<1, 8, true>), grid, dim3(256), lds_f, s, a);
     else if (fl.ept <= 1 && hidden / kQK == 8)  // the decode shape, compiled for hidden 2048
@@ -1853,8 +1857,9 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     if (int st = check_launch("sg_moe_layer/front")) return st;
     if (a.publish_only) {
       const dim3 gg((n_ff + rows_wg - 1) / rows_wg, ws.gmax);
-      if (is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow))
-        hipLaunchKernelGGL((layer_gateup_kernel<8, kShapeWindow>), gg, dim3(256), lds_g, s, a);
+      if (is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) && a.has_shared)
+        hipLaunchKernelGGL((layer_gateup_kernel<8, kShapeWindow, true>), gg, dim3(256), lds_g, s,
+                           a);
       else if (hidden / kQK == 8)
         hipLaunchKernelGGL((layer_gateup_kernel<8>), gg, dim3(256), lds_g, s, a);
       else
@@ -1866,13 +1871,16 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     // the decode geometry of n_ff = 512 at hidden >= 2048 compiled for its
     // constants; other shapes read them from the arguments
     const dim3 gb((hidden + rows - 1) / rows);
-    if (is_shape(n_tokens, hidden, n_ff, n_expert, k, 1) && rows == 8 &&
-        back_bufs == kBackWaves)  // the decode model shape
-      hipLaunchKernelGGL((layer_back_kernel<2, 8, 1>), gb, dim3(kBackThreads),
+    const bool geo = rows == 8 && back_bufs == kBackWaves;
+    if (geo && is_shape(n_tokens, hidden, n_ff, n_expert, k, 1) && a.has_shared)  // model shape
+      hipLaunchKernelGGL((layer_back_kernel<2, 8, 1, true>), gb, dim3(kBackThreads),
                          lds_b + back_bufs * buf_b, s, a);
-    else if (is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) && rows == 8 &&
-             back_bufs == kBackWaves)  // its verify window
-      hipLaunchKernelGGL((layer_back_kernel<2, 8, kShapeWindow>), gb, dim3(kBackThreads),
+    else if (geo && is_shape(n_tokens, hidden, n_ff, n_expert, k, 1))
+      hipLaunchKernelGGL((layer_back_kernel<2, 8, 1, false>), gb, dim3(kBackThreads),
+                         lds_b + back_bufs * buf_b, s, a);
+    else if (geo && is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) &&
+             a.has_shared)  // its verify window
+      hipLaunchKernelGGL((layer_back_kernel<2, 8, kShapeWindow, true>), gb, dim3(kBackThreads),
                          lds_b + back_bufs * buf_b, s, a);
     else if (n_ff / kQK == 2 && rows == 8)
       hipLaunchKernelGGL((layer_back_kernel<2, 8>), gb, dim3(kBackThreads),
