@@ -549,6 +549,7 @@ __device__ __forceinline__ void spec_select(const LayerArgs& a, int T, uint32_t*
       kr[j] = in ? sel_key(lr[j], i) : 0;
       if (j < L.ept && i < L.e32) lv[i] = lr[j];
     }
+    SG_MARK_FRONT(1);
     team_select<EPT>(L, kr, cand, top, tt, wait_copies && t0 == 0);
     if (ok && tt < m) spec[t * m + tt] = top[tt] ? sel_idx(top[tt]) : -1;
     if (t0 + L.nteams < T) bar();  // the next pass reuses cand/top
@@ -1382,6 +1383,7 @@ __global__ void __launch_bounds__(256) layer_gateup_kernel(LayerArgs args) {
 // out = residual + sum_kk fma(w_kk, y_kk) in slot order.
 constexpr int kBackWaves = 8;                    // waves per back workgroup
 constexpr int kBackThreads = 64 * kBackWaves;
+constexpr int kBackPreCopies = 3;  // copy instructions per wave issued at kernel start
 constexpr int kBackHSlots = 3;  // h blocks per wave preloaded at kernel start (T = 1, k = 8: 18)
 
 struct BackLds {
@@ -1412,16 +1414,53 @@ __host__ __device__ constexpr BackLds back_lds(int T, int k, int n_ff, int rows,
   return L;
 }
 
+// Q8_K of every (token, slot) h row of the back kernel into hq (LDS): wave w
+// quantizes blocks e = w + 8j, j < kBackHSlots from hpre (its registers) in
+// one interleaved pass (every block of a one-token layer with k <= 8), later
+// ones in passes of four loaded here.
+__device__ __forceinline__ void back_quantize_h(const LayerArgs& a, uint32_t* hq,
+                                                const float (&hpre)[kBackHSlots][4], int nq,
+                                                int wave, int lane) {
+  if (wave < nq) {
+    uint32_t* dst[kBackHSlots];
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < kBackHSlots; ++j) {
+      const int e = wave + kBackWaves * j;
+      dst[j] = hq + (e < nq ? e : wave) * kXStride;
+      n += e < nq;
+    }
+    quantize_n_lds<kBackHSlots>(hpre, dst, n, lane);
+  }
+  for (int e0 = wave + kBackWaves * kBackHSlots; e0 < nq; e0 += 4 * kBackWaves) {
+    float v[4][4];
+    uint32_t* dst[4];
+    int n = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = e0 + kBackWaves * u < nq ? e0 + kBackWaves * u : e0;
+      const float* hp = a.h + static_cast<long long>(e) * kQK + 4 * lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[u][i] = hp[i];
+      dst[u] = hq + e * kXStride;
+      n += e0 + kBackWaves * u < nq;
+    }
+    quantize_n_lds<4>(v, dst, n, lane);
+  }
+}
+
 // The down rows, Q8_K of h and combine of one chunk of `rows` output rows,
 // with the plan in LDS (off, wdown, tok, slot, wt, meta).  Wave w
 // quantizes h blocks w + 8j; hpre[j] holds the lane's 4 values of block
 // w + 8j for j < kBackHSlots (loaded at kernel start).
 // NBF, ROWS: n_ff / 256 and the rows per workgroup when known at compile
-// time (0 = read from a).
+// time (0 = read from a).  pre: the kernel start has already issued every
+// group's down-row copies (the packed one-pass layout) and quantized h,
+// and the barrier after them has passed.
 template <int NBF, int ROWS>
 __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, uint32_t* bd,
                           uint32_t (*wbuf)[64 * 36], int row0, int nr, float res0,
-                          const float (&hpre)[kBackHSlots][4]) {
+                          const float (&hpre)[kBackHSlots][4], bool pre) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, stride = k + 1;
   const int nbf = NBF ? NBF : a.n_ff / kQK;
@@ -1455,7 +1494,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
       // buffers (chunk c = group c / cpg, chunk c % cpg of its rows, at
       // wbuf[0] + 4c), the 1-KB copy instructions dealt round-robin to the
       // waves; each waits for its own before the barrier below
-      if (gb == 0) {
+      if (gb == 0 && !pre) {
         const int cpg = gwords / 4, cval = nr * nbf * 9, total = G * cpg;
         const uint64_t inv = ((1ull << 24) + cpg - 1) / cpg;  // c / cpg exact for c < 2^24 / cpg
         const long long roff = static_cast<long long>(row0) * nbf * kQ4Bytes;
@@ -1494,36 +1533,8 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
       }
     }
     SG_MARK_BACK(2);
-    if (gb == 0) {  // Q8_K of every (token, slot) h row while the rows stream in
-      // blocks e = wave + 8j: j < kBackHSlots from registers in one
-      // interleaved pass (every block of a one-token layer with k <= 8),
-      // later ones in passes of four loaded here
-      if (wave < nq) {
-        uint32_t* dst[kBackHSlots];
-        int n = 0;
-#pragma unroll
-        for (int j = 0; j < kBackHSlots; ++j) {
-          const int e = wave + kBackWaves * j;
-          dst[j] = hq + (e < nq ? e : wave) * kXStride;
-          n += e < nq;
-        }
-        quantize_n_lds<kBackHSlots>(hpre, dst, n, lane);
-      }
-      for (int e0 = wave + kBackWaves * kBackHSlots; e0 < nq; e0 += 4 * kBackWaves) {
-        float v[4][4];
-        uint32_t* dst[4];
-        int n = 0;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int e = e0 + kBackWaves * u < nq ? e0 + kBackWaves * u : e0;
-          const float* hp = a.h + static_cast<long long>(e) * kQK + 4 * lane;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[u][i] = hp[i];
-          dst[u] = hq + e * kXStride;
-          n += e0 + kBackWaves * u < nq;
-        }
-        quantize_n_lds<4>(v, dst, n, lane);
-      }
+    if (gb == 0 && !pre) {  // Q8_K of every (token, slot) h row while the rows stream in
+      back_quantize_h(a, hq, hpre, nq, wave, lane);
       SG_MARK_BACK(3);
       if (spread) wait_vm();  // this wave's share of the copies
       bar();
@@ -1647,6 +1658,30 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args
   }
   const float res0 = residual_pre(a, row0, nr);
 
+  // The packed one-pass copy layout of back_core, when every plan this
+  // launch can hold fits it (gmax groups, at most kBackPreCopies copy
+  // instructions per wave): each thread loads the down pointers of its
+  // chunks and the group count straight from the plan in global memory, so
+  // the copies are issued as soon as those land, and h is quantized before
+  // the first barrier.
+  const int lrow = NBF ? pow2_ceil(NBF) : a.back_lrow;
+  const int gpw = 64 / (rows * lrow);
+  const int gwords = rows * nbf * 36, cpg = gwords / 4;
+  const bool pre = gpw * gwords == 64 * 36 && a.gmax <= a.back_bufs * gpw &&
+                   a.gmax * cpg <= 64 * kBackWaves * kBackPreCopies;
+  const uint64_t inv = ((1ull << 24) + cpg - 1) / cpg;  // c / cpg exact for c < 2^24 / cpg
+  unsigned long long wdp[kBackPreCopies];
+  int gpre = 0;
+  if (pre) {
+    gpre = max(0, min(a.plan.meta[0], a.gmax));
+#pragma unroll
+    for (int i = 0; i < kBackPreCopies; ++i) {
+      const int c = 64 * (wave + kBackWaves * i) + lane;
+      const int gq = static_cast<int>((static_cast<uint64_t>(c) * inv) >> 24);
+      wdp[i] = a.plan.wdown[min(gq, a.gmax - 1)];
+    }
+  }
+
   // the plan and routing weights.  When every array fits one element per
   // thread, each thread issues all of its loads (clamped indices, no
   // branches) before it waits once; loads inside separate guarded loops
@@ -1680,11 +1715,33 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args
     for (int i = tid; i < nw; i += kBackThreads) wt[i] = a.weight[i];
     for (int i = tid; i < T; i += kBackThreads) sgl[i] = a.sgate ? a.sgate[i] : 1.f;
   }
+  uint32_t(*wbuf)[64 * 36] = reinterpret_cast<uint32_t(*)[64 * 36]>(dyn + L.total);
+  if (pre) {
+    // chunk c = 64 t + lane, t = wave + 8i: group c / cpg, chunk c % cpg of
+    // its rows, to wbuf[0] + 4c (what back_core's packed layout reads)
+    const int cval = nr * nbf * 9, total = gpre * cpg;
+    const long long roff = static_cast<long long>(row0) * nbf * kQ4Bytes;
+#pragma unroll
+    for (int i = 0; i < kBackPreCopies; ++i) {
+      const int t = wave + kBackWaves * i;
+      const int c = 64 * t + lane;
+      const int gq = static_cast<int>((static_cast<uint64_t>(c) * inv) >> 24);
+      const int w = c - gq * cpg;
+      if (c < total && wdp[i] && w < cval)
+        __builtin_amdgcn_global_load_lds(
+            (glb_void_p)(reinterpret_cast<const char*>(wdp[i]) + roff + 16 * w),
+            (lds_void_p)(wbuf[0] + 256 * t), 16, 0, 0);
+    }
+    if (tid == 0) meta[0] = gpre;
+  }
   for (int i = tid; i < T * stride * rows; i += kBackThreads) ys[i] = 0.f;
+  if (pre) {
+    back_quantize_h(a, dyn + L.hq, hpre, nq, wave, lane);
+    wait_vm();  // this wave's copies, visible to all after the barrier
+  }
   bar();
   SG_MARK_BACK(1);
-  uint32_t(*wbuf)[64 * 36] = reinterpret_cast<uint32_t(*)[64 * 36]>(dyn + L.total);
-  back_core<NBF, ROWS>(a, L, dyn, wbuf, row0, nr, res0, hpre);
+  back_core<NBF, ROWS>(a, L, dyn, wbuf, row0, nr, res0, hpre, pre);
 }
 
 static void back_geometry(int hidden, int n_ff, int& rows, int& lrow) {
