@@ -113,7 +113,7 @@ static LayerWs layer_ws(int T, int n_ff, int E, int k) {
 struct FrontLds {
   int nteams, tw, TT, ept, m, e32, ncp;
   int tabg, tabu, tabd, lv, ev, cand, top, red, zs, spec, ridx, rw, re, rfirst, poff, pexp,
-      ptok, pslot, ctrl, xs, total;
+      ptok, pslot, ctrl, kw, xs, total;
 };
 
 struct LayerArgs {
@@ -183,6 +183,7 @@ __host__ __device__ constexpr FrontLds front_lds(int T, int nbh, int E, int k, b
     L.ptok = take(T * k + T);
     L.pslot = take(T * k + T);
     L.ctrl = take(8 + T * k);
+    L.kw = take(4 * 128);  // one key per lane of every wave (team_select, one key per thread)
   }
   L.total = o;
   return L;
@@ -214,16 +215,21 @@ __device__ __forceinline__ int rank_n(const uint64_t* c, int n, uint64_t key) {
 }
 
 // Top-m selection of a team (tw waves) over the keys kr[] its threads hold
-// (0 = no key; keys are otherwise distinct).  Stage 1, per wave with no
-// LDS traffic: a bitwise radix search over ballot counts finds the wave's
-// m-th largest key - first on the value word, then, only when several keys
-// share the boundary value, on the index word - and the wave's m largest
-// keys go to cand[wave * m ...) in any order (zero-padded).  Stage 2: each
-// candidate's rank among the team's tw*m candidates places it in top[rank]
-// (0 = missing).  Two barriers; every thread of the workgroup takes part.
+// (0 = no key; keys are otherwise distinct).  Stage 1, per wave: the wave's
+// m largest keys go to cand[wave * m ...) (zero-padded).  With one key per
+// thread each key takes its rank among the wave's 64 keys, read back from
+// kwbase (LDS, 128 words per wave) with broadcast reads; with more, a
+// bitwise radix search over ballot counts finds the wave's m-th largest key
+// - first on the value word, then, only when several keys share the
+// boundary value, on the index word.  Stage 2: each candidate's rank among
+// the team's tw*m candidates places it in top[rank] (0 = missing); when
+// they fit one wave every wave of the team does this and writes the same
+// top[], so it is readable by each wave on return after one barrier,
+// otherwise the candidates are shared out and a second barrier follows.
+// Every thread of the workgroup takes part.
 template <int EPT>
 __device__ __forceinline__ void team_select(const FrontLds& L, const uint64_t* kr, uint64_t* cand, uint64_t* top,
-                            int tt, bool wait_before_rank = false) {
+                            uint32_t* kwbase, int tt, bool wait_before_rank = false) {
   const int m = L.m, lane = tt & 63, wit = tt >> 6;
   uint32_t hi[EPT], lo[EPT];
 #pragma unroll
@@ -231,44 +237,68 @@ __device__ __forceinline__ void team_select(const FrontLds& L, const uint64_t* k
     hi[j] = static_cast<uint32_t>(kr[j] >> 32);
     lo[j] = static_cast<uint32_t>(kr[j]);
   }
-  // th: the largest value word v with at least m keys of value >= v (0 when
-  // the wave has fewer than m keys of nonzero value)
-  uint32_t th = 0;
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t c = th | (1u << b);
-    int n = 0;
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) n += __popcll(__ballot(hi[j] >= c));
-    if (n >= m) th = c;
-  }
-  int n_gt = 0, n_eq = 0;
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    n_gt += __popcll(__ballot(hi[j] > th));
-    n_eq += __popcll(__ballot(hi[j] == th && kr[j] != 0));
-  }
-  const int need = m - n_gt;  // >= 1
-  // at the boundary value, the `need` largest index words (lowest experts)
-  uint32_t tl = 0;
-  if (n_eq > need) {
-    for (int b = 31; b >= 0; --b) {
-      const uint32_t c = tl | (1u << b);
-      int n = 0;
-#pragma unroll
-      for (int j = 0; j < EPT; ++j) n += __popcll(__ballot(hi[j] == th && kr[j] != 0 && lo[j] >= c));
-      if (n >= need) tl = c;
-    }
-  }
   uint64_t* wc = cand + wit * m;
   int base = 0;
+  if constexpr (EPT == 1) {
+    // one key per lane: its rank among the wave's 64 keys, by comparison
+    // with all of them read back from LDS (the wave's own writes, 16-B
+    // broadcast reads, no barrier); ranks below m place the key
+    uint64_t* kw = reinterpret_cast<uint64_t*>(kwbase) + 64 * (threadIdx.x >> 6);
+    kw[lane] = kr[0];
+    const u32x4* p = reinterpret_cast<const u32x4*>(kw);
+    int r = 0;
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const bool sel = kr[j] != 0 && (hi[j] > th || (hi[j] == th && lo[j] >= tl));
-    const uint64_t bm = __ballot(sel);
-    const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bm >> 32),
-                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bm), 0));
-    if (sel) wc[base + below] = kr[j];
-    base += __popcll(bm);
+    for (int q = 0; q < 32; q += 8) {
+      u32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = p[q + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint64_t a = (static_cast<uint64_t>(v[u].y) << 32) | v[u].x;
+        const uint64_t b = (static_cast<uint64_t>(v[u].w) << 32) | v[u].z;
+        r += (a > kr[0]) + (b > kr[0]);
+      }
+    }
+    if (kr[0] != 0 && r < m) wc[r] = kr[0];
+    base = __popcll(__ballot(kr[0] != 0));
+  } else {
+    // th: the largest value word v with at least m keys of value >= v (0 when
+    // the wave has fewer than m keys of nonzero value)
+    uint32_t th = 0;
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t c = th | (1u << b);
+      int n = 0;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) n += __popcll(__ballot(hi[j] >= c));
+      if (n >= m) th = c;
+    }
+    int n_gt = 0, n_eq = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      n_gt += __popcll(__ballot(hi[j] > th));
+      n_eq += __popcll(__ballot(hi[j] == th && kr[j] != 0));
+    }
+    const int need = m - n_gt;  // >= 1
+    // at the boundary value, the `need` largest index words (lowest experts)
+    uint32_t tl = 0;
+    if (n_eq > need) {
+      for (int b = 31; b >= 0; --b) {
+        const uint32_t c = tl | (1u << b);
+        int n = 0;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) n += __popcll(__ballot(hi[j] == th && kr[j] != 0 && lo[j] >= c));
+        if (n >= need) tl = c;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const bool sel = kr[j] != 0 && (hi[j] > th || (hi[j] == th && lo[j] >= tl));
+      const uint64_t bm = __ballot(sel);
+      const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bm >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bm), 0));
+      if (sel) wc[base + below] = kr[j];
+      base += __popcll(bm);
+    }
   }
   if (lane >= base && lane < m) wc[lane] = 0;
   const int nc = L.tw * m;
@@ -276,14 +306,26 @@ __device__ __forceinline__ void team_select(const FrontLds& L, const uint64_t* k
   if (tt < m) top[tt] = 0;
   if (wait_before_rank) wait_vm();  // the caller's copies are visible after the barrier
   bar();
-  if (tt < nc) {
-    const uint64_t key = cand[tt];
-    if (key != 0) {
-      const int r = rank_n(cand, L.ncp, key);
-      if (r < m) top[r] = key;
+  if (nc <= 64) {
+    // every wave of the team ranks all candidates and writes the same
+    // top[]: each wave reads its own writes, so no second barrier
+    if (lane < nc) {
+      const uint64_t key = cand[lane];
+      if (key != 0) {
+        const int r = rank_n(cand, L.ncp, key);
+        if (r < m) top[r] = key;
+      }
     }
+  } else {
+    if (tt < nc) {
+      const uint64_t key = cand[tt];
+      if (key != 0) {
+        const int r = rank_n(cand, L.ncp, key);
+        if (r < m) top[r] = key;
+      }
+    }
+    bar();
   }
-  bar();
 }
 
 // Expert-major plan from ridx[T*k] (ids outside [0, E) skipped): group 0 =
@@ -550,7 +592,7 @@ __device__ __forceinline__ void spec_select(const LayerArgs& a, int T, uint32_t*
       if (j < L.ept && i < L.e32) lv[i] = lr[j];
     }
     SG_MARK_FRONT(1);
-    team_select<EPT>(L, kr, cand, top, tt, wait_copies && t0 == 0);
+    team_select<EPT>(L, kr, cand, top, dyn + L.kw, tt, wait_copies && t0 == 0);
     if (ok && tt < m) spec[t * m + tt] = top[tt] ? sel_idx(top[tt]) : -1;
     if (t0 + L.nteams < T) bar();  // the next pass reuses cand/top
   }
@@ -778,7 +820,7 @@ __device__ __forceinline__ void route_direct_t1(const LayerArgs& a, uint32_t* dy
       const int i = tid + L.TT * j;
       kr[j] = (j < L.ept && i < E) ? sel_key(e[j] / z, i) : 0ull;
     }
-    team_select<EPT>(L, kr, cand, top, tid);
+    team_select<EPT>(L, kr, cand, top, dyn + L.kw, tid);
   }
   SG_MARK_FRONT(12);
   if (wave == 0) {
@@ -915,7 +957,7 @@ __device__ __forceinline__ void exact_route(const LayerArgs& a, uint32_t* dyn, c
         const int i = tt + L.TT * j;
         kr[j] = (j < L.ept && i < E && slow_team) ? sel_key(ev[i] / z, i) : 0;
       }
-      team_select<EPT>(L, kr, cand, top, tt);
+      team_select<EPT>(L, kr, cand, top, dyn + L.kw, tt);
     }
     if (wit == 0 && ok) {
       int fi;
