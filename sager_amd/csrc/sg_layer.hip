@@ -1019,8 +1019,29 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   if (publisher && bx != 0) return;  // one publisher per launch
   SG_MARK_FRONT(0);
   const bool shared_grp = a.has_shared && g == 0;
-  // the first routing pass's logits are the head of the routing chain:
-  // issued before anything else
+  const bool tabd_regs = publisher && E <= 256;
+  // expert pointer tables into LDS (gate and up; down for the publisher),
+  // issued first: the wait for the logits covers every load in flight, so
+  // copies issued after the logits would hold up the selection
+  if (!shared_grp && (wave < 2 || (wave == 2 && publisher && !tabd_regs))) {
+    // (one branch per table: a select between the argument block's pointer
+    // fields would make the compiler keep that block in scratch memory)
+    auto copy_table = [&](const sg_block_q4k* const* tab, int at) {
+      uint32_t* dst = dyn + at;
+      const char* src = reinterpret_cast<const char*>(tab);
+      dma_range([&](int c) { return src + 16 * c; }, E / 2, dst, lane);
+      if ((E & 1) && lane == 0)  // odd table length: the last pointer by a plain load
+        reinterpret_cast<unsigned long long*>(dst)[E - 1] =
+            reinterpret_cast<unsigned long long>(tab[E - 1]);
+    };
+    if (wave == 0)
+      copy_table(a.tab_gate, a.front_routed.tabg);
+    else if (wave == 1)
+      copy_table(a.tab_up, a.front_routed.tabu);
+    else
+      copy_table(a.tab_down, a.front_routed.tabd);
+  }
+  // the first routing pass's logits are the head of the routing chain
   float lr[EPT];
   if (a.logits && !shared_grp) logits_preload<EPT>(a, T, tid, lr);
   const FrontLds& L = shared_grp ? a.front_shared : a.front_routed;
@@ -1063,26 +1084,15 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   const int* ptok = reinterpret_cast<const int*>(dyn + L.ptok);
   const int* pslot = reinterpret_cast<const int*>(dyn + L.pslot);
 
-  // expert pointer tables into LDS (gate and up; down for the publisher).
   // The publisher's down table goes through registers when E <= 256: it is
   // written to LDS only when publishing, long after it landed, so no LDS
   // access of wave 2 waits for it meanwhile.
-  const bool tabd_regs = publisher && E <= 256;
   unsigned long long tdv[4];
   if (tabd_regs && wave == 2) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       tdv[j] = lane + 64 * j < E ? reinterpret_cast<unsigned long long>(a.tab_down[lane + 64 * j])
                                  : 0ull;
-  }
-  if (wave < 2 || (wave == 2 && publisher && !tabd_regs)) {
-    const sg_block_q4k* const* tab = wave == 0 ? a.tab_gate : (wave == 1 ? a.tab_up : a.tab_down);
-    uint32_t* dst = dyn + (wave == 0 ? L.tabg : (wave == 1 ? L.tabu : L.tabd));
-    const char* src = reinterpret_cast<const char*>(tab);
-    dma_range([&](int c) { return src + 16 * c; }, E / 2, dst, lane);
-    if ((E & 1) && lane == 0)  // odd table length: the last pointer by a plain load
-      reinterpret_cast<unsigned long long*>(dst)[E - 1] =
-          reinterpret_cast<unsigned long long>(tab[E - 1]);
   }
 
   // stream the gate/up rows of expert e (none when e < 0 or it is absent)
@@ -1274,33 +1284,41 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
     wait_vm();  // pointer tables
     bar();
     SG_MARK_FRONT(5);
+    // one array per wave, each lane's loads independent of the others' (a
+    // single wave doing all of it waited on one LDS read after another)
     const int* re = reinterpret_cast<const int*>(dyn + L.re);
     const int nv = ctrl[0];
-    for (int t = tid; t < T; t += 256) {
-      bool bad = false;  // bounds-kill: a row with an invalid id loses all its weights
-      for (int kk = 0; kk < k; ++kk) bad |= re[t * k + kk] < 0;
-      for (int q = 0; q <= k; ++q) a.weight[t * stride + q] = bad ? 0.f : rw[t * stride + q];
-      if (a.logits)
-        for (int kk = 0; kk < k; ++kk) a.idx[t * stride + kk] = ridx[t * k + kk];
-    }
-    for (int i = tid; i <= n_groups; i += 256) a.plan.off[i] = poff[i];
-    for (int i = tid; i < n_groups; i += 256) {
-      const int e = pexp[i];
-      a.plan.expert[i] = e;
-      const unsigned long long gp =
-          e >= 0 ? tabg[e] : reinterpret_cast<unsigned long long>(a.sh_gate);
-      const unsigned long long up = e >= 0 ? tabu[e] : reinterpret_cast<unsigned long long>(a.sh_up);
-      const unsigned long long dp =
-          e >= 0 ? tabd[e] : reinterpret_cast<unsigned long long>(a.sh_down);
-      a.plan.wdown[i] = (gp && up) ? dp : 0ull;
-      a.plan.wgate[i] = (gp && up) ? gp : 0ull;
-      a.plan.wup[i] = (gp && up) ? up : 0ull;
-    }
-    for (int i = tid; i < (a.has_shared ? T : 0) + nv; i += 256) {
-      a.plan.tok[i] = ptok[i];
-      a.plan.slot[i] = pslot[i];
-    }
-    if (tid == 0) {
+    if (wave == 0) {
+      for (int i = lane; i < T * stride; i += 64) {
+        const int t = i / stride, q = i - t * stride;
+        bool bad = false;  // bounds-kill: a row with an invalid id loses all its weights
+        for (int kk = 0; kk < k; ++kk) bad |= re[t * k + kk] < 0;
+        a.weight[i] = bad ? 0.f : rw[i];
+        if (a.logits && q < k) a.idx[i] = ridx[t * k + q];
+      }
+    } else if (wave == 1) {
+      for (int i = lane; i <= n_groups; i += 64) {
+        a.plan.off[i] = poff[i];
+        if (i < n_groups) {
+          const int e = pexp[i];
+          a.plan.expert[i] = e;
+          const unsigned long long gp =
+              e >= 0 ? tabg[e] : reinterpret_cast<unsigned long long>(a.sh_gate);
+          const unsigned long long up =
+              e >= 0 ? tabu[e] : reinterpret_cast<unsigned long long>(a.sh_up);
+          const unsigned long long dp =
+              e >= 0 ? tabd[e] : reinterpret_cast<unsigned long long>(a.sh_down);
+          a.plan.wdown[i] = (gp && up) ? dp : 0ull;
+          a.plan.wgate[i] = (gp && up) ? gp : 0ull;
+          a.plan.wup[i] = (gp && up) ? up : 0ull;
+        }
+      }
+    } else if (wave == 2) {
+      for (int i = lane; i < (a.has_shared ? T : 0) + nv; i += 64) {
+        a.plan.tok[i] = ptok[i];
+        a.plan.slot[i] = pslot[i];
+      }
+    } else if (lane == 0) {
       a.plan.meta[0] = n_groups;
       a.plan.meta[1] = a.has_shared;
       a.plan.meta[2] = nv;
