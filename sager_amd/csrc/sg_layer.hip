@@ -85,13 +85,13 @@ struct LayerPlan {
 };
 
 struct LayerWs {
-  size_t meta, off, expert, tok, slot, wdown, wgate, wup, sgate, h, total;
+  size_t meta, off, expert, tok, slot, wdown, wgate, wup, sgate, h, xq, total;
   int gmax, emax;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-static LayerWs layer_ws(int T, int n_ff, int E, int k) {
+static LayerWs layer_ws(int T, int hidden, int n_ff, int E, int k) {
   LayerWs w{};
   w.gmax = (T * k < E ? T * k : E) + 1;
   w.emax = T * k + T;
@@ -106,6 +106,9 @@ static LayerWs layer_ws(int T, int n_ff, int E, int k) {
   w.wup = o;    o = align256(o + w.gmax * sizeof(unsigned long long));
   w.sgate = o;  o = align256(o + static_cast<size_t>(T) * sizeof(float));
   w.h = o;      o = align256(o + static_cast<size_t>(T) * (k + 1) * n_ff * sizeof(float));
+  // several tokens: Q8_K of x in the LDS block layout (written by the routing
+  // launch, read by the gate/up launch)
+  w.xq = o;     o = align256(o + (T > 1 ? static_cast<size_t>(T) * (hidden / kQK) * kXStride * 4 : 0));
   w.total = o;
   return w;
 }
@@ -133,6 +136,7 @@ struct LayerArgs {
   LayerPlan plan;
   float* h;
   float* sgate;  // [T] sigmoid(sh_gate_w . x[t]) when sh_gate_w is set
+  uint32_t* xq;  // T > 1: Q8_K of x, kXStride words per block (token-major)
   int T, hidden, n_ff, n_expert, k, has_shared, gmax, emax;
   float shared_w;
   int back_rows, back_lrow;  // rows per back workgroup, lanes per row there
@@ -498,6 +502,104 @@ __device__ __forceinline__ void gateup_wave(bool present, int row0, int nrw, int
   }
 }
 
+// One wave's share of a gate/up workgroup of the several-token launch: its
+// nrw gate rows and the same up rows (in buf, landed and visible) against
+// the Q8_K x of each of the group's n entries, h = SiLU(g) * u per entry.
+// x comes from xq (global, kXStride words per block, token-major): entry
+// 0's token is already in x0 (LDS); the others are copied into the weight
+// buffers xspace (every wave's, kSpaceWords words) once every wave holds
+// its weights in registers, as many per round as fit.  x is read from LDS
+// one sub-block group at a time, which keeps the kernel within 128
+// registers (four workgroups per CU).  Every wave of the workgroup calls
+// this with the same n.
+constexpr int kSpaceWords = 4 * 64 * 36;
+template <typename Entry>
+__device__ __forceinline__ void gateup_group(bool present, int row0, int nrw, int nbh, int lpr,
+                                             const uint32_t* buf, uint32_t* xspace,
+                                             const uint32_t* x0, const uint32_t* xq, Entry entry,
+                                             int n, int stride, int n_ff, float* h, int lane,
+                                             int wave) {
+  const int half = lane >> 5, hl = lane & 31;
+  const int blk = hl & (lpr - 1), rr = hl / lpr;
+  const bool live = present && blk < nbh && rr < nrw;
+  uint32_t w36[36];
+  ScaleMins sm8{};
+  if (live) {
+    read_block_lds(buf + 36 * (half * nrw * nbh + rr * nbh + blk), w36);
+    sm8 = unpack_scales(w36[1], w36[2], w36[3]);
+  }
+  auto dot_store = [&](const uint32_t* xtok, int t, int sl) {
+    float s = 0.f;
+    if (live) {
+      const uint32_t* xb = xtok + blk * kXStride;
+      int32_t ip[8];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const u32x4* p4 = reinterpret_cast<const u32x4*>(xb + 16 * gq);
+        int32_t xg[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const u32x4 v = p4[i];
+          xg[4 * i] = static_cast<int32_t>(v.x);
+          xg[4 * i + 1] = static_cast<int32_t>(v.y);
+          xg[4 * i + 2] = static_cast<int32_t>(v.z);
+          xg[4 * i + 3] = static_cast<int32_t>(v.w);
+        }
+        int32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t w = w36[4 + 8 * gq + j];
+          lo = __builtin_amdgcn_sdot4(static_cast<int>(w & 0x0F0F0F0Fu), xg[j], lo, false);
+          hi = __builtin_amdgcn_sdot4(static_cast<int>((w >> 4) & 0x0F0F0F0Fu), xg[8 + j], hi,
+                                      false);
+        }
+        ip[2 * gq] = lo;
+        ip[2 * gq + 1] = hi;
+      }
+      float bsf[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) bsf[q] = __builtin_bit_cast(float, xb[65 + q]);
+      s = block_sum(w36[0], sm8, ip, __builtin_bit_cast(float, xb[64]), bsf);
+    }
+    const float acc = row_sum_last(s, blk, nbh);
+    const float up = __shfl_xor(acc, 32, 64);
+    if (half == 0 && blk == nbh - 1 && rr < nrw)
+      h[(static_cast<long long>(t) * stride + sl) * n_ff + row0 + rr] =
+          present ? silu_mul_kc(acc, up) : 0.f;
+  };
+  if (n > 0) {
+    int t, sl;
+    entry(0, t, sl);
+    dot_store(x0, t, sl);
+  }
+  const int xw = nbh * kXStride;    // words of one token's x
+  const int cw = xw / 4;            // its 16-B chunks
+  const int cap = kSpaceWords / xw;  // tokens per round in the weight buffers
+#pragma unroll 1
+  for (int e0 = 1; e0 < n; e0 += cap) {
+    const int ne = min(cap, n - e0);
+    bar();  // every wave's weights are in registers: the buffers are free
+    const int nch = ne * cw;
+#pragma unroll 1
+    for (int c0 = 64 * wave; c0 < nch; c0 += 256) {
+      const int c = min(c0 + lane, nch - 1);
+      const int ei = c / cw;
+      int t, sl;
+      entry(e0 + ei, t, sl);
+      const uint32_t* src = xq + static_cast<long long>(t) * xw + 4 * (c - ei * cw);
+      __builtin_amdgcn_global_load_lds((glb_void_p)src, (lds_void_p)(xspace + 4 * c0), 16, 0, 0);
+    }
+    wait_vm();
+    bar();
+#pragma unroll 1
+    for (int i = 0; i < ne; ++i) {
+      int t, sl;
+      entry(e0 + i, t, sl);
+      dot_store(xspace + i * xw, t, sl);
+    }
+  }
+}
+
 // Copy gate rows [row0, row0+nrw) and the same up rows into a wave buffer.
 // (part/nparts: this wave's share of the copy instructions, as dma_chunks)
 __device__ __forceinline__ void dma_gateup(const sg_block_q4k* wg, const sg_block_q4k* wu,
@@ -510,29 +612,37 @@ __device__ __forceinline__ void dma_gateup(const sg_block_q4k* wg, const sg_bloc
              lane, part, nparts);
 }
 
-// x values of a wave's first quantization pass, loaded at kernel start so
-// their latency overlaps the routing: one Q8_K block per 16-lane row, block
-// 4w + (lane >> 4), the lane's 16 values.  Waves w < nw take part.
+// x values of a wave's first P quantization passes, loaded at kernel start
+// so their latency overlaps the routing or the plan: one Q8_K block per
+// 16-lane row, pass p taking block 4 (p nw + w) + (lane >> 4), the lane's 16
+// values.  Waves w < nw take part.
+template <int P>
 __device__ __forceinline__ void x_preload(const float* x, int n_blocks, int w, int nw, int lane,
-                                          float (&pre)[16]) {
+                                          float (&pre)[P][16]) {
   if (w >= nw) return;
-  const int b = 4 * w + (lane >> 4);
-  const float* xb = x + static_cast<long long>(b < n_blocks ? b : 0) * kQK + 16 * (lane & 15);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) pre[i] = xb[i];
+  for (int p = 0; p < P; ++p) {
+    const int b = 4 * (p * nw + w) + (lane >> 4);
+    const float* xb = x + static_cast<long long>(b < n_blocks ? b : 0) * kQK + 16 * (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pre[p][i] = xb[i];
+  }
 }
 
 // Q8_K of the x rows into LDS (kXStride layout), one block per 16-lane row:
-// pass p of wave w takes block 4 (p nw + w) + (lane >> 4); pass 0's values
-// come from x_preload.
+// pass p of wave w takes block 4 (p nw + w) + (lane >> 4); the first P
+// passes' values come from x_preload.
+template <int P>
 __device__ __forceinline__ void quantize_x(const float* x, int n_blocks, uint32_t* xs, int w,
-                                           int nw, int lane, const float (&pre)[16]) {
+                                           int nw, int lane, const float (&pre)[P][16]) {
   if (w >= nw) return;
-  {
-    const int b = 4 * w + (lane >> 4);
-    quantize_row16_lds(pre, xs + (b < n_blocks ? b : 0) * kXStride, b < n_blocks, lane);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int b = 4 * (p * nw + w) + (lane >> 4);
+    if (p > 0 && 4 * p * nw >= n_blocks) break;  // wave-uniform
+    quantize_row16_lds(pre[p], xs + (b < n_blocks ? b : 0) * kXStride, b < n_blocks, lane);
   }
-  for (int b0 = 4 * nw; b0 < n_blocks; b0 += 4 * nw) {
+  for (int b0 = 4 * nw * P; b0 < n_blocks; b0 += 4 * nw) {
     const int b = b0 + 4 * w + (lane >> 4);
     const int bc = b < n_blocks ? b : 0;
     const float* xb = x + static_cast<long long>(bc) * kQK + 16 * (lane & 15);
@@ -1056,7 +1166,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   // while waves 0-2 issue the weight stream and quantize x
   const bool t1w = T == 1 && a.logits != nullptr && !shared_grp;
   const int nqw = t1w ? 3 : 4;
-  float xpre[16];
+  float xpre[1][16];
   if (!publisher) x_preload(a.x, nxb, wave, nqw, lane, xpre);
 
   if (shared_grp) {
@@ -1118,6 +1228,9 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
     // for three or more tokens, E <= 128 EPT for two)
     constexpr int kPl1 = EPT < 16 ? EPT : 16, kPl2 = 2 * EPT < 16 ? 2 * EPT : 16;
     float* evw = reinterpret_cast<float*>(dyn + L.ev) + wave * L.e32;
+    // x of the window for waves 1-3 to quantize while wave 0 builds the plan
+    float xw[3][16];
+    if (wave > 0) x_preload(a.x, nxb, wave - 1, 3, lane, xw);
     for (int t = wave; t < T; t += 4) {
       const float* lg = a.logits + static_cast<long long>(t) * E;
       if (T == 2)
@@ -1127,6 +1240,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
     }
     SG_MARK_FRONT(9);
     bar();
+    if (wave > 0) quantize_x(a.x, nxb, a.xq, wave - 1, 3, lane, xw);
     build_plan(dyn, L, T, k, E, a.has_shared, tid);
     SG_MARK_FRONT(10);
     n_groups = gbase + ctrl[1];
@@ -1260,6 +1374,11 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
       }
     }
   } else {
+    if (publisher && T > 1) {  // the gate/up launch reads x quantized
+      float xw[1][16];
+      x_preload(a.x, nxb, wave, 4, lane, xw);
+      quantize_x(a.x, nxb, a.xq, wave, 4, lane, xw);
+    }
     for (int i = tid; i < T * k; i += 256) ridx[i] = a.idx[(i / k) * stride + (i % k)];
     for (int i = tid; i < T * stride; i += 256) rw[i] = a.weight[i];
     bar();
@@ -1394,42 +1513,69 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs args) {
 // every compute workgroup would cost more than a launch.  Grid (row chunks
 // of 16, gmax); groups beyond the plan's count exit.
 template <int NBH, int kShapeT = 0, bool kSh = false>
-__global__ void __launch_bounds__(256) layer_gateup_kernel(LayerArgs args) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
+layer_gateup_kernel(LayerArgs args) {
   LayerArgs a = args;
   apply_shape<kShapeT, kSh>(a);
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
-  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];  // xs, then entry tok / slot
+  extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];  // x0, then entry tok / slot
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int T = a.T, k = a.k, stride = k + 1, g = blockIdx.y, bx = blockIdx.x;
+  const int k = a.k, stride = k + 1, g = blockIdx.y, bx = blockIdx.x;
   const int nbh = NBH ? NBH : a.hidden / kQK, lpr = NBH ? pow2_ceil(NBH) : pow2_ceil(nbh);
   const int rpw = 32 / lpr;
   const int row0 = bx * 4 * rpw + wave * rpw;
   const int nrw = max(0, min(rpw, a.n_ff - row0));
-  const int nxb = T * nbh;
-  float xpre[16];
-  x_preload(a.x, nxb, wave, 4, lane, xpre);
+  const int xw = nbh * kXStride;
+  SG_MARK_FRONT(0);
+  // every plan word this workgroup needs in one round (g < gmax: inside
+  // the plan arrays even past the live groups); the entry list too when it
+  // fits one wave (lane = entry, the same in every wave), so no load waits
+  // for off[]
   const int n_groups = a.plan.meta[0];
-  if (g >= n_groups) return;
   const unsigned long long wg = a.plan.wgate[g], wu = a.plan.wup[g];
+  const int off0 = a.plan.off[g], off1 = a.plan.off[g + 1];
+  const bool ent1 = a.emax <= 64;
+  const int v_tok = ent1 ? a.plan.tok[min(lane, a.emax - 1)] : 0;
+  const int v_slot = ent1 ? a.plan.slot[min(lane, a.emax - 1)] : 0;
+  if (g >= n_groups) return;
   const bool present = wg != 0ull && wu != 0ull;
+  // entries of the group (clamped to the plan's capacity), at etok/eslot[j0 ..]
+  const int j0 = min(max(off0, 0), a.emax);
+  const int n = min(max(off1, j0), a.emax) - j0;
+  SG_MARK_FRONT(1);
   if (present && nrw > 0)
     dma_gateup(reinterpret_cast<const sg_block_q4k*>(wg), reinterpret_cast<const sg_block_q4k*>(wu),
                row0, nrw, nbh, wbuf[wave], lane);
-  // entries of the group (clamped to the plan's capacity)
-  const int j0 = min(max(a.plan.off[g], 0), a.emax);
-  const int n = min(max(a.plan.off[g + 1], j0), a.emax) - j0;
-  uint32_t* xs = dyn;
-  int* etok = reinterpret_cast<int*>(dyn + ((T * nbh * kXStride + 3) & ~3));
-  int* eslot = etok + a.emax;
-  for (int i = tid; i < n; i += 256) {
-    etok[i] = a.plan.tok[j0 + i];
-    eslot[i] = a.plan.slot[j0 + i];
+  // the first entry's x (quantized by the routing launch) beside the
+  // weights, one copy instruction per wave
+  uint32_t* x0 = dyn;
+  if (n > 0) {
+    const int t0 = ent1 ? __shfl(v_tok, j0, 64) : a.plan.tok[j0];
+    const uint32_t* src = a.xq + static_cast<long long>(t0) * xw;
+    dma_chunks([&](int c) { return reinterpret_cast<const char*>(src) + 16 * c; }, xw / 4, x0,
+               lane, wave, 4);
   }
-  quantize_x(a.x, nxb, xs, wave, 4, lane, xpre);
+  SG_MARK_FRONT(2);
+  int* etok = reinterpret_cast<int*>(dyn + ((xw + 3) & ~3));
+  int* eslot = etok + a.emax;
+  if (ent1) {
+    if (tid < a.emax) {
+      etok[tid] = v_tok;
+      eslot[tid] = v_slot;
+    }
+  } else {
+    for (int i = tid; i < n; i += 256) {
+      etok[j0 + i] = a.plan.tok[j0 + i];
+      eslot[j0 + i] = a.plan.slot[j0 + i];
+    }
+  }
+  wait_vm();  // this wave's weights and its share of x0
   bar();
-  gateup_wave(present, row0, nrw, nbh, lpr, wbuf[wave], xs,
-              [&](int j, int& t, int& sl) { t = etok[j]; sl = eslot[j]; }, n, stride, a.n_ff, a.h,
-              lane);
+  SG_MARK_FRONT(3);
+  gateup_group(present, row0, nrw, nbh, lpr, wbuf[wave], &wbuf[0][0], x0, a.xq,
+               [&](int j, int& t, int& sl) { t = etok[j0 + j]; sl = eslot[j0 + j]; }, n, stride,
+               a.n_ff, a.h, lane, wave);
+  SG_MARK_FRONT(4);
   if (g == 0 && a.has_shared && a.sh_gate_w && bx == 0) shared_gate_tokens(a, tid);
 }
 
@@ -1475,24 +1621,25 @@ __host__ __device__ constexpr BackLds back_lds(int T, int k, int n_ff, int rows,
 }
 
 // Q8_K of every (token, slot) h row of the back kernel into hq (LDS): wave w
-// quantizes blocks e = w + 8j, j < kBackHSlots from hpre (its registers) in
+// quantizes blocks e = w + 8j, j < HS from hpre (its registers) in
 // one interleaved pass (every block of a one-token layer with k <= 8), later
 // ones in passes of four loaded here.
+template <int HS>
 __device__ __forceinline__ void back_quantize_h(const LayerArgs& a, uint32_t* hq,
-                                                const float (&hpre)[kBackHSlots][4], int nq,
+                                                const float (&hpre)[HS][4], int nq,
                                                 int wave, int lane) {
   if (wave < nq) {
-    uint32_t* dst[kBackHSlots];
+    uint32_t* dst[HS];
     int n = 0;
 #pragma unroll
-    for (int j = 0; j < kBackHSlots; ++j) {
+    for (int j = 0; j < HS; ++j) {
       const int e = wave + kBackWaves * j;
       dst[j] = hq + (e < nq ? e : wave) * kXStride;
       n += e < nq;
     }
-    quantize_n_lds<kBackHSlots>(hpre, dst, n, lane);
+    quantize_n_lds<HS>(hpre, dst, n, lane);
   }
-  for (int e0 = wave + kBackWaves * kBackHSlots; e0 < nq; e0 += 4 * kBackWaves) {
+  for (int e0 = wave + kBackWaves * HS; e0 < nq; e0 += 4 * kBackWaves) {
     float v[4][4];
     uint32_t* dst[4];
     int n = 0;
@@ -1512,15 +1659,15 @@ __device__ __forceinline__ void back_quantize_h(const LayerArgs& a, uint32_t* hq
 // The down rows, Q8_K of h and combine of one chunk of `rows` output rows,
 // with the plan in LDS (off, wdown, tok, slot, wt, meta).  Wave w
 // quantizes h blocks w + 8j; hpre[j] holds the lane's 4 values of block
-// w + 8j for j < kBackHSlots (loaded at kernel start).
+// w + 8j for j < HS (loaded at kernel start).
 // NBF, ROWS: n_ff / 256 and the rows per workgroup when known at compile
 // time (0 = read from a).  pre: the kernel start has already issued every
 // group's down-row copies (the packed one-pass layout) and quantized h,
 // and the barrier after them has passed.
-template <int NBF, int ROWS>
+template <int NBF, int ROWS, int HS>
 __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, uint32_t* bd,
                           uint32_t (*wbuf)[64 * 36], int row0, int nr, float res0,
-                          const float (&hpre)[kBackHSlots][4], bool pre) {
+                          const float (&hpre)[HS][4], bool pre) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, k = a.k, stride = k + 1;
   const int nbf = NBF ? NBF : a.n_ff / kQK;
@@ -1594,7 +1741,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
     }
     SG_MARK_BACK(2);
     if (gb == 0 && !pre) {  // Q8_K of every (token, slot) h row while the rows stream in
-      back_quantize_h(a, hq, hpre, nq, wave, lane);
+      back_quantize_h<HS>(a, hq, hpre, nq, wave, lane);
       SG_MARK_BACK(3);
       if (spread) wait_vm();  // this wave's share of the copies
       bar();
@@ -1702,13 +1849,14 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args
   const int nr = max(0, min(rows, a.hidden - row0));
   SG_MARK_BACK(0);
 
-  // loads that do not depend on the plan: this wave's first kBackHSlots h
+  // loads that do not depend on the plan: this wave's first HS h
   // blocks (block wave + 8j of the (token, slot) rows) and the residual
   const int nq = T * stride * nbf;
-  float hpre[kBackHSlots][4];
+  constexpr int HS = kShapeT == kShapeWindow ? 9 : kBackHSlots;  // the window: every block
+  float hpre[HS][4];
   if (wave < nq) {
 #pragma unroll
-    for (int j = 0; j < kBackHSlots; ++j) {
+    for (int j = 0; j < HS; ++j) {
       const int e0 = wave + kBackWaves * j;
       const int e = e0 < nq ? e0 : wave;
       const float* hp = a.h + static_cast<long long>(e) * kQK + 4 * lane;
@@ -1796,12 +1944,12 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args
   }
   for (int i = tid; i < T * stride * rows; i += kBackThreads) ys[i] = 0.f;
   if (pre) {
-    back_quantize_h(a, dyn + L.hq, hpre, nq, wave, lane);
+    back_quantize_h<HS>(a, dyn + L.hq, hpre, nq, wave, lane);
     wait_vm();  // this wave's copies, visible to all after the barrier
   }
   bar();
   SG_MARK_BACK(1);
-  back_core<NBF, ROWS>(a, L, dyn, wbuf, row0, nr, res0, hpre, pre);
+  back_core<NBF, ROWS, HS>(a, L, dyn, wbuf, row0, nr, res0, hpre, pre);
 }
 
 static void back_geometry(int hidden, int n_ff, int& rows, int& lrow) {
@@ -1851,7 +1999,7 @@ extern "C" {
 
 size_t sg_moe_layer_workspace_bytes(int n_tokens, int hidden, int n_ff, int n_expert, int k) {
   if (n_tokens <= 0 || hidden <= 0 || n_ff <= 0 || n_expert <= 0 || k <= 0) return 0;
-  return layer_ws(n_tokens, n_ff, n_expert, k).total;
+  return layer_ws(n_tokens, hidden, n_ff, n_expert, k).total;
 }
 
 int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
@@ -1884,7 +2032,7 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
                      n_expert, kLMaxExperts);
   int rows = 1, lrow = 64;
   back_geometry(hidden, n_ff, rows, lrow);
-  const LayerWs ws = layer_ws(n_tokens, n_ff, n_expert, k);
+  const LayerWs ws = layer_ws(n_tokens, hidden, n_ff, n_expert, k);
   if (workspace_bytes < ws.total)
     return set_error(SG_ERR_INVALID_ARGUMENT, "%s: workspace %zu < %zu bytes", nm,
                      workspace_bytes, ws.total);
@@ -1921,6 +2069,7 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
                      reinterpret_cast<unsigned long long*>(base + ws.wgate),
                      reinterpret_cast<unsigned long long*>(base + ws.wup)};
   a.h = reinterpret_cast<float*>(base + ws.h);
+  a.xq = n_tokens > 1 ? reinterpret_cast<uint32_t*>(base + ws.xq) : nullptr;
   a.sgate = a.sh_gate_w ? reinterpret_cast<float*>(base + ws.sgate) : nullptr;
   a.T = n_tokens;
   a.hidden = hidden;
@@ -1942,8 +2091,8 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   // several tokens: routing launch (the publisher alone), then the gate/up
   // launch reading its plan; one token: one fused launch whose compute
   // workgroups route speculatively beside their weight stream
-  const size_t lds_g =
-      (static_cast<size_t>((n_tokens * (hidden / kQK) * kXStride + 3) & ~3) + 2 * ws.emax) * 4;
+  // the gate/up launch: the first entry's x, then the entries
+  const size_t lds_g = static_cast<size_t>((((hidden / kQK) * kXStride + 3) & ~3) + 2 * ws.emax) * 4;
   a.publish_only = n_tokens > 1;
   if (a.publish_only && lds_g + 4 * buf_b > 160 * 1024)
     return set_error(SG_ERR_UNSUPPORTED, "%s: this shape needs more LDS than a workgroup has",

@@ -411,6 +411,8 @@ grouped_mfma_kernel(GroupedArgs a) {
     for (int i = 0; i < 4; ++i) acc[ti][i] = 0.f;
   for (int b = 0; b < nb; ++b) {
     const int s = b & 1;
+    if (b == 2) SG_PF_MARK(14);
+    if (b == 5) SG_PF_MARK(15);
     wait_vm();  // this wave's copies of block b have landed
     bar();      // ... and every wave's
     if (b < 8) SG_PF_MARK(2 + b);
