@@ -351,56 +351,49 @@ __device__ __forceinline__ void build_plan(uint32_t* dyn, const FrontLds& L, int
   const int gbase = has_shared, ebase = has_shared ? T : 0;
   if (R <= 64) {
     if (tid < 64) {
-      // every lane reads all R ids (and first flags) back from LDS with
-      // broadcast 16-B reads: the wave's own writes, visible to its later
-      // reads without a barrier (cross-lane register reads in a loop would
-      // wait on each other in turn)
+      // One wave sorts the routes by key = (expert, route index): each
+      // lane's rank is the count of smaller keys, read back from LDS with
+      // broadcast 16-B reads (the wave's own writes, visible to its later
+      // reads without a barrier).  Keys are below 2^17, so the comparison
+      // is the sign bit of an integer difference (no lane masks).  An
+      // invalid id sorts last and is left out.  Then the sorted keys come
+      // back in lane order: lane r holds the r-th entry, its expert starts
+      // a group when the previous entry's differs, and its group is the
+      // count of group starts below it (a ballot).
       const int lane = tid;
       int e = lane < R ? ridx[lane] : -1;
       if (e < 0 || e >= E) e = -1;
       if (lane < R) re[lane] = e;
-      // The flags are sign bits of integer differences (ids lie in
-      // [-1, 1024)), so the loops are plain integer arithmetic: comparisons
-      // would each make a lane mask, and 4 R of them exhaust the scalar
-      // registers.
-      // (a bit-field extract, which the compiler keeps as arithmetic)
-      auto lt = [](int x, int y) {
-        return static_cast<int>(__builtin_amdgcn_ubfe(static_cast<unsigned>(x - y), 31, 1));
-      };
-      auto eq = [](int x, int y) {
-        return static_cast<int>(__builtin_amdgcn_ubfe(static_cast<unsigned>((x ^ y) - 1), 31, 1));
-      };
-      int dup = 0, rank = 0;
+      const int key = lane < R ? (e >= 0 ? e : 1024) * 64 + lane : 0x7FFFFFFF;
+      int* keys = rfirst;  // the sort's scratch: R keys, then the sorted ones
+      if (lane < R) keys[lane] = key;
+      int rank = 0;
       for (int j0 = 0; j0 < R; j0 += 4) {
-        const int4 v = *reinterpret_cast<const int4*>(re + j0);
-        const int ev4[4] = {v.x, v.y, v.z, v.w};
+        const int4 v = *reinterpret_cast<const int4*>(keys + j0);
+        const int kv4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int j = j0 + u, ej = ev4[u];
-          const int ok = lt(j, R) & (1 - lt(ej, 0));
-          const int before = lt(j, lane), same = eq(ej, e);
-          rank += ok & (lt(ej, e) | (same & before));
-          dup |= ok & before & same;
-        }
+        for (int u = 0; u < 4; ++u)
+          if (j0 + u < R)
+            rank += static_cast<int>(__builtin_amdgcn_ubfe(static_cast<unsigned>(kv4[u] - key), 31, 1));
       }
-      const bool first = e >= 0 && !dup;
-      if (lane < R) rfirst[lane] = first;
-      int grp = 0;
-      for (int j0 = 0; j0 < R; j0 += 4) {
-        const int4 v = *reinterpret_cast<const int4*>(re + j0);
-        const int4 f = *reinterpret_cast<const int4*>(rfirst + j0);
-        const int ev4[4] = {v.x, v.y, v.z, v.w}, fv4[4] = {f.x, f.y, f.z, f.w};
-#pragma unroll
-        for (int u = 0; u < 4; ++u) grp += lt(j0 + u, R) & fv4[u] & lt(ev4[u], e);
-      }
+      int* sorted = ptok;  // placed here, then overwritten below with the entries' tokens
       const int nv = __popcll(__ballot(e >= 0));
-      const int nf = __popcll(__ballot(first));
-      if (e >= 0) {
-        ptok[ebase + rank] = lane / k;
-        pslot[ebase + rank] = lane % k;
+      if (lane < R) sorted[rank] = key;
+      const int sk = lane < nv ? sorted[lane] : 0;
+      const int sp = lane > 0 && lane < nv ? sorted[lane - 1] : -64;
+      const int se = sk >> 6, si = sk & 63;
+      const bool first = lane < nv && (lane == 0 || (sp >> 6) != se);
+      const uint64_t fm = __ballot(first);
+      const int grp = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(fm >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(fm), 0));
+      const int nf = __popcll(fm);
+      wait_lds();  // the sorted keys are read before the entries overwrite them
+      if (lane < nv) {
+        ptok[ebase + lane] = si / k;
+        pslot[ebase + lane] = si % k;
         if (first) {
-          poff[gbase + grp] = ebase + rank;
-          pexp[gbase + grp] = e;
+          poff[gbase + grp] = ebase + lane;
+          pexp[gbase + grp] = se;
         }
       }
       if (has_shared && lane < T) {
@@ -1526,7 +1519,7 @@ layer_gateup_kernel(LayerArgs args) {
   const int row0 = bx * 4 * rpw + wave * rpw;
   const int nrw = max(0, min(rpw, a.n_ff - row0));
   const int xw = nbh * kXStride;
-  SG_MARK_FRONT(0);
+  SG_MARK_FRONT(11);
   // every plan word this workgroup needs in one round (g < gmax: inside
   // the plan arrays even past the live groups); the entry list too when it
   // fits one wave (lane = entry, the same in every wave), so no load waits
@@ -1542,7 +1535,7 @@ layer_gateup_kernel(LayerArgs args) {
   // entries of the group (clamped to the plan's capacity), at etok/eslot[j0 ..]
   const int j0 = min(max(off0, 0), a.emax);
   const int n = min(max(off1, j0), a.emax) - j0;
-  SG_MARK_FRONT(1);
+  SG_MARK_FRONT(12);
   if (present && nrw > 0)
     dma_gateup(reinterpret_cast<const sg_block_q4k*>(wg), reinterpret_cast<const sg_block_q4k*>(wu),
                row0, nrw, nbh, wbuf[wave], lane);
@@ -1555,7 +1548,7 @@ layer_gateup_kernel(LayerArgs args) {
     dma_chunks([&](int c) { return reinterpret_cast<const char*>(src) + 16 * c; }, xw / 4, x0,
                lane, wave, 4);
   }
-  SG_MARK_FRONT(2);
+  SG_MARK_FRONT(13);
   int* etok = reinterpret_cast<int*>(dyn + ((xw + 3) & ~3));
   int* eslot = etok + a.emax;
   if (ent1) {
@@ -1571,11 +1564,11 @@ layer_gateup_kernel(LayerArgs args) {
   }
   wait_vm();  // this wave's weights and its share of x0
   bar();
-  SG_MARK_FRONT(3);
+  SG_MARK_FRONT(14);
   gateup_group(present, row0, nrw, nbh, lpr, wbuf[wave], &wbuf[0][0], x0, a.xq,
                [&](int j, int& t, int& sl) { t = etok[j0 + j]; sl = eslot[j0 + j]; }, n, stride,
                a.n_ff, a.h, lane, wave);
-  SG_MARK_FRONT(4);
+  SG_MARK_FRONT(8);
   if (g == 0 && a.has_shared && a.sh_gate_w && bx == 0) shared_gate_tokens(a, tid);
 }
 
