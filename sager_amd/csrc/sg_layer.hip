@@ -1859,27 +1859,41 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args
   }
   const float res0 = residual_pre(a, row0, nr);
 
-  // The packed one-pass copy layout of back_core, when every plan this
-  // launch can hold fits it (gmax groups, at most kBackPreCopies copy
-  // instructions per wave): each thread loads the down pointers of its
+  // The packed one-pass copy layout of back_core, when the plan fits it
+  // (its groups within the copy instructions issued here): each thread
+  // loads the down pointers of its
   // chunks and the group count straight from the plan in global memory, so
   // the copies are issued as soon as those land, and h is quantized before
   // the first barrier.
   const int lrow = NBF ? pow2_ceil(NBF) : a.back_lrow;
   const int gpw = 64 / (rows * lrow);
   const int gwords = rows * nbf * 36, cpg = gwords / 4;
-  const bool pre = gpw * gwords == 64 * 36 && a.gmax <= a.back_bufs * gpw &&
-                   a.gmax * cpg <= 64 * kBackWaves * kBackPreCopies;
+  // (PC copy instructions per wave: the groups they hold, cap, cover every
+  // plan of the one-token shape; whether a plan fits is decided once its
+  // group count has landed.  Nine per wave for the window's 32 groups
+  // measured slower than the copies of back_core.)
+  constexpr int PC = kBackPreCopies;
+  const int cap = min(a.back_bufs * gpw, 64 * kBackWaves * PC / cpg);
+  const bool pre_cand = kShapeT != kShapeWindow && gpw * gwords == 64 * 36 && cap > 0;
   const uint64_t inv = ((1ull << 24) + cpg - 1) / cpg;  // c / cpg exact for c < 2^24 / cpg
-  unsigned long long wdp[kBackPreCopies];
+  // (with up to 64 groups every wave loads them all, lane = group, and
+  // takes each chunk's pointer by a lane permute; otherwise one load per
+  // chunk)
+  const bool wd_lanes = a.gmax <= 64;
+  unsigned long long wdl = 0ull;
+  unsigned long long wdp[PC];
   int gpre = 0;
-  if (pre) {
+  if (pre_cand) {
     gpre = max(0, min(a.plan.meta[0], a.gmax));
+    if (wd_lanes) {
+      wdl = a.plan.wdown[min(lane, a.gmax - 1)];
+    } else {
 #pragma unroll
-    for (int i = 0; i < kBackPreCopies; ++i) {
-      const int c = 64 * (wave + kBackWaves * i) + lane;
-      const int gq = static_cast<int>((static_cast<uint64_t>(c) * inv) >> 24);
-      wdp[i] = a.plan.wdown[min(gq, a.gmax - 1)];
+      for (int i = 0; i < PC; ++i) {
+        const int c = 64 * (wave + kBackWaves * i) + lane;
+        const int gq = static_cast<int>((static_cast<uint64_t>(c) * inv) >> 24);
+        wdp[i] = a.plan.wdown[min(gq, a.gmax - 1)];
+      }
     }
   }
 
@@ -1917,20 +1931,30 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args
     for (int i = tid; i < T; i += kBackThreads) sgl[i] = a.sgate ? a.sgate[i] : 1.f;
   }
   uint32_t(*wbuf)[64 * 36] = reinterpret_cast<uint32_t(*)[64 * 36]>(dyn + L.total);
+  const bool pre = pre_cand && gpre <= cap;
   if (pre) {
     // chunk c = 64 t + lane, t = wave + 8i: group c / cpg, chunk c % cpg of
     // its rows, to wbuf[0] + 4c (what back_core's packed layout reads)
     const int cval = nr * nbf * 9, total = gpre * cpg;
     const long long roff = static_cast<long long>(row0) * nbf * kQ4Bytes;
 #pragma unroll
-    for (int i = 0; i < kBackPreCopies; ++i) {
+    for (int i = 0; i < PC; ++i) {
       const int t = wave + kBackWaves * i;
       const int c = 64 * t + lane;
       const int gq = static_cast<int>((static_cast<uint64_t>(c) * inv) >> 24);
       const int w = c - gq * cpg;
-      if (c < total && wdp[i] && w < cval)
+      unsigned long long wd;
+      if (wd_lanes) {
+        const int src = 4 * min(gq, 63);
+        const unsigned lo = __builtin_amdgcn_ds_bpermute(src, static_cast<int>(wdl));
+        const unsigned hi = __builtin_amdgcn_ds_bpermute(src, static_cast<int>(wdl >> 32));
+        wd = (static_cast<unsigned long long>(hi) << 32) | lo;
+      } else {
+        wd = wdp[i];
+      }
+      if (c < total && wd && w < cval)
         __builtin_amdgcn_global_load_lds(
-            (glb_void_p)(reinterpret_cast<const char*>(wdp[i]) + roff + 16 * w),
+            (glb_void_p)(reinterpret_cast<const char*>(wd) + roff + 16 * w),
             (lds_void_p)(wbuf[0] + 256 * t), 16, 0, 0);
     }
     if (tid == 0) meta[0] = gpre;
