@@ -1150,7 +1150,10 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   const FrontLds& L = shared_grp ? a.front_shared : a.front_routed;
   const int rpw = 32 / lpr;
   const int row0 = bx * 4 * rpw + wave * rpw;
-  const int nrw = max(0, min(rpw, a.n_ff - row0));
+  // (every chunk full when n_ff is a multiple of the workgroup's rows: then
+  // a constant in the shape instances, and the copies need no lane masks)
+  const bool full = a.n_ff % (4 * rpw) == 0;
+  const int nrw = full ? rpw : max(0, min(rpw, a.n_ff - row0));
   const int gbase = a.has_shared;
   uint32_t* buf = wbuf[wave];
   uint32_t* xs = dyn + L.xs;
@@ -1204,7 +1207,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   auto stream_rows = [&](int e, int w, int part = 0, int nparts = 1) {
     if (e < 0) return false;
     const int r0 = bx * 4 * rpw + w * rpw;
-    const int n = min(rpw, a.n_ff - r0);
+    const int n = full ? rpw : min(rpw, a.n_ff - r0);
     const sg_block_q4k* wg = reinterpret_cast<const sg_block_q4k*>(tabg[e]);
     const sg_block_q4k* wu = reinterpret_cast<const sg_block_q4k*>(tabu[e]);
     if (wg && wu && n > 0) dma_gateup(wg, wu, r0, n, nbh, wbuf[w], lane, part, nparts);
@@ -1268,8 +1271,14 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
           // rows) so wave 3 routes unblocked.
           const int want = g - gbase;
           const int idl = lane < k ? sel_idx(tk) : 0x7FFFFFFF;
+          // its rank among the k ids, which every lane reads from top[]
+          // (broadcast reads; ids < 2^16, so a comparison is the sign bit
+          // of a difference)
           int r = 0;
-          for (int i = 0; i < k; ++i) r += __builtin_amdgcn_readlane(idl, i) < idl;
+          const uint32_t* tw = reinterpret_cast<const uint32_t*>(top);
+          for (int i = 0; i < k; ++i)
+            r += static_cast<int>(__builtin_amdgcn_ubfe(
+                static_cast<unsigned>(sel_idx(tw[2 * i]) - idl), 31, 1));
           const uint64_t hit = __ballot(lane < k && r == want);
           slot_mine = hit ? __builtin_ctzll(hit) : -1;
           e_mine = hit ? __builtin_amdgcn_readlane(idl, slot_mine) : -1;
@@ -1517,7 +1526,10 @@ layer_gateup_kernel(LayerArgs args) {
   const int nbh = NBH ? NBH : a.hidden / kQK, lpr = NBH ? pow2_ceil(NBH) : pow2_ceil(nbh);
   const int rpw = 32 / lpr;
   const int row0 = bx * 4 * rpw + wave * rpw;
-  const int nrw = max(0, min(rpw, a.n_ff - row0));
+  // (every chunk full when n_ff is a multiple of the workgroup's rows: then
+  // a constant in the shape instances, and the copies need no lane masks)
+  const bool full = a.n_ff % (4 * rpw) == 0;
+  const int nrw = full ? rpw : max(0, min(rpw, a.n_ff - row0));
   const int xw = nbh * kXStride;
   SG_MARK_FRONT(11);
   // every plan word this workgroup needs in one round (g < gmax: inside
