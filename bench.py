@@ -434,8 +434,10 @@ def mfma_summary(counter_csv, out_md, command):
     rows = {}
     for d in disp.values():
         rows.setdefault(d["name"], []).append(d)
-    alg = {"grouped_mfma_kernel<true>": T5_ROUTES * 2 * F * H * 2,
-           "grouped_mfma_kernel<false>": T5_ROUTES * H * F * 2}
+    # by the first template argument (gate/up or down; the second says
+    # whether the down pass runs several column slices per workgroup)
+    alg = {"grouped_mfma_kernel<true": T5_ROUTES * 2 * F * H * 2,
+           "grouped_mfma_kernel<false": T5_ROUTES * H * F * 2}
     with open(out_md, "w") as fh:
         fh.write("# int8 MFMA work of the prefill grouped contractions (config 5)\n\n")
         fh.write(f"```\n{command}\n```\n\n")
@@ -453,7 +455,7 @@ def mfma_summary(counter_csv, out_md, command):
             us = med("ns") / 1e3
             ops = med("SQ_INSTS_VALU_MFMA_MOPS_I8") * 512
             key = name.replace("void ", "").replace("sg::", "")
-            aops = alg.get(key, 0)
+            aops = next((v for k, v in alg.items() if key.startswith(k)), 0)
             tops, atops = ops / (us * 1e-6) / 1e12, aops / (us * 1e-6) / 1e12
             fh.write(f"| `{name.replace('void ', '')}` | {len(ds)} | {us:.1f} | "
                      f"{med('SQ_INSTS_MFMA'):.3g} | {med('SQ_INSTS_VALU'):.3g} | "
