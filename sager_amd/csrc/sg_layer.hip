@@ -187,7 +187,7 @@ __host__ __device__ constexpr FrontLds front_lds(int T, int nbh, int E, int k, b
     L.ptok = take(T * k + T);
     L.pslot = take(T * k + T);
     L.ctrl = take(8 + T * k);
-    L.kw = take(4 * 128);  // one key per lane of every wave (team_select, one key per thread)
+    L.kw = take(4 * 64 + 4 * 128);  // team_select, one key per thread: value words, then keys
   }
   L.total = o;
   return L;
@@ -218,6 +218,8 @@ __device__ __forceinline__ int rank_n(const uint64_t* c, int n, uint64_t key) {
   return r;
 }
 
+constexpr int kWaves4 = 4;  // waves of a front workgroup
+
 // Top-m selection of a team (tw waves) over the keys kr[] its threads hold
 // (0 = no key; keys are otherwise distinct).  Stage 1, per wave: the wave's
 // m largest keys go to cand[wave * m ...) (zero-padded).  With one key per
@@ -244,26 +246,50 @@ __device__ __forceinline__ void team_select(const FrontLds& L, const uint64_t* k
   uint64_t* wc = cand + wit * m;
   int base = 0;
   if constexpr (EPT == 1) {
-    // one key per lane: its rank among the wave's 64 keys, by comparison
-    // with all of them read back from LDS (the wave's own writes, 16-B
-    // broadcast reads, no barrier); ranks below m place the key
-    uint64_t* kw = reinterpret_cast<uint64_t*>(kwbase) + 64 * (threadIdx.x >> 6);
-    kw[lane] = kr[0];
-    const u32x4* p = reinterpret_cast<const u32x4*>(kw);
+    // one key per lane: its rank among the wave's 64 keys by comparison
+    // with all of them, read back from LDS (the wave's own writes, 16-B
+    // broadcast reads, no barrier); ranks below m place the key.  First on
+    // the value word without its lowest bit (31 bits: a comparison is then
+    // the sign bit of a difference, plain arithmetic with no lane masks);
+    // two keys equal there take the same rank, so one overwrites the other
+    // in the candidate slots, which a read-back finds: then (rarely) the
+    // ranks are taken again on the whole keys.
+    uint32_t* kh = kwbase + 64 * (threadIdx.x >> 6);  // value words >> 1
+    const uint32_t hm = static_cast<uint32_t>(kr[0] >> 33);
+    kh[lane] = hm;
+    const u32x4* p = reinterpret_cast<const u32x4*>(kh);
     int r = 0;
 #pragma unroll
-    for (int q = 0; q < 32; q += 8) {
+    for (int q = 0; q < 16; q += 8) {
       u32x4 v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) v[u] = p[q + u];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const uint64_t a = (static_cast<uint64_t>(v[u].y) << 32) | v[u].x;
-        const uint64_t b = (static_cast<uint64_t>(v[u].w) << 32) | v[u].z;
-        r += (a > kr[0]) + (b > kr[0]);
+        r += static_cast<int>(__builtin_amdgcn_ubfe(hm - v[u].x, 31, 1)) +
+             static_cast<int>(__builtin_amdgcn_ubfe(hm - v[u].y, 31, 1)) +
+             static_cast<int>(__builtin_amdgcn_ubfe(hm - v[u].z, 31, 1)) +
+             static_cast<int>(__builtin_amdgcn_ubfe(hm - v[u].w, 31, 1));
       }
     }
-    if (kr[0] != 0 && r < m) wc[r] = kr[0];
+    const bool place = kr[0] != 0 && r < m;
+    if (place) wc[r] = kr[0];
+    // (read through volatile: the compiler would otherwise forward this
+    // lane's own store, which another lane's may have overwritten)
+    const bool lost = place && reinterpret_cast<volatile uint64_t*>(wc)[r] != kr[0];
+    if (__ballot(lost)) {
+      uint64_t* kw = reinterpret_cast<uint64_t*>(kwbase + 64 * kWaves4) + 64 * (threadIdx.x >> 6);
+      kw[lane] = kr[0];
+      const u32x4* p2 = reinterpret_cast<const u32x4*>(kw);
+      r = 0;
+      for (int q = 0; q < 32; ++q) {
+        const u32x4 v = p2[q];
+        const uint64_t a = (static_cast<uint64_t>(v.y) << 32) | v.x;
+        const uint64_t b = (static_cast<uint64_t>(v.w) << 32) | v.z;
+        r += (a > kr[0]) + (b > kr[0]);
+      }
+      if (kr[0] != 0 && r < m) wc[r] = kr[0];
+    }
     base = __popcll(__ballot(kr[0] != 0));
   } else {
     // th: the largest value word v with at least m keys of value >= v (0 when
