@@ -211,6 +211,18 @@ __device__ __forceinline__ void read_block_lds(const uint32_t* b, uint32_t* w36)
   }
 }
 
+// A double constant built in scalar registers (two s_mov_b32 through asm):
+// the compiler then keeps it there, as a scalar operand of the vector
+// instructions, instead of in a pair of vector registers.
+template <unsigned long long B>
+__device__ __forceinline__ double sconst() {
+  unsigned lo, hi;
+  asm("s_mov_b32 %0, %1" : "=s"(lo) : "n"(static_cast<unsigned>(B & 0xFFFFFFFFull)));
+  asm("s_mov_b32 %0, %1" : "=s"(hi) : "n"(static_cast<unsigned>(B >> 32)));
+  return __builtin_bit_cast(double, (static_cast<unsigned long long>(hi) << 32) | lo);
+}
+#define SG_SCONST(v) sconst<__builtin_bit_cast(unsigned long long, static_cast<double>(v))>()
+
 // ---- exp: double evaluation, one rounding to float ------------------------
 // x = k ln2 + r (|r| <= ln2/2, ln2 split in two doubles), e^r by its Taylor
 // series to degree 13 (remainder < 5e-18), scaled by 2^k, rounded once.
@@ -241,53 +253,51 @@ __host__ __device__ __forceinline__ float expf_sg(float xf) {
   return static_cast<float>(p * scale);
 }
 
-// SiLU(g) * u in the CPU chain's operation order (q4_avx2.cpp:187-191).
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  return g / (1.f + expf_sg(-g)) * u;
-}
-
-// A double constant built in scalar registers (two s_mov_b32 through asm):
-// the compiler then keeps it there, as a scalar operand of the vector
-// instructions, instead of in a pair of vector registers.
-template <unsigned long long B>
-__device__ __forceinline__ double sconst() {
-  unsigned lo, hi;
-  asm("s_mov_b32 %0, %1" : "=s"(lo) : "n"(static_cast<unsigned>(B & 0xFFFFFFFFull)));
-  asm("s_mov_b32 %0, %1" : "=s"(hi) : "n"(static_cast<unsigned>(B >> 32)));
-  return __builtin_bit_cast(double, (static_cast<unsigned long long>(hi) << 32) | lo);
-}
-#define SG_SCONST(v) sconst<__builtin_bit_cast(unsigned long long, static_cast<double>(v))>()
-
-// expf_sg with its double constants in scalar registers (sconst), for a
-// kernel short of vector registers: the same operations on the same
-// constants, so the same results.
+// expf_sg for the router and the window's gate/up kernel: the same
+// operations on the same constants (so the same results), with the double
+// constants built in scalar registers (sconst) rather than copied into
+// vector registers (four exps per lane in the router took 62 such moves,
+// and in the gate/up kernel the copies pushed it into spilling), and
+// branch-free: out-of-range and NaN arguments evaluate the polynomial at 0
+// and are replaced at the end, instead of a divergent region per exp.
 __device__ __forceinline__ float expf_sg_kc(float xf) {
-  if (xf != xf) return xf;
-  if (xf > 100.f) return __builtin_inff();
-  if (xf < -110.f) return 0.f;
-  const double x = static_cast<double>(xf);
-  const double kd = __builtin_rint(x * SG_SCONST(1.4426950408889634));
-  double r = __builtin_fma(-kd, SG_SCONST(6.9314718055994529e-01), x);
-  r = __builtin_fma(-kd, SG_SCONST(2.3190468138462996e-17), r);
+#define SG_EXPC(v) SG_SCONST(v)
+  const bool nan = !(xf == xf), big = xf > 100.f, small = xf < -110.f;
+  const float xs = (nan || big || small) ? 0.f : xf;
+  const double x = static_cast<double>(xs);
+  const double kd = __builtin_rint(x * SG_EXPC(1.4426950408889634));
+  double r = __builtin_fma(-kd, SG_EXPC(6.9314718055994529e-01), x);
+  r = __builtin_fma(-kd, SG_EXPC(2.3190468138462996e-17), r);
+  /* Estrin evaluation (short dependency chain): pairs, then r^2, r^4, r^8. */
   const double r2 = r * r, r4 = r2 * r2, r8 = r4 * r4;
   const double q0 = __builtin_fma(1.0, r, 1.0);
-  const double q1 = __builtin_fma(SG_SCONST(1.0 / 6.0), r, 0.5);
-  const double q2 = __builtin_fma(SG_SCONST(1.0 / 120.0), r, SG_SCONST(1.0 / 24.0));
-  const double q3 = __builtin_fma(SG_SCONST(1.0 / 5040.0), r, SG_SCONST(1.0 / 720.0));
-  const double q4 = __builtin_fma(SG_SCONST(1.0 / 362880.0), r, SG_SCONST(1.0 / 40320.0));
-  const double q5 = __builtin_fma(SG_SCONST(1.0 / 39916800.0), r, SG_SCONST(1.0 / 3628800.0));
-  const double q6 = __builtin_fma(SG_SCONST(1.0 / 6227020800.0), r, SG_SCONST(1.0 / 479001600.0));
+  const double q1 = __builtin_fma(SG_EXPC(1.0 / 6.0), r, 0.5);
+  const double q2 = __builtin_fma(SG_EXPC(1.0 / 120.0), r, SG_EXPC(1.0 / 24.0));
+  const double q3 = __builtin_fma(SG_EXPC(1.0 / 5040.0), r, SG_EXPC(1.0 / 720.0));
+  const double q4 = __builtin_fma(SG_EXPC(1.0 / 362880.0), r, SG_EXPC(1.0 / 40320.0));
+  const double q5 = __builtin_fma(SG_EXPC(1.0 / 39916800.0), r, SG_EXPC(1.0 / 3628800.0));
+  const double q6 = __builtin_fma(SG_EXPC(1.0 / 6227020800.0), r, SG_EXPC(1.0 / 479001600.0));
   const double s0 = __builtin_fma(q1, r2, q0), s1 = __builtin_fma(q3, r2, q2), s2 = __builtin_fma(q5, r2, q4);
   const double u0 = __builtin_fma(s1, r4, s0), u1 = __builtin_fma(q6, r4, s2);
   const double p = __builtin_fma(u1, r8, u0);
   const long long k = static_cast<long long>(kd);
   const double scale = __builtin_bit_cast(double, static_cast<unsigned long long>(k + 1023) << 52);
-  return static_cast<float>(p * scale);
+  float y = static_cast<float>(p * scale);
+  y = small ? 0.f : y;
+  y = big ? __builtin_inff() : y;
+  return nan ? xf : y;
+}
+#undef SG_EXPC
+
+// SiLU(g) * u in the CPU chain's operation order (q4_avx2.cpp:187-191).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g / (1.f + expf_sg(-g)) * u;
 }
 // silu_mul with expf_sg_kc
 __device__ __forceinline__ float silu_mul_kc(float g, float u) {
   return g / (1.f + expf_sg_kc(-g)) * u;
 }
+
 
 // fp16 bits <-> fp32; the conversion to fp16 rounds the fp32 value to
 // nearest even (__float2half of the reference's sth(), moe.cu:12-14).

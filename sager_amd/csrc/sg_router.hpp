@@ -151,7 +151,7 @@ __device__ __forceinline__ void router_wave(const float* __restrict__ lg, int n_
 #pragma unroll
   for (int j = 0; j < kPerLane; ++j) {
     const int i = lane + 64 * j;
-    if (i < n_expert) p[j] = expf_sg(p[j] - mx);
+    if (i < n_expert) p[j] = expf_sg_kc(p[j] - mx);
     if (i < e32) ev[i] = i < n_expert ? p[j] : 0.f;  // +0 padding leaves the sum unchanged
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
