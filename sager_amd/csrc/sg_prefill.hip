@@ -636,6 +636,11 @@ __global__ void __launch_bounds__(1024) scan_offsets_kernel(
   }
   // the bitmaps into LDS in one round of independent loads (the per-expert
   // loops below would otherwise wait for each global load in turn)
+  // the expert's matrix pointers for its tile records, loaded now so their
+  // latency overlaps the bitmaps' (they are written at the end)
+  const sg_block_q4k* t_mg = (trec && tid < E) ? tab_g[tid] : nullptr;
+  const sg_block_q4k* t_mu = (trec && tid < E) ? tab_u[tid] : nullptr;
+  const sg_block_q4k* t_md = (trec && tid < E) ? tab_d[tid] : nullptr;
   const int nbits = n_w * E;
   const bool in_lds = nbits <= kScanBitsLds;
   if (in_lds) {
@@ -711,11 +716,9 @@ __global__ void __launch_bounds__(1024) scan_offsets_kernel(
                           present ? reinterpret_cast<unsigned long long>(md) : 0ull, 0ull};
       };
       if (tid < E && tl > 0) {
-        const sg_block_q4k* mg = tab_g[tid];
-        const sg_block_q4k* mu = tab_u[tid];
-        const sg_block_q4k* md = tab_d[tid];
         for (int j = 0; j < tl; ++j)
-          put(pt + j, tid, ph + tok_per * j, min(ph + h, ph + tok_per * (j + 1)), mg, mu, md);
+          put(pt + j, tid, ph + tok_per * j, min(ph + h, ph + tok_per * (j + 1)), t_mg, t_mu,
+              t_md);
       }
       const int sh_t = (shared_tail + tok_per - 1) / tok_per;
       for (int j = tid; j < sh_t; j += nth)
