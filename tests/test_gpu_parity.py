@@ -366,6 +366,28 @@ def test_moe_layer_routed_edge_cases():
     assert_fp32_parity(host(out), ref)
 
 
+@pytest.mark.parametrize("T,K", [(2, 4), (8, 8)])
+def test_moe_layer_routed_duplicate_ids(T, K):
+    """Caller routing that repeats an id inside a row and across rows (the
+    plan's one-wave sort for up to 64 routes, and the general build past
+    it): each (token, slot) is its own entry of its expert's group."""
+    rng = np.random.default_rng(3100 + T)
+    H, F, E = 2048, 512, K  # (the layer takes at least k experts)
+    g, u, d = _expert_pool(rng, E + 1, H, F)
+    shared = (g.pop(), u.pop(), d.pop())
+    x = rng.normal(0, 1, (T, H)).astype(np.float32)
+    idx = np.full((T, K + 1), -1, np.int32)
+    idx[:, :K] = rng.integers(0, 3, (T, K))        # three experts: heavy repetition
+    idx[0, :K] = 1                                   # one row entirely on one expert
+    w = rng.uniform(0.05, 1.0, (T, K + 1)).astype(np.float32)
+    w[:, K] = 1.0
+    layer = _layer(g, u, d, shared, H, F, K, T)
+    out, _, wgt = layer.forward(dev(x), None, idx=dev(idx), weight=dev(w))
+    ref, _, rw = orc.moe_layer(g, u, d, shared, x, idx=idx, weight=w, hidden=H, n_ff=F, k=K)
+    np.testing.assert_array_equal(host(wgt), rw)
+    np.testing.assert_array_equal(host(out).view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("T", [2, 3, 4, 5])
 def test_moe_layer_routing_edge_cases(T):
     """Fused routing against the oracle where the logit order and the
