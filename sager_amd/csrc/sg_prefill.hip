@@ -531,7 +531,7 @@ grouped_mfma_kernel(GroupedArgs a) {
         const float gv = up_wave ? other : acc[ti][i], uv = up_wave ? acc[ti][i] : other;
         if (tt < nt)
           a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * (wave & 3) + lr] =
-              silu_mul(gv, uv);
+              silu_mul_kc(gv, uv);
       }
     }
   } else {
