@@ -171,7 +171,7 @@ def cpu_gemv_baseline(orc, mats, xq, budget_s=3.0):
                       f"nproc={os.cpu_count()}, cpu={cpu_model()}"}
 
 
-def run_config5(torch, np, ops, gen, orc, q4k_random_dev, reps=10):
+def run_config5(torch, np, ops, gen, orc, q4k_random_dev, reps=30):
     """Config 5: prefill chunk of 2048 tokens through the int8-MFMA path."""
     log("[bench] config-5 prefill chunk")
     T5 = 2048
@@ -192,7 +192,7 @@ def run_config5(torch, np, ops, gen, orc, q4k_random_dev, reps=10):
     # the median of 5 measurements of `reps` graph replays each, after a warm-up
     # measurement (a single measurement varied by up to 15 % between runs)
     fwd5 = lambda: pre.forward(x5, l5, out=o5, idx=i5, weight=w5)
-    time_graph(torch, fwd5, reps)
+    time_graph(torch, fwd5, 5 * reps)
     ms5_all = sorted(time_graph(torch, fwd5, reps)[0] for _ in range(5))
     ms5 = ms5_all[2]
     # parity: the first 64 tokens against the integer-first oracle (tokens are
