@@ -22,6 +22,7 @@
 // buffers (weights by global_load_lds, token rows gathered through
 // registers).
 #include "sg_common.hpp"
+#include "sg_router.hpp"
 
 namespace sg {
 
@@ -788,12 +789,11 @@ __global__ void __launch_bounds__(256) scan_place_kernel(const int* __restrict__
 // One block per 16-lane row (four per wave, 16 per workgroup): the lane's 16
 // values are four 16-B loads, and the block's max and bsums reduce inside a
 // DPP row.  Same arithmetic as quantize_block_wave.
-__global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __restrict__ in,
-                                                               unsigned char* __restrict__ out,
-                                                               long long n_blocks) {
-  const int lane = threadIdx.x & 63;
-  const long long blk =
-      (static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+// quantize_rows16 quantizes block `blk` in the lane's 16-lane row (blocks at
+// or past n_blocks store nothing).
+__device__ __forceinline__ void quantize_rows16(const float* __restrict__ in,
+                                                unsigned char* __restrict__ out,
+                                                long long n_blocks, long long blk, int lane) {
   const long long bc = blk < n_blocks ? blk : n_blocks - 1;  // rows past the end compute, never store
   const float* src = in + bc * kQK + 16 * (lane & 15);
   float v[16];
@@ -839,6 +839,34 @@ __global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __re
     ob[260 + (r >> 1)] = static_cast<unsigned char>(qsum & 127);
     ob[268 + (r >> 1)] = static_cast<unsigned char>((qsum >> 7) & 0xFF);
   }
+}
+__global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __restrict__ in,
+                                                               unsigned char* __restrict__ out,
+                                                               long long n_blocks) {
+  const int lane = threadIdx.x & 63;
+  quantize_rows16(in, out, n_blocks,
+                  (static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4),
+                  lane);
+}
+
+// The prefill's first launch: one-wave workgroups 0 .. n_rows - 1 route one
+// token each (router_wave, the standalone router's routine) and the
+// following ones quantize four blocks of x each, so the router's chains and
+// the quantization share one launch.
+template <int PL>
+__global__ void __launch_bounds__(64) route_quantize_kernel(
+    const float* __restrict__ logits, int* __restrict__ idx, float* __restrict__ weight,
+    int n_rows, int n_expert, int k, float shared_w, const float* __restrict__ x,
+    unsigned char* __restrict__ xq, long long n_blocks) {
+  __shared__ __attribute__((aligned(16))) float ev[64 * PL];
+  const int lane = threadIdx.x;
+  const long long w = blockIdx.x;
+  if (w < n_rows) {
+    router_wave<PL>(logits + w * n_expert, n_expert, k, shared_w, idx + w * (k + 1),
+                    weight + w * (k + 1), ev, lane);
+    return;
+  }
+  quantize_rows16(x, xq, n_blocks, (w - n_rows) * 4 + (lane >> 4), lane);
 }
 
 // out[t] = residual[t] + sum_kk fma(w[t][kk], y[pos(t, kk)]) in slot order;
@@ -1119,16 +1147,30 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   // the gate scales the shared expert only: without one it has nothing to scale
   float* sgate = has_shared && sh_gate_w ? reinterpret_cast<float*>(base + ws.sgate) : nullptr;
 
-  if (int st = quantize_split(x, xq, hidden / kQK, n_tokens, s, nm)) return st;
+  if (logits && n_expert <= 512) {  // routing and Q8_K of x in one launch
+    const long long nxb = static_cast<long long>(hidden / kQK) * n_tokens;
+    const unsigned grid = static_cast<unsigned>(n_tokens + (nxb + 3) / 4);
+    auto launch = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(64), 0, s, logits, idx, weight, n_tokens,
+                         n_expert, k, shared_w, x, reinterpret_cast<unsigned char*>(xq), nxb);
+    };
+    if (n_expert <= 64) launch(route_quantize_kernel<1>);
+    else if (n_expert <= 128) launch(route_quantize_kernel<2>);
+    else if (n_expert <= 256) launch(route_quantize_kernel<4>);
+    else launch(route_quantize_kernel<8>);
+    if (int st = check_launch("sg_moe_prefill/route_quantize")) return st;
+  } else {
+    if (int st = quantize_split(x, xq, hidden / kQK, n_tokens, s, nm)) return st;
+    if (logits)
+      if (int st = sg_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w,
+                                  stream))
+        return st;
+  }
   if (sgate) {
     hipLaunchKernelGGL(shared_gate_kernel, dim3((n_tokens + 7) / 8), dim3(256), 0, s, sh_gate_w, x,
                        sgate, n_tokens, hidden);
     if (int st = check_launch("sg_moe_prefill/shared_gate")) return st;
   }
-  if (logits)
-    if (int st = sg_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w,
-                                stream))
-      return st;
   if (int st = plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, trec, ws.max_tiles,
                            PlanTables{tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down},
                            base + ws.plan,
