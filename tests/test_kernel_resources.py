@@ -29,6 +29,7 @@ BUDGETS = [
     ("sg_gemv.hip", r"gemv_lat_plain_kernel", 0, None),
     ("sg_gemv.hip", r"gemv1_kernelINS_9PlainRowsENS_6F32OutELi4E", 0, None),
     ("sg_prefill.hip", r"grouped_mfma_kernelILb[01]ELb[01]E", 0, None),
+    ("sg_prefill.hip", r"route_quantize_kernel", 0, None),
     ("sg_q6.hip", r"gemv_q6_kernel", 0, None),
 ]
 
