@@ -554,6 +554,30 @@ def test_moe_prefill_small_pool(T, shared):
     assert_fp32_parity(host(out), ref)
 
 
+@pytest.mark.parametrize("E", [64, 100, 384, 600])
+def test_moe_prefill_router_widths(E):
+    """The prefill's routing at every router width: up to 512 experts it runs
+    in the launch that also quantizes x (64, 128, 256 and 512 experts per
+    wave), above that in its own launch.  Eight distinct matrices are cycled
+    over the pool to keep host memory small; the routing, plan and outputs are
+    bit-exact against the oracle."""
+    rng = np.random.default_rng(900 + E)
+    H, F, K, T = 2048, 512, 8, 40
+    g0, u0, d0 = _expert_pool(rng, 8, H, F)
+    g = [g0[e % 8] for e in range(E)]
+    u = [u0[(e // 8) % 8] for e in range(E)]
+    d = [d0[(e * 3) % 8] for e in range(E)]
+    x = rng.normal(0, 1, (T, H)).astype(np.float32)
+    lg = rng.normal(0, 1.5, (T, E)).astype(np.float32)
+    layer = _prefill(g, u, d, None, H, F, K, T)
+    out, idx, w = layer.forward(dev(x), dev(lg))
+    ref, ri, rw = orc.moe_layer(g, u, d, None, x, logits=lg, hidden=H, n_ff=F, k=K,
+                                prefill=True, n_threads=8)
+    np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K])
+    np.testing.assert_array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+    assert_fp32_parity(host(out), ref)
+
+
 def test_moe_prefill_routed_edge_cases():
     """Caller routing: an out-of-range id (bounds-kill), an absent expert,
     a token routed twice to one expert, no shared expert, residual = out."""
