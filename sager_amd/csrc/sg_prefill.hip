@@ -840,13 +840,19 @@ __device__ __forceinline__ void quantize_rows16(const float* __restrict__ in,
     ob[268 + (r >> 1)] = static_cast<unsigned char>((qsum >> 7) & 0xFF);
   }
 }
+// rows_used (optional, device): only the first *rows_used rows hold data
+// (the positions the plan filled); whole 16-lane rows past them exit before
+// any lane exchange.
 __global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __restrict__ in,
                                                                unsigned char* __restrict__ out,
-                                                               long long n_blocks) {
+                                                               long long n_blocks,
+                                                               const int* __restrict__ rows_used,
+                                                               int nb_row) {
   const int lane = threadIdx.x & 63;
-  quantize_rows16(in, out, n_blocks,
-                  (static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4),
-                  lane);
+  const long long blk =
+      (static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  if (rows_used && blk >= static_cast<long long>(*rows_used) * nb_row) return;
+  quantize_rows16(in, out, n_blocks, blk, lane);
 }
 
 // The prefill's first launch: one-wave workgroups 0 .. n_rows - 1 route one
@@ -989,11 +995,11 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
 
 // the grouped kernels' Q8_K input (split bsums)
 static int quantize_split(const float* in, sg_block_q8k* out, int nb_row, int n_rows,
-                          hipStream_t s, const char* nm) {
+                          hipStream_t s, const char* nm, const int* rows_used = nullptr) {
   const long long n_blocks = static_cast<long long>(nb_row) * n_rows;
   const unsigned grid = static_cast<unsigned>((n_blocks + 15) / 16);
   hipLaunchKernelGGL(prefill_quantize_kernel, dim3(grid), dim3(256), 0, s, in,
-                     reinterpret_cast<unsigned char*>(out), n_blocks);
+                     reinterpret_cast<unsigned char*>(out), n_blocks, rows_used, nb_row);
   return check_launch(nm);
 }
 
@@ -1196,7 +1202,8 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(tiles8 * ga.n_slices), dim3(kThreads),
                      kGroupedLds, s, ga);
   if (int st = check_launch("sg_moe_prefill/gate_up")) return st;
-  if (int st = quantize_split(h, hq, n_ff / kQK, ws.P, s, nm)) return st;
+  // h rows of the filled positions only: off[E + 1] = routes + shared rows
+  if (int st = quantize_split(h, hq, n_ff / kQK, ws.P, s, nm, off + n_expert + 1)) return st;
   GroupedArgs gd = ga;
   gd.xq = reinterpret_cast<const unsigned char*>(hq);
   gd.grows = nullptr;
