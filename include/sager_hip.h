@@ -347,7 +347,7 @@ int sg_moe_dispatch_plan(const int* idx, float* weight, int* gslot, int* grows, 
                          int shared_tail, void* stream);
 
 /* A whole MoE layer for a prefill chunk of n_tokens tokens (n_expert <=
- * 1024, k <= 32; no further limit on n_tokens), same arguments and semantics as sg_moe_layer: Q8_K(x),
+ * 1024, k <= 32, n_tokens * (k + 1) < 2^31), same arguments and semantics as sg_moe_layer: Q8_K(x),
  * router top-k (logits != NULL) or caller routing, the device plan, gate/up
  * + SiLU and down as grouped int8-MFMA contractions over every routed expert
  * (the shared expert as one more group), combine in slot order.  Replaces

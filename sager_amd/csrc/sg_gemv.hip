@@ -25,20 +25,6 @@
 
 namespace sg {
 
-// ---- latency timeline (built only with -DSG_TIMELINE; no code otherwise) ----
-#ifdef SG_TIMELINE
-constexpr int kGvMax = 4096;
-static __device__ unsigned long long gv_stamps[kGvMax * 16];
-__device__ __forceinline__ void gv_mark(int slot) {
-  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
-  const int i = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if ((threadIdx.x & 63) == 0 && i < kGvMax) gv_stamps[i * 16 + slot] = t;
-}
-#define SG_GV_MARK(slot) gv_mark(slot)
-#else
-#define SG_GV_MARK(slot) ((void)0)
-#endif
-
 constexpr int kMaxNb = 64;       // k <= 16384
 constexpr int kMaxTokens = 16;   // batched GEMV token tile
 constexpr int kWaves = 4;        // waves per workgroup
@@ -182,16 +168,13 @@ __global__ void __launch_bounds__(64 * NWV) gemv1_kernel(Rows rows,
   const int NW = gridDim.x * NWV;
   const int g_begin = blockIdx.x * NWV + wv, g_end = n_groups;
   auto rows_of = [&](int gg) { return min(rpw, n_rows - gg * rpw); };
-  SG_GV_MARK(0);
   // the first group's weights first: their HBM latency overlaps the staging
   if (g_begin < g_end) dma_rows(rows, g_begin * rpw, rows_of(g_begin), nb, wbuf[wv], lane);
-  SG_GV_MARK(1);
   stage_q8k(xq, nb, xs_dyn, threadIdx.x, blockDim.x);
   uint32_t* tab = xs_dyn + nb * kXStride;  // row table, when the rows have one
   rows.stage(tab, threadIdx.x, blockDim.x);
   float* res = reinterpret_cast<float*>(tab + rows.table_words()) + wv * gpw * rpw;
   bar();
-  SG_GV_MARK(2);
   rows.attach(tab);
 
   const int blk = lane & (lpr - 1);
@@ -204,7 +187,6 @@ __global__ void __launch_bounds__(64 * NWV) gemv1_kernel(Rows rows,
   for (int g = g_begin, li = 0; g < g_end; g += NW, ++li) {
     const int n = rows_of(g);
     wait_vm();  // group g has landed
-    if (li == 0) SG_GV_MARK(3);
     uint32_t w36[36];
     const bool live = active && rr < n;
     if (live) read_block_lds(wbuf[wv] + (rr * nb + blk) * 36, w36);
@@ -214,14 +196,12 @@ __global__ void __launch_bounds__(64 * NWV) gemv1_kernel(Rows rows,
     const float acc = row_sum_last(s, blk, nb);
     if (blk == nb - 1 && rr < n) res[li * rpw + rr] = acc;
   }
-  SG_GV_MARK(4);
   wait_lds();  // this wave's result writes (read back by its own lanes)
   // result li * rpw + row of the wave belongs to group g_begin + li * NW
   for (int i = lane; i < gpw * rpw; i += 64) {
     const int r = (g_begin + (i / rpw) * NW) * rpw + i % rpw;
     if (r < n_rows) out.store(r, res[i]);
   }
-  SG_GV_MARK(5);
 }
 
 // y[r] = W[r] . x for a small matrix (latency-bound: a few MB, read in one
@@ -236,10 +216,7 @@ __global__ void __launch_bounds__(64 * NWV) gemv1_kernel(Rows rows,
 // row shift, and the row's block sums are then added in block order by
 // row_sum_last after one lane permute.  nb <= 16 (k <= 4096).
 constexpr int kLatMaxNb = 16;
-#ifndef SG_LAT_WAVES
-#define SG_LAT_WAVES 4
-#endif
-constexpr int kLatWaves = SG_LAT_WAVES;  // waves per workgroup
+constexpr int kLatWaves = 4;  // waves per workgroup
 constexpr int kDppRowShr1 = 0x111;
 typedef uint32_t u32x4u __attribute__((ext_vector_type(4), aligned(4)));
 
@@ -253,7 +230,6 @@ __device__ __forceinline__ void gemv_lat_body(const Rows& rows, const unsigned c
   const int rpw = 16 >> lg;
   const int r = wave * rpw + rr;
   const bool live = blk < nb && r < n_rows;
-  SG_GV_MARK(0);
   // every lane loads (clamped to a valid block) and dead lanes zero their
   // words afterwards: no branch, so all arguments are fetched in one round
   const u32x4* wp = reinterpret_cast<const u32x4*>(rows.row(min(r, n_rows - 1)) +
@@ -279,7 +255,6 @@ __device__ __forceinline__ void gemv_lat_body(const Rows& rows, const unsigned c
     bs = 0;
     xd = 0.f;
   }
-  SG_GV_MARK(1);
   const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
   int32_t lo = 0, hi = 0;
 #pragma unroll
@@ -316,7 +291,6 @@ __device__ __forceinline__ void gemv_lat_body(const Rows& rows, const unsigned c
   const float row = row_sum_last(sb, cb, nb);
   const int ro = wave * rpw + (c >> lg);
   if (lane < 16 && cb == nb - 1 && ro < n_rows) out.store(ro, row);
-  SG_GV_MARK(2);
 }
 template <typename Rows, typename Out>
 __global__ void __launch_bounds__(64 * kLatWaves) gemv_lat_kernel(
@@ -448,11 +422,9 @@ static Gemv1Launch gemv1_launch(long long n_groups, int rpw) {
 // copies), it is faster up to 32768 x 2048 (2048 x 2048: 3.35 against
 // 4.84 us); from 65536 x 2048 on, the streaming kernel is (248320 x 2048:
 // 52 against 57 us).
-#ifndef SG_LAT_MAX_BLOCKS
-#define SG_LAT_MAX_BLOCKS 262144
-#endif
+constexpr long long kLatMaxBlocks = 262144;
 static bool use_lat(int n_rows, int nb) {
-  return nb <= kLatMaxNb && static_cast<long long>(n_rows) * nb <= SG_LAT_MAX_BLOCKS;
+  return nb <= kLatMaxNb && static_cast<long long>(n_rows) * nb <= kLatMaxBlocks;
 }
 template <typename Rows, typename Out>
 static void gemv_lat_go(hipStream_t s, Rows rows, const sg_block_q8k* x, Out out, int n_rows,
@@ -647,15 +619,5 @@ int sg_gemv_q4_k_q8_f16out_resadd(const sg_block_q4k* w, const sg_block_q8k* x, 
   return launch_gemv1(PlainRows{w, k / kQK}, x, F16ResAddOut{y, res_inout}, n_rows, k,
                       static_cast<hipStream_t>(stream), nm);
 }
-
-#ifdef SG_TIMELINE
-int sg_debug_gemv_timeline(unsigned long long* host) {
-  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(gv_stamps), sizeof(gv_stamps)) != hipSuccess)
-    return SG_ERR_HIP;
-  static unsigned long long zeros[kGvMax * 16];
-  return hipMemcpyToSymbol(HIP_SYMBOL(gv_stamps), zeros, sizeof(zeros)) == hipSuccess ? SG_OK
-                                                                                    : SG_ERR_HIP;
-}
-#endif
 
 }  // extern "C"

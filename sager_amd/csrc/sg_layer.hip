@@ -34,32 +34,6 @@
 
 namespace sg {
 
-// ---- latency timeline (built only with -DSG_TIMELINE; no code otherwise) ----
-// mark(kernel, slot) stores the 100 MHz real-time counter for the calling
-// wave into tl_stamps: front waves at ((wg * 4 + wave) * 16 + slot), back
-// waves from kTlBack on.  sg_debug_timeline() copies and clears it.
-#ifdef SG_TIMELINE
-constexpr int kTlBack = 1 << 15;
-static __device__ unsigned long long tl_stamps[2 * kTlBack];
-__device__ __forceinline__ void tl_mark(int base, int waves, int slot) {
-  const int wg = blockIdx.y * gridDim.x + blockIdx.x;
-  const int i = base + (wg * waves + (threadIdx.x >> 6)) * 16 + slot;
-  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
-  if ((threadIdx.x & 63) == 0 && i < base + kTlBack) tl_stamps[i] = t;
-  if (slot == 0 && (threadIdx.x & 63) == 0 && i + 15 < base + kTlBack) {
-    // slot 15: the XCC (bits 0-3 of HW_REG_XCC_ID) and the CU (HW_ID)
-    const unsigned xcc = __builtin_amdgcn_s_getreg((15 << 11) | 20);
-    const unsigned hwid = __builtin_amdgcn_s_getreg((31 << 11) | 4);
-    tl_stamps[i + 15] = (static_cast<unsigned long long>(hwid) << 32) | xcc | (1ull << 62);
-  }
-}
-#define SG_MARK_FRONT(slot) tl_mark(0, 4, slot)
-#define SG_MARK_BACK(slot) tl_mark(kTlBack, 8, slot)
-#else
-#define SG_MARK_FRONT(slot) ((void)0)
-#define SG_MARK_BACK(slot) ((void)0)
-#endif
-
 constexpr int kLMaxExperts = 1024;
 constexpr int kLMaxK = 32;
 constexpr int kLMaxTokens = 16;
@@ -720,7 +694,6 @@ __device__ __forceinline__ void spec_select(const LayerArgs& a, int T, uint32_t*
       kr[j] = in ? sel_key(lr[j], i) : 0;
       if (j < L.ept && i < L.e32) lv[i] = lr[j];
     }
-    SG_MARK_FRONT(1);
     team_select<EPT>(L, kr, cand, top, dyn + L.kw, tt, wait_copies && t0 == 0);
     if (ok && tt < m) spec[t * m + tt] = top[tt] ? sel_idx(top[tt]) : -1;
     if (t0 + L.nteams < T) bar();  // the next pass reuses cand/top
@@ -792,7 +765,7 @@ __device__ __forceinline__ void make_plan(uint32_t* dyn, const FrontLds& L, int 
 // (so z = sum e lies in [1, E], nothing degenerates), and along the logit
 // order each e_j = exp(l_j - max) either equals its successor's logit
 // (tie: index order on both sides) or exceeds the successor's e by more
-// than 2^-20 relative with the successor >= 2^-100 (the boundary pair k-1,
+// than 2^-19 relative with the successor >= 2^-100 (the boundary pair k-1,
 // k always strictly).  Then p_j = e_j / z > p_{j+1} for any z in [1, E]:
 // the quotients are normal and more than two floats apart, so route_wave's
 // check (p strictly decreasing or equal logits) passes.  A false result
@@ -927,7 +900,6 @@ __device__ __forceinline__ void route_direct_t1(const LayerArgs& a, uint32_t* dy
   for (int j = 0; j < EPT; ++j)
     if (j < L.ept && tid + L.TT * j < E) mx = fmaxf(mx, lr[j]);
   mx = team_max(mx, red, wave, L.tw, lane);
-  SG_MARK_FRONT(9);
   float e[EPT];
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
@@ -936,10 +908,8 @@ __device__ __forceinline__ void route_direct_t1(const LayerArgs& a, uint32_t* dy
     if (j < L.ept && i < L.e32) ev[i] = e[j];
   }
   bar();
-  SG_MARK_FRONT(10);
   if (tid == 0) zs[0] = serial_sum(ev, L.e32);
   bar();
-  SG_MARK_FRONT(11);
   const float z = zs[0];
   const bool degen = !(z == z) || z == 0.f;
   if (!degen) {
@@ -951,7 +921,6 @@ __device__ __forceinline__ void route_direct_t1(const LayerArgs& a, uint32_t* dy
     }
     team_select<EPT>(L, kr, cand, top, dyn + L.kw, tid);
   }
-  SG_MARK_FRONT(12);
   if (wave == 0) {
     int fi = 0;
     float pv = -1.f;
@@ -1045,17 +1014,14 @@ __device__ __forceinline__ void exact_route(const LayerArgs& a, uint32_t* dyn, c
     for (int j = 0; j < EPT; ++j)
       if (j < L.ept && tt + L.TT * j < E && ok) mx = fmaxf(mx, lr[j]);
     mx = team_max(mx, red, wit, tw, lane);
-    SG_MARK_FRONT(9);
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
       const int i = tt + L.TT * j;
       if (j < L.ept && i < L.e32) ev[i] = (ok && i < E) ? expf_sg(lr[j] - mx) : 0.f;
     }
     bar();
-    SG_MARK_FRONT(10);
     if (tt == 0) zs[team] = serial_sum(ev, L.e32);
     bar();
-    SG_MARK_FRONT(11);
     const float z = zs[team];
     const bool degen = !(z == z) || z == 0.f;
     bool fast = false;
@@ -1146,7 +1112,6 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   const int nbh = NBH ? NBH : a.hidden / kQK, lpr = NBH ? pow2_ceil(NBH) : pow2_ceil(nbh);
   const bool publisher = g == a.gmax;
   if (publisher && bx != 0) return;  // one publisher per launch
-  SG_MARK_FRONT(0);
   const bool shared_grp = a.has_shared && g == 0;
   const bool tabd_regs = publisher && E <= 256;
   // expert pointer tables into LDS (gate and up; down for the publisher),
@@ -1193,13 +1158,11 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
 
   if (shared_grp) {
     if (nrw > 0) dma_gateup(a.sh_gate, a.sh_up, row0, nrw, nbh, buf, lane);
-    SG_MARK_FRONT(3);
     quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);
     bar();
     // entries: tokens 0..T-1 in slot k, no plan needed
     gateup_wave(true, row0, nrw, nbh, lpr, buf, xs,
                 [&](int j, int& t, int& sl) { t = j; sl = k; }, T, stride, a.n_ff, a.h, lane);
-    SG_MARK_FRONT(6);
     if (a.sh_gate_w && bx == 0) shared_gate_tokens(a, tid);
     return;
   }
@@ -1260,27 +1223,19 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
       else
         router_wave<kPl1>(lg, E, k, a.shared_w, ridx + t * k, rw + t * stride, evw, lane);
     }
-    SG_MARK_FRONT(9);
     bar();
     if (wave > 0) quantize_x(a.x, nxb, a.xq, wave - 1, 3, lane, xw);
     build_plan(dyn, L, T, k, E, a.has_shared, tid);
-    SG_MARK_FRONT(10);
     n_groups = gbase + ctrl[1];
   } else if (a.logits && publisher && T == 1) {
     // the publisher routes exactly from the logits with every wave; it has
     // no stream to start and needs the weights, not the logit order
-#ifdef SG_TL_TWICE
     route_direct_t1<EPT>(a, dyn, L, lr, tid);  // and the plan
-    SG_MARK_FRONT(13);
-#endif
-    route_direct_t1<EPT>(a, dyn, L, lr, tid);  // and the plan
-    SG_MARK_FRONT(7);
     n_groups = gbase + ctrl[1];
   } else if (a.logits) {
     // waves 0-1 wait for the pointer tables inside the selection, so they
     // are readable when it returns
     spec_select<EPT>(a, T, dyn, L, lr, tid, wave < 2);
-    SG_MARK_FRONT(2);
     bool streamed = false, routed = false;
     if (T == 1) {
       // top[] of the single token is readable now: with k valid ids the
@@ -1312,7 +1267,6 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
           if (wave < 3) stream_rows(e_mine, 3, wave, 3);
           if (wave == 3 && e_mine >= 0) present_mine = tabg[e_mine] != 0ull && tabu[e_mine] != 0ull;
           streamed = true;
-          SG_MARK_FRONT(3);
         }
         // wave 3 routes exactly now (it reads top[] and lv[], complete since
         // the selection's last barrier) and writes ridx[] itself; the plan
@@ -1361,7 +1315,6 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
       // no weight stream to overlap: the whole workgroup routes exactly (one
       // exp per thread instead of four per lane of one wave)
       exact_route<EPT>(a, dyn, L, lr, tid);
-      SG_MARK_FRONT(7);
     } else if (t1w) {
       if (wave == 3) {
         if (!routed) route_wave<4 * EPT>(a, dyn, L, lane);
@@ -1369,15 +1322,12 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
         quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);  // overlaps the weight stream
         wait_vm();  // this wave's share of wave 3's rows
       }
-      SG_MARK_FRONT(4);
       bar();
-      SG_MARK_FRONT(5);
     } else {
       exact_route<EPT>(a, dyn, L, lr, tid);
     }
     const bool moved = ctrl[3] != 0;  // the exact routing changed an id
     if (moved) make_plan(dyn, L, T, k, E, a.has_shared, tid);
-    SG_MARK_FRONT(8);
     if (streamed && !moved) {
       // one token, routing as the logits ordered it: this group's expert,
       // presence and single entry (token 0, slot_mine) are known already
@@ -1388,7 +1338,6 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
       gateup_wave(present_mine, row0, nrw, nbh, lpr, buf, xs,
                   [&](int, int& t, int& sl) { t = 0; sl = slot_mine; }, 1, stride, a.n_ff, a.h,
                   lane);
-      SG_MARK_FRONT(6);
       return;
     }
     n_groups = gbase + ctrl[1];
@@ -1430,7 +1379,6 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
     }
     wait_vm();  // pointer tables
     bar();
-    SG_MARK_FRONT(5);
     // one array per wave, each lane's loads independent of the others' (a
     // single wave doing all of it waited on one LDS read after another)
     const int* re = reinterpret_cast<const int*>(dyn + L.re);
@@ -1470,7 +1418,6 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
       a.plan.meta[1] = a.has_shared;
       a.plan.meta[2] = nv;
     }
-    SG_MARK_FRONT(6);
     return;
   }
   if (g >= n_groups) {
@@ -1557,7 +1504,6 @@ layer_gateup_kernel(LayerArgs args) {
   const bool full = a.n_ff % (4 * rpw) == 0;
   const int nrw = full ? rpw : max(0, min(rpw, a.n_ff - row0));
   const int xw = nbh * kXStride;
-  SG_MARK_FRONT(11);
   // every plan word this workgroup needs in one round (g < gmax: inside
   // the plan arrays even past the live groups); the entry list too when it
   // fits one wave (lane = entry, the same in every wave), so no load waits
@@ -1573,7 +1519,6 @@ layer_gateup_kernel(LayerArgs args) {
   // entries of the group (clamped to the plan's capacity), at etok/eslot[j0 ..]
   const int j0 = min(max(off0, 0), a.emax);
   const int n = min(max(off1, j0), a.emax) - j0;
-  SG_MARK_FRONT(12);
   if (present && nrw > 0)
     dma_gateup(reinterpret_cast<const sg_block_q4k*>(wg), reinterpret_cast<const sg_block_q4k*>(wu),
                row0, nrw, nbh, wbuf[wave], lane);
@@ -1586,7 +1531,6 @@ layer_gateup_kernel(LayerArgs args) {
     dma_chunks([&](int c) { return reinterpret_cast<const char*>(src) + 16 * c; }, xw / 4, x0,
                lane, wave, 4);
   }
-  SG_MARK_FRONT(13);
   int* etok = reinterpret_cast<int*>(dyn + ((xw + 3) & ~3));
   int* eslot = etok + a.emax;
   if (ent1) {
@@ -1602,11 +1546,9 @@ layer_gateup_kernel(LayerArgs args) {
   }
   wait_vm();  // this wave's weights and its share of x0
   bar();
-  SG_MARK_FRONT(14);
   gateup_group(present, row0, nrw, nbh, lpr, wbuf[wave], &wbuf[0][0], x0, a.xq,
                [&](int j, int& t, int& sl) { t = etok[j0 + j]; sl = eslot[j0 + j]; }, n, stride,
                a.n_ff, a.h, lane, wave);
-  SG_MARK_FRONT(8);
   if (g == 0 && a.has_shared && a.sh_gate_w && bx == 0) shared_gate_tokens(a, tid);
 }
 
@@ -1770,15 +1712,12 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
               (lds_void_p)(buf + 256 * i), 16, 0, 0);
       }
     }
-    SG_MARK_BACK(2);
     if (gb == 0 && !pre) {  // Q8_K of every (token, slot) h row while the rows stream in
       back_quantize_h<HS>(a, hq, hpre, nq, wave, lane);
-      SG_MARK_BACK(3);
       if (spread) wait_vm();  // this wave's share of the copies
       bar();
     }
     wait_vm();
-    SG_MARK_BACK(4);
     const int gq = gb + wave * gpw + q;
     const bool has = gq < G && wave < nbw;
     const bool present = has && wdown[gq] != 0ull;
@@ -1811,7 +1750,6 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
     }
     wait_lds();
   }
-  SG_MARK_BACK(5);
   bar();
   // out = residual + sum over slots 0..k of fma(w, y) in slot order.  A slot
   // whose id was invalid (bounds-killed), whose expert is absent, or the
@@ -1840,7 +1778,6 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
     }
     a.out[o] = acc;
   }
-  SG_MARK_BACK(6);
 }
 
 // residual of the first combine pass (qo = tid), loaded early
@@ -1878,7 +1815,6 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args
   float* ys = reinterpret_cast<float*>(dyn + L.ys);
   const int row0 = blockIdx.x * rows;
   const int nr = max(0, min(rows, a.hidden - row0));
-  SG_MARK_BACK(0);
 
   // loads that do not depend on the plan: this wave's first HS h
   // blocks (block wave + 8j of the (token, slot) rows) and the residual
@@ -2003,7 +1939,6 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args
     wait_vm();  // this wave's copies, visible to all after the barrier
   }
   bar();
-  SG_MARK_BACK(1);
   back_core<NBF, ROWS, HS>(a, L, dyn, wbuf, row0, nr, res0, hpre, pre);
 }
 
@@ -2248,16 +2183,5 @@ int sg_moe_layer_noalloc(const sg_block_q4k* const* tab_gate, const sg_block_q4k
                              logits, residual, out, idx, weight, ws, kScratchBytes, n_tokens,
                              hidden, n_ff, n_expert, k, shared_w, 3, stream);
 }
-
-#ifdef SG_TIMELINE
-// copy the timeline stamps (2 * 32768 words) to host memory and clear them
-int sg_debug_timeline(unsigned long long* host) {
-  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(tl_stamps), sizeof(tl_stamps)) != hipSuccess)
-    return SG_ERR_HIP;
-  static unsigned long long zeros[2 * kTlBack];
-  return hipMemcpyToSymbol(HIP_SYMBOL(tl_stamps), zeros, sizeof(zeros)) == hipSuccess ? SG_OK
-                                                                                      : SG_ERR_HIP;
-}
-#endif
 
 }  // extern "C"

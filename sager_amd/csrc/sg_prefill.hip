@@ -228,23 +228,6 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(
   for (int t = tid; t < shared_tail; t += nth) grows[s_total + t] = t;
 }
 
-// ---- latency timeline (built only with -DSG_TIMELINE; no code otherwise) ----
-// Wave 0 of each grouped workgroup stores the 100 MHz real-time counter at
-// its marks: slot 0 start, 1 first copies issued, 2 + b after block b's
-// data landed (b < 8), 10 + b after block b's compute, 14 end ... folded
-// into 16 words per workgroup at pf_stamps[L * 16 + slot].
-#ifdef SG_TIMELINE
-constexpr int kPfMax = 1 << 16;
-static __device__ unsigned long long pf_stamps[kPfMax * 16];
-__device__ __forceinline__ void pf_mark(int base, int slot) {
-  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
-  if (threadIdx.x == 0 && blockIdx.x < kPfMax / 2) pf_stamps[(base + blockIdx.x) * 16 + slot] = t;
-}
-#define SG_PF_MARK(slot) pf_mark(kGateUp ? 0 : kPfMax / 2, slot)
-#else
-#define SG_PF_MARK(slot) ((void)0)
-#endif
-
 // ---- grouped int8-MFMA contraction ------------------------------------------------
 // Positions of one group per tile, in blocks of 16: 96 holds every expert's
 // routes at the config-5 shape (64 +- 8 per expert) in one tile, so each
@@ -263,10 +246,7 @@ constexpr int kXRow = 76;
 // run past the tile's rows, into this padding
 constexpr int kXBufWords = (kTokTile * kXRow + 255) / 256 * 256;  // 29 KB
 constexpr int kThreads = 512;                 // eight waves
-#ifndef SG_DOWN_SPW
-#define SG_DOWN_SPW 8
-#endif
-constexpr int kDownSlicesPerWg = SG_DOWN_SPW;  // down pass, nb <= 2
+constexpr int kDownSlicesPerWg = 8;  // down pass, nb <= 2
 // LDS: one weight buffer (each wave refills its own rows once it has read
 // them), two token buffers, then the tile's token rows: 77 KB
 constexpr size_t kGroupedLds = (kWBufWords + 2 * kXBufWords + kTokTile) * 4;
@@ -304,7 +284,6 @@ grouped_mfma_kernel(GroupedArgs a) {
   int* trow = reinterpret_cast<int*>(gl_lds + kWBufWords + 2 * kXBufWords);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   static_assert(kThreads == 512, "eight waves, one 16-row block each");
-  SG_PF_MARK(0);
   // the workgroup's slices: sgrp * spw .. sgrp * spw + spw - 1, in turn
   const int spw = kMulti ? a.spw : 1, S = a.n_slices / spw;
   const int L = blockIdx.x, xcd = L & 7, jx = L >> 3;
@@ -403,7 +382,6 @@ grouped_mfma_kernel(GroupedArgs a) {
 
   stage_x(0, 0);
   if (kMulti && nb > 1) stage_x(1, 1);  // the whole tile's rows, kept for every slice
-  SG_PF_MARK(1);
 #pragma unroll 1
   for (int q = 0; q < spw; ++q, c0 += kCols) {
 #pragma unroll
@@ -412,11 +390,8 @@ grouped_mfma_kernel(GroupedArgs a) {
     for (int i = 0; i < 4; ++i) acc[ti][i] = 0.f;
   for (int b = 0; b < nb; ++b) {
     const int s = b & 1;
-    if (b == 2) SG_PF_MARK(14);
-    if (b == 5) SG_PF_MARK(15);
     wait_vm();  // this wave's copies of block b have landed
     bar();      // ... and every wave's
-    if (b < 8) SG_PF_MARK(2 + b);
     // the lane's weight words of block b into registers: the header and,
     // per K group, 16 qs bytes; then the wave refills its rows with block
     // b + 1 while it computes (the rows are the wave's own: no barrier)
@@ -504,7 +479,6 @@ grouped_mfma_kernel(GroupedArgs a) {
       }
     }
   }
-  SG_PF_MARK(10);
   // outputs of the lane's tokens
   if (kGateUp) {  // h = silu(gate) * up; wave w (gate) and w + 4 (up) hold the same h
     // positions and each takes half of them: the first half of the token
@@ -552,15 +526,6 @@ grouped_mfma_kernel(GroupedArgs a) {
     }
   }
   }  // slices
-  SG_PF_MARK(11);
-  if (threadIdx.x == 0) {  // the tile's size, for the timeline reader
-    SG_PF_MARK(12);
-#ifdef SG_TIMELINE
-    if (blockIdx.x < kPfMax / 2)
-      pf_stamps[((kGateUp ? 0 : kPfMax / 2) + blockIdx.x) * 16 + 13] =
-          (static_cast<unsigned long long>(nt) << 32) | g;
-#endif
-  }
 }
 
 // Q8_K blocks for the grouped kernels: the standard block except that the
@@ -885,8 +850,11 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(
     float* __restrict__ out, const float* __restrict__ residual, const float* __restrict__ y,
     const float* __restrict__ weight, const int* __restrict__ gslot, const int* __restrict__ off,
     const float* __restrict__ sgate, int n_expert, int k, int hidden, int has_shared) {
-  const int t = blockIdx.y;
-  const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
+  // 1-D grid, token-major: ceil(hidden / 1024) workgroups per token, so the
+  // token count has no grid-dimension limit
+  const int nbx = (hidden + 1023) / 1024;
+  const int t = blockIdx.x / nbx;
+  const int i = ((blockIdx.x - t * nbx) * 256 + threadIdx.x) * 4;
   if (i >= hidden) return;
   const long long o = static_cast<long long>(t) * hidden + i;
   float4 acc = residual ? *reinterpret_cast<const float4*>(residual + o) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1224,20 +1192,9 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
     hipLaunchKernelGGL((grouped_mfma_kernel<false, false>), dim3(tiles8 * gd.n_slices),
                        dim3(kThreads), kGroupedLds, s, gd);
   if (int st = check_launch("sg_moe_prefill/down")) return st;
-  hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 1023) / 1024, n_tokens), dim3(256), 0, s,
+  hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 1023) / 1024 * n_tokens), dim3(256), 0, s,
                      out, residual, y, weight, gslot, off, sgate, n_expert, k, hidden, has_shared);
   return check_launch("sg_moe_prefill/combine");
 }
-
-#ifdef SG_TIMELINE
-int sg_debug_prefill_timeline(unsigned long long* host, int n_wg) {
-  if (n_wg > kPfMax) n_wg = kPfMax;
-  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(pf_stamps), size_t(n_wg) * 16 * 8) != hipSuccess)
-    return SG_ERR_HIP;
-  static unsigned long long zeros[kPfMax * 16];
-  return hipMemcpyToSymbol(HIP_SYMBOL(pf_stamps), zeros, sizeof(zeros)) == hipSuccess ? SG_OK
-                                                                                    : SG_ERR_HIP;
-}
-#endif
 
 }  // extern "C"

@@ -49,6 +49,15 @@ def _ptr(t):
     return t.data_ptr()
 
 
+def _dtypes(name, **args):
+    """Raise unless every (tensor, dtype) pair matches and the tensor is a
+    contiguous GPU tensor: the launchers read raw bits."""
+    for arg, (t, dt) in args.items():
+        if t.dtype != dt:
+            raise SagerError(f"{name}: {arg} must be {dt}, got {t.dtype}")
+        _ptr(t)
+
+
 def _check(status):
     if status != 0:
         raise SagerError(f"status {status}: {load().sg_last_error().decode()}")
@@ -236,7 +245,11 @@ def moe_combine_batched_f16(out, expert_y, weight):
     """cuda::moe_combine_batched_f16 (cuda_ops.hpp:379-381): out fp16
     [n_rows, hidden] holds the residual and receives the sum in place;
     expert_y fp16 [n_rows, n_used+1, hidden], weight fp32 [n_rows, n_used+1]."""
+    _dtypes("moe_combine_batched_f16", out=(out, torch.float16),
+            expert_y=(expert_y, torch.float16), weight=(weight, torch.float32))
     n_rows, slots, hidden = expert_y.shape
+    if out.shape != (n_rows, hidden) or weight.shape != (n_rows, slots):
+        raise SagerError("moe_combine_batched_f16: out [n_rows, hidden], weight [n_rows, slots]")
     _check(load().sg_moe_combine_batched_f16(_ptr(out), _ptr(expert_y), _ptr(weight), slots - 1,
                                              hidden, n_rows, _stream()))
     return out
@@ -245,6 +258,7 @@ def moe_combine_batched_f16(out, expert_y, weight):
 def sigmoid_gate_scalar_batched_f16(out, g):
     """cuda::sigmoid_gate_scalar_batched_f16 (cuda_ops.hpp:384-386):
     out fp16 [n_rows, hidden] *= sigmoid(g[row]) in place."""
+    _dtypes("sigmoid_gate_scalar_batched_f16", out=(out, torch.float16), g=(g, torch.float32))
     out2 = out.reshape(g.numel(), -1)
     _check(load().sg_sigmoid_gate_scalar_batched_f16(_ptr(out2), _ptr(g), out2.shape[0],
                                                      out2.shape[1], _stream()))
@@ -253,6 +267,7 @@ def sigmoid_gate_scalar_batched_f16(out, g):
 
 def sigmoid_gate_scalar_f16(out, g):
     """cuda::sigmoid_gate_scalar_f16 (cuda_ops.hpp:315-316): out fp16 [n] *= sigmoid(g[0])."""
+    _dtypes("sigmoid_gate_scalar_f16", out=(out, torch.float16), g=(g, torch.float32))
     _check(load().sg_sigmoid_gate_scalar_f16(_ptr(out), _ptr(g), out.numel(), _stream()))
     return out
 

@@ -1,0 +1,136 @@
+"""GPU parity of the fused decode layer at the model shape (hidden 2048,
+n_ff 512, 256 experts, top-8): the compile-time instances the launchers pick
+for that shape (one token, and the 4-token verify window, with and without a
+shared expert) against the pinned CPU oracle.
+
+The routing rows here are the hard ones for the one-token selection (ties
+inside and across the top-k boundary, signed zeros, -inf, NaN, logits one
+ulp apart, a gap at the logit-order shortcut's margin) and the qwen3.5
+shared-expert gate; both run through the same kernels the benchmark
+configurations dispatch.  Bar: indices, weights and outputs bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from sager_amd import ops
+from sager_amd.synth import q4k_random_dev
+
+pytestmark = pytest.mark.gpu
+H, F, E, K = 2048, 512, 256, 8
+BLOCKS = F * H // 256
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def assert_bits(got, ref):
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def pool():
+    """257 experts (the last one is the shared expert) on the device, the
+    pointer tables, and a host copy for the oracle."""
+    gen = torch.Generator(device="cuda").manual_seed(257)
+    p = q4k_random_dev(3 * (E + 1) * BLOCKS, gen).view(3, E + 1, BLOCKS, 144)
+    tabs = [torch.tensor([p[m, e].data_ptr() for e in range(E)], dtype=torch.int64,
+                         device="cuda") for m in range(3)]
+    hp = host(p)
+    return dict(dev=p, tabs=tabs, g=[hp[0, e] for e in range(E)], u=[hp[1, e] for e in range(E)],
+                d=[hp[2, e] for e in range(E)], sh=(hp[0, E], hp[1, E], hp[2, E]))
+
+
+def _layer(pool, T, shared, gate_w=None):
+    p = pool["dev"]
+    sh = (p[0, E], p[1, E], p[2, E]) if shared else None
+    return ops.MoeLayer(*pool["tabs"], sh, hidden=H, n_ff=F, n_expert=E, k=K, max_tokens=T,
+                        shared_gate_w=dev(gate_w) if gate_w is not None else None)
+
+
+def _edge_rows():
+    rng = np.random.default_rng(4711)
+    rows = []
+    base = rng.normal(0, 1, E).astype(np.float32)
+    o = np.argsort(-base, kind="stable")
+    r = base.copy(); r[o[3]] = r[o[2]]; rows.append(r)              # interior tie
+    r = base.copy(); r[o[K]] = r[o[K - 1]]; rows.append(r)          # tie across the boundary
+    r = base.copy(); r[[o[0], o[5]]] = r[o[1]]; rows.append(r)      # 3-way tie at the top
+    r = np.zeros(E, np.float32) - 3.0
+    r[[2, 5, 11, 200]] = [0.0, -0.0, 0.0, -0.0]; r[[1, 255]] = [-0.0, 0.0]   # signed zeros
+    rows.append(r)
+    r = np.full(E, 0.125, np.float32); rows.append(r)                # all equal
+    r = base.copy(); r[[0, 6, 255]] = -np.inf; rows.append(r)       # -inf: not all finite
+    r = base.copy(); r[9] = np.nan; rows.append(r)                  # degenerate
+    r = base.copy(); r[o[1]] = np.nextafter(r[o[0]], np.float32(-9.0)); rows.append(r)  # 1 ulp
+    r = base.copy(); r[o[K]] = r[o[K - 1]] - np.float32(2e-6); rows.append(r)   # at the margin
+    r = base.copy(); r[o[K]] = r[o[K - 1]] * np.float32(1 - 2**-20); rows.append(r)
+    r = (base * 40.0).astype(np.float32); rows.append(r)           # tiny tail probabilities
+    return rows
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_t1_routing_edge_rows_model_shape(pool, shared):
+    """One token through layer_front_kernel<1, 8, true, 1, shared>: every
+    edge row, indices, weights and output bits against the oracle."""
+    layer = _layer(pool, 1, shared)
+    rng = np.random.default_rng(62)
+    x = rng.normal(0, 1, (1, H)).astype(np.float32)
+    sh = pool["sh"] if shared else None
+    for n, lg in enumerate(_edge_rows()):
+        out, idx, w = layer.forward(dev(x), dev(lg[None]))
+        ref, ri, rw = orc.moe_layer(pool["g"], pool["u"], pool["d"], sh, x, logits=lg[None],
+                                    hidden=H, n_ff=F, k=K)
+        np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K], err_msg=f"row {n}")
+        assert_bits(host(w), rw)
+        assert_bits(host(out), ref)
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_window_routing_edge_rows_model_shape(pool, shared):
+    """The 4-token verify window (routing launch, gate/up launch, back
+    kernel at T = 4) with edge rows packed four to a window."""
+    layer = _layer(pool, 4, shared)
+    rng = np.random.default_rng(63)
+    rows = _edge_rows()
+    rows += [rng.normal(0, 1.5, E).astype(np.float32)] * (-len(rows) % 4)
+    sh = pool["sh"] if shared else None
+    for w0 in range(0, len(rows), 4):
+        lg = np.stack(rows[w0:w0 + 4])
+        x = rng.normal(0, 1, (4, H)).astype(np.float32)
+        res = rng.normal(0, 1, (4, H)).astype(np.float32)
+        out, idx, w = layer.forward(dev(x), dev(lg), residual=dev(res))
+        ref, ri, rw = orc.moe_layer(pool["g"], pool["u"], pool["d"], sh, x, logits=lg,
+                                    residual=res, hidden=H, n_ff=F, k=K, n_threads=4)
+        np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K], err_msg=f"window {w0 // 4}")
+        assert_bits(host(w), rw)
+        assert_bits(host(out), ref)
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_shared_gate_model_shape(pool, T):
+    """The qwen3.5 shared-expert gate sigmoid(shared_gate_w . x) through the
+    model-shape instances (T = 1 and the 4-token window)."""
+    rng = np.random.default_rng(70 + T)
+    gw = rng.normal(0, 0.03, H).astype(np.float32)
+    layer = _layer(pool, T, True, gate_w=gw)
+    for step in range(2):
+        x = rng.normal(0, 1, (T, H)).astype(np.float32)
+        lg = rng.normal(0, 1.5, (T, E)).astype(np.float32)
+        res = rng.normal(0, 1, (T, H)).astype(np.float32)
+        out, idx, w = layer.forward(dev(x), dev(lg), residual=dev(res))
+        ref, ri, rw = orc.moe_layer(pool["g"], pool["u"], pool["d"], pool["sh"], x, logits=lg,
+                                    residual=res, hidden=H, n_ff=F, k=K, shared_gate_w=gw,
+                                    n_threads=4)
+        np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K])
+        assert_bits(host(w), rw)
+        assert_bits(host(out), ref)
+        ref0, _, _ = orc.moe_layer(pool["g"], pool["u"], pool["d"], pool["sh"], x, logits=lg,
+                                   residual=res, hidden=H, n_ff=F, k=K, n_threads=4)
+        assert not np.array_equal(ref0, ref)  # the gate changed the result
