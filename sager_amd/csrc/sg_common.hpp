@@ -289,6 +289,95 @@ __device__ __forceinline__ float expf_sg_kc(float xf) {
 }
 #undef SG_EXPC
 
+// ---- exp from a 64-entry table: expf_sg's results, in fewer operations ----
+// 2^(j/64), j = 0..63: each the double nearest the exact value (evaluated
+// to 60 decimal digits).  Kernels that use expf_tab copy it into LDS.
+static __constant__ double kExp2Tab64[64] = {
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0,
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0,
+    0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0};
+
+// e^x for x in [-87, 88] (normal float results): x = (64 k + j) ln2/64 + r
+// with |r| <= ln2/128 (k j from rint(x * 64/ln2); ln2/64 split into a
+// 39-bit head, so k * head is exact, and a tail), e^x = 2^k * T[j] * e^r
+// with e^r to degree 5 (remainder below 2^-54 relative).  The double result
+// is within 2^-49 (relative) of e^x.  A lane whose result lies within 2^14
+// double ulps (at least 2^-39 relative) of a float rounding midpoint, or
+// whose x is outside the range or NaN, takes expf_sg_kc instead.  For every
+// other lane the exact e^x is at least 2^-40 from the midpoint, so rounding
+// this result gives the correctly rounded float - which expf_sg also returns
+// there, its own error being below 2^-50: the two agree bit for bit.
+// tab: kExp2Tab64 in LDS.
+// The fast evaluation alone; *ok tells whether its rounding is certain.
+__device__ __forceinline__ float expf_tab_fast(float xf, const double* tab, bool* ok) {
+  const bool in = xf >= -87.f && xf <= 88.f;
+  const double x = in ? static_cast<double>(xf) : 0.0;
+  const double kd = __builtin_rint(x * SG_SCONST(0x1.71547652b82fep+6));  // 64 / ln2
+  double r = __builtin_fma(-kd, SG_SCONST(0x1.62e42fefa4000p-7), x);     // ln2/64, head
+  r = __builtin_fma(-kd, SG_SCONST(-0x1.8432a1b0e2634p-49), r);           // ln2/64, tail
+  double p = __builtin_fma(SG_SCONST(1.0 / 120.0), r, SG_SCONST(1.0 / 24.0));
+  p = __builtin_fma(p, r, SG_SCONST(1.0 / 6.0));
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const int ki = static_cast<int>(kd);
+  const double scale =
+      __builtin_bit_cast(double, static_cast<unsigned long long>((ki >> 6) + 1023) << 52);
+  const double y = tab[ki & 63] * p * scale;
+  // the 29 double fraction bits that rounding to float drops: the midpoint
+  // between two floats is 0x10000000
+  const uint32_t lo = static_cast<uint32_t>(__builtin_bit_cast(unsigned long long, y)) & 0x1FFFFFFFu;
+  *ok = in && (lo - (0x10000000u - 0x4000u)) > 0x8000u;
+  return static_cast<float>(y);
+}
+
+__device__ __forceinline__ float expf_tab(float xf, const double* tab) {
+  bool ok;
+  float res = expf_tab_fast(xf, tab, &ok);
+  if (!ok) res = expf_sg_kc(xf);
+  return res;
+}
+
+// N SiLU products at once: the fast exps are independent chains that the
+// compiler interleaves, and the exact fallback runs only if some lane needs
+// it for some element.
+template <int N>
+__device__ __forceinline__ void silu_mul_tab_n(const float (&g)[N], const float (&u)[N],
+                                               float (&h)[N], const double* tab) {
+  float e[N];
+  bool ok[N], all = true;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    e[i] = expf_tab_fast(-g[i], tab, &ok[i]);
+    all = all && ok[i];
+  }
+  if (!all) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (!ok[i]) e[i] = expf_sg_kc(-g[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) h[i] = g[i] / (1.f + e[i]) * u[i];
+}
+
+// silu_mul with expf_tab (tab: kExp2Tab64 in LDS): the same bits
+__device__ __forceinline__ float silu_mul_tab(float g, float u, const double* tab) {
+  return g / (1.f + expf_tab(-g, tab)) * u;
+}
+
 // SiLU(g) * u in the CPU chain's operation order (q4_avx2.cpp:187-191).
 __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.f + expf_sg(-g)) * u;

@@ -32,11 +32,26 @@ __global__ void __launch_bounds__(64) router_kernel(const float* __restrict__ lo
                   weight + row * stride, ev, threadIdx.x);
 }
 
+// four SiLU products per thread through the table exp (silu_mul_tab_n),
+// the prefill gate/up kernel's arithmetic
 __global__ void __launch_bounds__(256) silu_kernel(float* __restrict__ out,
                                                    const float* __restrict__ g,
                                                    const float* __restrict__ u, long long n) {
-  const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
-  if (i < n) out[i] = silu_mul(g[i], u[i]);
+  __shared__ double tab[64];
+  if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Tab64[threadIdx.x];
+  __syncthreads();
+  const long long i0 = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  float gv[4], uv[4], hv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const long long i = i0 + j < n ? i0 + j : n - 1;
+    gv[j] = g[i];
+    uv[j] = u[i];
+  }
+  silu_mul_tab_n<4>(gv, uv, hv, tab);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (i0 + j < n) out[i0 + j] = hv[j];
 }
 
 __global__ void __launch_bounds__(256) combine_kernel(float* out, const float* residual,
@@ -142,7 +157,7 @@ int sg_router_topk(const float* logits, int* idx, float* weight, int n_expert, i
 int sg_silu_mul(float* out, const float* g, const float* u, int n, void* stream) {
   if (!out || !g || !u) return set_error(SG_ERR_INVALID_ARGUMENT, "sg_silu_mul: null pointer");
   if (n <= 0) return set_error(SG_ERR_GEOMETRY, "sg_silu_mul: n=%d", n);
-  hipLaunchKernelGGL(silu_kernel, dim3((n + 255) / 256), dim3(256), 0,
+  hipLaunchKernelGGL(silu_kernel, dim3((n + 1023) / 1024), dim3(256), 0,
                      static_cast<hipStream_t>(stream), out, g, u, static_cast<long long>(n));
   return check_launch("sg_silu_mul");
 }

@@ -238,9 +238,16 @@ constexpr int kTokBlocks = kTokTile / 16;
 constexpr int kRowsWg = 128;                 // weight rows per workgroup
 constexpr int kWRowWords = 36;               // one 144-B block
 constexpr int kWBufWords = kRowsWg * kWRowWords;   // 18 KB
-// staged Q8_K block: qs, bsums, d, pad.  76 words = 19 16-B chunks: the
-// stride is 12 banks mod 32, so eight lanes reading 16 B of eight
-// consecutive rows (one ds_read_b128 pass) touch every bank once.
+// prefill Q8 block ("Q8P", written by the prefill's own quantizers): a
+// 16-B header (fp32 d, 12 B zero), the 256 qs bytes, then each sub-block sum
+// s as two fp16 integers a = s >> 1 and b = s & 1 (eight a's, then eight
+// b's): the operands of the exact fp16 MFMA for the mins term.  19 16-B
+// chunks.
+constexpr int kQ8PBytes = 304;
+// staged Q8P block: qs (words 0-63), the a's (64-67), the b's (68-71), the
+// header (d in word 72).  76 words = 19 16-B chunks: the stride is 12 banks
+// mod 32, so eight lanes reading 16 B of eight consecutive rows (one
+// ds_read_b128 pass) touch every bank once.
 constexpr int kXRow = 76;
 // a whole number of 64-lane copy instructions (1 KB each): the last one may
 // run past the tile's rows, into this padding
@@ -248,13 +255,17 @@ constexpr int kXBufWords = (kTokTile * kXRow + 255) / 256 * 256;  // 29 KB
 constexpr int kThreads = 512;                 // eight waves
 constexpr int kDownSlicesPerWg = 8;  // down pass, nb <= 2
 // LDS: one weight buffer (each wave refills its own rows once it has read
-// them), two token buffers, then the tile's token rows: 77 KB
-constexpr size_t kGroupedLds = (kWBufWords + 2 * kXBufWords + kTokTile) * 4;
+// them), two token buffers, the tile's token rows and the SiLU's exp table
+// (64 doubles): 78 KB
+constexpr size_t kGroupedLds = (kWBufWords + 2 * kXBufWords + kTokTile + 128) * 4;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 struct GroupedArgs {
-  const unsigned char* xq;  // Q8_K rows: x [T][nb] (gate/up) or h [P][nb] (down)
+  const unsigned char* xq;  // Q8P rows: x [T][nb] (gate/up) or h [P][nb] (down)
   const int* off;           // [G+1] position range of each group
   const int* grows;         // [P] token of each position (gate/up only)
   const TileRec* trec;      // work list: one record per tile, group -1 past it
@@ -282,6 +293,7 @@ grouped_mfma_kernel(GroupedArgs a) {
   uint32_t* wbuf0 = gl_lds;
   uint32_t* xbuf0 = gl_lds + kWBufWords;
   int* trow = reinterpret_cast<int*>(gl_lds + kWBufWords + 2 * kXBufWords);
+  double* etab = reinterpret_cast<double*>(trow + kTokTile);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   static_assert(kThreads == 512, "eight waves, one 16-row block each");
   // the workgroup's slices: sgrp * spw .. sgrp * spw + spw - 1, in turn
@@ -336,12 +348,11 @@ grouped_mfma_kernel(GroupedArgs a) {
   };
   stage_w(0);  // the first weight block needs only the record: issued before the token rows
   // the tile's token rows of super-block b into token buffer s, 76 words per
-  // token in 16-B chunks: chunks 0-15 the 64 qs words, 16 the split bsums
-  // (eight lo bytes, eight hi bytes), 17 d and three pad words, 18 padding
-  // (a copy of chunk 17).  LDS chunk c = 19t + j is filled from the matching
-  // 16 B of token t's block (buffer_load_dwordx4 ... lds: lane-consecutive
-  // chunks land LDS-consecutive); offsets are set per tile, b*276 is the
-  // scalar offset.  Only the 16-token blocks that hold tokens are copied.
+  // token in 16-B chunks: LDS chunk c = 19t + j is filled from chunk
+  // (j + 1) % 19 of token t's Q8P block (buffer_load_dwordx4 ... lds:
+  // lane-consecutive chunks land LDS-consecutive); offsets are set per tile,
+  // b*304 is the scalar offset.  Only the 16-token blocks that hold tokens
+  // are copied.
   const int t0 = p0, nt = p1 - p0;
   const int ntb = (nt + 15) >> 4;  // token blocks holding tokens (wave-uniform)
   const int xchunks = ntb * 16 * 19;
@@ -353,10 +364,11 @@ grouped_mfma_kernel(GroupedArgs a) {
     for (int i = 0; i < kXInstr; ++i) {
       const int q = wave + 8 * i;  // the instruction's 64-chunk slice
       if (64 * q < xchunks)
-        dma16(xbuf0 + s * kXBufWords + 256 * q, xofs[i], rx4, b * kQ8Bytes);
+        dma16(xbuf0 + s * kXBufWords + 256 * q, xofs[i], rx4, b * kQ8PBytes);
     }
   };
 
+  if (kGateUp && tid < 64) etab[tid] = kExp2Tab64[tid];  // the SiLU's exp table
   if (tid < kTokTile) {  // block index of each token row (rows past nt repeat the first)
     const int t = tid < nt ? tid : 0;
     trow[tid] = (kGateUp ? a.grows[t0 + t] : t0 + t) * nb;
@@ -366,8 +378,7 @@ grouped_mfma_kernel(GroupedArgs a) {
   for (int i = 0; i < kXInstr; ++i) {
     const int c = min(64 * (wave + 8 * i) + lane, kTokTile * 19 - 1);
     const int t = c / 19, j = c - t * 19;
-    const int gw = j < 16 ? 1 + 4 * j : (j == 16 ? 65 : 0);  // qs, bsums, then d
-    xofs[i] = static_cast<uint32_t>(trow[t]) * kQ8Bytes + 4 * gw;
+    xofs[i] = static_cast<uint32_t>(trow[t]) * kQ8PBytes + 16 * (j == 18 ? 0 : j + 1);
   }
   // the wave's MFMA tiles: token blocks ti < ntb (16 tokens each) of weight
   // row block `wave`; the lane's four output tokens of block ti are the MFMA
@@ -441,14 +452,23 @@ grouped_mfma_kernel(GroupedArgs a) {
       bl[gq] = v4i{pmul(n0, sl), pmul(n1, sl), pmul(n2, sl), pmul(n3, sl)};
       bh[gq] = v4i{pmul(n0, sh), pmul(n1, sh), pmul(n2, sh), pmul(n3, sh)};
     }
-    // M = sum_s mn_s * bsum_s by MFMA: A = a token row's eight bsums split
-    // exactly as 128*hi + lo (hi in [-32, 31], lo in [0, 127], both int8,
-    // written so by the quantizer), B = the row's eight 6-bit mins in the
-    // first K quarter (lanes 0-15) and zeros elsewhere, so the other lanes'
-    // A bytes do not count.  M = 128 * C(hi) + C(lo).
+    // M = sum_s mn_s * bsum_s by one fp16 MFMA, exactly: with bsum = 2 a + b
+    // (a = bsum >> 1, b = bsum & 1, fp16 integers from the quantizer), K
+    // quarters 0-1 pair 2 mn_s with a_s and quarters 2-3 pair mn_s with b_s
+    // (s = 4 (lq & 1) + 0..3).  Every product and partial sum is an integer
+    // below 2^24 (|M| <= 8 * 63 * 4064), so the fp32 accumulation is exact
+    // and M arrives as the float the epilogue needs.
     const uint32_t dd = whdr.x;
-    const long bmn =
-        lq == 0 ? static_cast<long>(sm.mn_lo) | (static_cast<long>(sm.mn_hi) << 32) : 0l;
+    v4h bmn;
+    {
+      const uint32_t mw = (lq & 1) ? sm.mn_hi : sm.mn_lo;
+      const uint32_t m2 = lq < 2 ? mw << 1 : mw;  // bytes <= 126: no carry
+      // fp16 bits 0x6400 + v = 1024 + v; subtract 1024 exactly
+      const h2 k1024 = {static_cast<_Float16>(-1024.f), static_cast<_Float16>(-1024.f)};
+      const h2 f0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, m2, 0x04010400u)) + k1024;
+      const h2 f1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, m2, 0x04030402u)) + k1024;
+      bmn = v4h{f0.x, f0.y, f1.x, f1.y};
+    }
     const float d = half_bits_to_float(dd & 0xFFFFu);
     const float dmin = half_bits_to_float(dd >> 16);
 #pragma unroll
@@ -465,16 +485,13 @@ grouped_mfma_kernel(GroupedArgs a) {
         cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bl[gq], cl, 0, 0, 0);
         ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bh[gq], ch, 0, 0, 0);
       }
-      const long* bs = reinterpret_cast<const long*>(Xt + 64);
-      const v4i mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(bs[1], bmn, z, 0, 0, 0);
-      const v4i ml = __builtin_amdgcn_mfma_i32_16x16x32_i8(bs[0], bmn, z, 0, 0, 0);
+      const v4h ab = *reinterpret_cast<const v4h*>(Xt + 64 + 2 * lq);
+      const v4f mf = __builtin_amdgcn_mfma_f32_16x16x16f16(ab, bmn, v4f{}, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int I = ch[i] * 8 + cl[i];
-        const int M = mh[i] * 128 + ml[i];
-        const float xd = __builtin_bit_cast(float, X[(16 * ti + 4 * lq + i) * kXRow + 68]);
-        const float t =
-            __builtin_fmaf(d, static_cast<float>(I), -(dmin * static_cast<float>(M)));
+        const float xd = __builtin_bit_cast(float, X[(16 * ti + 4 * lq + i) * kXRow + 72]);
+        const float t = __builtin_fmaf(d, static_cast<float>(I), -(dmin * mf[i]));
         acc[ti][i] = __builtin_fmaf(xd, t, acc[ti][i]);
       }
     }
@@ -499,14 +516,19 @@ grouped_mfma_kernel(GroupedArgs a) {
     for (int tj = 0; tj < kTokBlocks / 2; ++tj) {
       const int ti = up_wave ? kTokBlocks / 2 + tj : tj;
       if (ti >= ntb) continue;
+      float gv[4], uv[4], hv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float other = pair[(partner * 2 * kTokBlocks + 4 * tj + i) * 64 + lane];
+        gv[i] = up_wave ? other : acc[ti][i];
+        uv[i] = up_wave ? acc[ti][i] : other;
+      }
+      silu_mul_tab_n<4>(gv, uv, hv, etab);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tt = 16 * ti + 4 * lq + i;
-        const float other = pair[(partner * 2 * kTokBlocks + 4 * tj + i) * 64 + lane];
-        const float gv = up_wave ? other : acc[ti][i], uv = up_wave ? acc[ti][i] : other;
         if (tt < nt)
-          a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * (wave & 3) + lr] =
-              silu_mul_kc(gv, uv);
+          a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * (wave & 3) + lr] = hv[i];
       }
     }
   } else {
@@ -528,10 +550,6 @@ grouped_mfma_kernel(GroupedArgs a) {
   }  // slices
 }
 
-// Q8_K blocks for the grouped kernels: the standard block except that the
-// 16-byte bsums field holds each sub-block sum s split as s = 128*hi + lo,
-// lo = s & 127 in bytes 0-7 and hi = s >> 7 (two's complement) in bytes
-// 8-15.
 // ---- the dispatch scan over many workgroups (prefill path) ----------------
 // The same arrays as dispatch_scan_kernel, in three launches so that the
 // per-route work runs on many CUs:
@@ -751,9 +769,11 @@ __global__ void __launch_bounds__(256) scan_place_kernel(const int* __restrict__
   }
 }
 
-// One block per 16-lane row (four per wave, 16 per workgroup): the lane's 16
-// values are four 16-B loads, and the block's max and bsums reduce inside a
-// DPP row.  Same arithmetic as quantize_block_wave.
+// Q8P blocks (the grouped kernels' input, see kQ8PBytes): one block per
+// 16-lane row (four per wave, 16 per workgroup); the lane's 16 values are
+// four 16-B loads and the block's max and sums reduce inside a DPP row.
+// The codes and d are quantize_row_q8_K's (q4_k.cpp:44-61), as in
+// quantize_block_wave; only the layout differs.
 // quantize_rows16 quantizes block `blk` in the lane's 16-lane row (blocks at
 // or past n_blocks store nothing).
 __device__ __forceinline__ void quantize_rows16(const float* __restrict__ in,
@@ -792,17 +812,15 @@ __device__ __forceinline__ void quantize_rows16(const float* __restrict__ in,
       packed[w] |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * i);
     }
   }
-  qsum += dpp_i<kDppXor1>(qsum);  // a bsum's 32 values: this lane and its neighbour
+  qsum += dpp_i<kDppXor1>(qsum);  // a sub-block sum's 32 values: this lane and its neighbour
   if (blk >= n_blocks) return;
-  unsigned char* ob = out + blk * kQ8Bytes;
+  unsigned char* ob = out + blk * kQ8PBytes;
   const int r = lane & 15;
-  uint32_t* qw = reinterpret_cast<uint32_t*>(ob + 4 + 16 * r);
-#pragma unroll
-  for (int w = 0; w < 4; ++w) qw[w] = packed[w];
-  if (r == 0) *reinterpret_cast<float*>(ob) = d;
-  if ((r & 1) == 0) {
-    ob[260 + (r >> 1)] = static_cast<unsigned char>(qsum & 127);
-    ob[268 + (r >> 1)] = static_cast<unsigned char>((qsum >> 7) & 0xFF);
+  *reinterpret_cast<u32x4*>(ob + 16 + 16 * r) = (u32x4){packed[0], packed[1], packed[2], packed[3]};
+  if (r == 0) *reinterpret_cast<u32x4*>(ob) = (u32x4){__builtin_bit_cast(uint32_t, d), 0u, 0u, 0u};
+  if ((r & 1) == 0) {  // sum = 2 a + b as fp16 integers (|a| <= 2032: exact)
+    *reinterpret_cast<_Float16*>(ob + 272 + r) = static_cast<_Float16>(static_cast<float>(qsum >> 1));
+    *reinterpret_cast<_Float16*>(ob + 288 + r) = static_cast<_Float16>(static_cast<float>(qsum & 1));
   }
 }
 // rows_used (optional, device): only the first *rows_used rows hold data
@@ -943,7 +961,7 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
   PrefillWs w{};
   w.P = T * k + T;
   size_t o = 0;
-  w.xq = o;    o = al256(o + static_cast<size_t>(T) * (hidden / kQK) * kQ8Bytes);
+  w.xq = o;    o = al256(o + static_cast<size_t>(T) * (hidden / kQK) * kQ8PBytes);
   w.gslot = o; o = al256(o + static_cast<size_t>(T) * k * 4);
   w.grows = o; o = al256(o + static_cast<size_t>(w.P) * 4);
   w.off = o;   o = al256(o + static_cast<size_t>(E + 2) * 4);
@@ -955,19 +973,19 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
   w.plan = o;  o = al256(o + plan_ws(T, E).total);
   w.sgate = o; o = al256(o + static_cast<size_t>(T) * 4);
   w.h = o;     o = al256(o + static_cast<size_t>(w.P) * n_ff * 4);
-  w.hq = o;    o = al256(o + static_cast<size_t>(w.P) * (n_ff / kQK) * kQ8Bytes);
+  w.hq = o;    o = al256(o + static_cast<size_t>(w.P) * (n_ff / kQK) * kQ8PBytes);
   w.y = o;     o = al256(o + static_cast<size_t>(w.P) * hidden * 4);
   w.total = o;
   return w;
 }
 
-// the grouped kernels' Q8_K input (split bsums)
-static int quantize_split(const float* in, sg_block_q8k* out, int nb_row, int n_rows,
+// the grouped kernels' Q8P input
+static int quantize_split(const float* in, unsigned char* out, int nb_row, int n_rows,
                           hipStream_t s, const char* nm, const int* rows_used = nullptr) {
   const long long n_blocks = static_cast<long long>(nb_row) * n_rows;
   const unsigned grid = static_cast<unsigned>((n_blocks + 15) / 16);
-  hipLaunchKernelGGL(prefill_quantize_kernel, dim3(grid), dim3(256), 0, s, in,
-                     reinterpret_cast<unsigned char*>(out), n_blocks, rows_used, nb_row);
+  hipLaunchKernelGGL(prefill_quantize_kernel, dim3(grid), dim3(256), 0, s, in, out, n_blocks,
+                     rows_used, nb_row);
   return check_launch(nm);
 }
 
@@ -1106,7 +1124,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   if (int st = plan_check(n_tokens, k, n_expert, kTokTile, nm)) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   unsigned char* base = static_cast<unsigned char*>(workspace);
-  auto* xq = reinterpret_cast<sg_block_q8k*>(base + ws.xq);
+  unsigned char* xq = base + ws.xq;
   int* gslot = reinterpret_cast<int*>(base + ws.gslot);
   int* grows = reinterpret_cast<int*>(base + ws.grows);
   int* off = reinterpret_cast<int*>(base + ws.off);
@@ -1115,7 +1133,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   int* tiles = reinterpret_cast<int*>(base + ws.tiles);
   TileRec* trec = reinterpret_cast<TileRec*>(base + ws.trec);
   float* h = reinterpret_cast<float*>(base + ws.h);
-  auto* hq = reinterpret_cast<sg_block_q8k*>(base + ws.hq);
+  unsigned char* hq = base + ws.hq;
   float* y = reinterpret_cast<float*>(base + ws.y);
   const int has_shared = n_sh == 3;
   // the gate scales the shared expert only: without one it has nothing to scale
@@ -1126,7 +1144,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
     const unsigned grid = static_cast<unsigned>(n_tokens + (nxb + 3) / 4);
     auto launch = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(grid), dim3(64), 0, s, logits, idx, weight, n_tokens,
-                         n_expert, k, shared_w, x, reinterpret_cast<unsigned char*>(xq), nxb);
+                         n_expert, k, shared_w, x, xq, nxb);
     };
     if (n_expert <= 64) launch(route_quantize_kernel<1>);
     else if (n_expert <= 128) launch(route_quantize_kernel<2>);
@@ -1153,7 +1171,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
     return st;
   const int G = n_expert + has_shared;
   GroupedArgs ga{};
-  ga.xq = reinterpret_cast<const unsigned char*>(xq);
+  ga.xq = xq;
   ga.off = off;
   ga.grows = grows;
   ga.trec = trec;
@@ -1173,7 +1191,7 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
   // h rows of the filled positions only: off[E + 1] = routes + shared rows
   if (int st = quantize_split(h, hq, n_ff / kQK, ws.P, s, nm, off + n_expert + 1)) return st;
   GroupedArgs gd = ga;
-  gd.xq = reinterpret_cast<const unsigned char*>(hq);
+  gd.xq = hq;
   gd.grows = nullptr;
   gd.out = y;
   gd.nb = n_ff / kQK;

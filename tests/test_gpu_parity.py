@@ -617,3 +617,19 @@ def test_moe_prefill_vs_decode_path():
     np.testing.assert_array_equal(host(i1), host(i2))
     np.testing.assert_array_equal(host(w1), host(w2))
     assert rel_err(host(o1), host(o2)) < 5e-3
+
+
+def test_silu_exp_table_sweep():
+    """The table exp (expf_tab, with its exact fallback near float rounding
+    midpoints and outside [-87, 88]) against the oracle's expf_sg through
+    SiLU: every 256th float bit pattern (all exponents, both signs, inf and
+    NaN patterns) with u = 1, bit for bit."""
+    bits = (np.arange(1 << 24, dtype=np.uint64) << np.uint64(8)).astype(np.uint32)
+    bits |= np.uint32(0x5A)  # low mantissa bits set, so patterns are not all round
+    g = bits.view(np.float32)
+    u = np.ones_like(g)
+    h = host(ops.silu_mul(dev(g), dev(u)))
+    ref = orc.silu_mul(g, u)
+    nan = np.isnan(ref)  # NaN payloads are not compared, only NaN-ness
+    np.testing.assert_array_equal(np.isnan(h), nan)
+    np.testing.assert_array_equal(h[~nan].view(np.uint32), ref[~nan].view(np.uint32))
