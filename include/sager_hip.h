@@ -267,6 +267,34 @@ int sg_moe_layer(const sg_block_q4k* const* tab_gate,
                  size_t workspace_bytes, int n_tokens, int hidden, int n_ff,
                  int n_expert, int k, float shared_w, void* stream);
 
+/* sg_moe_layer on the session's own fp16 buffers (Session::moe_dispatch_
+ * device, session.cpp:2482-3030, over x_ / xn_ of session.hpp:240):
+ *   xn       fp16 [n_tokens][hidden], the normed activations (the shared
+ *            gate's input; quantized to Q8_K when xq is NULL);
+ *   xq       optional Q8_K of xn the caller already made (the fused
+ *            norm+quantize's moe_xq_in_, session.cpp:1022, 1131), used as is
+ *            instead of quantizing xn again; xn may then be NULL unless the
+ *            shared gate is on;
+ *   residual fp16 [n_tokens][hidden] or NULL (0); may alias out (x_ is both
+ *            in the reference);
+ *   out      fp16 [n_tokens][hidden].
+ * The expert chain is sg_moe_layer's (fp32 h, as the CPU path computes);
+ * the slot outputs are stored as fp16, as the reference's f16out GEMVs
+ * store them, the shared one is gated on its fp16 value and stored again
+ * (sigmoid_gate_scalar_batched_f16), and the combine accumulates in fp32
+ * from the fp16 residual in slot order and stores fp16
+ * (moe_combine_batched_f16, moe.cu:265-280; session.cpp:3029).  Everything
+ * else (routing, idx/weight, workspace, limits) as sg_moe_layer. */
+int sg_moe_layer_f16(const sg_block_q4k* const* tab_gate,
+                     const sg_block_q4k* const* tab_up,
+                     const sg_block_q4k* const* tab_down,
+                     const sg_block_q4k* sh_gate, const sg_block_q4k* sh_up,
+                     const sg_block_q4k* sh_down, const float* sh_gate_w,
+                     const uint16_t* xn, const sg_block_q8k* xq, const float* logits,
+                     const uint16_t* residual, uint16_t* out, int* idx, float* weight,
+                     void* workspace, size_t workspace_bytes, int n_tokens, int hidden,
+                     int n_ff, int n_expert, int k, float shared_w, void* stream);
+
 /* sg_moe_layer without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
@@ -368,6 +396,20 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate,
                    int* idx, float* weight, void* workspace,
                    size_t workspace_bytes, int n_tokens, int hidden, int n_ff,
                    int n_expert, int k, float shared_w, void* stream);
+
+/* sg_moe_prefill on the session's fp16 buffers: the arguments and the
+ * fp16 slot-output / combine rounding of sg_moe_layer_f16 (xn fp16, xq an
+ * optional Q8_K of it used as is, residual/out fp16; session.cpp:2643-2840
+ * then moe_combine_batched_f16 at :3029). */
+int sg_moe_prefill_f16(const sg_block_q4k* const* tab_gate,
+                       const sg_block_q4k* const* tab_up,
+                       const sg_block_q4k* const* tab_down,
+                       const sg_block_q4k* sh_gate, const sg_block_q4k* sh_up,
+                       const sg_block_q4k* sh_down, const float* sh_gate_w,
+                       const uint16_t* xn, const sg_block_q8k* xq, const float* logits,
+                       const uint16_t* residual, uint16_t* out, int* idx, float* weight,
+                       void* workspace, size_t workspace_bytes, int n_tokens, int hidden,
+                       int n_ff, int n_expert, int k, float shared_w, void* stream);
 
 /* ---- GGUF expert pool (load time, host + HBM) ------------------------
  * Replaces Weights::load_expert_pool (weights.cpp:800-870, over the GGUF v3

@@ -36,6 +36,8 @@ def lib():
         L.orc_dequant_q6k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
         L.orc_sigmoid.restype = ctypes.c_float
         L.orc_sigmoid.argtypes = [ctypes.c_float]
+        L.orc_float_to_half.restype = ctypes.c_uint16
+        L.orc_float_to_half.argtypes = [ctypes.c_float]
         _lib = L
     return _lib
 
@@ -223,6 +225,53 @@ def moe_layer(gate, up, down, shared, x, logits=None, idx=None, weight=None, res
         bad = ((idx[:, :k] < 0) | (idx[:, :k] >= n_expert)).any(axis=1)
         weight[bad] = 0.0
     return out, idx, weight
+
+
+def float_to_half(x):
+    """fp32 -> fp16 bits, round to nearest even (orc_float_to_half)."""
+    x = _c(np.atleast_1d(x), np.float32)
+    h = np.zeros(x.shape, np.uint16)
+    lib().orc_float_to_half_n(P(x), P(h), ctypes.c_int64(x.size))
+    return h
+
+
+def moe_layer_f16(gate, up, down, shared, xn16, logits=None, idx=None, weight=None,
+                  residual16=None, hidden=2048, n_ff=512, k=8, shared_w=1.0, n_threads=1,
+                  prefill=False, shared_gate_w=None):
+    """The layer on the session's fp16 buffers (orc_moe_layer_f16io): xn16
+    fp16 [T, hidden] (normed activations), residual16 fp16 [T, hidden] or
+    None.  Returns out fp16 [T, hidden], idx, weight."""
+    x = _c(np.atleast_2d(xn16).astype(np.float16).astype(np.float32), np.float32)
+    T = x.shape[0]
+    n_expert = len(gate)
+    for lst in (gate, up, down):
+        for i, m in enumerate(lst):
+            if m is not None:
+                lst[i] = _c(m, np.uint8)
+    tg, tu, td = _ptr_table(gate), _ptr_table(up), _ptr_table(down)
+    sg = su = sd = None
+    if shared is not None:
+        shared = tuple(_c(m, np.uint8) for m in shared)
+        sg, su, sd = (m.ctypes.data for m in shared)
+    out = np.zeros((T, hidden), np.float32)
+    res = (_c(np.asarray(residual16).astype(np.float16).astype(np.float32), np.float32)
+           if residual16 is not None else None)
+    sgw = _c(shared_gate_w, np.float32) if shared_gate_w is not None else None
+    if logits is not None:
+        logits = _c(np.atleast_2d(logits), np.float32)
+        idx = np.full((T, k + 1), -1, np.int32)
+        weight = np.zeros((T, k + 1), np.float32)
+    else:
+        idx, weight = _c(idx, np.int32), _c(weight, np.float32).copy()
+    lib().orc_moe_layer_f16io(tg, tu, td, ctypes.c_void_p(sg), ctypes.c_void_p(su),
+                              ctypes.c_void_p(sd), P(sgw) if sgw is not None else None, P(x),
+                              P(logits) if logits is not None else None,
+                              P(res) if res is not None else None, P(out), P(idx), P(weight), T,
+                              hidden, n_ff, n_expert, k, ctypes.c_float(shared_w), n_threads,
+                              int(prefill))
+    bad = ((idx[:, :k] < 0) | (idx[:, :k] >= n_expert)).any(axis=1)
+    weight[bad] = 0.0
+    return out.astype(np.float16), idx, weight
 
 
 def dispatch_scan(idx, weight, k, n_expert, tok_per=1):

@@ -21,6 +21,11 @@
  *   orc_router_topk                        - numpy softmax + stable argsort,
  *                                            duplicated logits, NaN rows
  *   orc_moe_combine                        - fp64 closed form
+ *   orc_float_to_half                      - numpy float16 conversion (RNE)
+ *                                            over edge and random values
+ *   orc_moe_layer_f16io                    - composition: the fp32 layer's
+ *                                            slot outputs, rounded and
+ *                                            combined as written here
  *   orc_dispatch_scan                      - counting invariants
  *   orc_dequant_q6k                        - closed form per field (numpy)
  *   orc_q6k_subgroup_dots                  - brute force from the dequant
@@ -79,6 +84,35 @@ float orc_half_to_float(uint16_t h) {
   memcpy(&mag, &bits, 4);
   return mag;
 }
+
+/* fp32 -> fp16, round to nearest even (the __float2half of the reference's
+ * sth(), moe.cu:12-14): infinities and NaN map to fp16 inf / quiet NaN,
+ * values from 65520 up overflow to inf, values below 2^-14 become fp16
+ * subnormals (multiples of 2^-24, rounded by rintf, which rounds to
+ * nearest even). */
+uint16_t orc_float_to_half(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u);
+  if (ax >= 0x477ff000u) return sign | 0x7c00u;                 /* >= 65520: inf */
+  if (ax < 0x38800000u) {                                        /* < 2^-14 */
+    float a;
+    memcpy(&a, &ax, 4);
+    return sign | (uint16_t)rintf(a * 16777216.0f);              /* exact scaling by 2^24 */
+  }
+  uint32_t h = ((((ax >> 23) - 127u + 15u) << 10)) | ((ax >> 13) & 0x3ffu);
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;  /* a carry bumps the exponent */
+  return sign | (uint16_t)h;
+}
+
+void orc_float_to_half_n(const float* x, uint16_t* h, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) h[i] = orc_float_to_half(x[i]);
+}
+
+static float f16_round(float v) { return orc_half_to_float(orc_float_to_half(v)); }
 
 void orc_get_scale_min(int j, const uint8_t* q, uint8_t* d, uint8_t* m) {
   /* Sub-blocks 0..3: low 6 bits of bytes j and j+4. Sub-blocks 4..7: a
@@ -560,7 +594,7 @@ static void moe_layer_routed(const void* const* tab_gate, const void* const* tab
                              const float* x,
                              const int* idx, const float* weight, const float* residual,
                              float* out, int n_tokens, int hidden, int n_ff, int n_expert,
-                             int k, int n_threads, int int_first) {
+                             int k, int n_threads, int int_first, int f16_io) {
   const int nbh = hidden / 256;
   const int slots = k + 1;
   orc_q8k* xq = (orc_q8k*)malloc(sizeof(orc_q8k) * (size_t)nbh * n_tokens);
@@ -598,13 +632,31 @@ static void moe_layer_routed(const void* const* tab_gate, const void* const* tab
   pool_run(jobs, nj, n_threads);
   /* qwen3.5 shared-expert gate (session.cpp:2904-2909): the shared output
    * of token t is scaled by sigmoid(sh_gate_w . x[t]) before the combine */
-  if (sh_gate_w && sh_gate && sh_up && sh_down)
-    for (int t = 0; t < n_tokens; ++t) {
-      const float s = orc_sigmoid(rowdot_lanes32(sh_gate_w, x + (int64_t)t * hidden, hidden));
-      float* yk = ys + ((size_t)t * slots + k) * hidden;
-      for (int i = 0; i < hidden; ++i) yk[i] = yk[i] * s;
-    }
-  orc_moe_combine(out, residual, ys, w, k, hidden, n_tokens);
+  if (f16_io) {
+    /* the session's fp16 buffers (session.cpp:2850-2930, moe.cu:249-292):
+     * every slot output is stored as fp16 (the f16out GEMVs), the shared
+     * slot is gated in place on its fp16 value (sigmoid_gate_scalar_batched
+     * _f16: fp16(fp16(y) * s)), then moe_combine_batched_f16 accumulates
+     * acc = fp32(residual fp16), acc = fma(w, fp32(y fp16), acc) in slot
+     * order and stores fp16(acc).  residual holds fp16 values. */
+    for (size_t i = 0; i < (size_t)n_tokens * slots * hidden; ++i) ys[i] = f16_round(ys[i]);
+    if (sh_gate_w && sh_gate && sh_up && sh_down)
+      for (int t = 0; t < n_tokens; ++t) {
+        const float s = orc_sigmoid(rowdot_lanes32(sh_gate_w, x + (int64_t)t * hidden, hidden));
+        float* yk = ys + ((size_t)t * slots + k) * hidden;
+        for (int i = 0; i < hidden; ++i) yk[i] = f16_round(yk[i] * s);
+      }
+    orc_moe_combine(out, residual, ys, w, k, hidden, n_tokens);
+    for (size_t i = 0; i < (size_t)n_tokens * hidden; ++i) out[i] = f16_round(out[i]);
+  } else {
+    if (sh_gate_w && sh_gate && sh_up && sh_down)
+      for (int t = 0; t < n_tokens; ++t) {
+        const float s = orc_sigmoid(rowdot_lanes32(sh_gate_w, x + (int64_t)t * hidden, hidden));
+        float* yk = ys + ((size_t)t * slots + k) * hidden;
+        for (int i = 0; i < hidden; ++i) yk[i] = yk[i] * s;
+      }
+    orc_moe_combine(out, residual, ys, w, k, hidden, n_tokens);
+  }
   free(w);
   free(jobs);
   free(ys);
@@ -619,7 +671,7 @@ void orc_moe_layer_routed(const void* const* tab_gate, const void* const* tab_up
                           int n_tokens, int hidden, int n_ff, int n_expert, int k,
                           int n_threads) {
   moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w, x, idx,
-                   weight, residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads, 0);
+                   weight, residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads, 0, 0);
 }
 
 /* The prefill layer: the same routing, experts and combine as
@@ -633,7 +685,25 @@ void orc_moe_prefill(const void* const* tab_gate, const void* const* tab_up,
                      float shared_w, int n_threads) {
   if (logits) orc_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w);
   moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w, x, idx,
-                   weight, residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads, 1);
+                   weight, residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads, 1, 0);
+}
+
+/* The layer on the session's fp16 buffers: x holds the fp16 values of xn
+ * (as floats; quantized exactly as the Q8_K the session's fused norm makes
+ * from them), residual the fp16 values of the residual stream (NULL: 0),
+ * out receives the fp16-rounded combine (as floats).  logits != NULL routes
+ * first (idx/weight outputs); else idx/weight are inputs.  int_first: the
+ * prefill's GEMV order. */
+void orc_moe_layer_f16io(const void* const* tab_gate, const void* const* tab_up,
+                         const void* const* tab_down, const void* sh_gate, const void* sh_up,
+                         const void* sh_down, const float* sh_gate_w, const float* x,
+                         const float* logits, const float* residual, float* out, int* idx,
+                         float* weight, int n_tokens, int hidden, int n_ff, int n_expert, int k,
+                         float shared_w, int n_threads, int int_first) {
+  if (logits) orc_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w);
+  moe_layer_routed(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w, x, idx,
+                   weight, residual, out, n_tokens, hidden, n_ff, n_expert, k, n_threads,
+                   int_first, 1);
 }
 
 void orc_moe_layer(const void* const* tab_gate, const void* const* tab_up,

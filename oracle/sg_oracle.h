@@ -126,6 +126,23 @@ void orc_moe_prefill(const void* const* tab_gate, const void* const* tab_up,
                      float* weight, int n_tokens, int hidden, int n_ff, int n_expert, int k,
                      float shared_w, int n_threads);
 
+/* fp32 -> fp16 bits, round to nearest even (__float2half). */
+uint16_t orc_float_to_half(float f);
+void orc_float_to_half_n(const float* x, uint16_t* h, int64_t n);
+
+/* The layer on the session's fp16 buffers (x: fp16 values of xn as floats,
+ * residual: fp16 values or NULL, out: the fp16-rounded result as floats):
+ * slot outputs stored as fp16, the shared slot gated on its fp16 value,
+ * moe_combine_batched_f16's fp32 accumulation and fp16 store
+ * (moe.cu:249-292).  logits may be NULL (idx/weight then inputs);
+ * int_first selects the prefill's GEMV order. */
+void orc_moe_layer_f16io(const void* const* tab_gate, const void* const* tab_up,
+                         const void* const* tab_down, const void* sh_gate, const void* sh_up,
+                         const void* sh_down, const float* sh_gate_w, const float* x,
+                         const float* logits, const float* residual, float* out, int* idx,
+                         float* weight, int n_tokens, int hidden, int n_ff, int n_expert, int k,
+                         float shared_w, int n_threads, int int_first);
+
 /* Same as orc_moe_layer but with routing given (idx/weight [n_tokens][k+1]
  * already filled, e.g. sampled routing); no softmax. */
 void orc_moe_layer_routed(const void* const* tab_gate,

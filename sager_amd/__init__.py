@@ -51,6 +51,10 @@ SIGNATURES = {
     "sg_moe_layer_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "sg_moe_layer": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                           _VP, _SZ, _I, _I, _I, _I, _I, _F, _VP]),
+    "sg_moe_layer_f16": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                              _VP, _VP, _SZ, _I, _I, _I, _I, _I, _F, _VP]),
+    "sg_moe_prefill_f16": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                                _VP, _VP, _SZ, _I, _I, _I, _I, _I, _F, _VP]),
     "sg_moe_layer_noalloc": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                   _VP, _I, _I, _I, _I, _I, _F, _VP]),
     "sg_moe_layer_stages": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,

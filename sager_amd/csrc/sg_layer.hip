@@ -101,7 +101,7 @@ struct LayerArgs {
   const sg_block_q4k* sh_up;
   const sg_block_q4k* sh_down;
   const float* sh_gate_w;  // fp32 [hidden] shared-expert gate row, or null
-  const float* x;
+  const float* x;  // fp32 [T][hidden] (or null: x16 / xq_in below)
   const float* logits;
   const float* residual;
   float* out;
@@ -117,6 +117,15 @@ struct LayerArgs {
   int back_bufs;             // back waves with a down-row buffer (8, or 4 when LDS is short)
   int publish_only;          // front launch of the publisher alone (the routing launch)
   FrontLds front_routed, front_shared;  // front LDS layouts (routing groups, shared group)
+  // the session's fp16 buffers (after the fields above, whose layout the
+  // fp32 kernels read): fp16 x16 instead of x, or (with either, or alone
+  // without a shared gate) xq_in, a Q8_K of x made by the caller and used as
+  // is; fp16 res16 / out16 instead of residual / out, with the slot outputs
+  // stored as fp16 and combined as moe_combine_batched_f16
+  const uint16_t* x16;
+  const unsigned char* xq_in;
+  const uint16_t* res16;
+  uint16_t* out16;
 };
 
 // ---- front kernel LDS layout (dwords) -----------------------------------------------
@@ -605,20 +614,63 @@ __device__ __forceinline__ void dma_gateup(const sg_block_q4k* wg, const sg_bloc
              lane, part, nparts);
 }
 
+// The lane's 16 values of x block b (16-lane row layout: lane & 15 holds
+// values 16 (lane & 15) .. + 15) from the fp32 or fp16 x, or - with a
+// caller-made Q8_K - the lane's part of that block as raw words: v[0..3]
+// its 16 qs bytes, v[4] d, v[5] the block's bsum of its 32 values (even
+// lanes; int16 in the low half).
+__device__ __forceinline__ void x_load16(const LayerArgs& a, int b, int lane, float (&v)[16]) {
+  const int r = lane & 15;
+  if (a.xq_in) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a.xq_in + static_cast<long long>(b) * kQ8Bytes);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __builtin_bit_cast(float, q[1 + 4 * r + i]);
+    v[4] = __builtin_bit_cast(float, q[0]);
+    v[5] = __builtin_bit_cast(float, q[65 + (r >> 2)] >> (16 * ((r >> 1) & 1)));
+  } else if (a.x16) {
+    const uint16_t* xb = a.x16 + static_cast<long long>(b) * kQK + 16 * r;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = f16v(xb[i]);
+  } else {
+    const float* xb = a.x + static_cast<long long>(b) * kQK + 16 * r;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = xb[i];
+  }
+}
+
+// x_load16's values of block b into LDS in the kXStride layout: quantized
+// (quantize_row16_lds), or the caller's Q8_K block rearranged (the same
+// layout quantize_row16_lds writes).
+__device__ __forceinline__ void x_row16_lds(const LayerArgs& a, const float (&v)[16], uint32_t* dst,
+                                            bool active, int lane) {
+  if (a.xq_in) {
+    const int r = lane & 15;
+    if (active) {
+      *reinterpret_cast<u32x4*>(dst + 4 * r) =
+          (u32x4){__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                  __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])};
+      if (r == 0) dst[64] = __builtin_bit_cast(uint32_t, v[4]);
+      if ((r & 1) == 0)
+        dst[65 + (r >> 1)] = __builtin_bit_cast(
+            uint32_t, static_cast<float>(static_cast<int16_t>(__builtin_bit_cast(uint32_t, v[5]))));
+    }
+  } else {
+    quantize_row16_lds(v, dst, active, lane);
+  }
+}
+
 // x values of a wave's first P quantization passes, loaded at kernel start
 // so their latency overlaps the routing or the plan: one Q8_K block per
 // 16-lane row, pass p taking block 4 (p nw + w) + (lane >> 4), the lane's 16
 // values.  Waves w < nw take part.
 template <int P>
-__device__ __forceinline__ void x_preload(const float* x, int n_blocks, int w, int nw, int lane,
+__device__ __forceinline__ void x_preload(const LayerArgs& a, int n_blocks, int w, int nw, int lane,
                                           float (&pre)[P][16]) {
   if (w >= nw) return;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int b = 4 * (p * nw + w) + (lane >> 4);
-    const float* xb = x + static_cast<long long>(b < n_blocks ? b : 0) * kQK + 16 * (lane & 15);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) pre[p][i] = xb[i];
+    x_load16(a, b < n_blocks ? b : 0, lane, pre[p]);
   }
 }
 
@@ -626,23 +678,21 @@ __device__ __forceinline__ void x_preload(const float* x, int n_blocks, int w, i
 // pass p of wave w takes block 4 (p nw + w) + (lane >> 4); the first P
 // passes' values come from x_preload.
 template <int P>
-__device__ __forceinline__ void quantize_x(const float* x, int n_blocks, uint32_t* xs, int w,
+__device__ __forceinline__ void quantize_x(const LayerArgs& a, int n_blocks, uint32_t* xs, int w,
                                            int nw, int lane, const float (&pre)[P][16]) {
   if (w >= nw) return;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int b = 4 * (p * nw + w) + (lane >> 4);
     if (p > 0 && 4 * p * nw >= n_blocks) break;  // wave-uniform
-    quantize_row16_lds(pre[p], xs + (b < n_blocks ? b : 0) * kXStride, b < n_blocks, lane);
+    x_row16_lds(a, pre[p], xs + (b < n_blocks ? b : 0) * kXStride, b < n_blocks, lane);
   }
   for (int b0 = 4 * nw * P; b0 < n_blocks; b0 += 4 * nw) {
     const int b = b0 + 4 * w + (lane >> 4);
     const int bc = b < n_blocks ? b : 0;
-    const float* xb = x + static_cast<long long>(bc) * kQK + 16 * (lane & 15);
     float v[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = xb[i];
-    quantize_row16_lds(v, xs + bc * kXStride, b < n_blocks, lane);
+    x_load16(a, bc, lane, v);
+    x_row16_lds(a, v, xs + bc * kXStride, b < n_blocks, lane);
   }
 }
 
@@ -1096,8 +1146,10 @@ __device__ __forceinline__ void shared_gate_tokens(const LayerArgs& a, int tid) 
   const int l = tid & 31, half = tid >> 5;
   for (int t0 = 0; t0 < a.T; t0 += 8) {
     const int t = min(t0 + half, a.T - 1);
-    const float* xt = a.x + static_cast<long long>(t) * a.hidden;
-    const float gl = rowdot_f32_lanes32(a.sh_gate_w, [&](int i) { return xt[i]; }, a.hidden, l);
+    const long long o = static_cast<long long>(t) * a.hidden;
+    const float gl =
+        a.x16 ? rowdot_f32_lanes32(a.sh_gate_w, [&](int i) { return f16v(a.x16[o + i]); }, a.hidden, l)
+              : rowdot_f32_lanes32(a.sh_gate_w, [&](int i) { return a.x[o + i]; }, a.hidden, l);
     if (l == 0 && t0 + half < a.T) a.sgate[t] = sigmoid_sg(gl);
   }
 }
@@ -1154,11 +1206,11 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   const bool t1w = T == 1 && a.logits != nullptr && !shared_grp;
   const int nqw = t1w ? 3 : 4;
   float xpre[1][16];
-  if (!publisher) x_preload(a.x, nxb, wave, nqw, lane, xpre);
+  if (!publisher) x_preload(a, nxb, wave, nqw, lane, xpre);
 
   if (shared_grp) {
     if (nrw > 0) dma_gateup(a.sh_gate, a.sh_up, row0, nrw, nbh, buf, lane);
-    quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);
+    quantize_x(a, nxb, xs, wave, nqw, lane, xpre);
     bar();
     // entries: tokens 0..T-1 in slot k, no plan needed
     gateup_wave(true, row0, nrw, nbh, lpr, buf, xs,
@@ -1215,7 +1267,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
     float* evw = reinterpret_cast<float*>(dyn + L.ev) + wave * L.e32;
     // x of the window for waves 1-3 to quantize while wave 0 builds the plan
     float xw[3][16];
-    if (wave > 0) x_preload(a.x, nxb, wave - 1, 3, lane, xw);
+    if (wave > 0) x_preload(a, nxb, wave - 1, 3, lane, xw);
     for (int t = wave; t < T; t += 4) {
       const float* lg = a.logits + static_cast<long long>(t) * E;
       if (T == 2)
@@ -1224,7 +1276,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
         router_wave<kPl1>(lg, E, k, a.shared_w, ridx + t * k, rw + t * stride, evw, lane);
     }
     bar();
-    if (wave > 0) quantize_x(a.x, nxb, a.xq, wave - 1, 3, lane, xw);
+    if (wave > 0) quantize_x(a, nxb, a.xq, wave - 1, 3, lane, xw);
     build_plan(dyn, L, T, k, E, a.has_shared, tid);
     n_groups = gbase + ctrl[1];
   } else if (a.logits && publisher && T == 1) {
@@ -1319,7 +1371,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
       if (wave == 3) {
         if (!routed) route_wave<4 * EPT>(a, dyn, L, lane);
       } else {
-        quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);  // overlaps the weight stream
+        quantize_x(a, nxb, xs, wave, nqw, lane, xpre);  // overlaps the weight stream
         wait_vm();  // this wave's share of wave 3's rows
       }
       bar();
@@ -1353,8 +1405,8 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   } else {
     if (publisher && T > 1) {  // the gate/up launch reads x quantized
       float xw[1][16];
-      x_preload(a.x, nxb, wave, 4, lane, xw);
-      quantize_x(a.x, nxb, a.xq, wave, 4, lane, xw);
+      x_preload(a, nxb, wave, 4, lane, xw);
+      quantize_x(a, nxb, a.xq, wave, 4, lane, xw);
     }
     for (int i = tid; i < T * k; i += 256) ridx[i] = a.idx[(i / k) * stride + (i % k)];
     for (int i = tid; i < T * stride; i += 256) rw[i] = a.weight[i];
@@ -1427,7 +1479,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   const int e = pexp[g];
   const bool present = tabg[e] != 0ull && tabu[e] != 0ull;
   if (!t1w) {
-    quantize_x(a.x, nxb, xs, wave, nqw, lane, xpre);  // overlaps the weight stream
+    quantize_x(a, nxb, xs, wave, nqw, lane, xpre);  // overlaps the weight stream
     bar();
   }
   const int j0 = poff[g];
@@ -1443,8 +1495,22 @@ constexpr int kShapeWindow = 4;  // the verify window's tokens (one plus three d
 
 // The model shape with kT tokens, with or without a shared expert, as the
 // launcher derives it (kT = 0: none).
-template <int kT, bool kSh>
+// kIo: 0 = the buffers' precision read from the arguments; 1 = the fp32
+// buffers (x, residual, out) and 2 = the fp16 ones, fixed at compile time so
+// the other kind's branches compile away (their argument loads and tests
+// otherwise sit on the one-token critical chain)
+template <int kT, bool kSh, int kIo = 0>
 __device__ __forceinline__ void apply_shape(LayerArgs& a) {
+  if constexpr (kIo == 1) {
+    a.x16 = nullptr;
+    a.xq_in = nullptr;
+    a.res16 = nullptr;
+    a.out16 = nullptr;
+  } else if constexpr (kIo == 2) {
+    a.x = nullptr;
+    a.residual = nullptr;
+    a.out = nullptr;
+  }
   if constexpr (kT > 0) {
     a.T = kT;
     a.has_shared = kSh;
@@ -1462,10 +1528,10 @@ __host__ inline bool is_shape(int T, int hidden, int n_ff, int E, int k, int kT)
   return T == kT && hidden == kShapeHidden && n_ff == kShapeFf && E == kShapeE && k == kShapeK;
 }
 
-template <int EPT, int NBH, bool kOne = false, int kShapeT = 0, bool kSh = false>
+template <int EPT, int NBH, bool kOne = false, int kShapeT = 0, bool kSh = false, int kIo = 0>
 __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs args) {
   LayerArgs a = args;
-  apply_shape<kShapeT, kSh>(a);
+  apply_shape<kShapeT, kSh, kIo>(a);
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
   // Row y of the grid runs group g.  With a shared expert its row comes
@@ -1487,11 +1553,11 @@ __global__ void __launch_bounds__(256) layer_front_kernel(LayerArgs args) {
 // left in the workspace: several tokens (a verify window), where routing in
 // every compute workgroup would cost more than a launch.  Grid (row chunks
 // of 16, gmax); groups beyond the plan's count exit.
-template <int NBH, int kShapeT = 0, bool kSh = false>
+template <int NBH, int kShapeT = 0, bool kSh = false, int kIo = 0>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
 layer_gateup_kernel(LayerArgs args) {
   LayerArgs a = args;
-  apply_shape<kShapeT, kSh>(a);
+  apply_shape<kShapeT, kSh, kIo>(a);
   __shared__ __attribute__((aligned(16))) uint32_t wbuf[4][64 * 36];
   extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];  // x0, then entry tok / slot
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1758,7 +1824,8 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
   for (int qo = tid; qo < n_out; qo += kBackThreads) {
     const int t = qo / nr, r = qo - t * nr;
     const long long o = static_cast<long long>(t) * a.hidden + row0 + r;
-    float acc = a.residual ? (qo == tid ? res0 : a.residual[o]) : 0.f;
+    float acc = qo == tid ? res0
+                          : (a.residual ? a.residual[o] : (a.res16 ? f16v(a.res16[o]) : 0.f));
     // the shared slot's output scaled by its gate first (1.0 without a
     // gate, which leaves it unchanged), as sigmoid_gate_scalar_batched_f16
     // does before the combine (session.cpp:2904-2909)
@@ -1770,30 +1837,37 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
         const int i = t * stride + (k0 + u <= k ? k0 + u : k);
         yv[u] = ys[i * rows + r];
         wv[u] = wt[i];
-        if (k0 + u == k) yv[u] *= gs;
+        if (a.out16) {  // fp16 slot outputs; the shared one gated on its fp16 value
+          yv[u] = f16v(f16b(yv[u]));
+          if (k0 + u == k) yv[u] = f16v(f16b(yv[u] * gs));
+        } else if (k0 + u == k) {
+          yv[u] *= gs;
+        }
       }
 #pragma unroll
       for (int u = 0; u < 16; ++u)
         if (k0 + u <= k) acc = __builtin_fmaf(wv[u], yv[u], acc);
     }
-    a.out[o] = acc;
+    if (a.out16) a.out16[o] = f16b(acc);
+    else a.out[o] = acc;
   }
 }
 
 // residual of the first combine pass (qo = tid), loaded early
 __device__ __forceinline__ float residual_pre(const LayerArgs& a, int row0, int nr) {
   const int tid = threadIdx.x;
-  if (!a.residual || tid >= a.T * nr) return 0.f;
+  if ((!a.residual && !a.res16) || tid >= a.T * nr) return 0.f;
   const int t = tid / nr, r = tid - t * nr;
-  return a.residual[static_cast<long long>(t) * a.hidden + row0 + r];
+  const long long o = static_cast<long long>(t) * a.hidden + row0 + r;
+  return a.residual ? a.residual[o] : f16v(a.res16[o]);
 }
 
-template <int NBF, int ROWS, int kShapeT = 0, bool kSh = false>
+template <int NBF, int ROWS, int kShapeT = 0, bool kSh = false, int kIo = 0>
 __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args) {
   // kShapeT > 0 (the model shape with kShapeT tokens, as in the front
   // kernel): the shape and the LDS layout are constants
   LayerArgs a = args;
-  apply_shape<kShapeT, kSh>(a);
+  apply_shape<kShapeT, kSh, kIo>(a);
   if constexpr (kShapeT > 0) {
     a.back_rows = 8;
     a.back_lrow = 2;
@@ -1981,6 +2055,26 @@ static int scratch_address(void** out, const char* nm) {
   return SG_OK;
 }
 
+// the layer's activation and output buffers: fp32 (x, residual, out) or the
+// session's fp16 ones (x16 and/or its Q8_K xq, res16, out16)
+struct LayerIo {
+  const float* x;
+  const uint16_t* x16;
+  const unsigned char* xq;
+  const float* residual;
+  float* out;
+  const uint16_t* res16;
+  uint16_t* out16;
+};
+
+static int layer_launch(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
+                        const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
+                        const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
+                        const float* sh_gate_w, const LayerIo& io, const float* logits, int* idx,
+                        float* weight, void* workspace, size_t workspace_bytes, int n_tokens,
+                        int hidden, int n_ff, int n_expert, int k, float shared_w, int stages,
+                        void* stream, const char* nm);
+
 }  // namespace sg
 
 using namespace sg;
@@ -2001,9 +2095,45 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
                         int n_ff, int n_expert, int k, float shared_w, int stages,
                         void* stream) {
   const char* nm = "sg_moe_layer";
+  if (!x || !out) return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  return layer_launch(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w,
+                      LayerIo{x, nullptr, nullptr, residual, out, nullptr, nullptr}, logits, idx,
+                      weight, workspace, workspace_bytes, n_tokens, hidden, n_ff, n_expert, k,
+                      shared_w, stages, stream, nm);
+}
+
+int sg_moe_layer_f16(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
+                     const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
+                     const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
+                     const float* sh_gate_w, const uint16_t* xn, const sg_block_q8k* xq,
+                     const float* logits, const uint16_t* residual, uint16_t* out, int* idx,
+                     float* weight, void* workspace, size_t workspace_bytes, int n_tokens,
+                     int hidden, int n_ff, int n_expert, int k, float shared_w, void* stream) {
+  const char* nm = "sg_moe_layer_f16";
+  if ((!xn && !xq) || !out) return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  if (!xn && sh_gate_w && sh_gate && sh_up && sh_down)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: the shared gate needs xn", nm);
+  return layer_launch(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w,
+                      LayerIo{nullptr, xn, reinterpret_cast<const unsigned char*>(xq), nullptr,
+                              nullptr, residual, out},
+                      logits, idx, weight, workspace, workspace_bytes, n_tokens, hidden, n_ff,
+                      n_expert, k, shared_w, 3, stream, nm);
+}
+
+}  // extern "C"
+
+namespace sg {
+
+static int layer_launch(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
+                        const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
+                        const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
+                        const float* sh_gate_w, const LayerIo& io, const float* logits, int* idx,
+                        float* weight, void* workspace, size_t workspace_bytes, int n_tokens,
+                        int hidden, int n_ff, int n_expert, int k, float shared_w, int stages,
+                        void* stream, const char* nm) {
   if (stages <= 0 || stages > 3)
     return set_error(SG_ERR_INVALID_ARGUMENT, "%s: stages=%d not in 1..3", nm, stages);
-  if (!tab_gate || !tab_up || !tab_down || !x || !out || !idx || !weight || !workspace)
+  if (!tab_gate || !tab_up || !tab_down || !idx || !weight || !workspace)
     return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
   const int n_sh = (sh_gate != nullptr) + (sh_up != nullptr) + (sh_down != nullptr);
   if (n_sh != 0 && n_sh != 3)
@@ -2046,10 +2176,15 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   a.sh_down = sh_down;
   // the gate scales the shared expert only: without one it has nothing to scale
   a.sh_gate_w = n_sh == 3 ? sh_gate_w : nullptr;
-  a.x = x;
+  a.x = io.x;
+  a.x16 = io.x16;
+  a.xq_in = io.xq;
   a.logits = logits;
-  a.residual = residual;
-  a.out = out;
+  a.residual = io.residual;
+  a.out = io.out;
+  a.res16 = io.res16;
+  a.out16 = io.out16;
+  const bool f32io = io.x != nullptr;  // the fp32 entry (else the fp16 one)
   a.idx = idx;
   a.weight = weight;
   a.plan = LayerPlan{reinterpret_cast<int*>(base + ws.meta), reinterpret_cast<int*>(base + ws.off),
@@ -2091,13 +2226,24 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     // y < gmax: compute workgroups of group y; y == gmax: the publisher
     const dim3 grid = a.publish_only ? dim3(1, 1)
                                      : dim3((n_ff + rows_wg - 1) / rows_wg, ws.gmax + 1);
-    if (is_shape(n_tokens, hidden, n_ff, n_expert, k, 1) && a.has_shared)  // the model shape
-      hipLaunchKernelGGL((layer_front_kernel<1, 8, true, 1, true>), grid, dim3(256), lds_f, s, a);
-    else if (is_shape(n_tokens, hidden, n_ff, n_expert, k, 1))
-      hipLaunchKernelGGL((layer_front_kernel<1, 8, true, 1, false>), grid, dim3(256), lds_f, s, a);
-    else if (is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) && a.has_shared)
-      hipLaunchKernelGGL((layer_front_kernel<4, 8, false, kShapeWindow, true>), grid, dim3(256),
-                         lds_f, s, a);  // its verify window
+    if (is_shape(n_tokens, hidden, n_ff, n_expert, k, 1) && a.has_shared) {  // the model shape
+      if (f32io)
+        hipLaunchKernelGGL((layer_front_kernel<1, 8, true, 1, true, 1>), grid, dim3(256), lds_f, s, a);
+      else
+        hipLaunchKernelGGL((layer_front_kernel<1, 8, true, 1, true, 2>), grid, dim3(256), lds_f, s, a);
+    } else if (is_shape(n_tokens, hidden, n_ff, n_expert, k, 1)) {
+      if (f32io)
+        hipLaunchKernelGGL((layer_front_kernel<1, 8, true, 1, false, 1>), grid, dim3(256), lds_f, s, a);
+      else
+        hipLaunchKernelGGL((layer_front_kernel<1, 8, true, 1, false, 2>), grid, dim3(256), lds_f, s, a);
+    } else if (is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) && a.has_shared) {
+      if (f32io)  // its verify window
+        hipLaunchKernelGGL((layer_front_kernel<4, 8, false, kShapeWindow, true, 1>), grid, dim3(256),
+                           lds_f, s, a);
+      else
+        hipLaunchKernelGGL((layer_front_kernel<4, 8, false, kShapeWindow, true, 2>), grid, dim3(256),
+                           lds_f, s, a);
+    }
     else if (fl.ept <= 1 && hidden / kQK == 8 && n_tokens == 1)  // one-token decode, hidden 2048
       hipLaunchKernelGGL((layer_front_kernel<1, 8, true>), grid, dim3(256), lds_f, s, a);
     else if (fl.ept <= 1 && hidden / kQK == 8)  // the decode shape, compiled for hidden 2048
@@ -2113,8 +2259,11 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     if (int st = check_launch("sg_moe_layer/front")) return st;
     if (a.publish_only) {
       const dim3 gg((n_ff + rows_wg - 1) / rows_wg, ws.gmax);
-      if (is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) && a.has_shared)
-        hipLaunchKernelGGL((layer_gateup_kernel<8, kShapeWindow, true>), gg, dim3(256), lds_g, s,
+      if (is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) && a.has_shared && f32io)
+        hipLaunchKernelGGL((layer_gateup_kernel<8, kShapeWindow, true, 1>), gg, dim3(256), lds_g, s,
+                           a);
+      else if (is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) && a.has_shared)
+        hipLaunchKernelGGL((layer_gateup_kernel<8, kShapeWindow, true, 2>), gg, dim3(256), lds_g, s,
                            a);
       else if (hidden / kQK == 8)
         hipLaunchKernelGGL((layer_gateup_kernel<8>), gg, dim3(256), lds_g, s, a);
@@ -2128,16 +2277,26 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
     // constants; other shapes read them from the arguments
     const dim3 gb((hidden + rows - 1) / rows);
     const bool geo = rows == 8 && back_bufs == kBackWaves;
-    if (geo && is_shape(n_tokens, hidden, n_ff, n_expert, k, 1) && a.has_shared)  // model shape
-      hipLaunchKernelGGL((layer_back_kernel<2, 8, 1, true>), gb, dim3(kBackThreads),
-                         lds_b + back_bufs * buf_b, s, a);
-    else if (geo && is_shape(n_tokens, hidden, n_ff, n_expert, k, 1))
-      hipLaunchKernelGGL((layer_back_kernel<2, 8, 1, false>), gb, dim3(kBackThreads),
-                         lds_b + back_bufs * buf_b, s, a);
-    else if (geo && is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) &&
-             a.has_shared)  // its verify window
-      hipLaunchKernelGGL((layer_back_kernel<2, 8, kShapeWindow, true>), gb, dim3(kBackThreads),
-                         lds_b + back_bufs * buf_b, s, a);
+    const size_t lds_bb = lds_b + back_bufs * buf_b;
+    if (geo && is_shape(n_tokens, hidden, n_ff, n_expert, k, 1) && a.has_shared) {  // model shape
+      if (f32io)
+        hipLaunchKernelGGL((layer_back_kernel<2, 8, 1, true, 1>), gb, dim3(kBackThreads), lds_bb, s, a);
+      else
+        hipLaunchKernelGGL((layer_back_kernel<2, 8, 1, true, 2>), gb, dim3(kBackThreads), lds_bb, s, a);
+    } else if (geo && is_shape(n_tokens, hidden, n_ff, n_expert, k, 1)) {
+      if (f32io)
+        hipLaunchKernelGGL((layer_back_kernel<2, 8, 1, false, 1>), gb, dim3(kBackThreads), lds_bb, s, a);
+      else
+        hipLaunchKernelGGL((layer_back_kernel<2, 8, 1, false, 2>), gb, dim3(kBackThreads), lds_bb, s, a);
+    } else if (geo && is_shape(n_tokens, hidden, n_ff, n_expert, k, kShapeWindow) &&
+               a.has_shared) {  // its verify window
+      if (f32io)
+        hipLaunchKernelGGL((layer_back_kernel<2, 8, kShapeWindow, true, 1>), gb, dim3(kBackThreads),
+                           lds_bb, s, a);
+      else
+        hipLaunchKernelGGL((layer_back_kernel<2, 8, kShapeWindow, true, 2>), gb, dim3(kBackThreads),
+                           lds_bb, s, a);
+    }
     else if (n_ff / kQK == 2 && rows == 8)
       hipLaunchKernelGGL((layer_back_kernel<2, 8>), gb, dim3(kBackThreads),
                          lds_b + back_bufs * buf_b, s, a);
@@ -2148,6 +2307,10 @@ int sg_moe_layer_stages(const sg_block_q4k* const* tab_gate, const sg_block_q4k*
   }
   return SG_OK;
 }
+
+}  // namespace sg
+
+extern "C" {
 
 int sg_moe_layer(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
                  const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,

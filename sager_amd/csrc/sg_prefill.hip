@@ -775,21 +775,9 @@ __global__ void __launch_bounds__(256) scan_place_kernel(const int* __restrict__
 // The codes and d are quantize_row_q8_K's (q4_k.cpp:44-61), as in
 // quantize_block_wave; only the layout differs.
 // quantize_rows16 quantizes block `blk` in the lane's 16-lane row (blocks at
-// or past n_blocks store nothing).
-__device__ __forceinline__ void quantize_rows16(const float* __restrict__ in,
-                                                unsigned char* __restrict__ out,
+// or past n_blocks store nothing) from the lane's 16 values v.
+__device__ __forceinline__ void quantize_rows16(const float (&v)[16], unsigned char* __restrict__ out,
                                                 long long n_blocks, long long blk, int lane) {
-  const long long bc = blk < n_blocks ? blk : n_blocks - 1;  // rows past the end compute, never store
-  const float* src = in + bc * kQK + 16 * (lane & 15);
-  float v[16];
-#pragma unroll
-  for (int i = 0; i < 16; i += 4) {
-    const float4 f = *reinterpret_cast<const float4*>(src + i);
-    v[i] = f.x;
-    v[i + 1] = f.y;
-    v[i + 2] = f.z;
-    v[i + 3] = f.w;
-  }
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -823,6 +811,60 @@ __device__ __forceinline__ void quantize_rows16(const float* __restrict__ in,
     *reinterpret_cast<_Float16*>(ob + 288 + r) = static_cast<_Float16>(static_cast<float>(qsum & 1));
   }
 }
+
+// the lane's 16 values of block bc (fp32)
+__device__ __forceinline__ void load16(const float* __restrict__ in, long long bc, int lane,
+                                       float (&v)[16]) {
+  const float* src = in + bc * kQK + 16 * (lane & 15);
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    const float4 f = *reinterpret_cast<const float4*>(src + i);
+    v[i] = f.x;
+    v[i + 1] = f.y;
+    v[i + 2] = f.z;
+    v[i + 3] = f.w;
+  }
+}
+
+// the prefill's x: fp32, the session's fp16 xn, or a Q8_K of it the caller
+// made (moe_xq_in_, session.cpp:1022, 1131), used as is
+struct XSrc {
+  const float* f32;
+  const uint16_t* f16;
+  const unsigned char* q8;
+};
+
+// Q8P block blk of x in the lane's 16-lane row: quantized from fp32 or
+// fp16 values, or the caller's Q8_K block rearranged (its codes, d and
+// sub-block sums unchanged)
+__device__ __forceinline__ void x_block_q8p(const XSrc& x, unsigned char* __restrict__ out,
+                                            long long n_blocks, long long blk, int lane) {
+  const long long bc = blk < n_blocks ? blk : n_blocks - 1;  // rows past the end compute, never store
+  if (x.q8) {
+    if (blk >= n_blocks) return;
+    const int r = lane & 15;
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(x.q8 + bc * kQ8Bytes);
+    unsigned char* ob = out + blk * kQ8PBytes;
+    *reinterpret_cast<u32x4*>(ob + 16 + 16 * r) =
+        (u32x4){q[1 + 4 * r], q[2 + 4 * r], q[3 + 4 * r], q[4 + 4 * r]};
+    if (r == 0) *reinterpret_cast<u32x4*>(ob) = (u32x4){q[0], 0u, 0u, 0u};
+    if ((r & 1) == 0) {
+      const int sum = static_cast<int16_t>(q[65 + (r >> 2)] >> (16 * ((r >> 1) & 1)));
+      *reinterpret_cast<_Float16*>(ob + 272 + r) = static_cast<_Float16>(static_cast<float>(sum >> 1));
+      *reinterpret_cast<_Float16*>(ob + 288 + r) = static_cast<_Float16>(static_cast<float>(sum & 1));
+    }
+    return;
+  }
+  float v[16];
+  if (x.f16) {
+    const uint16_t* src = x.f16 + bc * kQK + 16 * (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = f16v(src[i]);
+  } else {
+    load16(x.f32, bc, lane, v);
+  }
+  quantize_rows16(v, out, n_blocks, blk, lane);
+}
 // rows_used (optional, device): only the first *rows_used rows hold data
 // (the positions the plan filled); whole 16-lane rows past them exit before
 // any lane exchange.
@@ -835,7 +877,18 @@ __global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __re
   const long long blk =
       (static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
   if (rows_used && blk >= static_cast<long long>(*rows_used) * nb_row) return;
-  quantize_rows16(in, out, n_blocks, blk, lane);
+  float v[16];
+  load16(in, blk < n_blocks ? blk : n_blocks - 1, lane, v);
+  quantize_rows16(v, out, n_blocks, blk, lane);
+}
+
+// Q8P of x (caller routing, or routers wider than route_quantize_kernel's)
+__global__ void __launch_bounds__(256) prefill_x_kernel(XSrc x, unsigned char* __restrict__ out,
+                                                        long long n_blocks) {
+  const int lane = threadIdx.x & 63;
+  const long long blk =
+      (static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  x_block_q8p(x, out, n_blocks, blk, lane);
 }
 
 // The prefill's first launch: one-wave workgroups 0 .. n_rows - 1 route one
@@ -845,8 +898,8 @@ __global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __re
 template <int PL>
 __global__ void __launch_bounds__(64) route_quantize_kernel(
     const float* __restrict__ logits, int* __restrict__ idx, float* __restrict__ weight,
-    int n_rows, int n_expert, int k, float shared_w, const float* __restrict__ x,
-    unsigned char* __restrict__ xq, long long n_blocks) {
+    int n_rows, int n_expert, int k, float shared_w, XSrc x, unsigned char* __restrict__ xq,
+    long long n_blocks) {
   __shared__ __attribute__((aligned(16))) float ev[64 * PL];
   const int lane = threadIdx.x;
   const long long w = blockIdx.x;
@@ -855,7 +908,7 @@ __global__ void __launch_bounds__(64) route_quantize_kernel(
                     weight + w * (k + 1), ev, lane);
     return;
   }
-  quantize_rows16(x, xq, n_blocks, (w - n_rows) * 4 + (lane >> 4), lane);
+  x_block_q8p(x, xq, n_blocks, (w - n_rows) * 4 + (lane >> 4), lane);
 }
 
 // out[t] = residual[t] + sum_kk fma(w[t][kk], y[pos(t, kk)]) in slot order;
@@ -864,8 +917,13 @@ __global__ void __launch_bounds__(64) route_quantize_kernel(
 // read first (uniform per workgroup), then their eight 16-B rows are loaded
 // together before the ordered fma chain, so each thread has eight loads in
 // flight instead of one.
+// With out16 (the session's fp16 buffers) the slot outputs are taken as
+// stored in fp16, the shared one gated on its fp16 value and stored again,
+// the accumulation starts from the fp16 res16 and the sum is stored as fp16
+// (sigmoid_gate_scalar_batched_f16, moe_combine_batched_f16: moe.cu:265-292).
 __global__ void __launch_bounds__(256) prefill_combine_kernel(
-    float* __restrict__ out, const float* __restrict__ residual, const float* __restrict__ y,
+    float* __restrict__ out, const float* __restrict__ residual, uint16_t* __restrict__ out16,
+    const uint16_t* __restrict__ res16, const float* __restrict__ y,
     const float* __restrict__ weight, const int* __restrict__ gslot, const int* __restrict__ off,
     const float* __restrict__ sgate, int n_expert, int k, int hidden, int has_shared) {
   // 1-D grid, token-major: ceil(hidden / 1024) workgroups per token, so the
@@ -875,7 +933,13 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(
   const int i = ((blockIdx.x - t * nbx) * 256 + threadIdx.x) * 4;
   if (i >= hidden) return;
   const long long o = static_cast<long long>(t) * hidden + i;
-  float4 acc = residual ? *reinterpret_cast<const float4*>(residual + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (residual) {
+    acc = *reinterpret_cast<const float4*>(residual + o);
+  } else if (res16) {
+    const uint2 r4 = *reinterpret_cast<const uint2*>(res16 + o);
+    acc = make_float4(f16v(r4.x & 0xFFFFu), f16v(r4.x >> 16), f16v(r4.y & 0xFFFFu), f16v(r4.y >> 16));
+  }
   const int shared_pos = off[n_expert] + t;
   // the shared slot's output scaled by its gate first (1.0 without a gate
   // leaves it unchanged), as sigmoid_gate_scalar_batched_f16 does before
@@ -895,14 +959,25 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(
     for (int u = 0; u < 8; ++u)
       yv[u] = pos[u] >= 0 ? *reinterpret_cast<const float4*>(y + static_cast<long long>(pos[u]) * hidden + i)
                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (out16) {
+      auto r16 = [](float v) { return f16v(f16b(v)); };
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (k0 + u == k) {
-        yv[u].x *= gs;
-        yv[u].y *= gs;
-        yv[u].z *= gs;
-        yv[u].w *= gs;
+      for (int u = 0; u < 8; ++u) {
+        yv[u] = make_float4(r16(yv[u].x), r16(yv[u].y), r16(yv[u].z), r16(yv[u].w));
+        if (k0 + u == k)
+          yv[u] = make_float4(r16(yv[u].x * gs), r16(yv[u].y * gs), r16(yv[u].z * gs),
+                              r16(yv[u].w * gs));
       }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u == k) {
+          yv[u].x *= gs;
+          yv[u].y *= gs;
+          yv[u].z *= gs;
+          yv[u].w *= gs;
+        }
+    }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       if (k0 + u <= k) {
@@ -913,22 +988,28 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(
       }
     }
   }
-  *reinterpret_cast<float4*>(out + o) = acc;
+  if (out16) {
+    *reinterpret_cast<uint2*>(out16 + o) =
+        make_uint2(f16b(acc.x) | (static_cast<uint32_t>(f16b(acc.y)) << 16),
+                   f16b(acc.z) | (static_cast<uint32_t>(f16b(acc.w)) << 16));
+  } else {
+    *reinterpret_cast<float4*>(out + o) = acc;
+  }
 }
 
 // sgate[t] = sigmoid(w . x[t]): the shared expert's scalar gate
 // (session.cpp:2904-2909, gemv_f32_out_f16x_batched then
 // sigmoid_gate_scalar_batched_f16), one token per 32-lane half-wave in the
 // reference's fp32 lane order.
-__global__ void __launch_bounds__(256) shared_gate_kernel(const float* __restrict__ w,
-                                                          const float* __restrict__ x,
+__global__ void __launch_bounds__(256) shared_gate_kernel(const float* __restrict__ w, XSrc x,
                                                           float* __restrict__ sgate, int n_tokens,
                                                           int hidden) {
   const int l = threadIdx.x & 31;
   const int t0 = blockIdx.x * 8 + (threadIdx.x >> 5);
   const int t = t0 < n_tokens ? t0 : n_tokens - 1;  // whole halves stay active for the shuffles
-  const float* xt = x + static_cast<long long>(t) * hidden;
-  const float g = rowdot_f32_lanes32(w, [&](int i) { return xt[i]; }, hidden, l);
+  const long long o = static_cast<long long>(t) * hidden;
+  const float g = x.f16 ? rowdot_f32_lanes32(w, [&](int i) { return f16v(x.f16[o + i]); }, hidden, l)
+                        : rowdot_f32_lanes32(w, [&](int i) { return x.f32[o + i]; }, hidden, l);
   if (l == 0 && t0 < n_tokens) sgate[t0] = sigmoid_sg(g);
 }
 
@@ -1099,15 +1180,26 @@ size_t sg_moe_prefill_workspace_bytes(int n_tokens, int hidden, int n_ff, int n_
   return prefill_ws(n_tokens, hidden, n_ff, n_expert, k).total;
 }
 
-int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
-                   const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
-                   const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
-                   const float* sh_gate_w, const float* x, const float* logits,
-                   const float* residual, float* out, int* idx, float* weight, void* workspace,
-                   size_t workspace_bytes, int n_tokens, int hidden, int n_ff, int n_expert, int k,
-                   float shared_w, void* stream) {
-  const char* nm = "sg_moe_prefill";
-  if (!tab_gate || !tab_up || !tab_down || !x || !out || !idx || !weight || !workspace)
+}  // extern "C"
+
+namespace sg {
+
+// the chunk's output: fp32 (residual, out) or the session's fp16 buffers
+struct PrefillOut {
+  const float* residual;
+  float* out;
+  const uint16_t* res16;
+  uint16_t* out16;
+};
+
+static int prefill_launch(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
+                          const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
+                          const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
+                          const float* sh_gate_w, const XSrc& x, const float* logits,
+                          const PrefillOut& po, int* idx, float* weight, void* workspace,
+                          size_t workspace_bytes, int n_tokens, int hidden, int n_ff, int n_expert,
+                          int k, float shared_w, void* stream, const char* nm) {
+  if (!tab_gate || !tab_up || !tab_down || !idx || !weight || !workspace)
     return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
   const int n_sh = (sh_gate != nullptr) + (sh_up != nullptr) + (sh_down != nullptr);
   if (n_sh != 0 && n_sh != 3)
@@ -1152,7 +1244,10 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
     else launch(route_quantize_kernel<8>);
     if (int st = check_launch("sg_moe_prefill/route_quantize")) return st;
   } else {
-    if (int st = quantize_split(x, xq, hidden / kQK, n_tokens, s, nm)) return st;
+    const long long nxb = static_cast<long long>(hidden / kQK) * n_tokens;
+    hipLaunchKernelGGL(prefill_x_kernel, dim3(static_cast<unsigned>((nxb + 15) / 16)), dim3(256),
+                       0, s, x, xq, nxb);
+    if (int st = check_launch(nm)) return st;
     if (logits)
       if (int st = sg_router_topk(logits, idx, weight, n_expert, k, k + 1, n_tokens, shared_w,
                                   stream))
@@ -1211,8 +1306,47 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* cons
                        dim3(kThreads), kGroupedLds, s, gd);
   if (int st = check_launch("sg_moe_prefill/down")) return st;
   hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 1023) / 1024 * n_tokens), dim3(256), 0, s,
-                     out, residual, y, weight, gslot, off, sgate, n_expert, k, hidden, has_shared);
+                     po.out, po.residual, po.out16, po.res16, y, weight, gslot, off, sgate,
+                     n_expert, k, hidden, has_shared);
   return check_launch("sg_moe_prefill/combine");
+}
+
+}  // namespace sg
+
+extern "C" {
+
+int sg_moe_prefill(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
+                   const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
+                   const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
+                   const float* sh_gate_w, const float* x, const float* logits,
+                   const float* residual, float* out, int* idx, float* weight, void* workspace,
+                   size_t workspace_bytes, int n_tokens, int hidden, int n_ff, int n_expert, int k,
+                   float shared_w, void* stream) {
+  const char* nm = "sg_moe_prefill";
+  if (!x || !out) return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  return prefill_launch(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w,
+                        XSrc{x, nullptr, nullptr}, logits,
+                        PrefillOut{residual, out, nullptr, nullptr}, idx, weight, workspace,
+                        workspace_bytes, n_tokens, hidden, n_ff, n_expert, k, shared_w, stream,
+                        nm);
+}
+
+int sg_moe_prefill_f16(const sg_block_q4k* const* tab_gate, const sg_block_q4k* const* tab_up,
+                       const sg_block_q4k* const* tab_down, const sg_block_q4k* sh_gate,
+                       const sg_block_q4k* sh_up, const sg_block_q4k* sh_down,
+                       const float* sh_gate_w, const uint16_t* xn, const sg_block_q8k* xq,
+                       const float* logits, const uint16_t* residual, uint16_t* out, int* idx,
+                       float* weight, void* workspace, size_t workspace_bytes, int n_tokens,
+                       int hidden, int n_ff, int n_expert, int k, float shared_w, void* stream) {
+  const char* nm = "sg_moe_prefill_f16";
+  if ((!xn && !xq) || !out) return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  if (!xn && sh_gate_w && sh_gate && sh_up && sh_down)
+    return set_error(SG_ERR_INVALID_ARGUMENT, "%s: the shared gate needs xn", nm);
+  return prefill_launch(tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down, sh_gate_w,
+                        XSrc{nullptr, xn, reinterpret_cast<const unsigned char*>(xq)}, logits,
+                        PrefillOut{nullptr, nullptr, residual, out}, idx, weight, workspace,
+                        workspace_bytes, n_tokens, hidden, n_ff, n_expert, k, shared_w, stream,
+                        nm);
 }
 
 }  // extern "C"

@@ -312,6 +312,45 @@ class MoeLayer:
             self.n_expert, self.k, self.shared_w, stages, _stream()))
         return out, idx, weight
 
+    _F16_ENTRY = "sg_moe_layer_f16"
+
+    def forward_f16(self, xn=None, xq=None, logits=None, residual=None, out=None, idx=None,
+                    weight=None, workspace=None):
+        """The layer on the session's fp16 buffers (sg_moe_layer_f16 /
+        sg_moe_prefill_f16): xn fp16 [T, hidden] and/or xq, a Q8_K of it
+        (uint8 [T, hidden/256*276], used as is); residual/out fp16 [T, hidden]
+        (may be the same tensor)."""
+        src = xn if xn is not None else xq
+        if src is None:
+            raise SagerError("forward_f16 needs xn or xq")
+        T = src.shape[0]
+        if T > self.max_tokens:
+            raise SagerError(f"{T} tokens > max_tokens={self.max_tokens}")
+        if xn is not None:
+            _dtypes(self._F16_ENTRY, xn=(xn, torch.float16))
+        if xq is not None:
+            _dtypes(self._F16_ENTRY, xq=(xq, torch.uint8))
+            if xq.numel() != T * (self.hidden // QK) * Q8K_BYTES:
+                raise SagerError("xq must hold T x hidden/256 Q8_K blocks")
+        dev = src.device
+        if out is None:
+            out = torch.empty((T, self.hidden), dtype=torch.float16, device=dev)
+        _dtypes(self._F16_ENTRY, out=(out, torch.float16))
+        if residual is not None:
+            _dtypes(self._F16_ENTRY, residual=(residual, torch.float16))
+        if idx is None:
+            idx = torch.full((T, self.k + 1), -1, dtype=torch.int32, device=dev)
+        if weight is None:
+            weight = torch.zeros((T, self.k + 1), dtype=torch.float32, device=dev)
+        sg, su, sd = self.shared if self.shared is not None else (None, None, None)
+        ws = self.workspace if workspace is None else workspace
+        _check(getattr(load(), self._F16_ENTRY)(
+            _ptr(self.tab_gate), _ptr(self.tab_up), _ptr(self.tab_down), _ptr(sg), _ptr(su),
+            _ptr(sd), _ptr(self.shared_gate_w), _ptr(xn), _ptr(xq), _ptr(logits),
+            _ptr(residual), _ptr(out), _ptr(idx), _ptr(weight), _ptr(ws), ws.numel(), T,
+            self.hidden, self.n_ff, self.n_expert, self.k, self.shared_w, _stream()))
+        return out, idx, weight
+
 
 def moe_dispatch_scan(idx, weight, n_expert, k, tok_per=64):
     """cuda::moe_dispatch_scan (cuda_ops.hpp:219-222) on the device: returns
@@ -355,6 +394,8 @@ def moe_dispatch_plan(idx, weight, n_expert, k, tok_per=64, shared_tail=0, tiles
 class MoePrefill(MoeLayer):
     """The same layer for a prefill chunk of up to max_tokens tokens: the
     device plan and int8-MFMA grouped contractions (sg_moe_prefill)."""
+
+    _F16_ENTRY = "sg_moe_prefill_f16"
 
     def __init__(self, tab_gate, tab_up, tab_down, shared=None, hidden=2048, n_ff=512,
                  n_expert=256, k=8, max_tokens=2048, shared_w=1.0, shared_gate_w=None):

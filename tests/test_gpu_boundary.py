@@ -288,3 +288,26 @@ def test_dispatch_plan_duplicate_ids_serial(n_rows):
     idx[50, 2] = 999
     w = rng.uniform(0, 1, (n_rows, k + 1)).astype(np.float32)
     _check_plan(idx, w, E, k, 16)
+
+
+# ---- the fp16-buffer entry points: argument checks -------------------------
+
+def test_layer_f16_argument_errors():
+    rng = np.random.default_rng(7)
+    H, F, E, K = 512, 256, 8, 2
+    g, u, d = _pool(rng, E + 1, H, F)
+    shared = (g.pop(), u.pop(), d.pop())
+    gw = rng.normal(0, 0.03, H).astype(np.float32)
+    layer = _build(ops.MoeLayer, g, u, d, shared, gw, H, F, K, 1)
+    xn = dev(rng.normal(0, 1, (1, H)).astype(np.float16))
+    xq = ops.quantize_q8_k(xn)
+    lg = dev(rng.normal(0, 1, (1, E)).astype(np.float32))
+    with pytest.raises(ops.SagerError, match="shared gate needs xn"):
+        layer.forward_f16(None, xq, lg)
+    with pytest.raises(ops.SagerError, match="must be torch.float16"):
+        layer.forward_f16(xn.float(), None, lg)
+    # with the gate off, the Q8_K alone is enough, and equals xn alone
+    layer.shared_gate_w = None
+    o1, _, _ = layer.forward_f16(None, xq, lg)
+    o2, _, _ = layer.forward_f16(xn, None, lg)
+    np.testing.assert_array_equal(host(o1).view(np.uint16), host(o2).view(np.uint16))

@@ -134,3 +134,68 @@ def test_shared_gate_model_shape(pool, T):
         ref0, _, _ = orc.moe_layer(pool["g"], pool["u"], pool["d"], pool["sh"], x, logits=lg,
                                    residual=res, hidden=H, n_ff=F, k=K, n_threads=4)
         assert not np.array_equal(ref0, ref)  # the gate changed the result
+
+
+# ---- the session's fp16 buffers (sg_moe_layer_f16 / sg_moe_prefill_f16) ----
+
+def _f16_case(rng, T, sigma):
+    xn = rng.normal(0, 1, (T, H)).astype(np.float16)
+    lg = rng.normal(0, sigma, (T, E)).astype(np.float32)
+    res = rng.normal(0, 1, (T, H)).astype(np.float16)
+    return xn, lg, res
+
+
+@pytest.mark.parametrize("T,mode", [(1, "xn"), (1, "xq"), (1, "both+gate"),
+                                    (4, "xn"), (4, "xq"), (4, "both+gate")])
+def test_layer_f16_session_buffers(pool, T, mode):
+    """Config 2 (T = 1) and config 3 (T = 4, N(0, 1.5) logits) through the
+    fp16-buffer entry: xn alone, the caller's Q8_K alone (no gate), or both
+    with the shared gate and the residual combined in place (out aliases
+    residual, as x_ in the session); fp16 output bits, indices and weights
+    against the oracle's fp16-buffer layer."""
+    rng = np.random.default_rng(80 + T + len(mode))
+    gate = mode.endswith("gate")
+    gw = rng.normal(0, 0.03, H).astype(np.float32) if gate else None
+    layer = _layer(pool, T, True, gate_w=gw)
+    for step in range(2):
+        xn, lg, res = _f16_case(rng, T, 1.0 if T == 1 else 1.5)
+        xn_d = dev(xn)
+        xq_d = ops.quantize_q8_k(xn_d) if mode != "xn" else None
+        if mode == "both+gate":
+            io = dev(res)
+            out, idx, w = layer.forward_f16(xn_d, xq_d, dev(lg), residual=io, out=io)
+        else:
+            out, idx, w = layer.forward_f16(xn_d if mode == "xn" else None, xq_d, dev(lg),
+                                            residual=dev(res))
+        ref, ri, rw = orc.moe_layer_f16(pool["g"], pool["u"], pool["d"], pool["sh"], xn,
+                                        logits=lg, residual16=res, hidden=H, n_ff=F, k=K,
+                                        shared_gate_w=gw, n_threads=4)
+        np.testing.assert_array_equal(host(idx)[:, :K], ri[:, :K])
+        assert_bits(host(w), rw)
+        np.testing.assert_array_equal(host(out).view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("T,mode", [(64, "xn+gate"), (200, "xq"), (2048, "xn")])
+def test_prefill_f16_session_buffers(pool, T, mode):
+    """The prefill chunk on the session's fp16 buffers at the model shape
+    (256 experts + shared expert), up to config 5's 2048 tokens."""
+    rng = np.random.default_rng(90 + T)
+    gate = mode.endswith("gate")
+    gw = rng.normal(0, 0.03, H).astype(np.float32) if gate else None
+    p = pool["dev"]
+    pre = ops.MoePrefill(*pool["tabs"], (p[0, E], p[1, E], p[2, E]), hidden=H, n_ff=F,
+                         n_expert=E, k=K, max_tokens=T,
+                         shared_gate_w=dev(gw) if gate else None)
+    xn = rng.normal(0, 1, (T, H)).astype(np.float16)
+    lg = rng.uniform(0, 1, (T, E)).astype(np.float32)
+    res = rng.normal(0, 1, (T, H)).astype(np.float16)
+    xn_d = dev(xn)
+    xq_d = ops.quantize_q8_k(xn_d) if mode == "xq" else None
+    out, idx, w = pre.forward_f16(None if mode == "xq" else xn_d, xq_d, dev(lg),
+                                  residual=dev(res))
+    n = min(T, 96)  # tokens are independent once routed: the oracle checks the first n
+    ref, ri, _ = orc.moe_layer_f16(pool["g"], pool["u"], pool["d"], pool["sh"], xn[:n],
+                                   logits=lg[:n], residual16=res[:n], hidden=H, n_ff=F, k=K,
+                                   shared_gate_w=gw, prefill=True, n_threads=8)
+    np.testing.assert_array_equal(host(idx)[:n, :K], ri[:, :K])
+    np.testing.assert_array_equal(host(out)[:n].view(np.uint16), ref.view(np.uint16))

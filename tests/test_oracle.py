@@ -558,3 +558,65 @@ def test_moe_layer_shared_gate_is_scaled_shared_slot(prefill):
     o2, _, _ = orc.moe_layer(g[:E], u[:E], d[:E], None, x, logits=lg, hidden=H, n_ff=F, k=K,
                              prefill=prefill)
     np.testing.assert_array_equal(o1, o2)
+
+
+# ---- the session's fp16 buffers ----------------------------------------------
+
+def test_float_to_half_matches_numpy():
+    """orc_float_to_half (round to nearest even) against numpy's float16
+    conversion: the boundaries (largest half, the overflow midpoint 65520,
+    subnormal and normal ranges, ties at every mantissa position) and 4M
+    random bit patterns."""
+    edge = np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, -65520.0, 1e30, -1e30,
+                     2.0**-14, 2.0**-24, 2.0**-25, 2.0**-25 * 1.0000001, 3 * 2.0**-25,
+                     2.0**-26, 1.0 + 2.0**-11, 1.0 + 3 * 2.0**-11, 1.0 + 2.0**-11 + 2.0**-20,
+                     2049.0, 2051.0, 6.1e-5, 5.96e-8, np.inf, -np.inf], np.float32)
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0, 2**32, 1 << 22, dtype=np.uint64).astype(np.uint32)
+    x = np.concatenate([edge, bits.view(np.float32)])
+    got = orc.float_to_half(x)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    np.testing.assert_array_equal(got[~nan], ref[~nan])
+    assert (got[nan] & 0x7c00 == 0x7c00).all() and (got[nan] & 0x3ff != 0).all()
+
+
+@pytest.mark.parametrize("prefill,gate", [(False, False), (False, True), (True, True)])
+def test_moe_layer_f16_is_rounded_composition(prefill, gate):
+    """The fp16-buffer layer = the fp32 layer's slot outputs stored as fp16
+    (numpy's own conversion here), the shared slot gated on its fp16 value
+    and stored again, combined in fp32 from the fp16 residual, stored as
+    fp16."""
+    rng = np.random.default_rng(45)
+    H, F, E, K, T = 512, 256, 8, 3, 3
+    g, u, d = _experts(rng, E + 1, H, F)
+    sh = (g[E], u[E], d[E])
+    xn = rng.normal(0, 1, (T, H)).astype(np.float16)
+    lg = rng.normal(0, 1, (T, E)).astype(np.float32)
+    gw = rng.normal(0, 0.05, H).astype(np.float32) if gate else None
+    res = rng.normal(0, 1, (T, H)).astype(np.float16)
+    out, idx, w = orc.moe_layer_f16(g[:E], u[:E], d[:E], sh, xn, logits=lg, residual16=res,
+                                    hidden=H, n_ff=F, k=K, shared_gate_w=gw, prefill=prefill,
+                                    shared_w=0.5)
+    assert out.dtype == np.float16
+    x = xn.astype(np.float32)
+    xq = orc.quantize_q8_k(x)
+    gl = orc.gemv_f32_lanes(gw[None], x)[:, 0] if gate else None
+    f16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+    for t in range(T):
+        ys = []
+        for m in list(idx[t, :K]) + [None]:
+            wg, wu, wd = sh if m is None else (g[m], u[m], d[m])
+            if prefill:
+                gg = orc.gemv_int(wg, xq[t], F, H)[0]
+                uu = orc.gemv_int(wu, xq[t], F, H)[0]
+                hh = orc.quantize_q8_k(orc.silu_mul(gg, uu))
+                ys.append(f16(orc.gemv_int(wd, hh, H, F)[0]))
+            else:
+                ys.append(f16(orc.expert_ffn(wg, wu, wd, x[t], H, F)))
+        if gate:
+            ys[-1] = f16(ys[-1] * orc.sigmoid(gl[t]))
+        ref = orc.moe_combine(np.stack(ys)[None], w[t:t + 1], res[t:t + 1].astype(np.float32))
+        np.testing.assert_array_equal(out[t].view(np.uint16),
+                                      ref[0].astype(np.float16).view(np.uint16))
