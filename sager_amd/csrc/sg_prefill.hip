@@ -550,43 +550,61 @@ grouped_mfma_kernel(GroupedArgs a) {
   }  // slices
 }
 
-// ---- the dispatch scan over many workgroups (prefill path) ----------------
-// The same arrays as dispatch_scan_kernel, in three launches so that the
-// per-route work runs on many CUs:
-// 1. scan_bits_kernel: workgroup w takes the 32 tokens 32w..32w+31 and
-//    writes wbits[w][e], the bitmap of its tokens routed to expert e, plus
-//    wflags[w] = bad routes | (duplicate id in a row) << 16; bad ids get
-//    bounds-kill (weights of the row zeroed, gslot -1).
-// 2. scan_offsets_kernel (one workgroup): the expert histogram as popcounts,
-//    the exclusive scans into off/toff/meta and the tile list, and
-//    woff[w][e] = off[e] + routes of expert e in workgroups before w.  A row
-//    with a duplicated id is rare caller routing: then this workgroup places
-//    every route itself, serially in (token, slot) order, as
+// ---- the dispatch plan over many workgroups (prefill path) ------------------
+// The same arrays as dispatch_scan_kernel, in two launches:
+// 1. plan_bits_kernel: workgroup w takes the R = 32 m tokens [R w, R w + R)
+//    and writes wbits[w][e] (m words: the bitmap of its tokens routed to
+//    expert e) and wflags[w] = bad routes | (duplicate id in a row) << 16;
+//    an invalid id zeroes its row's weights (bounds-kill) and gets gslot -1;
+// 2. plan_place_kernel: every workgroup sums the popcounts of each expert's
+//    bitmap column - all of it (hist) and the part before its own tokens
+//    (pre) - takes the exclusive scans (off, toff) and places its own
+//    routes: a route of token r to expert e goes to off[e] + pre[e] + the
+//    own routes of e from tokens below r, the token order within each expert,
+//    as in the scan.  Workgroup 0 also writes off/toff/meta, the tile list
+//    and the tile records.  A row with a duplicated id (caller routing only)
+//    is placed serially in (token, slot) order by workgroup 0 alone, as
 //    dispatch_scan_kernel does.
-// 3. scan_place_kernel: a route of token r to expert e goes to
-//    woff[w][e] + the routes of e from lower tokens of the same workgroup.
-constexpr int kScanTok = 32;  // tokens per workgroup in scan_bits / scan_place
-constexpr int kScanBitsLds = 24 * 1024;  // wbits words scan_offsets_kernel copies to LDS
+constexpr int kPlanThreads = 512;
+constexpr int kPlanMaxWg = 256;   // bitmap workgroups; m grows with T beyond 256 * 32 tokens
 
-__global__ void __launch_bounds__(256) scan_bits_kernel(const int* __restrict__ idx,
-                                                        float* __restrict__ weight,
-                                                        int* __restrict__ gslot,
-                                                        uint32_t* __restrict__ wbits,
-                                                        int* __restrict__ wflags, int n_rows,
-                                                        int k, int E) {
-  __shared__ uint32_t bm[1024];
+__device__ __forceinline__ int plan_scan(int v, int* tmp, int* total) {
+  // exclusive prefix sum over the workgroup (thread order); tmp: 16 ints
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) tmp[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int w = 0; w < nw; ++w) {
+    const int t = tmp[w];
+    before += w < wave ? t : 0;
+    all += t;
+  }
+  __syncthreads();
+  *total = all;
+  return before + x - v;
+}
+
+__global__ void __launch_bounds__(kPlanThreads) plan_bits_kernel(
+    const int* __restrict__ idx, float* __restrict__ weight, int* __restrict__ gslot,
+    uint32_t* __restrict__ wbits, int* __restrict__ wflags, int n_rows, int k, int E, int m) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t pb_lds[];  // [E][m]
   __shared__ int s_bad, s_dup;
-  const int w = blockIdx.x, tid = threadIdx.x;
-  for (int e = tid; e < E; e += 256) bm[e] = 0u;
+  const int w = blockIdx.x, tid = threadIdx.x, nth = blockDim.x;
+  const int R = 32 * m, lo = w * R, hi = min(n_rows, lo + R);
+  for (int i = tid; i < E * m; i += nth) pb_lds[i] = 0u;
   if (tid == 0) {
     s_bad = 0;
     s_dup = 0;
   }
   __syncthreads();
-  const int r0 = w * kScanTok;
-  for (int i = tid; i < kScanTok * k; i += 256) {
-    const int r = r0 + i / k, kk = i % k;
-    if (r >= n_rows) break;
+  for (int i = tid; i < (hi - lo) * k; i += nth) {
+    const int r = lo + i / k, kk = i - (i / k) * k;
     const int e = idx[static_cast<long long>(r) * (k + 1) + kk];
     if (e < 0 || e >= E) {
       for (int q = 0; q <= k; ++q) weight[static_cast<long long>(r) * (k + 1) + q] = 0.f;
@@ -594,103 +612,142 @@ __global__ void __launch_bounds__(256) scan_bits_kernel(const int* __restrict__ 
       atomicAdd(&s_bad, 1);
       continue;
     }
-    const uint32_t bit = 1u << (r & 31);
-    if (atomicOr(&bm[e], bit) & bit) s_dup = 1;
+    const uint32_t bit = 1u << ((r - lo) & 31);
+    if (atomicOr(&pb_lds[e * m + ((r - lo) >> 5)], bit) & bit) s_dup = 1;
   }
   __syncthreads();
-  for (int e = tid; e < E; e += 256) wbits[static_cast<long long>(w) * E + e] = bm[e];
+  for (int i = tid; i < E * m; i += nth) wbits[static_cast<long long>(w) * E * m + i] = pb_lds[i];
   if (tid == 0) wflags[w] = s_bad | (s_dup << 16);
 }
 
-__global__ void __launch_bounds__(1024) scan_offsets_kernel(
-    const int* __restrict__ idx, const uint32_t* __restrict__ wbits, const int* __restrict__ wflags,
-    int* __restrict__ woff, int* __restrict__ gslot, int* __restrict__ grows, int* __restrict__ off,
-    int* __restrict__ toff, int* __restrict__ meta, int* __restrict__ tiles,
+// Everything a workgroup reads is issued up front, so its latency is paid
+// about once: the flags, each expert's bitmap column (up to kColWords words
+// per thread in flight), its own bitmaps (into LDS), its own routes' ids and,
+// in workgroup 0, the experts' matrix pointers.
+constexpr int kColWords = 32;  // bitmap words of one expert's column per thread
+
+__global__ void __launch_bounds__(kPlanThreads) plan_place_kernel(
+    const int* __restrict__ idx, const uint32_t* __restrict__ wbits,
+    const int* __restrict__ wflags, int* __restrict__ gslot, int* __restrict__ grows,
+    int* __restrict__ off, int* __restrict__ toff, int* __restrict__ meta, int* __restrict__ tiles,
     TileRec* __restrict__ trec, int n_rec, const sg_block_q4k* const* tab_g,
     const sg_block_q4k* const* tab_u, const sg_block_q4k* const* tab_d, const sg_block_q4k* sh_g,
-    const sg_block_q4k* sh_u, const sg_block_q4k* sh_d, int n_rows, int k, int E, int n_w,
-    int tok_per, int shared_tail) {
-  __shared__ int hist[1024], part[1024];
-  __shared__ int s_bad, s_dup, s_total;
-  extern __shared__ uint32_t wb_lds[];  // a copy of wbits when it fits (kScanBitsLds words)
-  const int tid = threadIdx.x, nth = blockDim.x;
+    const sg_block_q4k* sh_u, const sg_block_q4k* sh_d, int n_rows, int k, int E, int m,
+    int n_w, int tok_per, int shared_tail) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t pp_lds[];  // own bitmaps [E][m]
+  __shared__ int hist[1024], pre[1024], offl[1024], part[kPlanThreads];
+  __shared__ int s_bad, s_dup, s_tmp[16];
+  const int tid = threadIdx.x, nth = blockDim.x, w = blockIdx.x;
+  const int R = 32 * m, lo = w * R, hi = min(n_rows, lo + R);
+  const int nwords = n_w * m;  // words of one expert's column
+  // thread group of expert pe: tpe threads, thread pq of it words
+  // [pq * wpt, pq * wpt + wpt) of the column (kColWords at a time)
+  const int tpe = max(1, nth / E), pe = tid / tpe, pq = tid - pe * tpe;
+  const int wpt = (nwords + tpe - 1) / tpe;
+  const int j0 = min(nwords, pq * wpt), j1 = min(nwords, j0 + wpt);
+  // --- loads
+  const int f = tid < n_w ? wflags[tid] : 0;  // n_w <= kPlanMaxWg <= nth
+  const int ni = (hi - lo) * k;
+  int my_e[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {  // own routes: (hi - lo) * k <= 32 m k, usually <= 2 per thread
+    const int i = tid + q * nth;
+    const int r = lo + i / k;
+    my_e[q] = i < ni ? idx[static_cast<long long>(r) * (k + 1) + (i - (i / k) * k)] : -1;
+  }
+  for (int i = tid; i < E * m; i += nth) pp_lds[i] = wbits[static_cast<long long>(w) * E * m + i];
+  const bool recs = w == 0 && trec;
+  const sg_block_q4k* mgp[2] = {nullptr, nullptr};
+  const sg_block_q4k* mup[2] = {nullptr, nullptr};
+  const sg_block_q4k* mdp[2] = {nullptr, nullptr};
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int e = 2 * tid + q;
+    if (recs && e < E) {
+      mgp[q] = tab_g[e];
+      mup[q] = tab_u[e];
+      mdp[q] = tab_d[e];
+    }
+  }
   if (tid == 0) {
     s_bad = 0;
     s_dup = 0;
   }
-  // the bitmaps into LDS in one round of independent loads (the per-expert
-  // loops below would otherwise wait for each global load in turn)
-  // the expert's matrix pointers for its tile records, loaded now so their
-  // latency overlaps the bitmaps' (they are written at the end)
-  const sg_block_q4k* t_mg = (trec && tid < E) ? tab_g[tid] : nullptr;
-  const sg_block_q4k* t_mu = (trec && tid < E) ? tab_u[tid] : nullptr;
-  const sg_block_q4k* t_md = (trec && tid < E) ? tab_d[tid] : nullptr;
-  const int nbits = n_w * E;
-  const bool in_lds = nbits <= kScanBitsLds;
-  if (in_lds) {
-#pragma unroll 8
-    for (int i = tid; i < nbits; i += 1024) wb_lds[i] = wbits[i];
+  // experts eb + pe, nth / tpe of them per pass (E > nth: one each, several passes)
+  for (int eb = 0; eb < E; eb += nth / tpe) {
+    const int e = eb + pe;
+    int h = 0, p = 0;
+    if (e < E) {
+      for (int c0 = j0; c0 < j1; c0 += kColWords) {
+        // unconditional loads of clamped addresses (a load under a condition
+        // is issued and waited for one at a time), masked afterwards
+        uint32_t v[kColWords];
+        int jw = c0 / m, jr = c0 - jw * m;  // word c0 of the column: workgroup jw, word jr
+#pragma unroll
+        for (int u = 0; u < kColWords; ++u) {
+          v[u] = wbits[(static_cast<long long>(jw) * E + e) * m + jr];
+          if (c0 + u + 1 < j1 && ++jr == m) {  // past the end: re-read the last word
+            jr = 0;
+            ++jw;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kColWords; ++u) {
+          const int c = (c0 + u) < j1 ? __popc(v[u]) : 0;
+          h += c;
+          p += (c0 + u) < w * m ? c : 0;
+        }
+      }
+    }
+    __syncthreads();  // part[] of the previous pass consumed; s_bad, s_dup set
+    part[tid] = h;
+    __syncthreads();
+    if (pq == 0 && e < E) {
+      int hh = 0;
+      for (int j = 0; j < tpe; ++j) hh += part[tid + j];
+      hist[e] = hh;
+    }
+    __syncthreads();
+    part[tid] = p;
+    __syncthreads();
+    if (pq == 0 && e < E) {
+      int pp = 0;
+      for (int j = 0; j < tpe; ++j) pp += part[tid + j];
+      pre[e] = pp;
+    }
   }
-  const uint32_t* wbs = in_lds ? wb_lds : wbits;
+  if (f & 0xFFFF) atomicAdd(&s_bad, f & 0xFFFF);
+  if (f >> 16) s_dup = 1;
   __syncthreads();
-  for (int w = tid; w < n_w; w += nth) {
-    const int f = wflags[w];
-    if (f & 0xFFFF) atomicAdd(&s_bad, f & 0xFFFF);
-    if (f >> 16) s_dup = 1;
+  if (s_dup) {  // duplicated ids in a row: workgroup 0 does it all, serially
+    if (w != 0) return;
+    if (tid == 0) {  // the bitmaps undercount a duplicated id: count the routes
+      for (int e = 0; e < E; ++e) hist[e] = 0;
+      for (int i = 0; i < n_rows * k; ++i) {
+        const int e = idx[static_cast<long long>(i / k) * (k + 1) + i % k];
+        if (e >= 0 && e < E) ++hist[e];
+      }
+    }
+    __syncthreads();
   }
-  // thread group of expert e: tpe threads, each over a range of workgroups
-  const int tpe = max(1, nth / E);
-  const int pe = tid / tpe, pq = tid - pe * tpe;
-  const int wpt = (n_w + tpe - 1) / tpe;
-  const int pw0 = min(n_w, pq * wpt), pw1 = min(n_w, pw0 + wpt);
-  int c = 0;
-  if (pe < E)
-    for (int w = pw0; w < pw1; ++w) c += __popc(wbs[static_cast<long long>(w) * E + pe]);
-  part[tid] = c;
-  __syncthreads();
-  if (!s_dup) {
-    if (tid < E) {
-      int h = 0;
-      for (int j = 0; j < tpe; ++j) h += part[tid * tpe + j];
-      hist[tid] = h;
-    }
-  } else if (tid == 0) {  // the bitmaps undercount a duplicated id: count the routes
-    for (int e = 0; e < E; ++e) hist[e] = 0;
-    for (int i = 0; i < n_rows * k; ++i) {
-      const int e = idx[static_cast<long long>(i / k) * (k + 1) + i % k];
-      if (e >= 0 && e < E) ++hist[e];
-    }
-  }
-  __syncthreads();
-  const int my_c = c;  // this thread's popcount share (the scans below reuse part[])
-  int ph = 0;
-  {  // exclusive prefix sums over the experts (E <= 1024: one per thread)
-    const int h = tid < E ? hist[tid] : 0;
-    const int tl = (h + tok_per - 1) / tok_per;
-    int tot_h, tot_t;
-    ph = block_exclusive_scan(h, part, &tot_h);
-    const int pt = block_exclusive_scan(tl, part, &tot_t);
-    if (tid < E) {
-      off[tid] = ph;
-      toff[tid] = pt;
-    }
-    if (tid == 0) {
-      off[E] = tot_h;
-      toff[E] = tot_t;
-      off[E + 1] = tot_h + shared_tail;
-      meta[0] = tot_h;
-      meta[1] = tot_t;
-      meta[2] = s_bad;
-      s_total = tot_h;
-    }
-    if (tiles) {
-      if (tid < E)
-        for (int j = 0; j < tl; ++j) tiles[1 + pt + j] = (tid << 16) | j;
-      const int sh_t = (shared_tail + tok_per - 1) / tok_per;
-      for (int j = tid; j < sh_t; j += nth) tiles[1 + tot_t + j] = (E << 16) | j;
-      if (tid == 0) tiles[0] = tot_t + sh_t;
-    }
-    if (trec) {  // the same work list as records with the matrices, group -1 beyond it
+  int tot_h = 0, tot_t = 0;
+  {  // exclusive scans over the experts (E <= 1024: two per thread)
+    const int e0 = 2 * tid, e1 = 2 * tid + 1;
+    const int h0 = e0 < E ? hist[e0] : 0, h1 = e1 < E ? hist[e1] : 0;
+    const int t0 = (h0 + tok_per - 1) / tok_per, t1 = (h1 + tok_per - 1) / tok_per;
+    const int ph = plan_scan(h0 + h1, s_tmp, &tot_h);
+    const int pt = plan_scan(t0 + t1, s_tmp, &tot_t);
+    if (e0 < E) offl[e0] = ph;
+    if (e1 < E) offl[e1] = ph + h0;
+    if (w == 0) {
+      if (e0 < E) {
+        off[e0] = ph;
+        toff[e0] = pt;
+      }
+      if (e1 < E) {
+        off[e1] = ph + h0;
+        toff[e1] = pt + t0;
+      }
       auto put = [&](int t, int g, int p0, int p1, const sg_block_q4k* mg, const sg_block_q4k* mu,
                      const sg_block_q4k* md) {
         const bool present = mg && mu && md;
@@ -699,74 +756,73 @@ __global__ void __launch_bounds__(1024) scan_offsets_kernel(
                           present ? reinterpret_cast<unsigned long long>(mu) : 0ull,
                           present ? reinterpret_cast<unsigned long long>(md) : 0ull, 0ull};
       };
-      if (tid < E && tl > 0) {
-        for (int j = 0; j < tl; ++j)
-          put(pt + j, tid, ph + tok_per * j, min(ph + h, ph + tok_per * (j + 1)), t_mg, t_mu,
-              t_md);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {  // the tiles of experts e0 and e1
+        const int e = q ? e1 : e0, hq = q ? h1 : h0, tl = q ? t1 : t0;
+        const int pb = q ? ph + h0 : ph, tb = q ? pt + t0 : pt;
+        if (e >= E) continue;
+        if (tiles)
+          for (int j = 0; j < tl; ++j) tiles[1 + tb + j] = (e << 16) | j;
+        if (trec)
+          for (int j = 0; j < tl; ++j)
+            put(tb + j, e, pb + tok_per * j, min(pb + hq, pb + tok_per * (j + 1)), mgp[q], mup[q],
+                mdp[q]);
       }
       const int sh_t = (shared_tail + tok_per - 1) / tok_per;
-      for (int j = tid; j < sh_t; j += nth)
-        put(tot_t + j, E, tot_h + tok_per * j, min(tot_h + shared_tail, tot_h + tok_per * (j + 1)),
-            sh_g, sh_u, sh_d);
-      for (int t = tot_t + sh_t + tid; t < n_rec; t += nth)
-        trec[t] = TileRec{-1, 0, 0, 0, 0ull, 0ull, 0ull, 0ull};
-    }
-    if (tid < E) hist[tid] = ph;  // hist now holds off[e]
-  }
-  __syncthreads();
-  if (!s_dup) {
-    // woff[w][e] = off[e] + routes of e in workgroups before w: the thread's
-    // share starts after its group's lower shares
-    part[tid] = my_c;
-    __syncthreads();
-    if (pe < E) {
-      int run = hist[pe];
-      for (int j = 0; j < pq; ++j) run += part[pe * tpe + j];
-      for (int w = pw0; w < pw1; ++w) {
-        woff[static_cast<long long>(w) * E + pe] = run;
-        run += __popc(wbs[static_cast<long long>(w) * E + pe]);
+      if (tiles)
+        for (int j = tid; j < sh_t; j += nth) tiles[1 + tot_t + j] = (E << 16) | j;
+      if (trec) {
+        for (int j = tid; j < sh_t; j += nth)
+          put(tot_t + j, E, tot_h + tok_per * j,
+              min(tot_h + shared_tail, tot_h + tok_per * (j + 1)), sh_g, sh_u, sh_d);
+        for (int t = tot_t + sh_t + tid; t < n_rec; t += nth)
+          trec[t] = TileRec{-1, 0, 0, 0, 0ull, 0ull, 0ull, 0ull};
+      }
+      if (tid == 0) {
+        off[E] = tot_h;
+        toff[E] = tot_t;
+        off[E + 1] = tot_h + shared_tail;
+        meta[0] = tot_h;
+        meta[1] = tot_t;
+        meta[2] = s_bad;
+        if (tiles) tiles[0] = tot_t + sh_t;
       }
     }
-  } else if (tid == 0) {  // duplicated ids in a row: serial placement in (token, slot) order
-    for (int i = 0; i < n_rows * k; ++i) {
-      const int r = i / k, kk = i - r * k;
-      const int e = idx[static_cast<long long>(r) * (k + 1) + kk];
-      if (e < 0 || e >= E) continue;
-      const int pos = hist[e]++;
-      gslot[i] = pos;
-      grows[pos] = r;
+  }
+  __syncthreads();
+  if (s_dup) {  // workgroup 0 only: serial placement, then the shared tail
+    if (tid == 0) {
+      for (int e = 0; e < E; ++e) hist[e] = offl[e];
+      for (int i = 0; i < n_rows * k; ++i) {
+        const int r = i / k, kk = i - r * k;
+        const int e = idx[static_cast<long long>(r) * (k + 1) + kk];
+        if (e < 0 || e >= E) continue;
+        const int pos = hist[e]++;
+        gslot[i] = pos;
+        grows[pos] = r;
+      }
     }
+    for (int t = tid; t < shared_tail; t += nth) grows[tot_h + t] = t;
+    return;
   }
-  __syncthreads();
-  for (int t = tid; t < shared_tail; t += nth) grows[s_total + t] = t;
-}
-
-__global__ void __launch_bounds__(256) scan_place_kernel(const int* __restrict__ idx,
-                                                         const uint32_t* __restrict__ wbits,
-                                                         const int* __restrict__ wflags,
-                                                         const int* __restrict__ woff,
-                                                         int* __restrict__ gslot,
-                                                         int* __restrict__ grows, int n_rows,
-                                                         int k, int E, int n_w) {
-  __shared__ int s_dup;
-  const int w = blockIdx.x, tid = threadIdx.x;
-  if (tid == 0) s_dup = 0;
-  __syncthreads();
-  for (int j = tid; j < n_w; j += 256)
-    if (wflags[j] >> 16) s_dup = 1;
-  __syncthreads();
-  if (s_dup) return;  // placed serially by scan_offsets_kernel
-  const int r0 = w * kScanTok;
-  for (int i = tid; i < kScanTok * k; i += 256) {
-    const int r = r0 + i / k, kk = i % k;
-    if (r >= n_rows) break;
-    const int e = idx[static_cast<long long>(r) * (k + 1) + kk];
-    if (e < 0 || e >= E) continue;
-    const long long we = static_cast<long long>(w) * E + e;
-    const int pos = woff[we] + __popc(wbits[we] & ((1u << (r & 31)) - 1u));
-    gslot[r * k + kk] = pos;
-    grows[pos] = r;
-  }
+  // the shared expert's positions of this workgroup's tokens: t at off[E] + t
+  for (int t = lo + tid; t < min(hi, shared_tail); t += nth) grows[tot_h + t] = t;
+  // this workgroup's routes (their ids were loaded at the start)
+  auto place = [&](int i, int e) {
+    const int r = lo + i / k, kk = i - (i / k) * k;
+    if (e < 0 || e >= E) return;
+    const int d = r - lo, wi = d >> 5;
+    const uint32_t* be = pp_lds + e * m;
+    int c = offl[e] + pre[e] + __popc(be[wi] & ((1u << (d & 31)) - 1u));
+    for (int j = 0; j < wi; ++j) c += __popc(be[j]);
+    gslot[r * k + kk] = c;
+    grows[c] = r;
+  };
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    if (tid + q * nth < ni) place(tid + q * nth, my_e[q]);
+  for (int i = tid + 2 * nth; i < ni; i += nth)
+    place(i, idx[static_cast<long long>(lo + i / k) * (k + 1) + (i - (i / k) * k)]);
 }
 
 // Q8P blocks (the grouped kernels' input, see kQ8PBytes): one block per
@@ -1016,19 +1072,21 @@ __global__ void __launch_bounds__(256) shared_gate_kernel(const float* __restric
 // ---- workspace ------------------------------------------------------------------
 static size_t al256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-// scratch of the three-launch plan: wbits and woff [n_w][E], wflags [n_w]
+// the plan's workgroups (R = 32 m tokens each) and its scratch: wbits
+// [n_w][E][m], wflags [n_w]
 struct PlanWs {
-  size_t wbits, woff, wflags, total;
-  int n_w;
+  int m, n_w;
+  size_t wbits, wflags, total, lds_bits;
 };
 static PlanWs plan_ws(int n_rows, int E) {
   PlanWs p{};
-  p.n_w = (n_rows + kScanTok - 1) / kScanTok;
+  p.m = (n_rows + 32 * kPlanMaxWg - 1) / (32 * kPlanMaxWg);
+  p.n_w = (n_rows + 32 * p.m - 1) / (32 * p.m);
   size_t o = 0;
-  p.wbits = o;  o = al256(o + static_cast<size_t>(p.n_w) * E * 4);
-  p.woff = o;   o = al256(o + static_cast<size_t>(p.n_w) * E * 4);
+  p.wbits = o;  o = al256(o + static_cast<size_t>(p.n_w) * E * p.m * 4);
   p.wflags = o; o = al256(o + static_cast<size_t>(p.n_w) * 4);
   p.total = o;
+  p.lds_bits = static_cast<size_t>(E) * p.m * 4;
   return p;
 }
 
@@ -1088,7 +1146,8 @@ static int scan_launch(const int* idx, float* weight, int* gslot, int* grows, in
   return check_launch(nm);
 }
 
-// the plan over many workgroups (bits, offsets, placement) on scratch `ws`
+// the plan over many workgroups (bitmaps, then offsets and placement) on
+// scratch `ws`
 struct PlanTables {  // the matrices the tile records carry (all null: no records)
   const sg_block_q4k* const* g;
   const sg_block_q4k* const* u;
@@ -1101,25 +1160,21 @@ static int plan_launch(const int* idx, float* weight, int* gslot, int* grows, in
                        const PlanTables& pt, unsigned char* ws, int n_rows, int k, int E,
                        int tok_per, int shared_tail, hipStream_t s, const char* nm) {
   const PlanWs p = plan_ws(n_rows, E);
+  if (p.lds_bits > 128 * 1024)
+    return set_error(SG_ERR_UNSUPPORTED, "%s: n_rows=%d x n_expert=%d: plan too large", nm,
+                     n_rows, E);
   uint32_t* wbits = reinterpret_cast<uint32_t*>(ws + p.wbits);
-  int* woff = reinterpret_cast<int*>(ws + p.woff);
   int* wflags = reinterpret_cast<int*>(ws + p.wflags);
-  hipLaunchKernelGGL(scan_bits_kernel, dim3(p.n_w), dim3(256), 0, s, idx, weight, gslot, wbits,
-                     wflags, n_rows, k, E);
+  hipLaunchKernelGGL(plan_bits_kernel, dim3(p.n_w), dim3(kPlanThreads), p.lds_bits, s, idx,
+                     weight, gslot, wbits, wflags, n_rows, k, E, p.m);
   if (int st = check_launch(nm)) return st;
-  const size_t bits_lds =
-      p.n_w * E <= kScanBitsLds ? static_cast<size_t>(p.n_w) * E * 4 : 0;
-  hipLaunchKernelGGL(scan_offsets_kernel, dim3(1), dim3(1024), bits_lds, s, idx, wbits, wflags,
-                     woff, gslot, grows, off, toff, meta, tiles, trec, n_rec, pt.g, pt.u, pt.d,
-                     pt.sg, pt.su, pt.sd, n_rows, k, E, p.n_w, tok_per, shared_tail);
-  if (int st = check_launch(nm)) return st;
-  hipLaunchKernelGGL(scan_place_kernel, dim3(p.n_w), dim3(256), 0, s, idx, wbits, wflags, woff,
-                     gslot, grows, n_rows, k, E, p.n_w);
+  hipLaunchKernelGGL(plan_place_kernel, dim3(p.n_w), dim3(kPlanThreads), p.lds_bits, s, idx, wbits, wflags,
+                     gslot, grows, off, toff, meta, tiles, trec, n_rec, pt.g, pt.u, pt.d, pt.sg,
+                     pt.su, pt.sd, n_rows, k, E, p.m, p.n_w, tok_per, shared_tail);
   return check_launch(nm);
 }
 
-// limits of the three-launch plan: E <= 1024 (one LDS bitmap word per
-// expert), int route and tile indices
+// limits of the plan: E <= 1024, k <= 32, int route and tile indices
 static int plan_check(int n_rows, int k, int E, int tok_per, const char* nm) {
   if (n_rows <= 0 || k <= 0 || k > 32 || E <= 0 || E > 1024 || tok_per <= 0)
     return set_error(SG_ERR_GEOMETRY, "%s: n_rows=%d k=%d (<=32) n_expert=%d (<=1024) tok_per=%d",
@@ -1260,8 +1315,8 @@ static int prefill_launch(const sg_block_q4k* const* tab_gate, const sg_block_q4
   }
   if (int st = plan_launch(idx, weight, gslot, grows, off, toff, meta, tiles, trec, ws.max_tiles,
                            PlanTables{tab_gate, tab_up, tab_down, sh_gate, sh_up, sh_down},
-                           base + ws.plan,
-                           n_tokens, k, n_expert, kTokTile, has_shared ? n_tokens : 0, s,
+                           base + ws.plan, n_tokens, k, n_expert, kTokTile,
+                           has_shared ? n_tokens : 0, s,
                            "sg_moe_prefill/plan"))
     return st;
   const int G = n_expert + has_shared;
