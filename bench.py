@@ -110,6 +110,41 @@ def time_graph(torch, fn, reps):
     return e0.elapsed_time(e1) / reps, g
 
 
+def launch_timing(torch, fn, nbytes, n_b2b=8, reps=5, n_ev=24):
+    """One GEMV launch timed three ways, each with HIP events on the launch
+    stream:
+    - single: a graph holding one launch, replayed (each replay pays the
+      graph launch, as a lone call between host synchronizations would);
+    - back_to_back: a graph of n_b2b launches, per launch (the launch inside
+      a captured decode step: only the gap between kernels is added);
+    - kernel: events recorded between eagerly enqueued launches while the
+      queue is kept full (long kernels only: the median event-to-event span
+      is the kernel's duration plus one event).
+    Returns us and GB/s / HBM fraction of nbytes for each."""
+    single, _ = time_graph(torch, fn, 20)
+    b2b, _ = time_graph(torch, lambda: [fn() for _ in range(n_b2b)], reps)
+    b2b /= n_b2b
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev + 1)]
+    with torch.cuda.stream(s):
+        for _ in range(4):
+            fn()
+        for i in range(n_ev):
+            evs[i].record(s)
+            fn()
+        evs[n_ev].record(s)
+    torch.cuda.synchronize()
+    spans = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(n_ev))
+    kern = spans[n_ev // 2]
+
+    def rate(ms):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    return {"event_single_launch": rate(single), "event_back_to_back": rate(b2b),
+            "event_kernel": rate(kern), "algorithmic_bytes": nbytes}
+
+
 def cpu_baseline(pool_l0, xs, lgs, budget_s=8.0):
     """The AVX2 CPU oracle (restatement of expert_ffn_q4 + pool + router +
     combine) on this host: 9 expert jobs on hardware_concurrency/2 workers
@@ -236,13 +271,14 @@ def run_q6_head(torch, np, ops, gen, orc, head_rows, xq):
     log("[bench] Q6_K LM head")
     w6 = q6k_random_dev(head_rows * 8, gen)
     y6 = torch.empty(head_rows, dtype=torch.float32, device="cuda")
-    ms6, _ = time_graph(torch, lambda: ops.gemv_q6_k_q8(w6, xq, head_rows, 2048, y=y6), 20)
     q6_bytes = head_rows * 8 * 210 + 8 * 276 + head_rows * 4
+    tm6 = launch_timing(torch, lambda: ops.gemv_q6_k_q8(w6, xq, head_rows, 2048, y=y6), q6_bytes)
+    ms6 = tm6["event_back_to_back"]["us"] * 1e-3
     ref = orc.gemv_q6k(w6.cpu().numpy(), xq.cpu().numpy()[0], head_rows, 2048)
     out = {"shape": f"{head_rows}x2048 Q6_K", "us": round(ms6 * 1e3, 2),
            "gbs": round(q6_bytes / (ms6 * 1e-3) / 1e9, 1),
            "frac": round(q6_bytes / (ms6 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-           "algorithmic_bytes": q6_bytes,
+           "algorithmic_bytes": q6_bytes, "timing": tm6,
            "parity": {"bit_exact": bool((y6.cpu().numpy() == ref).all())}}
     del w6
     torch.cuda.empty_cache()
@@ -693,9 +729,10 @@ def main():
     # the same 256 matrices as ONE pointer-table launch (gemv_ptrs)
     ptrs = torch.tensor([gemv_w[j].data_ptr() for j in range(n_rot)], dtype=torch.int64,
                         device="cuda")
-    ms_ptr, _ = time_graph(torch, lambda: ops.gemv_ptrs_q4_k_q8(ptrs, xq, n_rot, 2048, 2048,
-                                                                y=ys.view(-1)), 20)
     ptr_bytes = n_rot * 2048 * 8 * 144 + 8 * 276 + n_rot * 2048 * 4
+    tm_ptr = launch_timing(torch, lambda: ops.gemv_ptrs_q4_k_q8(ptrs, xq, n_rot, 2048, 2048,
+                                                                y=ys.view(-1)), ptr_bytes)
+    ms_ptr = tm_ptr["event_back_to_back"]["us"] * 1e-3
     cpu1 = None
     if not args.no_cpu:
         log("[bench] config-1 CPU baseline")
@@ -707,8 +744,10 @@ def main():
     head_rows = 248320
     head = q4k_random_dev(head_rows * 8, gen)
     yh = torch.empty(head_rows, dtype=torch.float32, device="cuda")
-    ms_head, _ = time_graph(torch, lambda: ops.gemv_q4_k_q8(head, xq, head_rows, 2048, y=yh), 20)
     head_bytes = head_rows * 8 * 144 + 8 * 276 + head_rows * 4
+    tm_head = launch_timing(torch, lambda: ops.gemv_q4_k_q8(head, xq, head_rows, 2048, y=yh),
+                            head_bytes)
+    ms_head = tm_head["event_back_to_back"]["us"] * 1e-3
     q6_head = run_q6_head(torch, np, ops, gen, orc, head_rows, xq)
 
     # config 4: 40 layers x 256 experts (18.1 GB) resident behind the device
@@ -875,6 +914,7 @@ def main():
                          "ptr_table_256_gbs": round(ptr_bytes / (ms_ptr * 1e-3) / 1e9, 1),
                          "ptr_table_256_frac": round(ptr_bytes / (ms_ptr * 1e-3) / 1e9
                                                      / PEAK_HBM_GBS, 4),
+                         "ptr_table_256_timing": tm_ptr,
                          "gbs": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1),
                          "frac": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                          "rotation": f"{n_rot} distinct 2048x2048 matrices, graph-replayed",
@@ -882,7 +922,8 @@ def main():
         "lm_head_q6k_gemv": q6_head,
         "lm_head_gemv": {"shape": "248320x2048", "us": round(ms_head * 1e3, 2),
                          "gbs": round(head_bytes / (ms_head * 1e-3) / 1e9, 1),
-                         "frac": round(head_bytes / (ms_head * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+                         "frac": round(head_bytes / (ms_head * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                         "timing": tm_head},
     }
     print(json.dumps(res), flush=True)
     return 0

@@ -168,12 +168,18 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
-// Wait until at most n (0..9) of this wave's vector memory operations are
+// Wait until at most n (0..15) of this wave's vector memory operations are
 // outstanding: with two weight streams in flight, the older has landed once
 // only the newer one's instructions remain.
 __device__ __forceinline__ void wait_vm_n(int n) {
   switch (n) {
-    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;  // vmcnt(9)
+    case 15: __builtin_amdgcn_s_waitcnt(0x0F7F); break;  // vmcnt(15)
+    case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
+    case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
+    case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
     case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
     case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
     case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;

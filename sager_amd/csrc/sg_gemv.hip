@@ -66,11 +66,15 @@ struct SegRows {
   __device__ bool contiguous(int r0, int n) const { return seg(r0) == seg(r0 + n - 1); }
   __device__ int table_words() const { return 0; }
 };
+typedef __attribute__((address_space(3))) const unsigned long long lds_u64;
 struct TableRows {
   const sg_block_q4k* const* ptrs;
   int rows_per, nb, n_ptrs;
   int shift;  // log2(rows_per) when it is a power of two, else -1
-  const unsigned long long* lds = nullptr;
+  // the staged table, as an LDS pointer: a generic pointer would make the
+  // lookup a flat load, which joins the vector-memory queue and is waited
+  // for together with the weight copies in flight
+  lds_u64* lds = nullptr;
   __device__ int matrix(int r) const { return shift >= 0 ? r >> shift : r / rows_per; }
   __device__ const char* row(int r) const {
     const int e = matrix(r);
@@ -86,7 +90,7 @@ struct TableRows {
     for (int i = tid; i < n_ptrs; i += nthreads) d[i] = reinterpret_cast<unsigned long long>(ptrs[i]);
   }
   __device__ void attach(const uint32_t* src) {
-    if (n_ptrs <= kMaxLdsPtrs) lds = reinterpret_cast<const unsigned long long*>(src);
+    if (n_ptrs <= kMaxLdsPtrs) lds = (lds_u64*)(src);
   }
   __device__ bool contiguous(int r0, int n) const { return matrix(r0) == matrix(r0 + n - 1); }
   // LDS words the staged table occupies (2 per pointer, when it is staged)

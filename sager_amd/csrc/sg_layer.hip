@@ -258,8 +258,11 @@ __device__ __forceinline__ void team_select(const FrontLds& L, const uint64_t* k
     const bool place = kr[0] != 0 && r < m;
     if (place) wc[r] = kr[0];
     // (read through volatile: the compiler would otherwise forward this
-    // lane's own store, which another lane's may have overwritten)
-    const bool lost = place && reinterpret_cast<volatile uint64_t*>(wc)[r] != kr[0];
+    // lane's own store, which another lane's may have overwritten; and as an
+    // LDS pointer: a generic one makes it a flat load, whose wait would also
+    // drain the vector loads in flight)
+    typedef __attribute__((address_space(3))) volatile uint64_t lds_vu64;
+    const bool lost = place && ((lds_vu64*)(wc))[r] != kr[0];
     if (__ballot(lost)) {
       uint64_t* kw = reinterpret_cast<uint64_t*>(kwbase + 64 * kWaves4) + 64 * (threadIdx.x >> 6);
       kw[lane] = kr[0];

@@ -93,6 +93,18 @@ __global__ void __launch_bounds__(256) gemv_q6_kernel(const unsigned char* __res
   for (int j = 0; j < kQ6Depth - 1; ++j)
     if (g + j * NW < g_end) issue(g + j * NW, ring + j * buf_words);
 
+  // the matrix's last d sits in a dword that ends past the buffer's size
+  // when the size is 2 mod 4 (the copy then returns zeros for it): it is
+  // read from memory here, once, so that no global load joins the copies'
+  // vmcnt queue inside the loop (its wait would drain every copy in flight)
+  // (the aligned dword holding it, by a scalar load: the vector loads' queue
+  // stays the copies' alone)
+  const size_t last_off = static_cast<size_t>(last_blk) * kQ6Bytes + 208;
+  const unsigned long long last_a =
+      reinterpret_cast<unsigned long long>(w6) + (last_off & ~static_cast<size_t>(3));
+  uint32_t last_w;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(last_w) : "s"(last_a));
+  const uint32_t last_d = (last_off & 2) ? last_w >> 16 : last_w & 0xFFFFu;
   // stage x: qs words, d, and the 16 sums of 16 codes per block
   for (int i = threadIdx.x; i < nb * 65; i += blockDim.x) {
     const int b = i / 65, j = i - b * 65;
@@ -146,13 +158,8 @@ __global__ void __launch_bounds__(256) gemv_q6_kernel(const unsigned char* __res
           const u32x4 ql = *reinterpret_cast<const u32x4*>(sl + ql_w);
           const u32x4 qh = *reinterpret_cast<const u32x4*>(sl + qh_w);
           const float sc = static_cast<float>(reinterpret_cast<const int8_t*>(sl)[192 + t]);
-          // the matrix's last d sits in a dword that ends past the buffer's
-          // size when the size is 2 mod 4 (the copy then returns zeros for
-          // it): read that one from memory
           const uint32_t gblk = static_cast<uint32_t>(r0 + row) * nb + blk;
-          const uint32_t dh = gblk == last_blk
-                                  ? *reinterpret_cast<const uint16_t*>(w6 + static_cast<size_t>(gblk) * kQ6Bytes + 208)
-                                  : reinterpret_cast<const uint16_t*>(sl)[104];
+          const uint32_t dh = gblk == last_blk ? last_d : reinterpret_cast<const uint16_t*>(sl)[104];
           const uint32_t* xb = xs + blk * kQ6XWords;
           const u32x4 xv = *reinterpret_cast<const u32x4*>(xb + xw);
           int isum = 0;
