@@ -113,9 +113,9 @@ __device__ __forceinline__ void dma_rows(const Rows& rows, int r0, int n, int nb
   const int cpr = nb * 9;  // 16-B chunks per row
   if (rows.contiguous(r0, n)) {
     const char* base = rows.row(r0);
-    dma_chunks([&](int c) { return base + 16 * c; }, n * cpr, buf, lane);
+    dma_chunks<kNt>([&](int c) { return base + 16 * c; }, n * cpr, buf, lane);
   } else {
-    dma_chunks([&](int c) { return rows.row(r0 + c / cpr) + 16 * (c % cpr); }, n * cpr, buf,
+    dma_chunks<kNt>([&](int c) { return rows.row(r0 + c / cpr) + 16 * (c % cpr); }, n * cpr, buf,
                lane);
   }
 }

@@ -613,8 +613,8 @@ __device__ __forceinline__ void dma_gateup(const sg_block_q4k* wg, const sg_bloc
   const char* pg = reinterpret_cast<const char*>(wg + static_cast<long long>(row0) * nbh);
   const char* pu = reinterpret_cast<const char*>(wu + static_cast<long long>(row0) * nbh);
   const int ncg = nrw * nbh * 9;
-  dma_chunks([&](int c) { return c < ncg ? pg + 16 * c : pu + 16 * (c - ncg); }, 2 * ncg, buf,
-             lane, part, nparts);
+  dma_chunks<kNt>([&](int c) { return c < ncg ? pg + 16 * c : pu + 16 * (c - ncg); }, 2 * ncg,
+                  buf, lane, part, nparts);
 }
 
 // The lane's 16 values of x block b (16-lane row layout: lane & 15 holds
@@ -1755,7 +1755,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
           if (wd && w < cval)
             __builtin_amdgcn_global_load_lds(
                 (glb_void_p)(reinterpret_cast<const char*>(wd) + roff + 16 * w),
-                (lds_void_p)(wbuf[0] + 256 * t), 16, 0, 0);
+                (lds_void_p)(wbuf[0] + 256 * t), 16, 0, kNt);
         }
       }
     } else {
@@ -1778,7 +1778,7 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
         if (wd && w < cval)
           __builtin_amdgcn_global_load_lds(
               (glb_void_p)(reinterpret_cast<const char*>(wd) + roff + 16 * w),
-              (lds_void_p)(buf + 256 * i), 16, 0, 0);
+              (lds_void_p)(buf + 256 * i), 16, 0, kNt);
       }
     }
     if (gb == 0 && !pre) {  // Q8_K of every (token, slot) h row while the rows stream in
@@ -2006,7 +2006,7 @@ __global__ void __launch_bounds__(kBackThreads) layer_back_kernel(LayerArgs args
       if (c < total && wd && w < cval)
         __builtin_amdgcn_global_load_lds(
             (glb_void_p)(reinterpret_cast<const char*>(wd) + roff + 16 * w),
-            (lds_void_p)(wbuf[0] + 256 * t), 16, 0, 0);
+            (lds_void_p)(wbuf[0] + 256 * t), 16, 0, kNt);
     }
     if (tid == 0) meta[0] = gpre;
   }

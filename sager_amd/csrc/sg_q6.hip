@@ -84,7 +84,7 @@ __global__ void __launch_bounds__(256) gemv_q6_kernel(const unsigned char* __res
       const int c = 64 * i + lane;
       const int slot = c / kQ6SlotChunks, j = c - slot * kQ6SlotChunks;
       if (64 * i < nch && c < nch)
-        dma16(buf + 256 * i, slot * kQ6Bytes + 16 * j, rw, base);
+        dma16<true>(buf + 256 * i, slot * kQ6Bytes + 16 * j, rw, base);
     }
   };
   // instructions a copy of group gg issues (for the vmcnt waits)
