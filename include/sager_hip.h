@@ -352,8 +352,8 @@ int sg_moe_dispatch_scan(const int* idx, float* weight, int* gslot, int* grows,
                          int* off, int* toff, int* meta, int n_rows, int k,
                          int n_expert, int tok_per, void* stream);
 
-/* The same plan built by three launches over many workgroups (32 tokens
- * each: bitmaps, then one workgroup of offsets, then placement), with no
+/* The same plan built by two launches over many workgroups (32 tokens
+ * each: bitmaps, then offsets and placement), with no
  * limit on n_rows beyond int indexing; the order inside an expert is the
  * same (token, then slot), so every array equals sg_moe_dispatch_scan's.
  * It is the plan sg_moe_prefill builds.  Extra outputs:
@@ -380,8 +380,8 @@ int sg_moe_dispatch_plan(const int* idx, float* weight, int* gslot, int* grows, 
  * + SiLU and down as grouped int8-MFMA contractions over every routed expert
  * (the shared expert as one more group), combine in slot order.  Replaces
  * the reference's prefill MoE (session.cpp:2643-2840: the TC dequant+GEMM
- * path and its dp4a grouped twin, cuda_ops.hpp:190-250).  Sub-block dots are
- * exact int32 (one MFMA per Q4_K sub-block); the fp32 epilogue is the
+ * path and its dp4a grouped twin, cuda_ops.hpp:190-250).  The super-block
+ * sums are exact int32 (int8 MFMAs); the fp32 epilogue is the
  * integer-first super-block order (t = fma(d, sum sc*ip, -(dmin * sum
  * mn*bsum)), acc = fma(xd, t, acc)).  workspace: at least
  * sg_moe_prefill_workspace_bytes(). */
@@ -410,6 +410,68 @@ int sg_moe_prefill_f16(const sg_block_q4k* const* tab_gate,
                        const uint16_t* residual, uint16_t* out, int* idx, float* weight,
                        void* workspace, size_t workspace_bytes, int n_tokens, int hidden,
                        int n_ff, int n_expert, int k, float shared_w, void* stream);
+
+/* ---- stage-by-stage launchers of the grouped path ----------------------
+ * For a session that keeps the reference's own stage order (plan, gather,
+ * grouped gate+up, SiLU, Q8_K of h, grouped down, scatter, combine) instead
+ * of calling sg_moe_layer / sg_moe_prefill.  The plan arrays are
+ * sg_moe_dispatch_scan's (meta[0] = routed rows, meta[1] = tiles).  Counts
+ * decided by the plan are read on the device; r_max / rows_max / n_max /
+ * tiles_max only bound the grids.  n_rows, r_max, tiles_max <= 65535. */
+
+/* dst[r] = src[src_rows[r]], whole Q8_K rows of row_blocks blocks.
+ * Replaces cuda::gather_rows_q8 (cuda_ops.hpp:364-366, moe.cu:237-247). */
+int sg_gather_rows_q8(sg_block_q8k* dst, const sg_block_q8k* src, const int* src_rows,
+                      int n_rows, int row_blocks, void* stream);
+/* The same for r < meta[0].  Replaces cuda::gather_rows_q8_n
+ * (cuda_ops.hpp:226-228, moe.cu:446-467). */
+int sg_gather_rows_q8_n(sg_block_q8k* dst, const sg_block_q8k* src, const int* src_rows,
+                        const int* meta, int r_max, int row_blocks, void* stream);
+/* fp16 rows of hidden values, r < meta[0].  Replaces cuda::gather_rows_f16_n
+ * (cuda_ops.hpp:229-231, moe.cu:472-491). */
+int sg_gather_rows_f16_n(uint16_t* dst, const uint16_t* src, const int* src_rows,
+                         const int* meta, int r_max, int hidden, void* stream);
+/* out = f16(SiLU(g) * u) over the first d_rows[0] * n_ff values (the SiLU
+ * of sg_silu_mul_f16).  Replaces cuda::silu_mul_f16_n (cuda_ops.hpp:232-234,
+ * norm_rotary.cu:145-156). */
+int sg_silu_mul_f16_n(uint16_t* out, const uint16_t* g, const uint16_t* u, const int* d_rows,
+                      int rows_max, int n_ff, void* stream);
+/* Q8_K of the first d_rows[0] * row_mult fp16 values (row_mult a multiple of
+ * 256; n_max = the most blocks), bit-exact as sg_quantize_q8_k_f16.
+ * Replaces cuda::quantize_q8_k_n (cuda_ops.hpp:235-237, q4_k.cu:1869-1924). */
+int sg_quantize_q8_k_n(const uint16_t* x, sg_block_q8k* out, const int* d_rows, int row_mult,
+                       int n_max, void* stream);
+/* Grouped gate+up over the plan: for tile t < meta[1] (expert e = the last
+ * with toff[e] <= t, positions off[e] + (t - toff[e]) * tok_per + j, at most
+ * tok_per of them), yg[p][r] = f16(Wg_e[r] . xq[p]) and yu[p][r] likewise,
+ * rows r < n_rows, each dot in the reference CPU order (as sg_gemv_q4_k_q8)
+ * rounded once.  A null wg_tab[e] or wu_tab[e] zeroes the tile's outputs and
+ * posts e to the mailbox (mail[atomicAdd(mail_n, 1)] = e while below
+ * n_expert).  k <= 4096.  Replaces cuda::gemv_grouped2_tab_q4_k_q8_f16out_mtok
+ * (cuda_ops.hpp:240-244, q4_k.cu:666-763, 1926-1957). */
+int sg_gemv_grouped2_tab_q4_k_q8_f16out(const sg_block_q4k* const* wg_tab,
+                                        const sg_block_q4k* const* wu_tab, const int* off,
+                                        const int* toff, const int* meta, int* mail, int* mail_n,
+                                        int tiles_max, const sg_block_q8k* xq, uint16_t* yg,
+                                        uint16_t* yu, int n_rows, int k, int n_expert, int tok_per,
+                                        void* stream);
+/* The same with one matrix table (the down projection), no mailbox.
+ * Replaces cuda::gemv_grouped_tab_q4_k_q8_f16out_mtok (cuda_ops.hpp:247-250,
+ * q4_k.cu:765-836, 1959-1987). */
+int sg_gemv_grouped_tab_q4_k_q8_f16out(const sg_block_q4k* const* w_tab, const int* off,
+                                       const int* toff, const int* meta, int tiles_max,
+                                       const sg_block_q8k* xq, uint16_t* y, int n_rows, int k,
+                                       int n_expert, int tok_per, void* stream);
+/* expert_y[row][kk] = grouped_out[gslot[row*n_used + kk]] for gslot >= 0
+ * (expert_y rows of n_used + 1 slots, the last the shared expert's, left as
+ * is).  Replaces cuda::scatter_routed_f16 (cuda_ops.hpp:372-374,
+ * moe.cu:249-262). */
+int sg_scatter_routed_f16(uint16_t* expert_y, const uint16_t* grouped_out, const int* gslot,
+                          int n_rows, int n_used, int hidden, void* stream);
+/* dst[dst_rows[i]] = src[i], fp16 rows.  Replaces cuda::scatter_rows_f16
+ * (cuda_ops.hpp:408-409, moe.cu:142-156). */
+int sg_scatter_rows_f16(uint16_t* dst, const uint16_t* src, const int* dst_rows, int n_rows,
+                        int hidden, void* stream);
 
 /* ---- GGUF expert pool (load time, host + HBM) ------------------------
  * Replaces Weights::load_expert_pool (weights.cpp:800-870, over the GGUF v3

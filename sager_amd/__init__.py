@@ -60,6 +60,17 @@ SIGNATURES = {
     "sg_moe_layer_stages": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                  _VP, _VP, _SZ, _I, _I, _I, _I, _I, _F, _I, _VP]),
     "sg_moe_dispatch_scan": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
+    "sg_gather_rows_q8": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
+    "sg_gather_rows_q8_n": (_I, [_VP, _VP, _VP, _VP, _I, _I, _VP]),
+    "sg_gather_rows_f16_n": (_I, [_VP, _VP, _VP, _VP, _I, _I, _VP]),
+    "sg_silu_mul_f16_n": (_I, [_VP, _VP, _VP, _VP, _I, _I, _VP]),
+    "sg_quantize_q8_k_n": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
+    "sg_gemv_grouped2_tab_q4_k_q8_f16out": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _VP, _VP,
+                                                 _VP, _I, _I, _I, _I, _VP]),
+    "sg_gemv_grouped_tab_q4_k_q8_f16out": (_I, [_VP, _VP, _VP, _VP, _I, _VP, _VP, _I, _I, _I, _I,
+                                                _VP]),
+    "sg_scatter_routed_f16": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
+    "sg_scatter_rows_f16": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
     "sg_moe_dispatch_plan_workspace_bytes": (_SZ, [_I, _I]),
     "sg_moe_dispatch_plan": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I,
                                   _I, _I, _VP]),

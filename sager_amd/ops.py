@@ -368,6 +368,109 @@ def moe_dispatch_scan(idx, weight, n_expert, k, tok_per=64):
     return dict(gslot=gslot, grows=grows, off=off, toff=toff, meta=meta)
 
 
+# ---- stage-by-stage launchers of the grouped path (sg_stages.hip) -------------
+
+def gather_rows_q8(src, src_rows, row_blocks, meta=None, r_max=None, out=None):
+    """cuda::gather_rows_q8 / gather_rows_q8_n (cuda_ops.hpp:364-366,
+    226-228): out[r] = src[src_rows[r]] for whole Q8_K rows (uint8 tensors of
+    row_blocks*276 bytes per row); with meta, only r < meta[0] (r_max rows
+    bound the grid)."""
+    n = r_max if meta is not None else src_rows.numel()
+    if out is None:
+        out = torch.empty((n, row_blocks * Q8K_BYTES), dtype=torch.uint8, device=src.device)
+    _dtypes("gather_rows_q8", src=(src, torch.uint8), out=(out, torch.uint8),
+            src_rows=(src_rows, torch.int32))
+    if meta is None:
+        _check(load().sg_gather_rows_q8(_ptr(out), _ptr(src), _ptr(src_rows), n, row_blocks,
+                                        _stream()))
+    else:
+        _dtypes("gather_rows_q8_n", meta=(meta, torch.int32))
+        _check(load().sg_gather_rows_q8_n(_ptr(out), _ptr(src), _ptr(src_rows), _ptr(meta), n,
+                                          row_blocks, _stream()))
+    return out
+
+
+def gather_rows_f16_n(src, src_rows, meta, r_max, out=None):
+    """cuda::gather_rows_f16_n (cuda_ops.hpp:229-231): out[r] = src[src_rows[r]]
+    for r < meta[0], fp16 rows."""
+    hidden = src.shape[-1]
+    if out is None:
+        out = torch.empty((r_max, hidden), dtype=torch.float16, device=src.device)
+    _dtypes("gather_rows_f16_n", src=(src, torch.float16), out=(out, torch.float16),
+            src_rows=(src_rows, torch.int32), meta=(meta, torch.int32))
+    _check(load().sg_gather_rows_f16_n(_ptr(out), _ptr(src), _ptr(src_rows), _ptr(meta), r_max,
+                                       hidden, _stream()))
+    return out
+
+
+def silu_mul_f16_n(g, u, d_rows, out=None):
+    """cuda::silu_mul_f16_n (cuda_ops.hpp:232-234): the first d_rows[0] rows of
+    fp16 [rows_max, n_ff] buffers."""
+    if out is None:
+        out = torch.empty_like(g)
+    _dtypes("silu_mul_f16_n", g=(g, torch.float16), u=(u, torch.float16),
+            out=(out, torch.float16), d_rows=(d_rows, torch.int32))
+    n_ff = g.shape[-1]
+    _check(load().sg_silu_mul_f16_n(_ptr(out), _ptr(g), _ptr(u), _ptr(d_rows), g.numel() // n_ff,
+                                    n_ff, _stream()))
+    return out
+
+
+def quantize_q8_k_n(x, d_rows, row_mult, n_max, out=None):
+    """cuda::quantize_q8_k_n (cuda_ops.hpp:235-237): Q8_K of the first
+    d_rows[0] * row_mult fp16 values of x."""
+    if out is None:
+        out = torch.empty((n_max * Q8K_BYTES,), dtype=torch.uint8, device=x.device)
+    _dtypes("quantize_q8_k_n", x=(x, torch.float16), out=(out, torch.uint8),
+            d_rows=(d_rows, torch.int32))
+    _check(load().sg_quantize_q8_k_n(_ptr(x), _ptr(out), _ptr(d_rows), row_mult, n_max,
+                                     _stream()))
+    return out
+
+
+def gemv_grouped2_tab_q4_k_q8_f16out(wg_tab, wu_tab, plan, tiles_max, xq, n_rows, k, n_expert,
+                                     tok_per, yg, yu, mail, mail_n):
+    """cuda::gemv_grouped2_tab_q4_k_q8_f16out_mtok (cuda_ops.hpp:240-244) over
+    a moe_dispatch_scan plan; yg/yu fp16 [positions, n_rows]."""
+    _dtypes("gemv_grouped2_tab", yg=(yg, torch.float16), yu=(yu, torch.float16),
+            mail=(mail, torch.int32), mail_n=(mail_n, torch.int32), xq=(xq, torch.uint8))
+    _check(load().sg_gemv_grouped2_tab_q4_k_q8_f16out(
+        _ptr(wg_tab), _ptr(wu_tab), _ptr(plan["off"]), _ptr(plan["toff"]), _ptr(plan["meta"]),
+        _ptr(mail), _ptr(mail_n), tiles_max, _ptr(xq), _ptr(yg), _ptr(yu), n_rows, k, n_expert,
+        tok_per, _stream()))
+    return yg, yu
+
+
+def gemv_grouped_tab_q4_k_q8_f16out(w_tab, plan, tiles_max, xq, n_rows, k, n_expert, tok_per, y):
+    """cuda::gemv_grouped_tab_q4_k_q8_f16out_mtok (cuda_ops.hpp:247-250)."""
+    _dtypes("gemv_grouped_tab", y=(y, torch.float16), xq=(xq, torch.uint8))
+    _check(load().sg_gemv_grouped_tab_q4_k_q8_f16out(
+        _ptr(w_tab), _ptr(plan["off"]), _ptr(plan["toff"]), _ptr(plan["meta"]), tiles_max,
+        _ptr(xq), _ptr(y), n_rows, k, n_expert, tok_per, _stream()))
+    return y
+
+
+def scatter_routed_f16(expert_y, grouped_out, gslot, n_rows, n_used):
+    """cuda::scatter_routed_f16 (cuda_ops.hpp:372-374): expert_y fp16
+    [n_rows, n_used+1, hidden] receives grouped_out[gslot[row*n_used+kk]]."""
+    hidden = expert_y.shape[-1]
+    _dtypes("scatter_routed_f16", expert_y=(expert_y, torch.float16),
+            grouped_out=(grouped_out, torch.float16), gslot=(gslot, torch.int32))
+    _check(load().sg_scatter_routed_f16(_ptr(expert_y), _ptr(grouped_out), _ptr(gslot), n_rows,
+                                        n_used, hidden, _stream()))
+    return expert_y
+
+
+def scatter_rows_f16(dst, src, dst_rows):
+    """cuda::scatter_rows_f16 (cuda_ops.hpp:408-409): dst[dst_rows[i]] = src[i]."""
+    hidden = src.shape[-1]
+    _dtypes("scatter_rows_f16", dst=(dst, torch.float16), src=(src, torch.float16),
+            dst_rows=(dst_rows, torch.int32))
+    _check(load().sg_scatter_rows_f16(_ptr(dst), _ptr(src), _ptr(dst_rows), src.shape[0], hidden,
+                                      _stream()))
+    return dst
+
+
 def moe_dispatch_plan(idx, weight, n_expert, k, tok_per=64, shared_tail=0, tiles=True):
     """The multi-workgroup plan (sg_moe_dispatch_plan): the arrays of
     moe_dispatch_scan plus the grouped kernels' tile list; `weight` is
