@@ -182,6 +182,16 @@ int sg_moe_combine(float* out, const float* residual, const float* expert_y,
                    const float* weight, int n_used, int hidden, int n_rows,
                    void* stream);
 
+/* Router GEMV (fp32 W [n_expert][hidden] times the fp16 x of one token) and
+ * top-k in one launch: the logits bit for bit sg_gemv_f32_out_f16x's, the
+ * selection and weights sg_router_topk's; writes idx[0..k) and
+ * weight[0..k) only (the shared slot is left as it is).  Uses a file-scope
+ * device array of logits and an arrival counter per GPU: calls that overlap
+ * on one GPU race.  n_expert <= 1024, n_expert_used <= 64.  Replaces
+ * cuda::router_topk_fused (cuda_ops.hpp:173-177, mmq.cu:459-522). */
+int sg_router_topk_fused(const float* w, const uint16_t* x, int* idx, float* weight,
+                         int n_expert, int n_expert_used, int hidden, void* stream);
+
 /* ---- fp16-buffer launchers (the session loop's own buffers) ------------
  * fp16 values are IEEE binary16 bits; every conversion to fp16 rounds to
  * nearest even (__float2half), conversions to fp32 are exact. */

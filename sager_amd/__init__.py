@@ -60,6 +60,7 @@ SIGNATURES = {
     "sg_moe_layer_stages": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                  _VP, _VP, _SZ, _I, _I, _I, _I, _I, _F, _I, _VP]),
     "sg_moe_dispatch_scan": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
+    "sg_router_topk_fused": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _VP]),
     "sg_gather_rows_q8": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
     "sg_gather_rows_q8_n": (_I, [_VP, _VP, _VP, _VP, _I, _I, _VP]),
     "sg_gather_rows_f16_n": (_I, [_VP, _VP, _VP, _VP, _I, _I, _VP]),

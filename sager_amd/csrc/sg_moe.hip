@@ -124,11 +124,70 @@ __global__ void __launch_bounds__(256) gemv_f32_f16x_kernel(const float* __restr
   if (l == 0 && row < n_rows) y[t * n_rows + row] = v;
 }
 
+// Router GEMV and top-k of one token in one launch (mmq.cu:459-511): the
+// logits y[e] = W[e] . f32(x) in gemv_f32_f16x_kernel's lane order (so bit
+// for bit sg_gemv_f32_out_f16x's), eight rows per workgroup; the workgroup
+// that arrives last (a counter, no waiting) routes them with router_wave
+// (sg_router_topk's semantics) and resets the counter.  Logits and counter
+// are file-scope device arrays: one set per GPU, so calls that overlap on
+// one GPU race.  Only the k routed slots are written (the shared slot k of
+// weight is left as it is, as the reference's fused kernel does).
+__device__ float g_router_logits[kMaxExperts];
+__device__ unsigned int g_router_arrivals;
+
+template <int PL>
+__global__ void __launch_bounds__(256) router_fused_kernel(const float* __restrict__ w,
+                                                           const uint16_t* __restrict__ x,
+                                                           int* __restrict__ idx,
+                                                           float* __restrict__ weight,
+                                                           int n_expert, int k, int hidden) {
+  __shared__ __attribute__((aligned(16))) float ev[64 * PL];
+  __shared__ bool s_last;
+  const int l = threadIdx.x & 31;
+  const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int r = row < n_expert ? row : n_expert - 1;
+  const float v = rowdot_f32_lanes32(w + static_cast<long long>(r) * hidden,
+                                     [&](int i) { return f16v(x[i]); }, hidden, l);
+  if (l == 0 && row < n_expert) g_router_logits[row] = v;
+  __threadfence();  // this workgroup's logits, visible before its arrival
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = atomicAdd(&g_router_arrivals, 1u) == gridDim.x - 1;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();  // every other workgroup's logits
+  if (threadIdx.x < 64)
+    router_wave<PL>(g_router_logits, n_expert, k, 0.f, idx, weight, ev, threadIdx.x, false);
+  if (threadIdx.x == 0) atomicExch(&g_router_arrivals, 0u);  // for the next launch
+}
+
 }  // namespace sg
 
 using namespace sg;
 
 extern "C" {
+
+int sg_router_topk_fused(const float* w, const uint16_t* x, int* idx, float* weight, int n_expert,
+                         int n_expert_used, int hidden, void* stream) {
+  const char* nm = "sg_router_topk_fused";
+  if (!w || !x || !idx || !weight) return set_error(SG_ERR_INVALID_ARGUMENT, "%s: null pointer", nm);
+  if (n_expert <= 0 || n_expert > kMaxExperts || n_expert_used <= 0 ||
+      n_expert_used > n_expert || n_expert_used > 64 || hidden <= 0)
+    return set_error(SG_ERR_GEOMETRY, "%s: n_expert=%d (<=%d) n_expert_used=%d hidden=%d", nm,
+                     n_expert, kMaxExperts, n_expert_used, hidden);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((n_expert + 7) / 8);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, w, x, idx, weight, n_expert, n_expert_used,
+                       hidden);
+  };
+  if (n_expert <= 64) launch(router_fused_kernel<1>);
+  else if (n_expert <= 128) launch(router_fused_kernel<2>);
+  else if (n_expert <= 256) launch(router_fused_kernel<4>);
+  else if (n_expert <= 512) launch(router_fused_kernel<8>);
+  else launch(router_fused_kernel<16>);
+  return check_launch(nm);
+}
 
 
 int sg_router_topk(const float* logits, int* idx, float* weight, int n_expert, int n_expert_used,

@@ -135,7 +135,7 @@ __device__ __forceinline__ float serial_sum(const float* x, int n32) {
 // (n_expert <= 64 PL).
 template <int PL>
 __device__ __forceinline__ void router_wave(const float* __restrict__ lg, int n_expert, int k, float shared_w,
-                            int* oi, float* ow, float* ev, int lane) {
+                            int* oi, float* ow, float* ev, int lane, bool shared_slot = true) {
   constexpr int kPerLane = PL;
   float p[kPerLane];
   float mx = -1e30f;
@@ -214,7 +214,7 @@ __device__ __forceinline__ void router_wave(const float* __restrict__ lg, int n_
     oi[lane] = my_i;
     ow[lane] = wsum > 0.f ? my_w / wsum : my_w;
   }
-  if (lane == 0) ow[k] = shared_w;
+  if (lane == 0 && shared_slot) ow[k] = shared_w;
 }
 
 }  // namespace sg

@@ -368,6 +368,22 @@ def moe_dispatch_scan(idx, weight, n_expert, k, tok_per=64):
     return dict(gslot=gslot, grows=grows, off=off, toff=toff, meta=meta)
 
 
+def router_topk_fused(w, x, k, idx=None, weight=None):
+    """cuda::router_topk_fused (cuda_ops.hpp:173-177): the router GEMV of one
+    fp16 token x [hidden] with fp32 W [n_expert, hidden] and its top-k in one
+    launch; idx/weight rows of k+1 slots (the shared slot is not written)."""
+    n_expert, hidden = w.shape
+    if idx is None:
+        idx = torch.full((k + 1,), -1, dtype=torch.int32, device=w.device)
+    if weight is None:
+        weight = torch.zeros(k + 1, dtype=torch.float32, device=w.device)
+    _dtypes("router_topk_fused", w=(w, torch.float32), x=(x, torch.float16),
+            idx=(idx, torch.int32), weight=(weight, torch.float32))
+    _check(load().sg_router_topk_fused(_ptr(w), _ptr(x), _ptr(idx), _ptr(weight), n_expert, k,
+                                       hidden, _stream()))
+    return idx, weight
+
+
 # ---- stage-by-stage launchers of the grouped path (sg_stages.hip) -------------
 
 def gather_rows_q8(src, src_rows, row_blocks, meta=None, r_max=None, out=None):

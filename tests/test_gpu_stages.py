@@ -179,3 +179,30 @@ def test_grouped_tab_gemvs_over_plan(hidden, n_ff, tok_per):
             continue
         rd = orc.float_to_half(orc.gemv(down[e], hq_h[p0:p1], hidden, n_ff, p1 - p0))
         np.testing.assert_array_equal(y_h[p0:p1].view(np.uint16), rd, err_msg=f"down e={e}")
+
+
+@pytest.mark.parametrize("n_expert,k,hidden", [(256, 8, 2048), (64, 4, 512), (1000, 8, 256)])
+def test_router_topk_fused(n_expert, k, hidden):
+    """Router GEMV + top-k in one launch against the two launches it fuses
+    (sg_gemv_f32_out_f16x, sg_router_topk) and the oracle; three calls in a
+    row (the arrival counter resets itself), the shared slot untouched."""
+    rng = np.random.default_rng(n_expert + k)
+    w = rng.normal(0, 0.05, (n_expert, hidden)).astype(np.float32)
+    wd = dev(w)
+    for call in range(3):
+        x = rng.normal(0, 1, hidden).astype(np.float16)
+        xd = dev(x)
+        idx = torch.full((k + 1,), -7, dtype=torch.int32, device="cuda")
+        wt = torch.full((k + 1,), 5.0, dtype=torch.float32, device="cuda")
+        ops.router_topk_fused(wd, xd, k, idx=idx, weight=wt)
+        lg = ops.gemv_f32_out_f16x(wd, xd.reshape(1, -1))
+        i2, w2 = ops.router_topk(lg[0], k, shared_w=0.25)
+        got_i, got_w = host(idx), host(wt)
+        np.testing.assert_array_equal(got_i[:k], host(i2)[:k], err_msg=f"call {call}")
+        np.testing.assert_array_equal(got_w[:k].view(np.uint32), host(w2)[:k].view(np.uint32))
+        assert got_i[k] == -7 and got_w[k] == 5.0
+        ref_lg = orc.gemv_f32_lanes(w, x.astype(np.float32))
+        np.testing.assert_array_equal(host(lg).view(np.uint32), ref_lg.view(np.uint32))
+        ri, rw = orc.router_topk(ref_lg, k)
+        np.testing.assert_array_equal(got_i[:k], ri[0, :k])
+        np.testing.assert_array_equal(got_w[:k].view(np.uint32), rw[0, :k].view(np.uint32))
