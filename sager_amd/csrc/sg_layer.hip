@@ -1737,6 +1737,106 @@ __device__ __forceinline__ void back_core(const LayerArgs& a, const BackLds& L, 
   // one pass with every buffer packed end to end: the copies are dealt to
   // all waves rather than issued by the waves that will read them
   const bool spread = G <= nbw * gpw && gpw * gwords == 64 * 36;
+  // The packed one-pass layout with every group in one pass (the one-token
+  // model shape): each super-block dot is split over two lanes, so that the
+  // dots of the G groups spread over 16 G lanes (up to eight waves) instead
+  // of 8 G.  Lane (rr, blk, hf) of a 32-lane group computes sub-blocks
+  // 4 hf .. 4 hf + 3 of row rr's block blk; the block's fp32 chain (sum =
+  // fma(xd, t_s, sum), s = 0..7) runs over lane hf = 0 and then, one DPP
+  // shift later, lane hf = 1; the row's block sums are added in block order
+  // one more shift later (row_sum_last's order).  The same operations as the
+  // one-lane form, so the same bits.
+  if (pre && spread && NBF == 2 && G <= 2 * kBackWaves) {
+    const int gq = 2 * wave + (lane >> 5);
+    const int rr2 = (lane >> 2) & 7, blk2 = (lane >> 1) & 1, hf = lane & 1;
+    const bool has = gq < G && rr2 < rows;
+    const bool present = has && wdown[gq] != 0ull;
+    const bool live = present && rr2 < nr;
+    const uint32_t* wb = wbuf[0] + gq * gwords + 36 * (rr2 * 2 + blk2);
+    uint32_t wq[16];
+    uint32_t dd = 0;
+    ScaleMins sm8{};
+    if (live) {
+      const u32x4* w4 = reinterpret_cast<const u32x4*>(wb);
+      const u32x4 hd = w4[0];
+      dd = hd.x;
+      sm8 = unpack_scales(hd.y, hd.z, hd.w);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 v = w4[1 + 4 * hf + i];
+        wq[4 * i] = v.x;
+        wq[4 * i + 1] = v.y;
+        wq[4 * i + 2] = v.z;
+        wq[4 * i + 3] = v.w;
+      }
+    }
+    const float d = half_bits_to_float(dd & 0xFFFFu);
+    const float dmin = half_bits_to_float(dd >> 16);
+    const int jb = has ? min(max(off[gq], 0), a.emax) : 0;
+    const int je = has ? min(max(off[gq + 1], jb), a.emax) : 0;
+    const int cnt = wave_max_i32(je - jb);
+    for (int ji = 0; ji < cnt; ++ji) {
+      const int j = jb + ji;
+      const bool ok = j < je;
+      const int hs = ok ? tok[j] * stride + slot[j] : 0;
+      float part = 0.f;  // hf = 0: the chain of sub-blocks 0..3 from 0
+      float tv[4] = {0.f, 0.f, 0.f, 0.f};
+      float xd = 0.f;
+      if (live && ok) {
+        const uint32_t* xb = hq + (hs * 2 + blk2) * kXStride;
+        const u32x4* x4 = reinterpret_cast<const u32x4*>(xb + 32 * hf);
+        int32_t xw[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const u32x4 v = x4[i];
+          xw[4 * i] = static_cast<int32_t>(v.x);
+          xw[4 * i + 1] = static_cast<int32_t>(v.y);
+          xw[4 * i + 2] = static_cast<int32_t>(v.z);
+          xw[4 * i + 3] = static_cast<int32_t>(v.w);
+        }
+        xd = __builtin_bit_cast(float, xb[64]);
+        int32_t ip[4];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {  // sub-block group 2 hf + g: sub-blocks 4 hf + 2g, + 1
+          int32_t lo = 0, hi = 0;
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) {
+            const uint32_t w = wq[8 * g + jj];
+            lo = __builtin_amdgcn_sdot4(static_cast<int>(w & 0x0F0F0F0Fu), xw[16 * g + jj], lo,
+                                        false);
+            hi = __builtin_amdgcn_sdot4(static_cast<int>((w >> 4) & 0x0F0F0F0Fu),
+                                        xw[16 * g + 8 + jj], hi, false);
+          }
+          ip[2 * g] = lo;
+          ip[2 * g + 1] = hi;
+        }
+        const uint32_t scw = hf ? sm8.sc_hi : sm8.sc_lo;
+        const uint32_t mnw = hf ? sm8.mn_hi : sm8.mn_lo;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const float sd = d * byte_f(scw, s4);
+          const float smv = dmin * byte_f(mnw, s4);
+          const float bs = __builtin_bit_cast(float, xb[65 + 4 * hf + s4]);
+          tv[s4] = __builtin_fmaf(sd, static_cast<float>(ip[s4]), -(smv * bs));
+        }
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) part = __builtin_fmaf(xd, tv[s4], part);
+      }
+      // hf = 1 continues the chain from lane hf = 0's partial sum
+      const float prev = dpp_f<0x111>(part);  // row_shr:1 (lane - 1, within 16-lane rows)
+      float bsum = part;
+      if (hf == 1) {
+        bsum = prev;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) bsum = __builtin_fmaf(xd, tv[s4], bsum);
+      }
+      // row sum in block order: 0 + block 0, then + block 1 (lanes hf = 1)
+      const float acc0 = 0.f + bsum;
+      const float prev2 = dpp_f<0x112>(acc0);  // row_shr:2: block 0's lane to block 1's
+      const float acc = blk2 == 1 ? prev2 + bsum : acc0;
+      if (ok && has && hf == 1 && blk2 == 1 && rr2 < nr) ys[hs * rows + rr2] = present ? acc : 0.f;
+    }
+  } else
   for (int gb = 0; gb < G; gb += nbw * gpw) {
     if (spread) {
       // every group's down rows as one run of 16-B chunks over all the
