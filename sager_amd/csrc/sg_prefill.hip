@@ -271,6 +271,7 @@ struct GroupedArgs {
   const TileRec* trec;      // work list: one record per tile, group -1 past it
   int n_rec;                // records in trec
   float* out;               // [P][n_out]: h (gate/up pass) or y (down)
+  uint16_t* out16;          // [P][n_out] fp16 y (the down pass's kF16Out instances)
   int nb;                   // super-blocks per weight row
   int n_rows;               // rows of each weight matrix
   int n_out;                // output row stride (= n_rows)
@@ -286,9 +287,12 @@ struct GroupedArgs {
 // XCD x's j-th workgroup takes tile x + 8 (j / S), slice j % S.  The tile's
 // token rows are then fetched from HBM once and served to its other slices
 // from that XCD's L2.
-template <bool kGateUp, bool kMulti = false>
+// kF16Out (down pass): y is stored rounded to fp16 in out16, the form the
+// session's fp16 combine reads it in (its f16out GEMVs, moe.cu:265-292).
+template <bool kGateUp, bool kMulti = false, bool kF16Out = false>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
 grouped_mfma_kernel(GroupedArgs a) {
+  static_assert(!(kGateUp && kF16Out), "h stays fp32 (it is quantized next)");
   extern __shared__ __attribute__((aligned(16))) uint32_t gl_lds[];
   uint32_t* wbuf0 = gl_lds;
   uint32_t* xbuf0 = gl_lds + kWBufWords;
@@ -317,7 +321,10 @@ grouped_mfma_kernel(GroupedArgs a) {
 
   if (!ma) {  // absent expert (a null gate, up or down matrix): its outputs are zero
     for (long long p = p0; p < p1; ++p)
-      for (int r = tid; r < spw * kCols; r += kThreads) a.out[p * a.n_out + c0 + r] = 0.f;
+      for (int r = tid; r < spw * kCols; r += kThreads) {
+        if (kF16Out) a.out16[p * a.n_out + c0 + r] = 0;
+        else a.out[p * a.n_out + c0 + r] = 0.f;
+      }
     return;
   }
 
@@ -537,13 +544,18 @@ grouped_mfma_kernel(GroupedArgs a) {
     int tl0 = t0 + 4 * lq;
     asm volatile("" : "+v"(tl0));
     float* ob = a.out + c0 + 16 * wave + lr;
+    uint16_t* ob16 = a.out16 + c0 + 16 * wave + lr;
 #pragma unroll
     for (int ti = 0; ti < kTokBlocks; ++ti) {
       if (ti >= ntb) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tt = 16 * ti + 4 * lq + i;
-        if (tt < nt) ob[static_cast<long long>(tl0 + 16 * ti + i) * a.n_out] = acc[ti][i];
+        if (tt < nt) {
+          const long long o = static_cast<long long>(tl0 + 16 * ti + i) * a.n_out;
+          if (kF16Out) ob16[o] = f16b(acc[ti][i]);
+          else ob[o] = acc[ti][i];
+        }
       }
     }
   }
@@ -947,24 +959,28 @@ __global__ void __launch_bounds__(256) prefill_x_kernel(XSrc x, unsigned char* _
   x_block_q8p(x, out, n_blocks, blk, lane);
 }
 
-// The prefill's first launch: one-wave workgroups 0 .. n_rows - 1 route one
-// token each (router_wave, the standalone router's routine) and the
-// following ones quantize four blocks of x each, so the router's chains and
-// the quantization share one launch.
+// The prefill's first launch: four-wave workgroups.  The first
+// ceil(n_rows / 4) route one token per wave (router_wave, the standalone
+// router's routine); the following ones quantize four blocks of x per wave,
+// so the router's chains and the quantization share one launch.
+constexpr int kRqWaves = 4;
 template <int PL>
-__global__ void __launch_bounds__(64) route_quantize_kernel(
+__global__ void __launch_bounds__(64 * kRqWaves) route_quantize_kernel(
     const float* __restrict__ logits, int* __restrict__ idx, float* __restrict__ weight,
     int n_rows, int n_expert, int k, float shared_w, XSrc x, unsigned char* __restrict__ xq,
     long long n_blocks) {
-  __shared__ __attribute__((aligned(16))) float ev[64 * PL];
-  const int lane = threadIdx.x;
-  const long long w = blockIdx.x;
-  if (w < n_rows) {
-    router_wave<PL>(logits + w * n_expert, n_expert, k, shared_w, idx + w * (k + 1),
-                    weight + w * (k + 1), ev, lane);
+  __shared__ __attribute__((aligned(16))) float ev[kRqWaves][64 * PL];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n_rwg = (n_rows + kRqWaves - 1) / kRqWaves;  // routing workgroups
+  if (static_cast<int>(blockIdx.x) < n_rwg) {
+    const long long w = static_cast<long long>(blockIdx.x) * kRqWaves + wave;
+    if (w < n_rows)
+      router_wave<PL>(logits + w * n_expert, n_expert, k, shared_w, idx + w * (k + 1),
+                      weight + w * (k + 1), ev[wave], lane);
     return;
   }
-  x_block_q8p(x, xq, n_blocks, (w - n_rows) * 4 + (lane >> 4), lane);
+  const long long qw = (static_cast<long long>(blockIdx.x) - n_rwg) * kRqWaves + wave;
+  x_block_q8p(x, xq, n_blocks, qw * 4 + (lane >> 4), lane);
 }
 
 // out[t] = residual[t] + sum_kk fma(w[t][kk], y[pos(t, kk)]) in slot order;
@@ -976,10 +992,12 @@ __global__ void __launch_bounds__(64) route_quantize_kernel(
 // With out16 (the session's fp16 buffers) the slot outputs are taken as
 // stored in fp16, the shared one gated on its fp16 value and stored again,
 // the accumulation starts from the fp16 res16 and the sum is stored as fp16
-// (sigmoid_gate_scalar_batched_f16, moe_combine_batched_f16: moe.cu:265-292).
+// (sigmoid_gate_scalar_batched_f16, moe_combine_batched_f16: moe.cu:265-292);
+// the down pass then stores y in fp16 already (y16), half the bytes to read.
 __global__ void __launch_bounds__(256) prefill_combine_kernel(
     float* __restrict__ out, const float* __restrict__ residual, uint16_t* __restrict__ out16,
     const uint16_t* __restrict__ res16, const float* __restrict__ y,
+    const uint16_t* __restrict__ y16,
     const float* __restrict__ weight, const int* __restrict__ gslot, const int* __restrict__ off,
     const float* __restrict__ sgate, int n_expert, int k, int hidden, int has_shared) {
   // 1-D grid, token-major: ceil(hidden / 1024) workgroups per token, so the
@@ -1011,10 +1029,24 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(
       wv[u] = kk <= k ? weight[t * (k + 1) + kk] : 0.f;
     }
     float4 yv[8];
+    if (y16) {
+      uint2 yh[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      yv[u] = pos[u] >= 0 ? *reinterpret_cast<const float4*>(y + static_cast<long long>(pos[u]) * hidden + i)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int u = 0; u < 8; ++u)
+        yh[u] = pos[u] >= 0
+                    ? *reinterpret_cast<const uint2*>(y16 + static_cast<long long>(pos[u]) * hidden + i)
+                    : make_uint2(0u, 0u);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        yv[u] = make_float4(f16v(yh[u].x & 0xFFFFu), f16v(yh[u].x >> 16), f16v(yh[u].y & 0xFFFFu),
+                            f16v(yh[u].y >> 16));
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        yv[u] = pos[u] >= 0
+                    ? *reinterpret_cast<const float4*>(y + static_cast<long long>(pos[u]) * hidden + i)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     if (out16) {
       auto r16 = [](float v) { return f16v(f16b(v)); };
 #pragma unroll
@@ -1051,6 +1083,73 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(
   } else {
     *reinterpret_cast<float4*>(out + o) = acc;
   }
+}
+
+// The combine on the fp16 buffers with fp16 slot outputs (the session's
+// path): the arithmetic of prefill_combine_kernel's out16 branch, eight
+// columns per thread so every slot row is read with 16-B loads, one
+// workgroup of 256 threads per 2048 columns of a token.
+__global__ void __launch_bounds__(256) prefill_combine16_kernel(
+    uint16_t* __restrict__ out16, const uint16_t* __restrict__ res16,
+    const uint16_t* __restrict__ y16, const float* __restrict__ weight,
+    const int* __restrict__ gslot, const int* __restrict__ off, const float* __restrict__ sgate,
+    int n_expert, int k, int hidden, int has_shared) {
+  const int nbx = (hidden + 2047) / 2048;
+  const int t = blockIdx.x / nbx;
+  const int i = ((blockIdx.x - t * nbx) * 256 + threadIdx.x) * 8;
+  if (i >= hidden) return;
+  const long long o = static_cast<long long>(t) * hidden + i;
+  auto unpack = [](const uint4 v, float (&f)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f[2 * j] = f16v(w[j] & 0xFFFFu);
+      f[2 * j + 1] = f16v(w[j] >> 16);
+    }
+  };
+  float acc[8];
+  if (res16) {
+    unpack(*reinterpret_cast<const uint4*>(res16 + o), acc);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  }
+  const int shared_pos = off[n_expert] + t;
+  const float gs = sgate ? sgate[t] : 1.f;
+  for (int k0 = 0; k0 <= k; k0 += 8) {
+    int pos[8];
+    float wv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int kk = k0 + u;
+      pos[u] = kk < k ? gslot[t * k + kk] : (kk == k && has_shared ? shared_pos : -1);
+      wv[u] = kk <= k ? weight[t * (k + 1) + kk] : 0.f;
+    }
+    uint4 yh[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      yh[u] = pos[u] >= 0
+                  ? *reinterpret_cast<const uint4*>(y16 + static_cast<long long>(pos[u]) * hidden + i)
+                  : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (k0 + u > k) continue;
+      float yv[8];
+      unpack(yh[u], yv);
+      if (k0 + u == k) {  // the shared slot, gated on its fp16 value and rounded again
+#pragma unroll
+        for (int j = 0; j < 8; ++j) yv[j] = f16v(f16b(yv[j] * gs));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(wv[u], yv[j], acc[j]);
+    }
+  }
+  uint4 r;
+  r.x = f16b(acc[0]) | (static_cast<uint32_t>(f16b(acc[1])) << 16);
+  r.y = f16b(acc[2]) | (static_cast<uint32_t>(f16b(acc[3])) << 16);
+  r.z = f16b(acc[4]) | (static_cast<uint32_t>(f16b(acc[5])) << 16);
+  r.w = f16b(acc[6]) | (static_cast<uint32_t>(f16b(acc[7])) << 16);
+  *reinterpret_cast<uint4*>(out16 + o) = r;
 }
 
 // sgate[t] = sigmoid(w . x[t]): the shared expert's scalar gate
@@ -1282,15 +1381,19 @@ static int prefill_launch(const sg_block_q4k* const* tab_gate, const sg_block_q4
   float* h = reinterpret_cast<float*>(base + ws.h);
   unsigned char* hq = base + ws.hq;
   float* y = reinterpret_cast<float*>(base + ws.y);
+  // fp16 session buffers: y in fp16 (the combine rounds it to fp16 on use anyway)
+  uint16_t* y16 = po.out16 ? reinterpret_cast<uint16_t*>(base + ws.y) : nullptr;
   const int has_shared = n_sh == 3;
   // the gate scales the shared expert only: without one it has nothing to scale
   float* sgate = has_shared && sh_gate_w ? reinterpret_cast<float*>(base + ws.sgate) : nullptr;
 
   if (logits && n_expert <= 512) {  // routing and Q8_K of x in one launch
     const long long nxb = static_cast<long long>(hidden / kQK) * n_tokens;
-    const unsigned grid = static_cast<unsigned>(n_tokens + (nxb + 3) / 4);
+    const long long qwaves = (nxb + 3) / 4;  // four blocks per wave
+    const unsigned grid = static_cast<unsigned>((n_tokens + kRqWaves - 1) / kRqWaves +
+                                                (qwaves + kRqWaves - 1) / kRqWaves);
     auto launch = [&](auto kern) {
-      hipLaunchKernelGGL(kern, dim3(grid), dim3(64), 0, s, logits, idx, weight, n_tokens,
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRqWaves), 0, s, logits, idx, weight, n_tokens,
                          n_expert, k, shared_w, x, xq, nxb);
     };
     if (n_expert <= 64) launch(route_quantize_kernel<1>);
@@ -1344,6 +1447,7 @@ static int prefill_launch(const sg_block_q4k* const* tab_gate, const sg_block_q4
   gd.xq = hq;
   gd.grows = nullptr;
   gd.out = y;
+  gd.out16 = y16;
   gd.nb = n_ff / kQK;
   gd.n_rows = hidden;
   gd.n_out = hidden;
@@ -1353,15 +1457,27 @@ static int prefill_launch(const sg_block_q4k* const* tab_gate, const sg_block_q4
   gd.spw = 1;
   if (gd.nb <= 2)
     while (gd.spw < kDownSlicesPerWg && gd.n_slices % (2 * gd.spw) == 0) gd.spw *= 2;
-  if (gd.spw > 1)
-    hipLaunchKernelGGL((grouped_mfma_kernel<false, true>), dim3(tiles8 * (gd.n_slices / gd.spw)),
-                       dim3(kThreads), kGroupedLds, s, gd);
-  else
-    hipLaunchKernelGGL((grouped_mfma_kernel<false, false>), dim3(tiles8 * gd.n_slices),
-                       dim3(kThreads), kGroupedLds, s, gd);
+  auto down = [&](auto kern, int n_wg) {
+    hipLaunchKernelGGL(kern, dim3(tiles8 * n_wg), dim3(kThreads), kGroupedLds, s, gd);
+  };
+  if (gd.spw > 1) {
+    if (y16) down(grouped_mfma_kernel<false, true, true>, gd.n_slices / gd.spw);
+    else down(grouped_mfma_kernel<false, true>, gd.n_slices / gd.spw);
+  } else {
+    if (y16) down(grouped_mfma_kernel<false, false, true>, gd.n_slices);
+    else down(grouped_mfma_kernel<false, false>, gd.n_slices);
+  }
   if (int st = check_launch("sg_moe_prefill/down")) return st;
+  // (16-B loads of the caller's fp16 buffers need them 16-B aligned)
+  const bool al16 = (reinterpret_cast<uintptr_t>(po.out16) | reinterpret_cast<uintptr_t>(po.res16)) % 16 == 0;
+  if (y16 && al16) {
+    hipLaunchKernelGGL(prefill_combine16_kernel, dim3((hidden + 2047) / 2048 * n_tokens), dim3(256),
+                       0, s, po.out16, po.res16, y16, weight, gslot, off, sgate, n_expert, k,
+                       hidden, has_shared);
+    return check_launch("sg_moe_prefill/combine");
+  }
   hipLaunchKernelGGL(prefill_combine_kernel, dim3((hidden + 1023) / 1024 * n_tokens), dim3(256), 0, s,
-                     po.out, po.residual, po.out16, po.res16, y, weight, gslot, off, sgate,
+                     po.out, po.residual, po.out16, po.res16, y, y16, weight, gslot, off, sgate,
                      n_expert, k, hidden, has_shared);
   return check_launch("sg_moe_prefill/combine");
 }

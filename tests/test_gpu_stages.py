@@ -137,7 +137,7 @@ def test_grouped_tab_gemvs_over_plan(hidden, n_ff, tok_per):
     R, tiles = int(meta[0]), int(meta[1])
     assert R == T * k
 
-    x = rng.normal(0, 1, (T, hidden)).astype(np.float32)
+    x = rng.normal(0, 0.002, (T, hidden)).astype(np.float32)  # fp16 outputs stay finite
     xq = orc.quantize_q8_k(x)
     xg = ops.gather_rows_q8(dev(xq), plan["grows"], nbh, meta=plan["meta"], r_max=T * k)
     np.testing.assert_array_equal(host(xg)[:R], xq[grows[:R]])
@@ -178,6 +178,7 @@ def test_grouped_tab_gemvs_over_plan(hidden, n_ff, tok_per):
         if p1 == p0:
             continue
         rd = orc.float_to_half(orc.gemv(down[e], hq_h[p0:p1], hidden, n_ff, p1 - p0))
+        assert np.isfinite(rd.view(np.float16).astype(np.float32)).all()
         np.testing.assert_array_equal(y_h[p0:p1].view(np.uint16), rd, err_msg=f"down e={e}")
 
 
