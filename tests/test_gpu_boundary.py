@@ -263,10 +263,13 @@ def _check_plan(idx, w, E, k, tok_per, shared_tail=0):
 
 @pytest.mark.parametrize("n_rows,E,k,shared", [(2048, 256, 8, 0), (2048, 256, 8, 1),
                                                (4096, 256, 8, 0), (300, 1024, 4, 1),
-                                               (33, 32, 8, 0)])
+                                               (33, 32, 8, 0), (9000, 64, 4, 1),
+                                               (60000, 16, 2, 0)])
 def test_dispatch_plan_matches_oracle(n_rows, E, k, shared):
     """T=2048, E=256 is config 5's plan; T=4096, E=256 takes the global-memory
-    bitmap path (n_w * E beyond the LDS copy); invalid ids sit past token 32."""
+    bitmap path (n_w * E beyond the LDS copy); invalid ids sit past token 32.
+    9000 rows take two bitmap words per expert and workgroup (byte counts),
+    60000 rows eight (counts in words: 32 * 8 > 255)."""
     rng = np.random.default_rng(n_rows * 3 + E + shared)
     idx = _routes(rng, n_rows, E, k)
     idx[3, 1] = E + 5
