@@ -347,7 +347,8 @@ def traffic_run(torch, np, ops, gen, layers, n_steps=32):
     (the scale reference: it reads and writes exactly 256 MiB), then n_steps
     config-2 decode steps on rotated layers as separate front and back
     launches, 32 config-1 GEMVs on distinct 2048 x 2048 matrices, and one
-    config-5 prefill chunk (2048 tokens)."""
+    config-5 prefill chunk (2048 tokens) through the fp32 entry and one on the
+    session's fp16 buffers."""
     from sager_amd.synth import q4k_random_dev
     src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
@@ -382,6 +383,10 @@ def traffic_run(torch, np, ops, gen, layers, n_steps=32):
     l5 = torch.from_numpy(rng5.uniform(0, 1, (T5, E)).astype(np.float32)).cuda()
     pre.forward(x5, l5)
     torch.cuda.synchronize()
+    xn5 = (x5 * 0.005).half()
+    r5 = torch.zeros((T5, H), dtype=torch.float16, device="cuda")
+    pre.forward_f16(xn5, None, l5, residual=r5, out=r5)
+    torch.cuda.synchronize()
     print(json.dumps({"traffic_run": {"copy_bytes": 2 * src.numel() * 4, "steps": n_steps}}),
           flush=True)
     return 0
@@ -409,12 +414,20 @@ TRAFFIC_KERNELS = {
                           9 * MAT_BYTES + 9 * F * 4 + 2 * 9 * H * 4 + H * 4),
     "gemv_lat_plain_kernel": ("GEMV 2048x2048 (config 1)",
                                                2048 * 8 * 144 + 8 * 276 + 2048 * 4),
-    "grouped_mfma_kernel<true>": ("prefill gate/up + SiLU (config 5)",
-                                  E * 2 * MAT_BYTES + 2048 * 8 * 276 + T5_ROUTES * F * 4),
-    "grouped_mfma_kernel<false>": ("prefill down (config 5)",
-                                   E * MAT_BYTES + T5_ROUTES * 2 * 276 + T5_ROUTES * H * 4),
-    "prefill_combine_kernel": ("prefill combine (config 5)",
+    "grouped_mfma_kernel<true, false, false>": ("prefill gate/up + SiLU (config 5)",
+                                                E * 2 * MAT_BYTES + 2048 * 8 * 276 +
+                                                T5_ROUTES * F * 4),
+    "grouped_mfma_kernel<false, true, false>": ("prefill down, fp32 slot outputs (config 5)",
+                                                E * MAT_BYTES + T5_ROUTES * 2 * 276 +
+                                                T5_ROUTES * H * 4),
+    "grouped_mfma_kernel<false, true, true>": ("prefill down, fp16 slot outputs (config 5, "
+                                               "fp16 buffers)",
+                                               E * MAT_BYTES + T5_ROUTES * 2 * 276 +
+                                               T5_ROUTES * H * 2),
+    "prefill_combine_kernel": ("prefill combine, fp32 (config 5)",
                                T5_ROUTES * H * 4 + 2048 * H * 4),
+    "prefill_combine16_kernel": ("prefill combine on the fp16 buffers (config 5)",
+                                 T5_ROUTES * H * 2 + 2 * 2048 * H * 2),
 }
 
 
@@ -438,7 +451,8 @@ def traffic_summary(fetch_csv, write_csv):
     f_scale, w_scale = copy_kib / copy_med(fe), copy_kib / copy_med(wr)
     out = {"workload": "bench.py --only traffic: 32 config-2 decode steps (front and back "
                        "launches) on 16 rotated layers, 32 config-1 GEMVs on distinct "
-                       "matrices, one config-5 prefill chunk",
+                       "matrices, one config-5 prefill chunk through the fp32 entry and one "
+                       "on the fp16 buffers",
            "source_hash": source_hash(),
            "copy_reference": {"bytes_each_way": (64 << 20) * 4,
                               "fetch_kib_median": copy_med(fe), "write_kib_median": copy_med(wr),
