@@ -288,9 +288,13 @@ int sg_moe_layer(const sg_block_q4k* const* tab_gate,
  *   residual fp16 [n_tokens][hidden] or NULL (0); may alias out (x_ is both
  *            in the reference);
  *   out      fp16 [n_tokens][hidden].
- * The expert chain is sg_moe_layer's (fp32 h, as the CPU path computes);
- * the slot outputs are stored as fp16, as the reference's f16out GEMVs
- * store them, the shared one is gated on its fp16 value and stored again
+ * The expert chain rounds where the session stores fp16: each expert's
+ * gate and up outputs are rounded to fp16 (the f16out GEMVs), h =
+ * fp16(SiLU(g) * u) (silu_mul_f16) and Q8_K of h is taken from those
+ * values (session.cpp:1862-1869, 2791-2803, 2893-2898); the GEMVs' own
+ * arithmetic is sg_moe_layer's.  The slot outputs are stored as fp16, as the
+ * reference's f16out GEMVs store them, the shared one is gated on its fp16
+ * value and stored again
  * (sigmoid_gate_scalar_batched_f16), and the combine accumulates in fp32
  * from the fp16 residual in slot order and stores fp16
  * (moe_combine_batched_f16, moe.cu:265-280; session.cpp:3029).  Everything
@@ -408,9 +412,10 @@ int sg_moe_prefill(const sg_block_q4k* const* tab_gate,
                    int n_expert, int k, float shared_w, void* stream);
 
 /* sg_moe_prefill on the session's fp16 buffers: the arguments and the
- * fp16 slot-output / combine rounding of sg_moe_layer_f16 (xn fp16, xq an
- * optional Q8_K of it used as is, residual/out fp16; session.cpp:2643-2840
- * then moe_combine_batched_f16 at :3029). */
+ * fp16 roundings of sg_moe_layer_f16 (g, u and h of every expert, the slot
+ * outputs, the combine; xn fp16, xq an optional Q8_K of it used as is,
+ * residual/out fp16; session.cpp:2643-2840 then moe_combine_batched_f16 at
+ * :3029). */
 int sg_moe_prefill_f16(const sg_block_q4k* const* tab_gate,
                        const sg_block_q4k* const* tab_up,
                        const sg_block_q4k* const* tab_down,

@@ -24,8 +24,9 @@
  *   orc_float_to_half                      - numpy float16 conversion (RNE)
  *                                            over edge and random values
  *   orc_moe_layer_f16io                    - composition: the fp32 layer's
- *                                            slot outputs, rounded and
- *                                            combined as written here
+ *                                            GEMVs with g, u, h and the
+ *                                            slot outputs rounded, combined
+ *                                            as written here
  *   orc_dispatch_scan                      - counting invariants
  *   orc_dequant_q6k                        - closed form per field (numpy)
  *   orc_q6k_subgroup_dots                  - brute force from the dequant
@@ -412,8 +413,12 @@ void orc_silu_mul(const float* g, const float* u, float* h, int n) {
 
 /* ---- expert FFN (q4_avx2.cpp:175-196) ---------------------------------- */
 
+/* f16_mid: the session's fp16 buffers - g and u stored as fp16 by the
+ * f16out GEMVs, h = fp16(SiLU(g) * u) by silu_mul_f16, and h quantized from
+ * those fp16 values (session.cpp:1862-1869, 2791-2803, 2893-2898). */
 static void ffn_q8(const void* wg, const void* wu, const void* wd,
-                   const orc_q8k* xq, float* y, int hidden, int n_ff, int int_first) {
+                   const orc_q8k* xq, float* y, int hidden, int n_ff, int int_first,
+                   int f16_mid) {
   float* g = (float*)malloc(sizeof(float) * 3 * (size_t)n_ff);
   float* u = g + n_ff;
   float* h = u + n_ff;
@@ -422,7 +427,14 @@ static void ffn_q8(const void* wg, const void* wu, const void* wd,
       int_first ? orc_gemv_q4k_q8_int : orc_gemv_q4k_q8;
   gemv(wg, xq, g, n_ff, hidden, 1);
   gemv(wu, xq, u, n_ff, hidden, 1);
+  if (f16_mid)
+    for (int i = 0; i < n_ff; ++i) {
+      g[i] = f16_round(g[i]);
+      u[i] = f16_round(u[i]);
+    }
   orc_silu_mul(g, u, h, n_ff);
+  if (f16_mid)
+    for (int i = 0; i < n_ff; ++i) h[i] = f16_round(h[i]);
   orc_quantize_q8_k(h, hq, n_ff, 1);
   gemv(wd, hq, y, hidden, n_ff, 1);
   free(hq);
@@ -433,7 +445,7 @@ void orc_expert_ffn(const void* wg, const void* wu, const void* wd,
                     const float* x, float* y, int hidden, int n_ff) {
   orc_q8k* xq = (orc_q8k*)malloc(sizeof(orc_q8k) * (size_t)(hidden / 256));
   orc_quantize_q8_k(x, xq, hidden, 1);
-  ffn_q8(wg, wu, wd, xq, y, hidden, n_ff, 0);
+  ffn_q8(wg, wu, wd, xq, y, hidden, n_ff, 0, 0);
   free(xq);
 }
 
@@ -524,7 +536,7 @@ typedef struct {
   const void *wg, *wu, *wd;
   const orc_q8k* xq;
   float* y;
-  int hidden, n_ff, int_first;
+  int hidden, n_ff, int_first, f16_mid;
 } ffn_job;
 
 typedef struct {
@@ -544,7 +556,7 @@ static void run_job(const ffn_job* j) {
     memset(j->y, 0, sizeof(float) * (size_t)j->hidden);
     return;
   }
-  ffn_q8(j->wg, j->wu, j->wd, j->xq, j->y, j->hidden, j->n_ff, j->int_first);
+  ffn_q8(j->wg, j->wu, j->wd, j->xq, j->y, j->hidden, j->n_ff, j->int_first, j->f16_mid);
 }
 
 static void* worker(void* arg) {
@@ -612,6 +624,7 @@ static void moe_layer_routed(const void* const* tab_gate, const void* const* tab
       j->hidden = hidden;
       j->n_ff = n_ff;
       j->int_first = int_first;
+      j->f16_mid = f16_io;
       if (kk < k) {
         const int e = idx[t * slots + kk];
         if (e < 0 || e >= n_expert) {
@@ -634,7 +647,8 @@ static void moe_layer_routed(const void* const* tab_gate, const void* const* tab
    * of token t is scaled by sigmoid(sh_gate_w . x[t]) before the combine */
   if (f16_io) {
     /* the session's fp16 buffers (session.cpp:2850-2930, moe.cu:249-292):
-     * every slot output is stored as fp16 (the f16out GEMVs), the shared
+     * each expert's g, u and h were fp16 (ffn_q8's f16_mid above); every
+     * slot output is stored as fp16 (the f16out GEMVs), the shared
      * slot is gated in place on its fp16 value (sigmoid_gate_scalar_batched
      * _f16: fp16(fp16(y) * s)), then moe_combine_batched_f16 accumulates
      * acc = fp32(residual fp16), acc = fma(w, fp32(y fp16), acc) in slot

@@ -424,6 +424,9 @@ __device__ __forceinline__ uint16_t f16b(float v) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 
+// v rounded to fp16 and read back as fp32 (a value stored in an fp16 buffer)
+__device__ __forceinline__ float f16r(float v) { return f16v(f16b(v)); }
+
 // sigmoid(g) = 1 / (1 + exp(-g)), the shared-expert gate
 // (moe.cu:289, norm_rotary.cu:182).
 __host__ __device__ __forceinline__ float sigmoid_sg(float g) {

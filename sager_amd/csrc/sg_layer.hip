@@ -474,10 +474,14 @@ __device__ __forceinline__ void build_plan(uint32_t* dyn, const FrontLds& L, int
 // bytes the wave already copied into buf (gate rows, then up rows), for the
 // n entries (tok[j], slot[j]); x in LDS as staged Q8_K (xs).  Lanes 0-31
 // hold gate super-blocks, lanes 32-63 the same up rows.
+// r16 (the layer on the session's fp16 buffers): g and u are rounded to
+// fp16 before the SiLU and h after it, as the session stores them
+// (gemv_ptrs_q4_k_q8_f16out, then silu_mul_f16: session.cpp:1862-1869).
 template <typename Entry>
 __device__ __forceinline__ void gateup_wave(bool present, int row0, int nrw, int nbh, int lpr,
                                             const uint32_t* buf, const uint32_t* xs, Entry entry,
-                                            int n, int stride, int n_ff, float* h, int lane) {
+                                            int n, int stride, int n_ff, float* h, int lane,
+                                            bool r16) {
   const int half = lane >> 5, hl = lane & 31;
   const int blk = hl & (lpr - 1), rr = hl / lpr;
   const bool live = present && blk < nbh && rr < nrw;
@@ -503,7 +507,7 @@ __device__ __forceinline__ void gateup_wave(bool present, int row0, int nrw, int
     const float up = __shfl_xor(acc, 32, 64);
     if (half == 0 && blk == nbh - 1 && rr < nrw)
       h[(static_cast<long long>(t) * stride + sl) * n_ff + row0 + rr] =
-          present ? silu_mul(acc, up) : 0.f;
+          !present ? 0.f : r16 ? f16r(silu_mul(f16r(acc), f16r(up))) : silu_mul(acc, up);
   }
 }
 
@@ -516,14 +520,15 @@ __device__ __forceinline__ void gateup_wave(bool present, int row0, int nrw, int
 // its weights in registers, as many per round as fit.  x is read from LDS
 // one sub-block group at a time, which keeps the kernel within 128
 // registers (four workgroups per CU).  Every wave of the workgroup calls
-// this with the same n.
+// this with the same n.  r16: fp16 g, u and h, as in gateup_wave (the
+// session's grouped path: session.cpp:2791-2803).
 constexpr int kSpaceWords = 4 * 64 * 36;
 template <typename Entry>
 __device__ __forceinline__ void gateup_group(bool present, int row0, int nrw, int nbh, int lpr,
                                              const uint32_t* buf, uint32_t* xspace,
                                              const uint32_t* x0, const uint32_t* xq, Entry entry,
                                              int n, int stride, int n_ff, float* h, int lane,
-                                             int wave) {
+                                             int wave, bool r16) {
   const int half = lane >> 5, hl = lane & 31;
   const int blk = hl & (lpr - 1), rr = hl / lpr;
   const bool live = present && blk < nbh && rr < nrw;
@@ -570,7 +575,7 @@ __device__ __forceinline__ void gateup_group(bool present, int row0, int nrw, in
     const float up = __shfl_xor(acc, 32, 64);
     if (half == 0 && blk == nbh - 1 && rr < nrw)
       h[(static_cast<long long>(t) * stride + sl) * n_ff + row0 + rr] =
-          present ? silu_mul_kc(acc, up) : 0.f;
+          !present ? 0.f : r16 ? f16r(silu_mul_kc(f16r(acc), f16r(up))) : silu_mul_kc(acc, up);
   };
   if (n > 0) {
     int t, sl;
@@ -1217,7 +1222,8 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
     bar();
     // entries: tokens 0..T-1 in slot k, no plan needed
     gateup_wave(true, row0, nrw, nbh, lpr, buf, xs,
-                [&](int j, int& t, int& sl) { t = j; sl = k; }, T, stride, a.n_ff, a.h, lane);
+                [&](int j, int& t, int& sl) { t = j; sl = k; }, T, stride, a.n_ff, a.h, lane,
+                a.out16 != nullptr);
     if (a.sh_gate_w && bx == 0) shared_gate_tokens(a, tid);
     return;
   }
@@ -1392,7 +1398,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
       }
       gateup_wave(present_mine, row0, nrw, nbh, lpr, buf, xs,
                   [&](int, int& t, int& sl) { t = 0; sl = slot_mine; }, 1, stride, a.n_ff, a.h,
-                  lane);
+                  lane, a.out16 != nullptr);
       return;
     }
     n_groups = gbase + ctrl[1];
@@ -1488,7 +1494,7 @@ __device__ __forceinline__ void front_body(const LayerArgs& a, int bx, int g, ui
   const int j0 = poff[g];
   gateup_wave(present, row0, nrw, nbh, lpr, buf, xs,
               [&](int j, int& t, int& sl) { t = ptok[j0 + j]; sl = pslot[j0 + j]; },
-              poff[g + 1] - j0, stride, a.n_ff, a.h, lane);
+              poff[g + 1] - j0, stride, a.n_ff, a.h, lane, a.out16 != nullptr);
 }
 
 // The decode model shape (one token, hidden 2048, n_ff 512, 256 experts,
@@ -1617,7 +1623,7 @@ layer_gateup_kernel(LayerArgs args) {
   bar();
   gateup_group(present, row0, nrw, nbh, lpr, wbuf[wave], &wbuf[0][0], x0, a.xq,
                [&](int j, int& t, int& sl) { t = etok[j0 + j]; sl = eslot[j0 + j]; }, n, stride,
-               a.n_ff, a.h, lane, wave);
+               a.n_ff, a.h, lane, wave, a.out16 != nullptr);
   if (g == 0 && a.has_shared && a.sh_gate_w && bx == 0) shared_gate_tokens(a, tid);
 }
 

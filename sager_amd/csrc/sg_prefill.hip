@@ -279,6 +279,8 @@ struct GroupedArgs {
   int n_slices;             // column slices per tile
   int spw;                  // slices per workgroup (the kMulti down pass, nb <= 2: the
                             // token rows stay in LDS across them), a divisor of n_slices
+  int r16;                  // gate/up pass on the session's fp16 buffers: g, u and h rounded
+                            // to fp16 as the session stores them (session.cpp:2791-2803)
 };
 
 // One workgroup = one column slice of one tile (up to 128 positions of one
@@ -530,7 +532,18 @@ grouped_mfma_kernel(GroupedArgs a) {
         gv[i] = up_wave ? other : acc[ti][i];
         uv[i] = up_wave ? acc[ti][i] : other;
       }
+      if (a.r16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          gv[i] = f16r(gv[i]);
+          uv[i] = f16r(uv[i]);
+        }
+      }
       silu_mul_tab_n<4>(gv, uv, hv, etab);
+      if (a.r16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hv[i] = f16r(hv[i]);
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tt = 16 * ti + 4 * lq + i;
@@ -1438,6 +1451,7 @@ static int prefill_launch(const sg_block_q4k* const* tab_gate, const sg_block_q4
   const int tiles8 = (ws.max_tiles + 7) / 8 * 8;
   ga.n_slices = n_ff / (kRowsWg / 2);
   ga.spw = 1;
+  ga.r16 = po.out16 != nullptr;
   hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(tiles8 * ga.n_slices), dim3(kThreads),
                      kGroupedLds, s, ga);
   if (int st = check_launch("sg_moe_prefill/gate_up")) return st;

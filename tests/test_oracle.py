@@ -584,10 +584,11 @@ def test_float_to_half_matches_numpy():
 
 @pytest.mark.parametrize("prefill,gate", [(False, False), (False, True), (True, True)])
 def test_moe_layer_f16_is_rounded_composition(prefill, gate):
-    """The fp16-buffer layer = the fp32 layer's slot outputs stored as fp16
-    (numpy's own conversion here), the shared slot gated on its fp16 value
-    and stored again, combined in fp32 from the fp16 residual, stored as
-    fp16."""
+    """The fp16-buffer layer = the fp32 layer's GEMVs with each expert's g
+    and u stored as fp16, h = fp16(SiLU(g) * u) quantized, the slot outputs
+    stored as fp16 (numpy's own conversion here), the shared slot gated on
+    its fp16 value and stored again, combined in fp32 from the fp16
+    residual, stored as fp16."""
     rng = np.random.default_rng(45)
     H, F, E, K, T = 512, 256, 8, 3, 3
     g, u, d = _experts(rng, E + 1, H, F)
@@ -605,19 +606,25 @@ def test_moe_layer_f16_is_rounded_composition(prefill, gate):
     xq = orc.quantize_q8_k(x)
     gl = orc.gemv_f32_lanes(gw[None], x)[:, 0] if gate else None
     f16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+    mv = orc.gemv_int if prefill else orc.gemv
+    n_differ = 0
     for t in range(T):
-        ys = []
-        for m in list(idx[t, :K]) + [None]:
-            wg, wu, wd = sh if m is None else (g[m], u[m], d[m])
-            if prefill:
-                gg = orc.gemv_int(wg, xq[t], F, H)[0]
-                uu = orc.gemv_int(wu, xq[t], F, H)[0]
-                hh = orc.quantize_q8_k(orc.silu_mul(gg, uu))
-                ys.append(f16(orc.gemv_int(wd, hh, H, F)[0]))
-            else:
-                ys.append(f16(orc.expert_ffn(wg, wu, wd, x[t], H, F)))
-        if gate:
-            ys[-1] = f16(ys[-1] * orc.sigmoid(gl[t]))
-        ref = orc.moe_combine(np.stack(ys)[None], w[t:t + 1], res[t:t + 1].astype(np.float32))
-        np.testing.assert_array_equal(out[t].view(np.uint16),
-                                      ref[0].astype(np.float16).view(np.uint16))
+        refs = []
+        for r_mid in (f16, lambda a: np.asarray(a, np.float32)):
+            ys = []
+            for m in list(idx[t, :K]) + [None]:
+                wg, wu, wd = sh if m is None else (g[m], u[m], d[m])
+                # g and u stored as fp16, h = fp16(SiLU(g) * u), Q8_K of those values
+                gg = r_mid(mv(wg, xq[t], F, H)[0])
+                uu = r_mid(mv(wu, xq[t], F, H)[0])
+                hh = orc.quantize_q8_k(r_mid(orc.silu_mul(gg, uu)))
+                ys.append(f16(mv(wd, hh, H, F)[0]))
+            if gate:
+                ys[-1] = f16(ys[-1] * orc.sigmoid(gl[t]))
+            ref = orc.moe_combine(np.stack(ys)[None], w[t:t + 1], res[t:t + 1].astype(np.float32))
+            refs.append(ref[0].astype(np.float16).view(np.uint16))
+        np.testing.assert_array_equal(out[t].view(np.uint16), refs[0])
+        n_differ += int((refs[0] != refs[1]).sum())
+    # the intermediate fp16 roundings change the output: this test tells the
+    # two compositions apart
+    assert n_differ > 0
