@@ -271,7 +271,8 @@ struct GroupedArgs {
   const TileRec* trec;      // work list: one record per tile, group -1 past it
   int n_rec;                // records in trec
   float* out;               // [P][n_out]: h (gate/up pass) or y (down)
-  uint16_t* out16;          // [P][n_out] fp16 y (the down pass's kF16Out instances)
+  uint16_t* out16;          // [P][n_out] fp16 y (the down pass's kF16Out instances), or
+                            // fp16 h (gate/up pass with r16: h is an fp16 value there)
   int nb;                   // super-blocks per weight row
   int n_rows;               // rows of each weight matrix
   int n_out;                // output row stride (= n_rows)
@@ -324,7 +325,7 @@ grouped_mfma_kernel(GroupedArgs a) {
   if (!ma) {  // absent expert (a null gate, up or down matrix): its outputs are zero
     for (long long p = p0; p < p1; ++p)
       for (int r = tid; r < spw * kCols; r += kThreads) {
-        if (kF16Out) a.out16[p * a.n_out + c0 + r] = 0;
+        if (kF16Out || (kGateUp && a.r16)) a.out16[p * a.n_out + c0 + r] = 0;
         else a.out[p * a.n_out + c0 + r] = 0.f;
       }
     return;
@@ -548,7 +549,11 @@ grouped_mfma_kernel(GroupedArgs a) {
       for (int i = 0; i < 4; ++i) {
         const int tt = 16 * ti + 4 * lq + i;
         if (tt < nt)
-          a.out[static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * (wave & 3) + lr] = hv[i];
+        {
+          const long long o = static_cast<long long>(t0 + tt) * a.n_out + c0 + 16 * (wave & 3) + lr;
+          if (a.r16) a.out16[o] = f16b(hv[i]);
+          else a.out[o] = hv[i];
+        }
       }
     }
   } else {
@@ -949,7 +954,9 @@ __device__ __forceinline__ void x_block_q8p(const XSrc& x, unsigned char* __rest
 // rows_used (optional, device): only the first *rows_used rows hold data
 // (the positions the plan filled); whole 16-lane rows past them exit before
 // any lane exchange.
+// in16 (instead of in): fp16 values (h of the fp16-buffer path).
 __global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __restrict__ in,
+                                                               const uint16_t* __restrict__ in16,
                                                                unsigned char* __restrict__ out,
                                                                long long n_blocks,
                                                                const int* __restrict__ rows_used,
@@ -958,8 +965,23 @@ __global__ void __launch_bounds__(256) prefill_quantize_kernel(const float* __re
   const long long blk =
       (static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
   if (rows_used && blk >= static_cast<long long>(*rows_used) * nb_row) return;
+  const long long bc = blk < n_blocks ? blk : n_blocks - 1;
   float v[16];
-  load16(in, blk < n_blocks ? blk : n_blocks - 1, lane, v);
+  if (in16) {
+    const uint4* src = reinterpret_cast<const uint4*>(in16 + bc * kQK + 16 * (lane & 15));
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint4 w = src[q];
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[8 * q + 2 * i] = f16v(ww[i] & 0xFFFFu);
+        v[8 * q + 2 * i + 1] = f16v(ww[i] >> 16);
+      }
+    }
+  } else {
+    load16(in, bc, lane, v);
+  }
   quantize_rows16(v, out, n_blocks, blk, lane);
 }
 
@@ -1231,12 +1253,13 @@ static PrefillWs prefill_ws(int T, int hidden, int n_ff, int E, int k) {
 }
 
 // the grouped kernels' Q8P input
-static int quantize_split(const float* in, unsigned char* out, int nb_row, int n_rows,
-                          hipStream_t s, const char* nm, const int* rows_used = nullptr) {
+static int quantize_split(const float* in, const uint16_t* in16, unsigned char* out, int nb_row,
+                          int n_rows, hipStream_t s, const char* nm,
+                          const int* rows_used = nullptr) {
   const long long n_blocks = static_cast<long long>(nb_row) * n_rows;
   const unsigned grid = static_cast<unsigned>((n_blocks + 15) / 16);
-  hipLaunchKernelGGL(prefill_quantize_kernel, dim3(grid), dim3(256), 0, s, in, out, n_blocks,
-                     rows_used, nb_row);
+  hipLaunchKernelGGL(prefill_quantize_kernel, dim3(grid), dim3(256), 0, s, in, in16, out,
+                     n_blocks, rows_used, nb_row);
   return check_launch(nm);
 }
 
@@ -1452,11 +1475,16 @@ static int prefill_launch(const sg_block_q4k* const* tab_gate, const sg_block_q4
   ga.n_slices = n_ff / (kRowsWg / 2);
   ga.spw = 1;
   ga.r16 = po.out16 != nullptr;
+  // fp16 h on the fp16 buffers (its values are fp16 there): half the bytes
+  uint16_t* h16 = ga.r16 ? reinterpret_cast<uint16_t*>(h) : nullptr;
+  ga.out16 = h16;
   hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(tiles8 * ga.n_slices), dim3(kThreads),
                      kGroupedLds, s, ga);
   if (int st = check_launch("sg_moe_prefill/gate_up")) return st;
   // h rows of the filled positions only: off[E + 1] = routes + shared rows
-  if (int st = quantize_split(h, hq, n_ff / kQK, ws.P, s, nm, off + n_expert + 1)) return st;
+  if (int st = quantize_split(h16 ? nullptr : h, h16, hq, n_ff / kQK, ws.P, s, nm,
+                              off + n_expert + 1))
+    return st;
   GroupedArgs gd = ga;
   gd.xq = hq;
   gd.grows = nullptr;

@@ -599,6 +599,30 @@ def test_moe_prefill_routed_edge_cases():
     assert_fp32_parity(host(out), ref)
 
 
+def test_moe_prefill_f16_routed_edge_cases():
+    """The same caller routing on the session's fp16 buffers (fp16 g, u and
+    h, fp16 slot outputs; the absent expert's zeroed h rows are fp16 there),
+    the fp16 residual updated in place."""
+    rng = np.random.default_rng(79)
+    H, F, E, K, T = 512, 256, 8, 2, 5
+    g, u, d = _expert_pool(rng, E, H, F)
+    g[3] = None
+    xn = rng.normal(0, 0.02, (T, H)).astype(np.float16)
+    idx = np.array([[1, 99, -1], [2, 3, -1], [3, 5, -1], [4, 4, -1], [0, 7, -1]], np.int32)
+    w = rng.uniform(0.1, 1, (T, K + 1)).astype(np.float32)
+    res = rng.normal(0, 1, (T, H)).astype(np.float16)
+    layer = _prefill(g, u, d, None, H, F, K, T)
+    io = dev(res)
+    wd = dev(w)
+    out, _, wgt = layer.forward_f16(dev(xn), None, None, residual=io, out=io, idx=dev(idx),
+                                    weight=wd)
+    ref, _, rw = orc.moe_layer_f16(g, u, d, None, xn, idx=idx, weight=w, residual16=res,
+                                   hidden=H, n_ff=F, k=K, prefill=True)
+    assert np.isfinite(ref.astype(np.float32)).all()
+    np.testing.assert_array_equal(host(wgt), rw)
+    np.testing.assert_array_equal(host(out).view(np.uint16), ref.view(np.uint16))
+
+
 def test_moe_prefill_vs_decode_path():
     """The prefill path and the decode path agree on indices and weights and,
     through their different fp32 epilogue orders, on the outputs to within
