@@ -623,6 +623,31 @@ def test_moe_prefill_f16_routed_edge_cases():
     np.testing.assert_array_equal(host(out).view(np.uint16), ref.view(np.uint16))
 
 
+def test_moe_prefill_f16_unaligned_buffers():
+    """The fp16 combine reads and writes 16 B per thread only when the
+    residual and output are 16-B aligned; buffers 8 B off that alignment
+    take the 8-B path, with the same bits."""
+    rng = np.random.default_rng(81)
+    H, F, E, K, T = 512, 256, 8, 2, 7
+    g, u, d = _expert_pool(rng, E, H, F)
+    xn = rng.normal(0, 0.02, (T, H)).astype(np.float16)
+    lg = rng.normal(0, 1, (T, E)).astype(np.float32)
+    res = rng.normal(0, 1, (T, H)).astype(np.float16)
+    layer = _prefill(g, u, d, None, H, F, K, T)
+    out_a, _, _ = layer.forward_f16(dev(xn), None, dev(lg), residual=dev(res))
+    flat_r = torch.zeros(T * H + 4, dtype=torch.float16, device="cuda")
+    flat_o = torch.zeros(T * H + 4, dtype=torch.float16, device="cuda")
+    r_u = flat_r[4:].view(T, H)
+    o_u = flat_o[4:].view(T, H)
+    r_u.copy_(dev(res))
+    assert r_u.data_ptr() % 16 == 8 and o_u.data_ptr() % 16 == 8
+    out_u, _, _ = layer.forward_f16(dev(xn), None, dev(lg), residual=r_u, out=o_u)
+    np.testing.assert_array_equal(host(out_u).view(np.uint16), host(out_a).view(np.uint16))
+    ref, _, _ = orc.moe_layer_f16(g, u, d, None, xn, logits=lg, residual16=res, hidden=H,
+                                  n_ff=F, k=K, prefill=True)
+    np.testing.assert_array_equal(host(out_a).view(np.uint16), ref.view(np.uint16))
+
+
 def test_moe_prefill_vs_decode_path():
     """The prefill path and the decode path agree on indices and weights and,
     through their different fp32 epilogue orders, on the outputs to within
