@@ -133,6 +133,17 @@ __device__ __forceinline__ float serial_sum(const float* x, int n32) {
 // slot k = shared_w.  oi/ow may point to LDS or global memory; lane 0
 // writes them.  All 64 lanes must be active.  PL = experts per lane
 // (n_expert <= 64 PL).
+//
+// The model shape (256 experts, top-8, PL = 4) first tries a shorter chain:
+// the k + 1 selection rounds run on the exps e_i, interleaved with the
+// serial normalizer (every lane adds the same values, so no lane waits for
+// another), since p_i = e_i / z orders like e_i.  Let c_0 .. c_k be the
+// picks in e order.  If no two consecutive ones have equal probabilities,
+// then p(c_0) > ... > p(c_k) and every other expert has p <= p(c_k), so the
+// reference's k picks are c_0 .. c_(k-1) in that order.  An equality (from
+// equal logits, or from the division's rounding), a NaN normalizer or a
+// degenerate round among the first k falls back to the exact rounds below
+// with the same z.
 template <int PL>
 __device__ __forceinline__ void router_wave(const float* __restrict__ lg, int n_expert, int k, float shared_w,
                             int* oi, float* ow, float* ev, int lane, bool shared_slot = true) {
@@ -157,9 +168,79 @@ __device__ __forceinline__ void router_wave(const float* __restrict__ lg, int n_
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // normalizer z = (((0 + e_0) + e_1) + ...) in index order, by one lane
-  float z = lane == 0 ? serial_sum(ev, e32) : 0.f;
-  z = readlane_f(z, 0);
+  float z = 0.f;
+  bool have_z = false;
+  if constexpr (PL == 4) {
+    constexpr int kE = 256, kK = 8, kR = kK + 1, kNb = kE / 32;
+    if (n_expert == kE && k == kK) {
+      uint32_t he[kPerLane];
+#pragma unroll
+      for (int j = 0; j < kPerLane; ++j)
+        he[j] = p[j] == p[j] ? static_cast<uint32_t>(sel_key(p[j], lane + 64 * j) >> 32) : 0u;
+      const float4* x4 = reinterpret_cast<const float4*>(ev);
+      int my_i = 0;
+      float my_e = -1.f;
+      bool degen = false;
+#pragma unroll
+      for (int r = 0; r < (kR > kNb ? kR : kNb); ++r) {
+        if (r < kNb) {  // 32 more terms of the normalizer, in index order
+          float4 v[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) v[q] = x4[8 * r + q];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            z += v[q].x;
+            z += v[q].y;
+            z += v[q].z;
+            z += v[q].w;
+          }
+        }
+        if (r < kR) {  // selection round r on the exps
+          uint32_t h = he[0];
+#pragma unroll
+          for (int j = 1; j < kPerLane; ++j) h = max(h, he[j]);
+          h = wave_max_u32(h);
+          int jb = kPerLane;
+          uint64_t mb = 0;
+#pragma unroll
+          for (int j = kPerLane - 1; j >= 0; --j) {
+            const uint64_t m = __ballot(he[j] == h);
+            jb = m ? j : jb;
+            mb = m ? m : mb;
+          }
+          const bool none = h == 0u;
+          const int bi = none ? r % kE : 64 * jb + __builtin_ctzll(mb | (1ull << 63));
+          const float be = none ? -1.f : sel_val(static_cast<uint64_t>(h) << 32);
+          degen = degen || (none && r < kK);
+#pragma unroll
+          for (int j = 0; j < kPerLane; ++j) he[j] = lane + 64 * j == bi ? 0u : he[j];
+          my_i = lane == r ? bi : my_i;
+          my_e = lane == r ? be : my_e;
+        }
+      }
+      have_z = true;
+      // p of the picks (lane r), and the check of consecutive picks
+      const float pp = my_e < 0.f ? -1.f : my_e / z;
+      const float pn = __shfl_down(pp, 1, 64);
+      const bool tie = lane < kK && pp == pn;
+      if (z == z && !degen && __ballot(tie) == 0ull) {
+        float wsum = 0.f;
+#pragma unroll
+        for (int r = 0; r < kK; ++r) wsum += readlane_f(pp, r);
+        if (lane < kK) {
+          oi[lane] = my_i;
+          ow[lane] = wsum > 0.f ? pp / wsum : pp;
+        }
+        if (lane == 0 && shared_slot) ow[k] = shared_w;
+        return;
+      }
+    }
+  }
+  if (!have_z) {
+    // normalizer z = (((0 + e_0) + e_1) + ...) in index order, by one lane
+    z = lane == 0 ? serial_sum(ev, e32) : 0.f;
+    z = readlane_f(z, 0);
+  }
 #pragma unroll
   for (int j = 0; j < kPerLane; ++j)
     if (lane + 64 * j < n_expert) p[j] = p[j] / z;

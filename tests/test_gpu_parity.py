@@ -225,6 +225,32 @@ def test_router_ties_nan_degenerate():
     assert list(ri[3, :2]) == [17, 200]
 
 
+def test_router_near_ties_model_shape():
+    """256 experts, top-8 (the shape whose rounds run on the exps beside the
+    normalizer): rows where two logits are equal or one or two ulps apart,
+    at the top-k boundary and inside it, with the larger one at the higher
+    index - their exps differ by an ulp or two and their probabilities may
+    round equal, when the reference's lower-index rule decides the order."""
+    rng = np.random.default_rng(99)
+    rows = []
+    for n in range(96):
+        r = rng.normal(0, 1, 256).astype(np.float32)
+        o = np.argsort(-r, kind="stable")
+        pos = [0, 3, 6, 7, 8, 2][n % 6]
+        a, b = o[pos], o[pos + 1]
+        lo, hi = (a, b) if a < b else (b, a)  # hi: the higher index
+        base = r[lo]
+        r[hi] = base
+        for _ in range(n % 3):  # 0, 1 or 2 ulps above, at the higher index
+            r[hi] = np.nextafter(r[hi], np.float32(np.inf))
+        rows.append(r)
+    lg = np.stack(rows)
+    idx, w = ops.router_topk_batched(dev(lg), 8, shared_w=1.0)
+    ri, rw = orc.router_topk(lg, 8, 1.0)
+    np.testing.assert_array_equal(host(idx)[:, :8], ri[:, :8])
+    np.testing.assert_array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+
+
 def test_silu_bit_exact():
     rng = np.random.default_rng(12)
     g = (rng.normal(0, 4, 100000)).astype(np.float32)
